@@ -1,0 +1,172 @@
+/*
+ * mkmoe: the decode-step MoE block of one TP rank on one MI355X (gfx950), as a
+ * C ABI. One call runs the router GEMV, grouped top-k, the routed experts'
+ * gate_up GEMM, SwiGLU, the down GEMM, the shared expert and the weighted
+ * combine, and writes the bf16 partial output before the TP all-reduce.
+ *
+ * Plain C: device pointers, sizes and a HIP stream passed as void*. No C++ or
+ * torch types cross the boundary; no call allocates device memory. The caller
+ * owns every buffer, including the workspace (one per concurrent stream).
+ *
+ * Reference interfaces replaced (paths under the reference repository):
+ *   - mkmoe_forward replaces the MoE half of the FFN launch,
+ *     DSV41MonoRunner.ffn -> self.ffn_kernel(M)(...ptrs...)
+ *     (sgl_amd_mono/deepseek_v41/gfx950/runner.py:436-510), whose MoE
+ *     arguments are the ARGS tuple of gfx950/stages/moe.py:119-132
+ *     (x, gate_w, bias, w13, w13_s, w2, w2_s, sgu, sgu_s, sw2, sw2_s, out);
+ *     the launch itself is build_mono_ffn (gfx950/layer.py:601-767).
+ *   - mkmoe_workspace_bytes / mkmoe_init_workspace replace the runner's
+ *     per-width scratch and epoch buffers (runner.py:339-350,
+ *     gfx950/layer.py:113-141, moe.py:136-163 scratch_layout).
+ *   - mkmoe_read_errors / mkmoe_clear_errors replace the guard's error words
+ *     (sgl_amd_mono/common/guard.py:22-32,194-210).
+ *   - mkmoe_status_string replaces the RuntimeError reasons of
+ *     runner.py:79-119.
+ */
+#ifndef MKMOE_H
+#define MKMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MKMOE_ABI_VERSION 1
+
+/* weight formats */
+#define MKMOE_FMT_FP8_B128 1 /* e4m3, fp32 scale per 128 x 128 block */
+#define MKMOE_FMT_MXFP4 2    /* e2m1 (2 a byte, even K low nibble), E8M0 per 32 K */
+
+/* status codes (negative: an error; the call enqueued nothing) */
+#define MKMOE_OK 0
+#define MKMOE_ERR_NULL (-1)        /* a required pointer is NULL */
+#define MKMOE_ERR_SHAPE (-2)       /* no compiled specialisation has this shape */
+#define MKMOE_ERR_ROWS (-3)        /* rows < 1 or rows > max_rows */
+#define MKMOE_ERR_ALIGN (-4)       /* a pointer is not 16-byte aligned */
+#define MKMOE_ERR_WORKSPACE (-5)   /* workspace smaller than mkmoe_workspace_bytes */
+#define MKMOE_ERR_LAUNCH (-6)      /* the HIP launch failed */
+#define MKMOE_ERR_DEVICE (-7)      /* the device cannot hold the persistent grid */
+#define MKMOE_ERR_ARG (-8)         /* another invalid argument */
+#define MKMOE_ERR_HIP (-9)         /* a HIP runtime call failed */
+
+/* error words kept in the workspace (mkmoe_read_errors) */
+#define MKMOE_ERRW_CODE 0    /* 0, or the first device error's code */
+#define MKMOE_ERRW_STAGE 1   /* the stage whose wait ran past its deadline */
+#define MKMOE_ERRW_BLOCK 2   /* the workgroup that saw it */
+#define MKMOE_ERRW_COUNT 3   /* how many waits ran past their deadline */
+#define MKMOE_ERRW_WORDS 8
+#define MKMOE_DEVERR_DEADLINE 1
+
+/* One TP rank's MoE block. Routing is DeepSeek-V3's grouped top-k on sigmoid
+ * scores: choice = score + bias; groups ranked by the sum of their top two
+ * choices; topk experts chosen from the topk_group best groups; weights =
+ * score * routed_scale / sum (renorm) or score * routed_scale. */
+typedef struct mkmoe_shape {
+  int32_t hidden;        /* H */
+  int32_t experts;       /* E routed experts */
+  int32_t topk;          /* picks a row */
+  int32_t n_group;       /* expert groups (1: no groups) */
+  int32_t topk_group;    /* groups kept */
+  int32_t inter;         /* a routed expert's intermediate width on this rank */
+  int32_t shared_inter;  /* the shared expert's (FP8 128 x 128) */
+  int32_t routed_fmt;    /* MKMOE_FMT_* */
+  int32_t router_parts;  /* router K parts, summed in order */
+  int32_t renorm;        /* 1: normalise the top-k scores */
+  int32_t use_norm;      /* 1: RMSNorm x first (norm weight required) */
+  int32_t max_rows;      /* rows a call takes at most (<= 48) */
+  float routed_scale;
+  float swiglu_limit;
+  float norm_eps;
+  float reserved;
+} mkmoe_shape;
+
+/* Device pointers, read in place. Layouts (E experts, H hidden, I inter,
+ * S shared_inter; e4m3 and e2m1 as raw bytes):
+ *   gate_w bf16 [E][H]; bias fp32 [E]; norm bf16 [H] (use_norm only)
+ *   FP8_B128: w13 [E][2I][H], w13_s fp32 [E][2I/128][H/128],
+ *             w2 [E][H][I],   w2_s fp32 [E][H/128][I/128]
+ *   MXFP4:    w13 [E][2I][H/2], w13_s E8M0 [E][2I][H/32],
+ *             w2 [E][H][I/2],   w2_s E8M0 [E][H][I/32]
+ *   sgu e4m3 [2S][H] (gate rows, then up rows), sgu_s fp32 [2S/128][H/128],
+ *   sw2 e4m3 [H][S], sw2_s fp32 [H/128][S/128]
+ * w13 holds each expert's gate rows [0, I) then its up rows [I, 2I). */
+typedef struct mkmoe_weights {
+  const void* gate_w;
+  const void* bias;
+  const void* w13;
+  const void* w13_s;
+  const void* w2;
+  const void* w2_s;
+  const void* sgu;
+  const void* sgu_s;
+  const void* sw2;
+  const void* sw2_s;
+  const void* norm;
+} mkmoe_weights;
+
+int mkmoe_abi_version(void);
+
+/* 1 when this shape has a compiled specialisation, else 0. */
+int mkmoe_shape_supported(const mkmoe_shape* shape);
+
+/* Bytes of workspace one stream needs for calls of up to shape->max_rows rows. */
+int mkmoe_workspace_bytes(const mkmoe_shape* shape, size_t* bytes);
+
+/* Zero the workspace's counters and error words (enqueued on stream; not for
+ * use inside graph capture). Required once before the first forward. */
+int mkmoe_init_workspace(const mkmoe_shape* shape, void* ws, size_t ws_bytes, void* stream);
+
+/* One MoE block for rows bf16 rows x [rows][H] -> out bf16 [rows][H] (this
+ * rank's partial, before the all-reduce). topk_ids int32 [rows][topk] and
+ * topk_w fp32 [rows][topk] receive the routing when not NULL. Enqueues exactly
+ * one kernel on stream: no allocation, no host synchronisation, safe to
+ * capture in a graph (the kernel leaves its counters zeroed). Calls that may
+ * overlap need distinct workspaces. */
+int mkmoe_forward(const mkmoe_shape* shape, const mkmoe_weights* w, const void* x, int32_t rows,
+                  void* out, int32_t* topk_ids, float* topk_w, void* ws, size_t ws_bytes,
+                  void* stream);
+
+/* The same results in one launch per stage (norm, router + quantize, route +
+ * shared gate_up, routed gate_up, down + combine); for diagnosis and
+ * per-stage profiles. */
+int mkmoe_forward_staged(const mkmoe_shape* shape, const mkmoe_weights* w, const void* x,
+                         int32_t rows, void* out, int32_t* topk_ids, float* topk_w, void* ws,
+                         size_t ws_bytes, void* stream);
+
+/* Device wait deadline, in seconds, for the persistent launch's hand-offs
+ * (default 2.0). A wait past it sets the error words and the launch ends. */
+int mkmoe_set_deadline(double seconds);
+
+/* Copy the MKMOE_ERRW_WORDS error words to host memory (synchronises stream). */
+int mkmoe_read_errors(const void* ws, int32_t* words, int32_t n, void* stream);
+int mkmoe_clear_errors(void* ws, void* stream);
+
+/* Byte offset and size of a workspace region, for tests that read
+ * intermediate results: 0 x normed, 1 x codes (routed rule), 2 x scales,
+ * 3 x codes (shared rule), 4 x scales (shared rule), 5 router part sums
+ * fp32 [rows][E][parts], 6 ids int32 [rows][topk], 7 weights fp32
+ * [rows][topk], 8 shared intermediate bf16 [rows][S], 9 routed intermediate
+ * bf16 [rows * topk][I]. */
+int mkmoe_workspace_region(const mkmoe_shape* shape, int32_t region, size_t* offset,
+                           size_t* bytes);
+
+const char* mkmoe_status_string(int status);
+
+/* Device decode of n bytes (device pointers): fp8[i] = e4m3 value of codes[i],
+ * fp4[2i], fp4[2i + 1] = the e2m1 values of its low and high nibble, through
+ * the same hardware converts the kernels use (for tests of those converts). */
+int mkmoe_device_decode(const uint8_t* codes, float* fp8, float* fp4, int32_t n, void* stream);
+
+/* Host builds of the kernels' exact arithmetic (no device needed): */
+void mkmoe_host_e4m3_encode(const float* x, uint8_t* out, int64_t n);
+void mkmoe_host_sigmoid(const float* x, float* out, int64_t n);
+/* grouped top-k of one row of fp32 scores [E] with fp32 bias */
+void mkmoe_host_topk(const mkmoe_shape* shape, const float* scores, const float* bias,
+                     int32_t* ids, float* weights);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MKMOE_H */

@@ -1,0 +1,118 @@
+"""Seeded CPU generation of one MoE layer's inputs and weights, per workload.
+
+TEST INFRASTRUCTURE ONLY (the oracle side): imported by ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg.
+
+Every tensor has its own CPU ``torch.Generator`` seeded base + a stable id, and
+every routed expert is generated alone (seed base + 100000 + e), so the oracle
+and a GPU test can materialise only the experts a step routes to. The
+reference draws its inputs from device generators
+(``test/kernels/deepseek_v41/check_ffn.py:133-134``), which cannot be
+reproduced off the GPU; these are drawn on the CPU instead.
+
+Distributions (per workload):
+- x ~ N(0, 1) bf16 [R, H]
+- router weight: N(0, 0.02) bf16 for the 1024-wide plumbing layer; N(0, 1/H)
+  for the 7168-wide layers, so the logits x . w are ~N(0, 1)
+- router bias ~ N(0, 0.02) fp32 (check_ffn.py:153-155)
+- routed and shared expert weights ~ N(0, 0.02) fp32, then quantized (FP8 with
+  fp32 128 x 128 scales, or MXFP4)
+- RMSNorm weight 1 + N(0, 0.1) bf16 (check_ffn.py:152)
+- the Zipf(1.2) stress: hidden element 0 of every row is 1.0 and router column
+  0 holds bf16(log p_e) for p_e ~ rank(e)^-1.2 over a seeded permutation of the
+  experts, so the logits are log p_e plus N(0, 1) noise.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import formats as fm
+from .moe import FP8_B128, MXFP4
+
+T_X, T_GATE, T_BIAS, T_NORM, T_SGU, T_SW2, T_ZIPF = 1, 2, 3, 4, 5, 6, 7
+EXPERT_SEED = 100000
+
+
+def _gen(seed: int) -> torch.Generator:
+    return torch.Generator().manual_seed(int(seed))
+
+
+def randn(shape, seed: int, std: float = 1.0) -> torch.Tensor:
+    return torch.randn(*shape, generator=_gen(seed)) * std
+
+
+def make_x(p: dict, rows: int, seed: int) -> torch.Tensor:
+    x = randn((rows, p["hidden"]), seed * 1000 + T_X)
+    if p.get("zipf_s"):
+        x[:, 0] = 1.0
+    return x.to(torch.bfloat16)
+
+
+def quant_weight(w: torch.Tensor, fmt: str):
+    if fmt == FP8_B128:
+        return fm.quant_fp8_b128(w)
+    if fmt == MXFP4:
+        return fm.quant_mxfp4(w)
+    raise ValueError(fmt)
+
+
+def make_dense(p: dict, seed: int) -> dict:
+    """The router, bias, norm and shared expert (everything but the routed experts)."""
+    h, e = p["hidden"], p["experts"]
+    std = 0.02 if h <= 1024 else 1.0 / math.sqrt(h)
+    gate = randn((e, h), seed * 1000 + T_GATE, std)
+    if p.get("zipf_s"):
+        perm = torch.randperm(e, generator=_gen(seed * 1000 + T_ZIPF))
+        rank = torch.empty(e)
+        rank[perm] = torch.arange(1, e + 1, dtype=torch.float32)
+        logp = -p["zipf_s"] * torch.log(rank)
+        logp = logp - torch.logsumexp(logp, 0)
+        gate[:, 0] = logp
+    w = {
+        "gate_w": gate.to(torch.bfloat16),
+        "bias": randn((e,), seed * 1000 + T_BIAS, 0.02).float(),
+    }
+    if p.get("norm_eps") is not None:
+        w["norm"] = (1 + randn((h,), seed * 1000 + T_NORM, 0.1)).to(torch.bfloat16)
+    ish = p["shared_inter"]
+    w["sgu"], w["sgu_s"] = fm.quant_fp8_b128(randn((2 * ish, h), seed * 1000 + T_SGU, 0.02))
+    w["sw2"], w["sw2_s"] = fm.quant_fp8_b128(randn((h, ish), seed * 1000 + T_SW2, 0.02))
+    return w
+
+
+class LazyExperts:
+    """Routed expert e's quantized (w13, w13_s, w2, w2_s), generated on first use from seed + e."""
+
+    def __init__(self, p: dict, seed: int):
+        self.p, self.seed, self.cache = p, seed, {}
+
+    def get(self, e: int):
+        if e not in self.cache:
+            p = self.p
+            h, i = p["hidden"], p["inter"]
+            base = self.seed * 1000 + EXPERT_SEED + 4 * e
+            w13 = randn((2 * i, h), base, 0.02)
+            w2 = randn((h, i), base + 1, 0.02)
+            self.cache[e] = quant_weight(w13, p["routed_fmt"]) + quant_weight(w2, p["routed_fmt"])
+        return self.cache[e]
+
+
+def expert_shapes(p: dict) -> dict:
+    """Shapes and dtypes (as torch dtypes of the raw bytes) of the stacked routed-expert tensors."""
+    e, h, i = p["experts"], p["hidden"], p["inter"]
+    if p["routed_fmt"] == FP8_B128:
+        return {
+            "w13": ((e, 2 * i, h), torch.uint8),
+            "w13_s": ((e, -(-2 * i // 128), -(-h // 128)), torch.float32),
+            "w2": ((e, h, i), torch.uint8),
+            "w2_s": ((e, -(-h // 128), -(-i // 128)), torch.float32),
+        }
+    return {
+        "w13": ((e, 2 * i, h // 2), torch.uint8),
+        "w13_s": ((e, 2 * i, h // 32), torch.uint8),
+        "w2": ((e, h, i // 2), torch.uint8),
+        "w2_s": ((e, h, i // 32), torch.uint8),
+    }

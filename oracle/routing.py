@@ -1,0 +1,209 @@
+"""Router logits, scores, grouped top-k and RMSNorm in the exact order the kernel computes them.
+
+TEST INFRASTRUCTURE ONLY (the oracle): imported by ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg, never by the
+product path.
+
+The reference's golden model routes with an fp32 matmul of unspecified order
+(``test/kernels/deepseek_v41/check_ffn.py:201-206``) and tolerates routing
+disagreement (``check_ffn.py:339-341``); its kernel sums the router GEMM in
+one fixed order (``sgl_amd_mono/deepseek_v41/gfx950/stages/router.py:1-28``,
+parts added in order at ``stages/moe.py:337-342``). Routing here must match
+the kernel bit for bit, so every step below is a fixed sequence of IEEE fp32
+(or fp64) operations that the HIP kernel performs in the same order:
+
+1. Router logits (fixed order, ``router_logits``). Chunk c covers hidden
+   elements [512 c, 512 c + 512); its "lane" l (0..63) covers the 8 elements
+   from 512 c + 8 l. Part p covers chunks [p C / P, (p + 1) C / P) of the
+   C = H / 512 chunks. For each part, lane l sums x * w over its elements in
+   order (chunks ascending, then the 8 elements ascending), starting from 0;
+   the 64 lane sums are added as a halving tree (lanes l and l + d for
+   d = 32, 16, 8, 4, 2, 1); the logit is 0 + S_0 + S_1 + ... in part order.
+   A bf16 x bf16 product is exact in fp32, so an FMA would give the same sum;
+   the kernel still uses separate multiply and add.
+2. Scores (``sigmoid_exact``): sigmoid in fp64 from IEEE operations only
+   (Cody-Waite reduction by ln 2, a degree-13 Taylor polynomial, an exact
+   power-of-two scaling), rounded once to fp32; the input is clamped to
+   [-60, 60] first. The same steps run on the GPU with FP contraction off, so
+   the fp32 score is identical.
+3. Selection (``grouped_topk``): DeepSeek-V3's ``noaux_tc`` grouped top-k.
+   choice = score + bias (fp32); a group's score is its largest plus its
+   second largest choice; the top ``topk_group`` groups by group score (a tie
+   goes to the lower group); then the top ``topk`` experts by choice among
+   those groups, in descending order (a tie goes to the lower expert id). With
+   one group this is the plain biased top-k of the reference's
+   ``stage_route`` (``stages/moe.py:305-391``).
+4. Weights: w_k = score_k * (scale / max(total, 1e-20)) with total summed in
+   selection order from 0 (``stages/moe.py:374-390``; the golden's
+   ``wt * (SCALE / wt.sum(1))``, ``check_ffn.py:205-206``); without
+   normalisation w_k = score_k * scale.
+5. RMSNorm (``rmsnorm_exact``, only for the fused norm preset): the sum of
+   squares in the router's chunk / lane / tree order over the whole row,
+   rstd = 1 / sqrt(sum / H + eps), y = bf16((x * rstd) * w) as the reference's
+   ``stage_norm`` orders it (``stages/seam.py:325-378``).
+
+Parity pins (tests/test_oracle_routing.py): the fixed-order logits against an
+fp64 matmul (within fp32 rounding) and against an independent scalar
+restatement on small shapes; the fp64 sigmoid against ``math.exp`` within 1
+fp64 ulp of the rounded fp32; the grouped top-k against brute-force
+enumeration of every group subset and expert subset at E = 16.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+CHUNK = 512  # hidden elements of a router chunk: 64 lanes x 8
+LANES = 64
+SIG_CLAMP = 60.0
+LN2_HI = float.fromhex("0x1.62e42fee00000p-1")  # 32 trailing zero bits: n * LN2_HI is exact
+LN2_LO = float.fromhex("0x1.a39ef35793c76p-33")
+INV_LN2 = 1.4426950408889634
+EXP_TERMS = 14  # Taylor terms 1 / k!, k = 0 .. 13: |r| <= 0.35 leaves < 1e-17
+
+
+def _tree64(a: np.ndarray) -> np.ndarray:
+    """Sum the last axis (64 lanes) as a halving tree: lanes l and l + d, d = 32 .. 1."""
+    assert a.shape[-1] == LANES
+    d = LANES // 2
+    while d >= 1:
+        a = a[..., :d] + a[..., d : 2 * d]
+        d //= 2
+    return a[..., 0]
+
+
+def router_part_sums(x: torch.Tensor, gate_w: torch.Tensor, parts: int) -> np.ndarray:
+    """Fixed-order part sums S_p [R, E, P] of bf16 x [R, H] and bf16 gate_w [E, H] (step 1)."""
+    xs = x.float().numpy().astype(np.float32)
+    ws = gate_w.float().numpy().astype(np.float32)
+    r, h = xs.shape
+    e = ws.shape[0]
+    chunks = h // CHUNK
+    assert chunks * CHUNK == h and chunks % parts == 0, (h, parts)
+    per = chunks // parts
+    # [R or E, chunk, lane, 8]
+    xv = xs.reshape(r, chunks, LANES, 8)
+    wv = ws.reshape(e, chunks, LANES, 8)
+    out = np.zeros((r, e, parts), np.float32)
+    for p in range(parts):
+        acc = np.zeros((r, e, LANES), np.float32)
+        for c in range(p * per, (p + 1) * per):
+            for j in range(8):
+                prod = xv[:, None, c, :, j] * wv[None, :, c, :, j]  # [R, E, 64] fp32
+                acc = acc + prod
+        out[:, :, p] = _tree64(acc)
+    return out
+
+
+def logits_from_parts(parts: np.ndarray) -> np.ndarray:
+    """0 + S_0 + S_1 + ... in part order (fp32)."""
+    logit = np.zeros(parts.shape[:2], np.float32)
+    for p in range(parts.shape[2]):
+        logit = logit + parts[:, :, p]
+    return logit
+
+
+def router_logits(x: torch.Tensor, gate_w: torch.Tensor, parts: int) -> np.ndarray:
+    """Fixed-order fp32 logits [R, E] (step 1)."""
+    return logits_from_parts(router_part_sums(x, gate_w, parts))
+
+
+def exp_nonpos(y: np.ndarray) -> np.ndarray:
+    """exp(y) for fp64 y <= 0 from IEEE operations only (step 2)."""
+    y = np.asarray(y, np.float64)
+    n = np.rint(y * INV_LN2)
+    r = (y - n * LN2_HI) - n * LN2_LO
+    p = np.full_like(r, 1.0 / math.factorial(EXP_TERMS - 1))
+    for k in range(EXP_TERMS - 2, -1, -1):
+        p = p * r + 1.0 / math.factorial(k)
+    return np.ldexp(p, n.astype(np.int32))
+
+
+def sigmoid_exact(logit: np.ndarray) -> np.ndarray:
+    """fp32 sigmoid of fp32 logits via fp64 (step 2)."""
+    xd = np.clip(np.asarray(logit, np.float32).astype(np.float64), -SIG_CLAMP, SIG_CLAMP)
+    t = exp_nonpos(-np.abs(xd))
+    den = 1.0 + t
+    s = np.where(xd >= 0, 1.0 / den, t / den)
+    return s.astype(np.float32)
+
+
+def grouped_topk(
+    scores: np.ndarray,
+    bias: np.ndarray,
+    topk: int,
+    n_group: int,
+    topk_group: int,
+    scale: float,
+    renorm: bool = True,
+):
+    """Steps 3 and 4 on fp32 scores [R, E] -> (ids int32 [R, k], weights fp32 [R, k])."""
+    scores = np.asarray(scores, np.float32)
+    bias = np.asarray(bias, np.float32)
+    r, e = scores.shape
+    choice = scores + bias[None, :]
+    per = e // n_group
+    ids = np.zeros((r, topk), np.int32)
+    wts = np.zeros((r, topk), np.float32)
+    for t in range(r):
+        c = choice[t]
+        if n_group > 1:
+            grp = c.reshape(n_group, per)
+            top2 = np.sort(grp, axis=1)[:, ::-1]
+            gs = top2[:, 0] + top2[:, 1]
+            gorder = np.argsort(-gs, kind="stable")  # ties: lower group first
+            keep = np.zeros(e, bool)
+            for g in gorder[:topk_group]:
+                keep[g * per : (g + 1) * per] = True
+        else:
+            keep = np.ones(e, bool)
+        cand = np.where(keep)[0]
+        order = cand[np.argsort(-c[cand], kind="stable")][:topk]  # ties: lower id first
+        ids[t] = order
+        w = scores[t, order]
+        if renorm:
+            total = np.float32(0.0)
+            for v in w:
+                total = np.float32(total + v)
+            f = np.float32(np.float32(scale) / max(total, np.float32(1e-20)))
+        else:
+            f = np.float32(scale)
+        wts[t] = (w * f).astype(np.float32)
+    return ids, wts
+
+
+def route(x, gate_w, bias, preset) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Logits, then ids and weights, for a preset dict (see ``oracle.moe``)."""
+    logit = router_logits(x, gate_w, preset["router_parts"])
+    sc = sigmoid_exact(logit)
+    ids, wts = grouped_topk(
+        sc,
+        np.asarray(bias, np.float32),
+        preset["topk"],
+        preset["n_group"],
+        preset["topk_group"],
+        preset["routed_scale"],
+        preset.get("renorm", True),
+    )
+    return logit, ids, wts
+
+
+def rmsnorm_exact(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """bf16 RMSNorm of bf16 rows x [R, H] with bf16 weight w [H] in the kernel's order (step 5)."""
+    xs = x.float().numpy().astype(np.float32)
+    r, h = xs.shape
+    chunks = h // CHUNK
+    xv = xs.reshape(r, chunks, LANES, 8)
+    acc = np.zeros((r, LANES), np.float32)
+    for c in range(chunks):
+        for j in range(8):
+            v = xv[:, c, :, j]
+            acc = acc + v * v
+    ss = _tree64(acc)
+    mean = (ss / np.float32(h)).astype(np.float32)
+    rstd = (np.float32(1.0) / np.sqrt(mean + np.float32(eps))).astype(np.float32)
+    y = (xs * rstd[:, None]).astype(np.float32) * w.float().numpy().astype(np.float32)[None, :]
+    return torch.from_numpy(y.astype(np.float32)).to(torch.bfloat16)

@@ -1,0 +1,1418 @@
+// The decode-step MoE block of one TP rank on gfx950 (MI355X): HIP kernels and the C ABI.
+//
+// One persistent launch (grid = one 512-thread workgroup per CU) runs five
+// stages separated by device-scope arrival counters (every wait has a
+// deadline, so a launch always ends):
+//   N  RMSNorm of x (fused-norm shape only)                   wave per row
+//   A  router GEMV part sums (fixed order) + activation quantization
+//                                                              wave per (expert, K part) / (row, 512 cols)
+//   B  routing (sigmoid, grouped top-k, weights)               wave per row
+//      + shared expert gate_up, SwiGLU                         wave per 2 intermediate columns
+//   C  routed gate_up + SwiGLU for the step's union of experts wave per (expert, 2 columns)
+//   D  down GEMVs (shared + routed) and the weighted combine   workgroup per tile of output rows
+// The staged entry point runs the same stage functions as one launch each.
+//
+// Reference: the stages of sgl_amd_mono/deepseek_v41/gfx950/stages/moe.py
+// (run_moe :1348-1418; stage_xq :181-263; stage_router :267-301; stage_route
+// :305-391; load_route :394-489; stage_shared :502-563; stage_ug :770-832 and
+// ug_epilogue :907-947; stage_down :950-1005; down_combine :1156-1184) and
+// the fused norm of stages/seam.py:325-378. The weights are read in place in
+// the checkpoint's row-major layouts (include/mkmoe.h).
+
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+#include <stdio.h>
+
+#include <atomic>
+#include <mutex>
+
+#include "../../include/mkmoe.h"
+#include "mkmoe_numerics.h"
+
+namespace mkmoe {
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / 64;
+constexpr int kRowsMax = 48;  // rows a launch takes at most
+constexpr int kTileMax = 32;  // output rows of a down tile, at most
+constexpr int kFp8 = MKMOE_FMT_FP8_B128;
+constexpr int kFp4 = MKMOE_FMT_MXFP4;
+
+// control words at the start of the workspace
+constexpr int kCtlNorm = 0, kCtlA = 1, kCtlB = 2, kCtlC = 3, kCtlExit = 5;
+constexpr int kCtlCounters = 8;
+constexpr int kCtlErr = 8;  // MKMOE_ERRW_WORDS error words from here
+constexpr int kCtlBytes = 256;
+
+enum Stage { kStageNorm = 1, kStageA = 2, kStageB = 3, kStageC = 4, kStageD = 5 };
+
+template <int H_, int E_, int K_, int NG_, int TG_, int I_, int S_, int FMT_, int P_, bool NORM_>
+struct Cfg {
+  static constexpr int H = H_, E = E_, K = K_, NG = NG_, TG = TG_, I = I_, S = S_, FMT = FMT_,
+                       P = P_;
+  static constexpr bool NORM = NORM_;
+  static constexpr int CH512 = H / 512;  // router / quantize chunks of a row
+  static_assert(H % 512 == 0 && CH512 % P == 0, "router chunks");
+  static_assert(I % 128 == 0 && S % 128 == 0, "widths");
+  static_assert(E <= 1024 && (NG == 1 || (E % NG == 0)), "experts");
+  // down-stage mid batch: picks whose quantized rows fit 32 KB of LDS
+  static constexpr int PB = 32768 / I;
+  static constexpr int SCB = FMT == kFp4 ? I / 32 : (I / 128) * 4;  // scale bytes a mid row
+};
+
+using CfgPlumbing = Cfg<1024, 16, 4, 1, 1, 512, 512, kFp8, 2, false>;
+using CfgTp4Fp8 = Cfg<7168, 256, 8, 8, 4, 512, 512, kFp8, 7, false>;
+using CfgTp4Fp4 = Cfg<7168, 256, 8, 8, 4, 512, 512, kFp4, 7, false>;
+using CfgTp2Fp4Norm = Cfg<7168, 256, 8, 8, 4, 1024, 1024, kFp4, 7, true>;
+
+// ---------------------------------------------------------------- workspace layout
+struct Layout {
+  size_t off[10];
+  size_t size[10];
+  size_t total;
+};
+
+MKMOE_HD inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+MKMOE_HD inline Layout make_layout(int H, int E, int K, int I, int S, int fmt, int P, int norm,
+                                   int rm) {
+  Layout L;
+  size_t sz[10];
+  sz[0] = norm ? (size_t)rm * H * 2 : 0;                              // x normed, bf16
+  sz[1] = (size_t)rm * H;                                             // x codes, routed rule
+  sz[2] = fmt == kFp4 ? (size_t)rm * (H / 32) : (size_t)rm * (H / 128) * 4;  // its scales
+  sz[3] = fmt == kFp4 ? (size_t)rm * H : 0;                           // x codes, shared rule
+  sz[4] = fmt == kFp4 ? (size_t)rm * (H / 128) * 4 : 0;               // its fp32 scales
+  sz[5] = (size_t)rm * E * P * 4;                                     // router part sums
+  sz[6] = (size_t)rm * K * 4;                                         // ids
+  sz[7] = (size_t)rm * K * 4;                                         // weights
+  sz[8] = (size_t)rm * S * 2;                                         // shared mid, bf16
+  sz[9] = (size_t)rm * K * I * 2;                                     // routed mid, bf16
+  size_t off = kCtlBytes;
+  for (int i = 0; i < 10; ++i) {
+    L.off[i] = off;
+    L.size[i] = sz[i];
+    off = align256(off + sz[i]);
+  }
+  L.total = off;
+  return L;
+}
+
+struct Params {
+  const uint16_t* x;
+  uint16_t* out;
+  int32_t* ids_out;
+  float* w_out;
+  const uint16_t* gate_w;
+  const float* bias;
+  const uint16_t* norm_w;
+  const uint8_t* w13;
+  const void* w13_s;
+  const uint8_t* w2;
+  const void* w2_s;
+  const uint8_t* sgu;
+  const float* sgu_s;
+  const uint8_t* sw2;
+  const float* sw2_s;
+  uint8_t* ws;
+  int rows;
+  int rmax;
+  int renorm;
+  int tile_rows;
+  float scale;
+  float limit;
+  float eps;
+  unsigned long long deadline;  // s_memrealtime ticks (100 MHz)
+  size_t off[10];
+};
+
+// ---------------------------------------------------------------- small device helpers
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; }
+__device__ __forceinline__ u32x4 ld16_nt(const void* p) {
+  return __builtin_nontemporal_load((const u32x4*)p);
+}
+
+template <class T>
+__device__ __forceinline__ T* wsp(const Params& p, int region) {
+  return (T*)(p.ws + p.off[region]);
+}
+__device__ __forceinline__ uint32_t* ctl(const Params& p) { return (uint32_t*)p.ws; }
+
+__device__ __forceinline__ float bf_lo(uint32_t w) { return u2f(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return u2f(w & 0xffff0000u); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+  // halving tree: lanes l and l + d, d = 32 .. 1 (every lane ends with the sum)
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v = v + __shfl_xor(v, d);
+  return v;
+}
+// sum over groups of G lanes (G a power of two)
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int d = G / 2; d >= 1; d >>= 1) v = v + __shfl_xor(v, d);
+  return v;
+}
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int d = G / 2; d >= 1; d >>= 1) {
+    float o = __shfl_xor(v, d);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ float silu(float z) { return z / (1.0f + __expf(-z)); }
+
+// 16 e4m3 weights . 16 e4m3 activations, unscaled
+__device__ __forceinline__ float dot16_fp8(u32x4 w, u32x4 x) {
+  float s = 0.0f;
+  const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+  const uint32_t xv[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    auto w01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)wv[q], false);
+    auto w23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)wv[q], true);
+    auto x01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)xv[q], false);
+    auto x23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)xv[q], true);
+    s = fmaf(w01[0], x01[0], s);
+    s = fmaf(w01[1], x01[1], s);
+    s = fmaf(w23[0], x23[0], s);
+    s = fmaf(w23[1], x23[1], s);
+  }
+  return s;
+}
+
+// byte B of weight dword wq: elements 2B (low nibble), 2B + 1 (high) against x bytes 2B, 2B + 1
+template <int B>
+__device__ __forceinline__ float fp4_pair(uint32_t wq, uint32_t x_lo, uint32_t x_hi, float s) {
+  auto wf = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wq, 1.0f, B);
+  auto xf = __builtin_amdgcn_cvt_pk_f32_fp8((int)(B < 2 ? x_lo : x_hi), (B & 1) != 0);
+  s = fmaf(wf[0], xf[0], s);
+  return fmaf(wf[1], xf[1], s);
+}
+
+// 32 e2m1 weights (16 bytes, even element in the low nibble) . 32 e4m3 activations, unscaled
+__device__ __forceinline__ float dot32_fp4(u32x4 w, u32x4 xa, u32x4 xb) {
+  float s = 0.0f;
+  const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+  const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    // weight dword q: elements 8q .. 8q + 7 = x dwords 2q, 2q + 1
+    s = fp4_pair<0>(wv[q], xv[2 * q], xv[2 * q + 1], s);
+    s = fp4_pair<1>(wv[q], xv[2 * q], xv[2 * q + 1], s);
+    s = fp4_pair<2>(wv[q], xv[2 * q], xv[2 * q + 1], s);
+    s = fp4_pair<3>(wv[q], xv[2 * q], xv[2 * q + 1], s);
+  }
+  return s;
+}
+
+// ---------------------------------------------------------------- hand-offs
+__device__ void record_error(const Params& p, int stage) {
+  uint32_t* e = ctl(p) + kCtlErr;
+  uint32_t prev = atomicCAS(&e[MKMOE_ERRW_CODE], 0u, (uint32_t)MKMOE_DEVERR_DEADLINE);
+  if (prev == 0u) {
+    atomicExch(&e[MKMOE_ERRW_STAGE], (uint32_t)stage);
+    atomicExch(&e[MKMOE_ERRW_BLOCK], (uint32_t)blockIdx.x);
+  }
+  atomicAdd(&e[MKMOE_ERRW_COUNT], 1u);
+}
+
+// this workgroup is done with a stage: its stores before the count (device scope)
+__device__ __forceinline__ void arrive(const Params& p, int which) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __hip_atomic_fetch_add(ctl(p) + which, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// wait until ``target`` workgroups arrived at ``which`` (or the deadline passed)
+__device__ __forceinline__ void await_all(const Params& p, int which, uint32_t target, int stage) {
+  if (threadIdx.x == 0) {
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    while (__hip_atomic_load(ctl(p) + which, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      __builtin_amdgcn_s_sleep(1);
+      if (__builtin_amdgcn_s_memrealtime() - t0 > p.deadline) {
+        record_error(p, stage);
+        break;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+  __syncthreads();
+}
+
+// the last workgroup out zeroes the counters for the next launch (graph replay safe)
+__device__ void leave(const Params& p) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t n = __hip_atomic_fetch_add(ctl(p) + kCtlExit, 1u, __ATOMIC_ACQ_REL,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    if (n == gridDim.x - 1) {
+      for (int i = 0; i < kCtlCounters; ++i)
+        __hip_atomic_store(ctl(p) + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- stage N: RMSNorm
+template <class C>
+__device__ void norm_row(const Params& p, int r, int lane) {
+#pragma clang fp contract(off)
+  constexpr int CH = C::CH512;
+  const uint16_t* x = p.x + (size_t)r * C::H;
+  u32x4 v[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) v[c] = ld16(x + c * 512 + lane * 8);
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const uint32_t w4[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float f = (j & 1) ? bf_hi(w4[j >> 1]) : bf_lo(w4[j >> 1]);
+      acc = acc + f * f;
+    }
+  }
+  float ss = wave_sum(acc);
+  float mean = ss / (float)C::H;
+  float rstd = 1.0f / sqrtf(mean + p.eps);
+  uint16_t* y = wsp<uint16_t>(p, 0) + (size_t)r * C::H;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const uint32_t w4[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+    u32x4 nw = ld16(p.norm_w + c * 512 + lane * 8);
+    const uint32_t n4[4] = {nw.x, nw.y, nw.z, nw.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float a = bf_lo(w4[q]) * rstd, b = bf_hi(w4[q]) * rstd;
+      a = a * bf_lo(n4[q]);
+      b = b * bf_hi(n4[q]);
+      o[q] = (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+    }
+    *(u32x4*)(y + c * 512 + lane * 8) = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+template <class C>
+__device__ void stage_norm(const Params& p, int b, int nwg) {
+  const int lane = threadIdx.x & 63, gw = b * kWaves + (threadIdx.x >> 6);
+  for (int r = gw; r < p.rows; r += nwg * kWaves) norm_row<C>(p, r, lane);
+}
+
+template <class C>
+__device__ __forceinline__ const uint16_t* x_in(const Params& p) {
+  return C::NORM ? wsp<const uint16_t>(p, 0) : p.x;
+}
+
+// ---------------------------------------------------------------- stage A
+// router part sums: logit part (e, part) of every row, in the fixed order
+template <class C>
+__device__ void router_unit(const Params& p, int e, int part, int lane) {
+#pragma clang fp contract(off)
+  constexpr int CPP = C::CH512 / C::P;
+  const uint16_t* x = x_in<C>(p);
+  u32x4 wv[CPP];
+#pragma unroll
+  for (int i = 0; i < CPP; ++i)
+    wv[i] = ld16_nt(p.gate_w + (size_t)e * C::H + (part * CPP + i) * 512 + lane * 8);
+  float* out = wsp<float>(p, 5);
+  for (int r = 0; r < p.rows; ++r) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPP; ++i) {
+      u32x4 xv = ld16(x + (size_t)r * C::H + (part * CPP + i) * 512 + lane * 8);
+      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+      const uint32_t ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc = acc + bf_lo(xw[q]) * bf_lo(ww[q]);
+        acc = acc + bf_hi(xw[q]) * bf_hi(ww[q]);
+      }
+    }
+    float s = wave_sum(acc);
+    if (lane == 0) out[((size_t)r * C::E + e) * C::P + part] = s;
+  }
+}
+
+// quantize 512 columns of row r: group-128 fp8 (fp32 scale) and, for MXFP4
+// experts, MXFP8 per 32 ("aiter" rule)
+template <class C>
+__device__ void quant_unit(const Params& p, int r, int c, int lane) {
+#pragma clang fp contract(off)
+  const uint16_t* x = x_in<C>(p) + (size_t)r * C::H + c * 512 + lane * 8;
+  u32x4 xv = ld16(x);
+  const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+  float v[8];
+  float am = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    v[2 * q] = bf_lo(xw[q]);
+    v[2 * q + 1] = bf_hi(xw[q]);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) am = fabsf(v[j]) > am ? fabsf(v[j]) : am;
+  const size_t col = (size_t)r * C::H + c * 512 + lane * 8;
+  // group-128 fp8: 16 lanes a group
+  {
+    float g = group_max<16>(am);
+    float s = group_scale(g);
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) lo |= e4m3_encode(v[j] / s) << (8 * j);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) hi |= e4m3_encode(v[4 + j] / s) << (8 * j);
+    const int rq = C::FMT == kFp4 ? 3 : 1, rs = C::FMT == kFp4 ? 4 : 2;
+    *(u32x2*)(wsp<uint8_t>(p, rq) + col) = u32x2{lo, hi};
+    if ((lane & 15) == 0) wsp<float>(p, rs)[(size_t)r * (C::H / 128) + c * 4 + lane / 16] = s;
+  }
+  if constexpr (C::FMT == kFp4) {
+    float g = group_max<4>(am);
+    int code = mx_code(g);
+    float inv = mx_inv(code);
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) lo |= e4m3_encode(v[j] * inv) << (8 * j);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) hi |= e4m3_encode(v[4 + j] * inv) << (8 * j);
+    *(u32x2*)(wsp<uint8_t>(p, 1) + col) = u32x2{lo, hi};
+    if ((lane & 3) == 0) wsp<uint8_t>(p, 2)[(size_t)r * (C::H / 32) + c * 16 + lane / 4] = (uint8_t)code;
+  }
+}
+
+template <class C>
+__device__ void stage_a(const Params& p, int b, int nwg) {
+  const int lane = threadIdx.x & 63, gw = b * kWaves + (threadIdx.x >> 6);
+  const int n_router = C::E * C::P, n_quant = p.rows * C::CH512;
+  for (int u = gw; u < n_router + n_quant; u += nwg * kWaves) {
+    if (u < n_router)
+      router_unit<C>(p, u / C::P, u % C::P, lane);
+    else
+      quant_unit<C>(p, (u - n_router) / C::CH512, (u - n_router) % C::CH512, lane);
+  }
+}
+
+// ---------------------------------------------------------------- stage B: routing
+template <class C>
+__device__ void route_row(const Params& p, int r, int lane) {
+#pragma clang fp contract(off)
+  constexpr int EPL = (C::E + 63) / 64;
+  const float* part = wsp<const float>(p, 5) + (size_t)r * C::E * C::P;
+  float sc[EPL], ch[EPL];
+  bool alive[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    if (e < C::E) {
+      float logit = 0.0f;
+#pragma unroll
+      for (int q = 0; q < C::P; ++q) logit = logit + part[e * C::P + q];
+      // a NaN score weighs 0 and its choice never wins (as the reference's route)
+      const float sg = sigmoid_exact(logit);
+      sc[i] = sg != sg ? 0.0f : sg;
+      const float cv = sc[i] + p.bias[e];
+      ch[i] = cv != cv ? -INFINITY : cv;
+      alive[i] = true;
+    } else {
+      sc[i] = 0.0f;
+      ch[i] = -INFINITY;
+      alive[i] = false;
+    }
+  }
+  if constexpr (C::NG > 1) {
+    constexpr int GS = C::E / C::NG;  // experts a group
+    static_assert(GS <= 64 && (64 % GS) == 0, "group size");
+    constexpr int GPI = 64 / GS;  // groups a 64-expert slice
+    float gsv[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      // segmented top-2 over the GS lanes of this group: (value, lowest lane) of the max
+      float v1 = ch[i];
+      int l1 = lane;
+#pragma unroll
+      for (int d = GS / 2; d >= 1; d >>= 1) {
+        float ov = __shfl_xor(v1, d);
+        int ol = __shfl_xor(l1, d);
+        if (ov > v1 || (ov == v1 && ol < l1)) {
+          v1 = ov;
+          l1 = ol;
+        }
+      }
+      float v2 = lane == l1 ? -INFINITY : ch[i];
+#pragma unroll
+      for (int d = GS / 2; d >= 1; d >>= 1) {
+        float ov = __shfl_xor(v2, d);
+        v2 = ov > v2 ? ov : v2;
+      }
+      gsv[i] = v1 + v2;
+    }
+    // every lane: the group scores, then the topk_group best groups
+    float gs[C::NG];
+#pragma unroll
+    for (int g = 0; g < C::NG; ++g) gs[g] = __shfl(gsv[g / GPI], (g % GPI) * GS);
+    uint64_t gmask = 0;
+#pragma unroll
+    for (int t = 0; t < C::TG; ++t) {
+      int best = -1;
+      float bv = -INFINITY;
+#pragma unroll
+      for (int g = 0; g < C::NG; ++g) {
+        bool free_g = ((gmask >> g) & 1ull) == 0ull;
+        if (free_g && (best < 0 || better(gs[g], g, bv, best))) {
+          best = g;
+          bv = gs[g];
+        }
+      }
+      gmask |= 1ull << best;
+    }
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      alive[i] = alive[i] && ((gmask >> (e / GS)) & 1ull) != 0ull;
+    }
+  }
+  float total = 0.0f;
+  int my_id = 0;
+  float my_w = 0.0f;
+  for (int k = 0; k < C::K; ++k) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      if (alive[i] && (bi == 0x7fffffff || better(ch[i], e, bv, bi))) {
+        bv = ch[i];
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+      float ov = __shfl_xor(bv, d);
+      int oi = __shfl_xor(bi, d);
+      if (better(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    bi = bi < 0 || bi >= C::E ? 0 : bi;  // unreachable with >= topk candidates; keeps ids in range
+    // the winner's owner lane retires it and hands out its score
+    float ws = 0.0f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      if (lane + 64 * i == bi) {
+        alive[i] = false;
+        ws = sc[i];
+      }
+    }
+    ws = __shfl(ws, bi & 63);
+    total = total + ws;
+    if (lane == k) {
+      my_id = bi;
+      my_w = ws;
+    }
+  }
+  float f = p.scale;
+  if (p.renorm) f = p.scale / (total > 1e-20f ? total : 1e-20f);
+  if (lane < C::K) {
+    const float w = my_w * f;
+    wsp<int32_t>(p, 6)[r * C::K + lane] = my_id;
+    wsp<float>(p, 7)[r * C::K + lane] = w;
+    if (p.ids_out) p.ids_out[r * C::K + lane] = my_id;
+    if (p.w_out) p.w_out[r * C::K + lane] = w;
+  }
+}
+
+// ---------------------------------------------------------------- GEMV of weight rows
+// A unit of NR weight rows of length KD elements is streamed by one wave; the
+// wave's lanes split into G sub-groups of LPR = 64 / G lanes, sub-group g
+// taking rows g, g + G, ...; each lane loads CPL 16-byte chunks of a row.
+// ``acts(t)`` -> activation pointers of token t. Results per (row, token) are
+// summed over the sub-group's lanes.
+template <int FMT, int KD>
+struct RowShape {
+  static constexpr int CPR = FMT == kFp4 ? KD / 32 : KD / 16;  // 16-byte chunks a row
+  // sub-groups: the fewest that split a row evenly over a sub-group's lanes
+  static constexpr int G = CPR % 64 == 0 ? 1 : CPR % 32 == 0 ? 2 : CPR % 16 == 0 ? 4 : 8;
+  static constexpr int LPR = 64 / G;
+  static constexpr int CPL = CPR / LPR;                          // chunks a lane a row
+  static constexpr int RB = FMT == kFp4 ? KD / 2 : KD;           // bytes a row
+  static_assert(CPR % LPR == 0, "row chunks");
+};
+
+// fp8 rows with fp32 128 x 128 scales: ``srow[q]`` points at row q's scales
+// (one per 128 K), activations e4m3 with a fp32 scale per 128
+// rows[q * G + g] for this lane's sub-group g, without indexing a register array
+template <int G, class T>
+__device__ __forceinline__ T sub_pick(const T* arr, int q, int g) {
+  T v = arr[q * G];
+#pragma unroll
+  for (int k = 1; k < G; ++k)
+    if (g == k) v = arr[q * G + k];
+  return v;
+}
+
+template <int KD, int NR>
+struct Fp8Rows {
+  using S = RowShape<kFp8, KD>;
+  static constexpr int RPG = NR / S::G;  // rows a sub-group
+  u32x4 w[RPG][S::CPL];
+  float s[RPG][S::CPL];
+
+  __device__ __forceinline__ void load(const uint8_t* const* rows, const float* const* srow,
+                                       int lane) {
+    const int g = lane / S::LPR, l = lane % S::LPR;
+#pragma unroll
+    for (int q = 0; q < RPG; ++q) {
+#pragma unroll
+      for (int i = 0; i < S::CPL; ++i) {
+        const int c = l + S::LPR * i;
+        w[q][i] = ld16_nt(sub_pick<S::G>(rows, q, g) + c * 16);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < RPG; ++q) {
+      const float* sr = sub_pick<S::G>(srow, q, g);
+#pragma unroll
+      for (int i = 0; i < S::CPL; ++i) s[q][i] = sr[(l + S::LPR * i) / 8];
+    }
+  }
+  // row partial sums (this lane) against one token's activations
+  __device__ __forceinline__ void dot(const uint8_t* xq, const float* xs, int lane,
+                                      float (&acc)[RPG]) const {
+    const int l = lane % S::LPR;
+#pragma unroll
+    for (int q = 0; q < RPG; ++q) acc[q] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < S::CPL; ++i) {
+      const int c = l + S::LPR * i;
+      const u32x4 xv = ld16(xq + c * 16);
+      const float sx = xs[c / 8];
+#pragma unroll
+      for (int q = 0; q < RPG; ++q) {
+        // opaque to the optimiser: the weight conversions stay inside the token loop
+        // (hoisted, the unit's weights as fp32 would not fit the register file)
+        u32x4 wq = w[q][i];
+        asm volatile("" : "+v"(wq));
+        acc[q] = fmaf(dot16_fp8(wq, xv), s[q][i] * sx, acc[q]);
+      }
+    }
+  }
+};
+
+// MXFP4 rows (E8M0 per 32 K): ``srow[q]`` points at row q's scale bytes;
+// activations MXFP8 (E8M0 per 32)
+template <int KD, int NR>
+struct Fp4Rows {
+  using S = RowShape<kFp4, KD>;
+  static constexpr int RPG = NR / S::G;
+  u32x4 w[RPG][S::CPL];
+  int s[RPG][S::CPL];
+
+  __device__ __forceinline__ void load(const uint8_t* const* rows, const uint8_t* const* srow,
+                                       int lane) {
+    const int g = lane / S::LPR, l = lane % S::LPR;
+#pragma unroll
+    for (int q = 0; q < RPG; ++q) {
+#pragma unroll
+      for (int i = 0; i < S::CPL; ++i)
+        w[q][i] = ld16_nt(sub_pick<S::G>(rows, q, g) + (l + S::LPR * i) * 16);
+    }
+#pragma unroll
+    for (int q = 0; q < RPG; ++q) {
+      const uint8_t* sr = sub_pick<S::G>(srow, q, g);
+#pragma unroll
+      for (int i = 0; i < S::CPL; ++i) s[q][i] = sr[l + S::LPR * i];
+    }
+  }
+  __device__ __forceinline__ void dot(const uint8_t* xq, const uint8_t* xs, int lane,
+                                      float (&acc)[RPG]) const {
+    const int l = lane % S::LPR;
+#pragma unroll
+    for (int q = 0; q < RPG; ++q) acc[q] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < S::CPL; ++i) {
+      const int c = l + S::LPR * i;
+      const u32x4 xa = ld16(xq + c * 32), xb = ld16(xq + c * 32 + 16);
+      const int sx = xs[c];
+#pragma unroll
+      for (int q = 0; q < RPG; ++q) {
+        u32x4 wq = w[q][i];
+        asm volatile("" : "+v"(wq));
+        acc[q] = acc[q] + ldexpf(dot32_fp4(wq, xa, xb), s[q][i] + sx - 254);
+      }
+    }
+  }
+};
+
+// ---------------------------------------------------------------- stage B: shared gate_up
+// unit u: intermediate columns 2u, 2u + 1 of the shared expert for every row
+template <class C>
+__device__ void shared_gu_unit(const Params& p, int u, int lane) {
+  using R = Fp8Rows<C::H, 4>;
+  const int j0 = 2 * u;
+  // rows in sub-group order: (gate j0, gate j0+1, up j0, up j0+1) so that a
+  // sub-group holds a (gate, up) pair when G = 2 and all four when G = 1
+  const int rid[4] = {j0, j0 + 1, C::S + j0, C::S + j0 + 1};
+  const uint8_t* rows[4];
+  const float* srow[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    rows[q] = p.sgu + (size_t)rid[q] * C::H;
+    srow[q] = p.sgu_s + (size_t)(rid[q] / 128) * (C::H / 128);
+  }
+  R wr;
+  wr.load(rows, srow, lane);
+  const uint8_t* xq = wsp<uint8_t>(p, C::FMT == kFp4 ? 3 : 1);
+  const float* xs = wsp<float>(p, C::FMT == kFp4 ? 4 : 2);
+  uint16_t* smid = wsp<uint16_t>(p, 8);
+  const float lim = p.limit;
+  for (int t = 0; t < p.rows; ++t) {
+    float acc[R::RPG];
+    wr.dot(xq + (size_t)t * C::H, xs + (size_t)t * (C::H / 128), lane, acc);
+#pragma unroll
+    for (int q = 0; q < R::RPG; ++q) acc[q] = group_sum<R::S::LPR>(acc[q]);
+    // G = 1: acc = (g0, g1, u0, u1); G = 2: sub-group g holds (g_g, u_g)
+    if constexpr (R::S::G == 1) {
+      if (lane == 0) {
+        float m0 = bf_round(silu(bf_round(fminf(acc[0], lim))) * bf_round(fminf(fmaxf(acc[2], -lim), lim)));
+        float m1 = bf_round(silu(bf_round(fminf(acc[1], lim))) * bf_round(fminf(fmaxf(acc[3], -lim), lim)));
+        *(uint32_t*)(smid + (size_t)t * C::S + j0) = (uint32_t)f2bf(m0) | ((uint32_t)f2bf(m1) << 16);
+      }
+    } else {
+      if ((lane % R::S::LPR) == 0) {
+        const int g = lane / R::S::LPR;
+        float m = bf_round(silu(bf_round(fminf(acc[0], lim))) * bf_round(fminf(fmaxf(acc[1], -lim), lim)));
+        smid[(size_t)t * C::S + j0 + g] = f2bf(m);
+      }
+    }
+  }
+}
+
+template <class C>
+__device__ void stage_b(const Params& p, int b, int nwg) {
+  const int lane = threadIdx.x & 63, gw = b * kWaves + (threadIdx.x >> 6);
+  const int n_route = p.rows, n_sh = C::S / 2;
+  for (int u = gw; u < n_route + n_sh; u += nwg * kWaves) {
+    if (u < n_route)
+      route_row<C>(p, u, lane);
+    else
+      shared_gu_unit<C>(p, u - n_route, lane);
+  }
+}
+
+// ---------------------------------------------------------------- the step's union (LDS)
+template <class C>
+struct Union {
+  int cnt[C::E];
+  int slot_of[C::E];
+  int slot_e[C::E];
+  int slot_start[C::E + 1];
+  int picks[kRowsMax * C::K];
+  float wts[kRowsMax * C::K];
+  int n;
+};
+
+// experts picked by any row (ascending id) and their picks (pick = row * K + k)
+template <class C>
+__device__ void build_union(const Params& p, Union<C>& un) {
+  const int tid = threadIdx.x;
+  const int npk = p.rows * C::K;
+  const int32_t* rid = wsp<const int32_t>(p, 6);
+  const float* rw = wsp<const float>(p, 7);
+  __syncthreads();
+  for (int e = tid; e < C::E; e += kThreads) un.cnt[e] = 0;
+  __syncthreads();
+  for (int t = tid; t < npk; t += kThreads) {
+    const int e = min(max((int)rid[t], 0), C::E - 1);
+    atomicAdd(&un.cnt[e], 1);
+    un.wts[t] = rw[t];
+  }
+  __syncthreads();
+  if (tid < 64) {
+    constexpr int EPL = (C::E + 63) / 64;
+    const int e0 = tid * EPL;
+    int ns = 0, np = 0;
+    for (int i = 0; i < EPL; ++i) {
+      const int e = e0 + i;
+      if (e < C::E && un.cnt[e] > 0) {
+        ns += 1;
+        np += un.cnt[e];
+      }
+    }
+    // exclusive prefix over lanes
+    int is = ns, ip = np;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      int os = __shfl_up(is, d), op = __shfl_up(ip, d);
+      if (tid >= d) {
+        is += os;
+        ip += op;
+      }
+    }
+    int s = is - ns, pk = ip - np;
+    for (int i = 0; i < EPL; ++i) {
+      const int e = e0 + i;
+      if (e < C::E && un.cnt[e] > 0) {
+        un.slot_of[e] = s;
+        un.slot_e[s] = e;
+        un.slot_start[s] = pk;
+        const int c = un.cnt[e];
+        un.cnt[e] = pk;  // fill cursor
+        s += 1;
+        pk += c;
+      }
+    }
+    if (tid == 63) {
+      un.n = is;
+      un.slot_start[is] = ip;
+    }
+  }
+  __syncthreads();
+  for (int t = tid; t < npk; t += kThreads) {
+    const int e = min(max((int)rid[t], 0), C::E - 1);
+    const int pos = atomicAdd(&un.cnt[e], 1);
+    un.picks[pos] = t;
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------- stage C: routed gate_up
+template <class C>
+__device__ void routed_gu_unit(const Params& p, const Union<C>& un, int slot, int jp, int lane) {
+  const int e = un.slot_e[slot];
+  const int j0 = 2 * jp;
+  const int rid[4] = {j0, j0 + 1, C::I + j0, C::I + j0 + 1};
+  const int first = un.slot_start[slot], last = un.slot_start[slot + 1];
+  uint16_t* mid = wsp<uint16_t>(p, 9);
+  const float lim = p.limit;
+  if constexpr (C::FMT == kFp8) {
+    using R = Fp8Rows<C::H, 4>;
+    const uint8_t* rows[4];
+    const float* srow[4];
+    const float* s13 = (const float*)p.w13_s + (size_t)e * (2 * C::I / 128) * (C::H / 128);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      rows[q] = p.w13 + ((size_t)e * 2 * C::I + rid[q]) * C::H;
+      srow[q] = s13 + (size_t)(rid[q] / 128) * (C::H / 128);
+    }
+    R wr;
+    wr.load(rows, srow, lane);
+    const uint8_t* xq = wsp<uint8_t>(p, 1);
+    const float* xs = wsp<float>(p, 2);
+    for (int j = first; j < last; ++j) {
+      const int pk = un.picks[j], t = pk / C::K;
+      float acc[R::RPG];
+      wr.dot(xq + (size_t)t * C::H, xs + (size_t)t * (C::H / 128), lane, acc);
+#pragma unroll
+      for (int q = 0; q < R::RPG; ++q) acc[q] = group_sum<R::S::LPR>(acc[q]);
+      if constexpr (R::S::G == 1) {
+        if (lane == 0) {
+          float m0 = bf_round(silu(fminf(acc[0], lim)) * fminf(fmaxf(acc[2], -lim), lim));
+          float m1 = bf_round(silu(fminf(acc[1], lim)) * fminf(fmaxf(acc[3], -lim), lim));
+          *(uint32_t*)(mid + (size_t)pk * C::I + j0) = (uint32_t)f2bf(m0) | ((uint32_t)f2bf(m1) << 16);
+        }
+      } else if ((lane % R::S::LPR) == 0) {
+        const int g = lane / R::S::LPR;
+        float m = bf_round(silu(fminf(acc[0], lim)) * fminf(fmaxf(acc[1], -lim), lim));
+        mid[(size_t)pk * C::I + j0 + g] = f2bf(m);
+      }
+    }
+  } else {
+    using R = Fp4Rows<C::H, 4>;
+    const uint8_t* rows[4];
+    const uint8_t* srow[4];
+    const uint8_t* s13 = (const uint8_t*)p.w13_s;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const size_t row = (size_t)e * 2 * C::I + rid[q];
+      rows[q] = p.w13 + row * (C::H / 2);
+      srow[q] = s13 + row * (C::H / 32);
+    }
+    R wr;
+    wr.load(rows, srow, lane);
+    const uint8_t* xq = wsp<uint8_t>(p, 1);
+    const uint8_t* xs = wsp<uint8_t>(p, 2);
+    for (int j = first; j < last; ++j) {
+      const int pk = un.picks[j], t = pk / C::K;
+      float acc[R::RPG];
+      wr.dot(xq + (size_t)t * C::H, xs + (size_t)t * (C::H / 32), lane, acc);
+#pragma unroll
+      for (int q = 0; q < R::RPG; ++q) acc[q] = group_sum<R::S::LPR>(acc[q]);
+      if constexpr (R::S::G == 1) {
+        if (lane == 0) {
+          float m0 = bf_round(silu(fminf(acc[0], lim)) * fminf(fmaxf(acc[2], -lim), lim));
+          float m1 = bf_round(silu(fminf(acc[1], lim)) * fminf(fmaxf(acc[3], -lim), lim));
+          *(uint32_t*)(mid + (size_t)pk * C::I + j0) = (uint32_t)f2bf(m0) | ((uint32_t)f2bf(m1) << 16);
+        }
+      } else if ((lane % R::S::LPR) == 0) {
+        const int g = lane / R::S::LPR;
+        float m = bf_round(silu(fminf(acc[0], lim)) * fminf(fmaxf(acc[1], -lim), lim));
+        mid[(size_t)pk * C::I + j0 + g] = f2bf(m);
+      }
+    }
+  }
+}
+
+template <class C>
+__device__ void stage_c(const Params& p, const Union<C>& un, int b, int nwg) {
+  const int lane = threadIdx.x & 63, gw = b * kWaves + (threadIdx.x >> 6);
+  const int per = C::I / 2;
+  const int n = un.n * per;
+  for (int u = gw; u < n; u += nwg * kWaves) routed_gu_unit<C>(p, un, u / per, u % per, lane);
+}
+
+// ---------------------------------------------------------------- stage D: down + combine
+template <class C>
+struct DownSmem {
+  float contrib[kRowsMax * C::K * kTileMax];
+  float ysh[kRowsMax * kTileMax];
+  union {
+    struct {
+      uint8_t q[kRowsMax * C::S];
+      float s[kRowsMax * (C::S / 128)];
+    } sh;
+    struct {
+      uint8_t q[C::PB * C::I];
+      uint8_t s[C::PB * C::SCB];
+    } mid;
+  } u;
+};
+
+// quantize bf16 rows [n][W] (global) into LDS codes [n][W] and scales: group-128 fp8 (fp32
+// scales) or MXFP8 (E8M0 bytes); row i of the source is ``src_row(i)``
+template <int FMT, int W, class RowFn>
+__device__ void quant_rows_lds(RowFn src_row, int n, uint8_t* q, void* s) {
+#pragma clang fp contract(off)
+  constexpr int PER = W / 8;  // 8-value chunks a row
+  const int tid = threadIdx.x;
+  // a wave's lanes cover consecutive chunks so that a group's lanes are adjacent
+  const int total = n * PER;
+  for (int base = 0; base < total; base += kThreads) {
+    const int idx = base + tid;
+    const bool ok = idx < total;
+    const int i = ok ? idx / PER : 0, c = ok ? idx % PER : 0;
+    float v[8];
+    float am = 0.0f;
+    if (ok) {
+      u32x4 xv = ld16(src_row(i) + c * 8);
+      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[2 * k] = bf_lo(xw[k]);
+        v[2 * k + 1] = bf_hi(xw[k]);
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) am = fabsf(v[k]) > am ? fabsf(v[k]) : am;
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = 0.0f;
+    }
+    if constexpr (FMT == kFp8) {
+      float g = group_max<16>(am);
+      float sc = group_scale(g);
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) lo |= e4m3_encode(v[k] / sc) << (8 * k);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) hi |= e4m3_encode(v[4 + k] / sc) << (8 * k);
+      if (ok) {
+        *(u32x2*)(q + (size_t)i * W + c * 8) = u32x2{lo, hi};
+        if ((c & 15) == 0) ((float*)s)[i * (W / 128) + c / 16] = sc;
+      }
+    } else {
+      float g = group_max<4>(am);
+      int code = mx_code(g);
+      float inv = mx_inv(code);
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) lo |= e4m3_encode(v[k] * inv) << (8 * k);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) hi |= e4m3_encode(v[4 + k] * inv) << (8 * k);
+      if (ok) {
+        *(u32x2*)(q + (size_t)i * W + c * 8) = u32x2{lo, hi};
+        if ((c & 3) == 0) ((uint8_t*)s)[i * (W / 32) + c / 4] = (uint8_t)code;
+      }
+    }
+  }
+}
+
+template <class C>
+__device__ void down_tile(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int R = p.rows;
+  // ---- shared expert: quantize SMID (every row) into LDS, then its down rows
+  {
+    const uint16_t* smid = wsp<const uint16_t>(p, 8);
+    quant_rows_lds<kFp8, C::S>([&](int i) { return smid + (size_t)i * C::S; }, R, sm.u.sh.q,
+                               sm.u.sh.s);
+    __syncthreads();
+    using RS = RowShape<kFp8, C::S>;
+    using W = Fp8Rows<C::S, RS::G>;
+    // a unit: G consecutive rows (one per sub-group)
+    const int n_units = hn / RS::G;
+    for (int v = wave; v < n_units; v += kWaves) {
+      const uint8_t* rows[RS::G];
+      const float* srow[RS::G];
+#pragma unroll
+      for (int g = 0; g < RS::G; ++g) {
+        const int h = h0 + v * RS::G + g;
+        rows[g] = p.sw2 + (size_t)h * C::S;
+        srow[g] = p.sw2_s + (size_t)(h / 128) * (C::S / 128);
+      }
+      W wr;
+      wr.load(rows, srow, lane);
+      const int g = lane / RS::LPR;
+      for (int t = 0; t < R; ++t) {
+        float acc[1];
+        wr.dot(sm.u.sh.q + (size_t)t * C::S, sm.u.sh.s + t * (C::S / 128), lane, acc);
+        float y = group_sum<RS::LPR>(acc[0]);
+        if ((lane % RS::LPR) == 0) sm.ysh[t * kTileMax + v * RS::G + g] = bf_round(y);
+      }
+    }
+    __syncthreads();
+  }
+  // ---- routed experts, in batches of PB picks (slot order)
+  const int npk = R * C::K;
+  using RD = RowShape<C::FMT, C::I>;
+  const int rg = hn / RD::G;  // row groups of the tile
+  for (int pb0 = 0; pb0 < npk; pb0 += C::PB) {
+    const int pbn = min(C::PB, npk - pb0);
+    {
+      const uint16_t* mid = wsp<const uint16_t>(p, 9);
+      quant_rows_lds<C::FMT, C::I>(
+          [&](int i) { return mid + (size_t)un.picks[pb0 + i] * C::I; }, pbn, sm.u.mid.q,
+          sm.u.mid.s);
+    }
+    __syncthreads();
+    // slots with picks in [pb0, pb0 + pbn)
+    int s_lo = 0;
+    {
+      // the slot of pick position pb0 (binary search over slot_start)
+      int lo = 0, hi = un.n - 1;
+      while (lo < hi) {
+        int mid = (lo + hi + 1) >> 1;
+        if (un.slot_start[mid] <= pb0) lo = mid; else hi = mid - 1;
+      }
+      s_lo = lo;
+    }
+    int s_hi = s_lo;
+    while (s_hi + 1 < un.n && un.slot_start[s_hi + 1] < pb0 + pbn) ++s_hi;
+    const int n_units = (s_hi - s_lo + 1) * rg;
+    for (int v = wave; v < n_units; v += kWaves) {
+      const int slot = s_lo + v / rg, r0 = (v % rg) * RD::G;
+      const int e = un.slot_e[slot];
+      const int j0 = max(un.slot_start[slot], pb0), j1 = min(un.slot_start[slot + 1], pb0 + pbn);
+      const int g = lane / RD::LPR;
+      if constexpr (C::FMT == kFp8) {
+        using W = Fp8Rows<C::I, RD::G>;
+        const uint8_t* rows[RD::G];
+        const float* srow[RD::G];
+        const float* s2 = (const float*)p.w2_s + (size_t)e * (C::H / 128) * (C::I / 128);
+#pragma unroll
+        for (int q = 0; q < RD::G; ++q) {
+          const int h = h0 + r0 + q;
+          rows[q] = p.w2 + ((size_t)e * C::H + h) * C::I;
+          srow[q] = s2 + (size_t)(h / 128) * (C::I / 128);
+        }
+        W wr;
+        wr.load(rows, srow, lane);
+        for (int j = j0; j < j1; ++j) {
+          const int lp = j - pb0;
+          float acc[1];
+          wr.dot(sm.u.mid.q + (size_t)lp * C::I, (const float*)(sm.u.mid.s) + lp * (C::I / 128),
+                 lane, acc);
+          float y = group_sum<RD::LPR>(acc[0]);
+          if ((lane % RD::LPR) == 0) sm.contrib[un.picks[j] * kTileMax + r0 + g] = y;
+        }
+      } else {
+        using W = Fp4Rows<C::I, RD::G>;
+        const uint8_t* rows[RD::G];
+        const uint8_t* srow[RD::G];
+#pragma unroll
+        for (int q = 0; q < RD::G; ++q) {
+          const size_t row = (size_t)e * C::H + h0 + r0 + q;
+          rows[q] = p.w2 + row * (C::I / 2);
+          srow[q] = (const uint8_t*)p.w2_s + row * (C::I / 32);
+        }
+        W wr;
+        wr.load(rows, srow, lane);
+        for (int j = j0; j < j1; ++j) {
+          const int lp = j - pb0;
+          float acc[1];
+          wr.dot(sm.u.mid.q + (size_t)lp * C::I, sm.u.mid.s + lp * (C::I / 32), lane, acc);
+          float y = group_sum<RD::LPR>(acc[0]);
+          if ((lane % RD::LPR) == 0) sm.contrib[un.picks[j] * kTileMax + r0 + g] = y;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  // ---- combine: top-k order, bf16 at every add, then + shared
+  for (int idx = tid; idx < R * hn; idx += kThreads) {
+    const int t = idx / hn, hl = idx % hn;
+    float routed = 0.0f;
+#pragma unroll
+    for (int k = 0; k < C::K; ++k) {
+      const int pk = t * C::K + k;
+      routed = bf_round(routed + bf_round(sm.contrib[pk * kTileMax + hl] * un.wts[pk]));
+    }
+    p.out[(size_t)t * C::H + h0 + hl] = f2bf(routed + sm.ysh[t * kTileMax + hl]);
+  }
+  __syncthreads();
+}
+
+template <class C>
+__device__ void stage_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg) {
+  const int tr = p.tile_rows;
+  const int n_tiles = (C::H + tr - 1) / tr;
+  for (int tile = b; tile < n_tiles; tile += nwg) {
+    const int h0 = tile * tr;
+    down_tile<C>(p, un, sm, h0, min(tr, C::H - h0));
+  }
+}
+
+// ---------------------------------------------------------------- kernels
+template <class C>
+__global__ __launch_bounds__(kThreads) void k_fused(Params p) {
+  __shared__ Union<C> un;
+  __shared__ DownSmem<C> sm;
+  const int b = blockIdx.x, nwg = gridDim.x;
+  if constexpr (C::NORM) {
+    stage_norm<C>(p, b, nwg);
+    arrive(p, kCtlNorm);
+    await_all(p, kCtlNorm, nwg, kStageNorm);
+  }
+  stage_a<C>(p, b, nwg);
+  arrive(p, kCtlA);
+  await_all(p, kCtlA, nwg, kStageA);
+  stage_b<C>(p, b, nwg);
+  arrive(p, kCtlB);
+  await_all(p, kCtlB, nwg, kStageB);
+  build_union<C>(p, un);
+  stage_c<C>(p, un, b, nwg);
+  arrive(p, kCtlC);
+  await_all(p, kCtlC, nwg, kStageC);
+  stage_d<C>(p, un, sm, b, nwg);
+  leave(p);
+}
+
+template <class C>
+__global__ __launch_bounds__(kThreads) void k_norm(Params p) {
+  stage_norm<C>(p, blockIdx.x, gridDim.x);
+}
+template <class C>
+__global__ __launch_bounds__(kThreads) void k_a(Params p) {
+  stage_a<C>(p, blockIdx.x, gridDim.x);
+}
+template <class C>
+__global__ __launch_bounds__(kThreads) void k_b(Params p) {
+  stage_b<C>(p, blockIdx.x, gridDim.x);
+}
+template <class C>
+__global__ __launch_bounds__(kThreads) void k_c(Params p) {
+  __shared__ Union<C> un;
+  build_union<C>(p, un);
+  stage_c<C>(p, un, blockIdx.x, gridDim.x);
+}
+template <class C>
+__global__ __launch_bounds__(kThreads) void k_d(Params p) {
+  __shared__ Union<C> un;
+  __shared__ DownSmem<C> sm;
+  build_union<C>(p, un);
+  stage_d<C>(p, un, sm, blockIdx.x, gridDim.x);
+}
+
+// decode byte i as e4m3 (the fp8 convert the GEMVs use) and as two e2m1 (the fp4 convert)
+__global__ void k_decode(const uint8_t* codes, float* fp8, float* fp4, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    const uint32_t b = codes[i];
+    auto f = __builtin_amdgcn_cvt_pk_f32_fp8((int)b, false);
+    fp8[i] = f[0];
+    auto g = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(b, 1.0f, 0);
+    fp4[2 * i] = g[0];
+    fp4[2 * i + 1] = g[1];
+  }
+}
+
+}  // namespace mkmoe
+
+// ================================================================ host side
+using namespace mkmoe;
+
+namespace {
+
+struct DevInfo {
+  int cus = 0;
+  bool ok = false;
+};
+
+std::mutex g_mu;
+DevInfo g_dev[64];
+double g_deadline_s = 2.0;
+
+int device_info(int dev, DevInfo* out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (dev < 0 || dev >= 64) return MKMOE_ERR_DEVICE;
+  if (!g_dev[dev].ok) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return MKMOE_ERR_HIP;
+    g_dev[dev].cus = prop.multiProcessorCount;
+    g_dev[dev].ok = true;
+  }
+  *out = g_dev[dev];
+  return MKMOE_OK;
+}
+
+enum CfgId { kNone = -1, kIdPlumbing = 0, kIdTp4Fp8, kIdTp4Fp4, kIdTp2Fp4Norm };
+
+template <class C>
+bool shape_is(const mkmoe_shape* s) {
+  return s->hidden == C::H && s->experts == C::E && s->topk == C::K && s->n_group == C::NG &&
+         s->topk_group == C::TG && s->inter == C::I && s->shared_inter == C::S &&
+         s->routed_fmt == C::FMT && s->router_parts == C::P && (s->use_norm != 0) == C::NORM;
+}
+
+int cfg_id(const mkmoe_shape* s) {
+  if (!s) return kNone;
+  if (shape_is<CfgPlumbing>(s)) return kIdPlumbing;
+  if (shape_is<CfgTp4Fp8>(s)) return kIdTp4Fp8;
+  if (shape_is<CfgTp4Fp4>(s)) return kIdTp4Fp4;
+  if (shape_is<CfgTp2Fp4Norm>(s)) return kIdTp2Fp4Norm;
+  return kNone;
+}
+
+int check_shape(const mkmoe_shape* s) {
+  if (!s) return MKMOE_ERR_NULL;
+  if (cfg_id(s) == kNone) return MKMOE_ERR_SHAPE;
+  if (s->max_rows < 1 || s->max_rows > kRowsMax) return MKMOE_ERR_ROWS;
+  return MKMOE_OK;
+}
+
+Layout layout_of(const mkmoe_shape* s) {
+  return make_layout(s->hidden, s->experts, s->topk, s->inter, s->shared_inter, s->routed_fmt,
+                     s->router_parts, s->use_norm, s->max_rows);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+template <class C>
+int launch(const Params& p, int nwg, hipStream_t st, bool staged) {
+  dim3 grid(nwg), block(kThreads);
+  if (!staged) {
+    hipLaunchKernelGGL(k_fused<C>, grid, block, 0, st, p);
+  } else {
+    if constexpr (C::NORM) hipLaunchKernelGGL(k_norm<C>, grid, block, 0, st, p);
+    hipLaunchKernelGGL(k_a<C>, grid, block, 0, st, p);
+    hipLaunchKernelGGL(k_b<C>, grid, block, 0, st, p);
+    hipLaunchKernelGGL(k_c<C>, grid, block, 0, st, p);
+    hipLaunchKernelGGL(k_d<C>, grid, block, 0, st, p);
+  }
+  return hipGetLastError() == hipSuccess ? MKMOE_OK : MKMOE_ERR_LAUNCH;
+}
+
+template <class C>
+int occupancy_ok(int cus) {
+  int per = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_fused<C>, kThreads, 0) != hipSuccess)
+    return MKMOE_ERR_HIP;
+  return per >= 1 ? MKMOE_OK : MKMOE_ERR_DEVICE;
+}
+
+int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, int32_t rows,
+                 void* out, int32_t* ids, float* wts, void* ws, size_t ws_bytes, void* stream,
+                 bool staged) {
+  int rc = check_shape(s);
+  if (rc) return rc;
+  if (!w || !x || !out || !ws) return MKMOE_ERR_NULL;
+  if (!w->gate_w || !w->bias || !w->w13 || !w->w13_s || !w->w2 || !w->w2_s || !w->sgu ||
+      !w->sgu_s || !w->sw2 || !w->sw2_s)
+    return MKMOE_ERR_NULL;
+  if (s->use_norm && !w->norm) return MKMOE_ERR_NULL;
+  if (rows < 1 || rows > s->max_rows) return MKMOE_ERR_ROWS;
+  const void* al[] = {x, out, ws, w->gate_w, w->w13, w->w2, w->sgu, w->sw2};
+  for (const void* q : al)
+    if (!aligned16(q)) return MKMOE_ERR_ALIGN;
+  if (s->use_norm && !aligned16(w->norm)) return MKMOE_ERR_ALIGN;
+  Layout L = layout_of(s);
+  if (ws_bytes < L.total) return MKMOE_ERR_WORKSPACE;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return MKMOE_ERR_HIP;
+  DevInfo di;
+  rc = device_info(dev, &di);
+  if (rc) return rc;
+  const int nwg = di.cus;
+
+  Params p;
+  p.x = (const uint16_t*)x;
+  p.out = (uint16_t*)out;
+  p.ids_out = ids;
+  p.w_out = wts;
+  p.gate_w = (const uint16_t*)w->gate_w;
+  p.bias = (const float*)w->bias;
+  p.norm_w = (const uint16_t*)w->norm;
+  p.w13 = (const uint8_t*)w->w13;
+  p.w13_s = w->w13_s;
+  p.w2 = (const uint8_t*)w->w2;
+  p.w2_s = w->w2_s;
+  p.sgu = (const uint8_t*)w->sgu;
+  p.sgu_s = (const float*)w->sgu_s;
+  p.sw2 = (const uint8_t*)w->sw2;
+  p.sw2_s = (const float*)w->sw2_s;
+  p.ws = (uint8_t*)ws;
+  p.rows = rows;
+  p.rmax = s->max_rows;
+  p.renorm = s->renorm;
+  int tr = (s->hidden + nwg - 1) / nwg;
+  tr = (tr + 3) / 4 * 4;
+  if (tr > kTileMax) tr = kTileMax;
+  p.tile_rows = tr;
+  p.scale = s->routed_scale;
+  p.limit = s->swiglu_limit;
+  p.eps = s->norm_eps;
+  double dl;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    dl = g_deadline_s;
+  }
+  p.deadline = (unsigned long long)(dl * 1e8);
+  for (int i = 0; i < 10; ++i) p.off[i] = L.off[i];
+  hipStream_t st = (hipStream_t)stream;
+  switch (cfg_id(s)) {
+    case kIdPlumbing:
+      if (!staged && (rc = occupancy_ok<CfgPlumbing>(nwg))) return rc;
+      return launch<CfgPlumbing>(p, nwg, st, staged);
+    case kIdTp4Fp8:
+      if (!staged && (rc = occupancy_ok<CfgTp4Fp8>(nwg))) return rc;
+      return launch<CfgTp4Fp8>(p, nwg, st, staged);
+    case kIdTp4Fp4:
+      if (!staged && (rc = occupancy_ok<CfgTp4Fp4>(nwg))) return rc;
+      return launch<CfgTp4Fp4>(p, nwg, st, staged);
+    case kIdTp2Fp4Norm:
+      if (!staged && (rc = occupancy_ok<CfgTp2Fp4Norm>(nwg))) return rc;
+      return launch<CfgTp2Fp4Norm>(p, nwg, st, staged);
+  }
+  return MKMOE_ERR_SHAPE;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mkmoe_abi_version(void) { return MKMOE_ABI_VERSION; }
+
+int mkmoe_shape_supported(const mkmoe_shape* shape) { return check_shape(shape) == MKMOE_OK; }
+
+int mkmoe_workspace_bytes(const mkmoe_shape* shape, size_t* bytes) {
+  int rc = check_shape(shape);
+  if (rc) return rc;
+  if (!bytes) return MKMOE_ERR_NULL;
+  *bytes = layout_of(shape).total;
+  return MKMOE_OK;
+}
+
+int mkmoe_workspace_region(const mkmoe_shape* shape, int32_t region, size_t* offset,
+                           size_t* bytes) {
+  int rc = check_shape(shape);
+  if (rc) return rc;
+  if (!offset || !bytes) return MKMOE_ERR_NULL;
+  if (region < 0 || region >= 10) return MKMOE_ERR_ARG;
+  Layout L = layout_of(shape);
+  *offset = L.off[region];
+  *bytes = L.size[region];
+  return MKMOE_OK;
+}
+
+int mkmoe_init_workspace(const mkmoe_shape* shape, void* ws, size_t ws_bytes, void* stream) {
+  int rc = check_shape(shape);
+  if (rc) return rc;
+  if (!ws) return MKMOE_ERR_NULL;
+  if (ws_bytes < layout_of(shape).total) return MKMOE_ERR_WORKSPACE;
+  if (hipMemsetAsync(ws, 0, kCtlBytes, (hipStream_t)stream) != hipSuccess) return MKMOE_ERR_HIP;
+  return MKMOE_OK;
+}
+
+int mkmoe_forward(const mkmoe_shape* shape, const mkmoe_weights* w, const void* x, int32_t rows,
+                  void* out, int32_t* topk_ids, float* topk_w, void* ws, size_t ws_bytes,
+                  void* stream) {
+  return forward_impl(shape, w, x, rows, out, topk_ids, topk_w, ws, ws_bytes, stream, false);
+}
+
+int mkmoe_forward_staged(const mkmoe_shape* shape, const mkmoe_weights* w, const void* x,
+                         int32_t rows, void* out, int32_t* topk_ids, float* topk_w, void* ws,
+                         size_t ws_bytes, void* stream) {
+  return forward_impl(shape, w, x, rows, out, topk_ids, topk_w, ws, ws_bytes, stream, true);
+}
+
+int mkmoe_set_deadline(double seconds) {
+  if (!(seconds > 0.0) || seconds > 3600.0) return MKMOE_ERR_ARG;
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_deadline_s = seconds;
+  return MKMOE_OK;
+}
+
+int mkmoe_read_errors(const void* ws, int32_t* words, int32_t n, void* stream) {
+  if (!ws || !words) return MKMOE_ERR_NULL;
+  if (n < 1 || n > MKMOE_ERRW_WORDS) return MKMOE_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  if (hipMemcpyAsync(words, (const uint8_t*)ws + kCtlErr * 4, n * 4, hipMemcpyDeviceToHost, st) !=
+      hipSuccess)
+    return MKMOE_ERR_HIP;
+  if (hipStreamSynchronize(st) != hipSuccess) return MKMOE_ERR_HIP;
+  return MKMOE_OK;
+}
+
+int mkmoe_clear_errors(void* ws, void* stream) {
+  if (!ws) return MKMOE_ERR_NULL;
+  if (hipMemsetAsync((uint8_t*)ws + kCtlErr * 4, 0, MKMOE_ERRW_WORDS * 4, (hipStream_t)stream) !=
+      hipSuccess)
+    return MKMOE_ERR_HIP;
+  return MKMOE_OK;
+}
+
+const char* mkmoe_status_string(int status) {
+  switch (status) {
+    case MKMOE_OK: return "ok";
+    case MKMOE_ERR_NULL: return "a required pointer is NULL";
+    case MKMOE_ERR_SHAPE: return "no compiled specialisation has this MoE shape";
+    case MKMOE_ERR_ROWS: return "rows out of range (1 .. max_rows, max_rows <= 48)";
+    case MKMOE_ERR_ALIGN: return "a buffer is not 16-byte aligned";
+    case MKMOE_ERR_WORKSPACE: return "workspace smaller than mkmoe_workspace_bytes";
+    case MKMOE_ERR_LAUNCH: return "the HIP kernel launch failed";
+    case MKMOE_ERR_DEVICE: return "the device cannot keep the persistent grid resident";
+    case MKMOE_ERR_ARG: return "invalid argument";
+    case MKMOE_ERR_HIP: return "a HIP runtime call failed";
+  }
+  return "unknown status";
+}
+
+int mkmoe_device_decode(const uint8_t* codes, float* fp8, float* fp4, int32_t n, void* stream) {
+  if (!codes || !fp8 || !fp4) return MKMOE_ERR_NULL;
+  if (n < 1) return MKMOE_ERR_ARG;
+  hipLaunchKernelGGL(k_decode, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, codes, fp8,
+                     fp4, n);
+  return hipGetLastError() == hipSuccess ? MKMOE_OK : MKMOE_ERR_LAUNCH;
+}
+
+void mkmoe_host_e4m3_encode(const float* x, uint8_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = (uint8_t)e4m3_encode(x[i]);
+}
+
+void mkmoe_host_sigmoid(const float* x, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = sigmoid_exact(x[i]);
+}
+
+void mkmoe_host_topk(const mkmoe_shape* s, const float* scores, const float* bias, int32_t* ids,
+                     float* weights) {
+  topk_host(s->experts, s->topk, s->n_group, s->topk_group, s->renorm, s->routed_scale, scores,
+            bias, ids, weights);
+}
+
+}  // extern "C"

@@ -1,0 +1,183 @@
+// Exact arithmetic of the decode MoE block, compiled for the host and for gfx950.
+//
+// Everything routing depends on is a fixed sequence of IEEE operations with
+// floating-point contraction off, so the device result equals the host build's
+// and the CPU oracle's bit for bit:
+//   - bf16 <-> fp32 (round to nearest even)
+//   - e4m3 encode (clamp to +-448, round to nearest even) in integer steps
+//   - MX scale codes (the "aiter" rule, reference gfx950 common/mx.py:26-37 and
+//     test/kernels/deepseek_v41/check_ffn.py:87-105)
+//   - sigmoid in fp64 from add / multiply / divide / rint / ldexp only, rounded
+//     once to fp32 (an exp by Cody-Waite reduction and a degree-13 Taylor
+//     polynomial; the input clamped to [-60, 60])
+#pragma once
+
+#include <stdint.h>
+#include <string.h>
+#include <math.h>
+
+#ifndef MKMOE_HD
+#define MKMOE_HD __host__ __device__
+#endif
+
+namespace mkmoe {
+
+constexpr float kFp8Max = 448.0f;
+constexpr float kAmaxFloor = 1e-10f;
+constexpr float kInv448 = (float)(1.0 / 448.0);
+constexpr double kSigClamp = 60.0;
+
+MKMOE_HD inline uint32_t f2u(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+MKMOE_HD inline float u2f(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+MKMOE_HD inline float bf2f(uint16_t b) { return u2f((uint32_t)b << 16); }
+// fp32 -> bf16 bits, nearest even (inputs are finite)
+MKMOE_HD inline uint16_t f2bf(float f) {
+  uint32_t u = f2u(f);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+MKMOE_HD inline float bf_round(float f) { return bf2f(f2bf(f)); }
+
+// fp32 -> e4m3 code (OCP fn), v finite: clamped to +-448, then nearest even.
+MKMOE_HD inline uint32_t e4m3_encode(float v) {
+  v = v > kFp8Max ? kFp8Max : (v < -kFp8Max ? -kFp8Max : v);
+  uint32_t b = f2u(v);
+  uint32_t s = (b >> 24) & 0x80u;
+  uint32_t a = b & 0x7fffffffu;
+  uint32_t code;
+  if (a < 0x3c800000u) {  // |v| < 2^-6: subnormal e4m3, m * 2^-9, m = 0..8
+    float t = u2f(a) * 512.0f;  // exact
+    code = (uint32_t)rintf(t);
+  } else {
+    // keep 3 mantissa bits, nearest even, then rebias exponent 127 -> 7
+    uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+    code = (r >> 20) - (120u << 3);
+  }
+  return s | code;
+}
+
+// biased exponent of the smallest power of two >= v (v > 0 finite)
+MKMOE_HD inline int code_ceil(float v) {
+  uint32_t b = f2u(v);
+  return (int)((b >> 23) & 0xffu) + ((b & 0x7fffffu) != 0u ? 1 : 0);
+}
+// the MXFP8 "aiter" code of a group amax: [1, 254]
+MKMOE_HD inline int mx_code(float amax) {
+  float a = amax > kAmaxFloor ? amax : kAmaxFloor;
+  int c = code_ceil(a * kInv448);
+  return c < 1 ? 1 : (c > 254 ? 254 : c);
+}
+// 2^(127 - code), exact for code in [1, 253]; code 254 gives 2^-127 (subnormal)
+MKMOE_HD inline float mx_inv(int code) {
+  return code <= 253 ? u2f((uint32_t)(254 - code) << 23) : u2f(0x00200000u);
+}
+// per-token-group fp8 scale: max(amax, 1e-10) / 448
+MKMOE_HD inline float group_scale(float amax) {
+#pragma clang fp contract(off)
+  float a = amax > kAmaxFloor ? amax : kAmaxFloor;
+  return a / kFp8Max;
+}
+
+// exp(y) for y <= 0 (fp64, IEEE steps only)
+MKMOE_HD inline double exp_nonpos(double y) {
+#pragma clang fp contract(off)
+  const double kInvLn2 = 1.4426950408889634;
+  const double kLn2Hi = 0x1.62e42fee00000p-1;
+  const double kLn2Lo = 0x1.a39ef35793c76p-33;
+  double n = rint(y * kInvLn2);
+  double r = (y - n * kLn2Hi) - n * kLn2Lo;
+  double p = 1.0 / 6227020800.0;  // 1/13!
+  p = p * r + 1.0 / 479001600.0;  // 1/12!
+  p = p * r + 1.0 / 39916800.0;
+  p = p * r + 1.0 / 3628800.0;
+  p = p * r + 1.0 / 362880.0;
+  p = p * r + 1.0 / 40320.0;
+  p = p * r + 1.0 / 5040.0;
+  p = p * r + 1.0 / 720.0;
+  p = p * r + 1.0 / 120.0;
+  p = p * r + 1.0 / 24.0;
+  p = p * r + 1.0 / 6.0;
+  p = p * r + 1.0 / 2.0;
+  p = p * r + 1.0;
+  p = p * r + 1.0;
+  return ldexp(p, (int)n);
+}
+
+MKMOE_HD inline float sigmoid_exact(float x) {
+#pragma clang fp contract(off)
+  double d = (double)x;
+  d = d > kSigClamp ? kSigClamp : (d < -kSigClamp ? -kSigClamp : d);
+  double t = exp_nonpos(-fabs(d));
+  double den = 1.0 + t;
+  double s = d >= 0.0 ? 1.0 / den : t / den;
+  return (float)s;
+}
+
+// a > b in the selection order: larger value, or equal value and lower index
+MKMOE_HD inline bool better(float va, int ia, float vb, int ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+// Host restatement of the grouped top-k (the device runs it on one wave).
+// choice = score + bias; group score = top-1 + top-2 choice of the group; the
+// topk_group best groups (ties: lower group); topk experts of those groups by
+// choice (ties: lower id), in selection order; weights score * f with
+// f = scale / max(sum, 1e-20) summed in selection order (renorm) or f = scale.
+inline void topk_host(int E, int K, int NG, int TG, int renorm, float scale, const float* score,
+                      const float* bias, int32_t* ids, float* wts) {
+#pragma clang fp contract(off)
+  float choice[1024];
+  bool keep[1024];
+  int per = E / NG;
+  for (int e = 0; e < E; ++e) {
+    choice[e] = score[e] + bias[e];
+    keep[e] = NG <= 1;
+  }
+  if (NG > 1) {
+    float gs[64];
+    bool gsel[64];
+    for (int g = 0; g < NG; ++g) {
+      int b1 = -1, b2 = -1;
+      for (int e = g * per; e < (g + 1) * per; ++e) {
+        if (b1 < 0 || better(choice[e], e, choice[b1], b1)) {
+          b2 = b1;
+          b1 = e;
+        } else if (b2 < 0 || better(choice[e], e, choice[b2], b2)) {
+          b2 = e;
+        }
+      }
+      gs[g] = choice[b1] + choice[b2];
+      gsel[g] = false;
+    }
+    for (int t = 0; t < TG; ++t) {
+      int best = -1;
+      for (int g = 0; g < NG; ++g)
+        if (!gsel[g] && (best < 0 || better(gs[g], g, gs[best], best))) best = g;
+      gsel[best] = true;
+      for (int e = best * per; e < (best + 1) * per; ++e) keep[e] = true;
+    }
+  }
+  float total = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    int best = -1;
+    for (int e = 0; e < E; ++e)
+      if (keep[e] && (best < 0 || better(choice[e], e, choice[best], best))) best = e;
+    keep[best] = false;
+    ids[k] = best;
+    wts[k] = score[best];
+    total = total + score[best];
+  }
+  float f = scale;
+  if (renorm) f = scale / (total > 1e-20f ? total : 1e-20f);
+  for (int k = 0; k < K; ++k) wts[k] = wts[k] * f;
+}
+
+}  // namespace mkmoe

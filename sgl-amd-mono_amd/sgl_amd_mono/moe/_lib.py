@@ -1,0 +1,149 @@
+"""ctypes binding of the in-tree HIP library (the C ABI of ``include/mkmoe.h``).
+
+The library is loaded from this directory only. There is no fallback: a missing
+or unloadable library raises, so a GPU run can never silently take another path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libmkmoe.so"
+
+FMT_FP8_B128 = 1
+FMT_MXFP4 = 2
+ERRW_WORDS = 8
+ERRW_CODE, ERRW_STAGE, ERRW_BLOCK, ERRW_COUNT = 0, 1, 2, 3
+REGIONS = {
+    "x_normed": 0,
+    "x_codes": 1,
+    "x_scales": 2,
+    "x_codes_shared": 3,
+    "x_scales_shared": 4,
+    "router_parts": 5,
+    "ids": 6,
+    "weights": 7,
+    "shared_mid": 8,
+    "mid": 9,
+}
+STAGES = {1: "norm", 2: "router + quantize", 3: "route + shared gate_up", 4: "routed gate_up", 5: "down"}
+
+# every symbol include/mkmoe.h declares
+EXPORTS = (
+    "mkmoe_abi_version",
+    "mkmoe_shape_supported",
+    "mkmoe_workspace_bytes",
+    "mkmoe_init_workspace",
+    "mkmoe_forward",
+    "mkmoe_forward_staged",
+    "mkmoe_set_deadline",
+    "mkmoe_read_errors",
+    "mkmoe_clear_errors",
+    "mkmoe_workspace_region",
+    "mkmoe_status_string",
+    "mkmoe_device_decode",
+    "mkmoe_host_e4m3_encode",
+    "mkmoe_host_sigmoid",
+    "mkmoe_host_topk",
+)
+
+
+class Shape(ctypes.Structure):
+    _fields_ = [
+        ("hidden", ctypes.c_int32),
+        ("experts", ctypes.c_int32),
+        ("topk", ctypes.c_int32),
+        ("n_group", ctypes.c_int32),
+        ("topk_group", ctypes.c_int32),
+        ("inter", ctypes.c_int32),
+        ("shared_inter", ctypes.c_int32),
+        ("routed_fmt", ctypes.c_int32),
+        ("router_parts", ctypes.c_int32),
+        ("renorm", ctypes.c_int32),
+        ("use_norm", ctypes.c_int32),
+        ("max_rows", ctypes.c_int32),
+        ("routed_scale", ctypes.c_float),
+        ("swiglu_limit", ctypes.c_float),
+        ("norm_eps", ctypes.c_float),
+        ("reserved", ctypes.c_float),
+    ]
+
+
+class Weights(ctypes.Structure):
+    _fields_ = [
+        (n, ctypes.c_void_p)
+        for n in ("gate_w", "bias", "w13", "w13_s", "w2", "w2_s", "sgu", "sgu_s", "sw2", "sw2_s", "norm")
+    ]
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises when it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python sgl-amd-mono_amd/build.py` "
+                "(the MoE block has no other implementation)"
+            )
+        L = ctypes.CDLL(str(LIB_PATH))
+        vp, i32, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_size_t
+        sp, wp = ctypes.POINTER(Shape), ctypes.POINTER(Weights)
+        L.mkmoe_abi_version.restype = ctypes.c_int
+        L.mkmoe_shape_supported.argtypes = [sp]
+        L.mkmoe_workspace_bytes.argtypes = [sp, ctypes.POINTER(sz)]
+        L.mkmoe_init_workspace.argtypes = [sp, vp, sz, vp]
+        fwd = [sp, wp, vp, i32, vp, vp, vp, vp, sz, vp]
+        L.mkmoe_forward.argtypes = fwd
+        L.mkmoe_forward_staged.argtypes = fwd
+        L.mkmoe_set_deadline.argtypes = [ctypes.c_double]
+        L.mkmoe_read_errors.argtypes = [vp, ctypes.POINTER(i32), i32, vp]
+        L.mkmoe_clear_errors.argtypes = [vp, vp]
+        L.mkmoe_workspace_region.argtypes = [sp, i32, ctypes.POINTER(sz), ctypes.POINTER(sz)]
+        L.mkmoe_status_string.argtypes = [ctypes.c_int]
+        L.mkmoe_status_string.restype = ctypes.c_char_p
+        L.mkmoe_device_decode.argtypes = [vp, vp, vp, i32, vp]
+        L.mkmoe_host_e4m3_encode.argtypes = [vp, vp, ctypes.c_int64]
+        L.mkmoe_host_e4m3_encode.restype = None
+        L.mkmoe_host_sigmoid.argtypes = [vp, vp, ctypes.c_int64]
+        L.mkmoe_host_sigmoid.restype = None
+        L.mkmoe_host_topk.argtypes = [sp, vp, vp, vp, vp]
+        L.mkmoe_host_topk.restype = None
+        _lib = L
+    return _lib
+
+
+def status_string(rc: int) -> str:
+    return lib().mkmoe_status_string(rc).decode()
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what}: {status_string(rc)} ({rc})")
+
+
+def shape_of(preset, max_rows: int | None = None) -> Shape:
+    """The C shape of a ``presets.MoePreset``."""
+    from .presets import FMT_CODES
+
+    return Shape(
+        hidden=preset.hidden,
+        experts=preset.experts,
+        topk=preset.topk,
+        n_group=preset.n_group,
+        topk_group=preset.topk_group,
+        inter=preset.inter,
+        shared_inter=preset.shared_inter,
+        routed_fmt=FMT_CODES[preset.routed_fmt],
+        router_parts=preset.router_parts,
+        renorm=1 if preset.renorm else 0,
+        use_norm=0 if preset.norm_eps is None else 1,
+        max_rows=preset.max_rows if max_rows is None else max_rows,
+        routed_scale=preset.routed_scale,
+        swiglu_limit=preset.swiglu_limit,
+        norm_eps=0.0 if preset.norm_eps is None else preset.norm_eps,
+        reserved=0.0,
+    )

@@ -1,0 +1,171 @@
+"""Parity of the HIP MoE block (through the C ABI) with the CPU oracle, on an MI355X.
+
+Bars: router part sums, activation codes, expert ids and routing weights bit
+for bit; the bf16 output within max-abs 2e-2 and relative L2 1e-2 of the
+oracle; the persistent and the staged launches bit for bit alike; repeated and
+graph-replayed launches bit for bit alike.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, REL_L2 = 2e-2, 1e-2
+CASES = [
+    ("cfg1_plumbing_fp8", 4),
+    ("cfg2_tp4_fp8", 1),
+    ("cfg2_tp4_fp8", 8),
+    ("cfg2_tp4_fp8", 48),
+    ("cfg3_tp4_mxfp4", 1),
+    ("cfg3_tp4_mxfp4", 8),
+    ("cfg3_tp4_mxfp4", 48),
+    ("cfg4_tp4_mxfp4_zipf", 48),
+    ("cfg5_tp2_mxfp4_norm", 1),
+    ("cfg5_tp2_mxfp4_norm", 8),
+    ("cfg5_tp2_mxfp4_norm", 48),
+]
+_cache = {}
+
+
+def _case(workload, rows):
+    from gpu_case import build
+
+    key = (workload, rows)
+    if key not in _cache:
+        _cache.clear()  # one layer's weights on the GPU at a time
+        torch.cuda.empty_cache()
+        _cache[key] = build(workload, rows)
+    return _cache[key]
+
+
+def _runner(case):
+    from sgl_amd_mono.moe.runner import MoeRunner
+
+    return MoeRunner(case.preset, "cuda")
+
+
+def test_device_decode_matches_tables():
+    from oracle import formats as fm
+    from sgl_amd_mono.moe import _lib
+
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8).cuda()
+    f8 = torch.empty(256, device="cuda")
+    f4 = torch.empty(512, device="cuda")
+    _lib.check(
+        _lib.lib().mkmoe_device_decode(codes.data_ptr(), f8.data_ptr(), f4.data_ptr(), 256, torch.cuda.current_stream().cuda_stream),
+        "decode",
+    )
+    torch.cuda.synchronize()
+    tab = fm.e4m3_table()
+    got = f8.cpu().double().numpy()
+    ok = ~np.isnan(tab)
+    assert np.array_equal(got[ok], tab[ok]) and np.all(np.isnan(got[~ok]))
+    want4 = fm.fp4_unpack(torch.arange(256, dtype=torch.int32).to(torch.uint8)).numpy()
+    assert np.array_equal(f4.cpu().numpy(), want4)
+
+
+@pytest.mark.parametrize("workload,rows", CASES)
+def test_parity(workload, rows):
+    from gpu_case import errors
+
+    c = _case(workload, rows)
+    run = _runner(c)
+    ids = torch.zeros(rows, c.p["topk"], dtype=torch.int32, device="cuda")
+    wts = torch.zeros(rows, c.p["topk"], dtype=torch.float32, device="cuda")
+    out = run.moe(c.w, c.x, topk_ids=ids, topk_w=wts)
+    torch.cuda.synchronize()
+    run.raise_on_device_error()
+    print(f"\n{workload} R={rows}", flush=True)
+    # router part sums, bit for bit
+    parts = run.region("router_parts")[: rows * c.p["experts"] * c.p["router_parts"] * 4]
+    parts = parts.view(torch.float32).cpu().numpy().reshape(rows, c.p["experts"], c.p["router_parts"])
+    assert np.array_equal(parts.view(np.uint32), c.parts.view(np.uint32)), "router part sums"
+    # routing, bit for bit
+    assert np.array_equal(ids.cpu().numpy(), c.ids), "expert ids"
+    assert np.array_equal(wts.cpu().numpy().view(np.uint32), c.wts.view(np.uint32)), "routing weights"
+    e = errors(out[torch.from_numpy(c.check).cuda()], c.ref)
+    print(f"  out vs oracle: {e}", flush=True)
+    assert not e["nan"] and not torch.isnan(out).any()
+    assert e["rel_l2"] <= REL_L2, e
+    assert e["max_abs"] <= MAX_ABS, e
+
+
+@pytest.mark.parametrize("workload,rows", [("cfg2_tp4_fp8", 8), ("cfg3_tp4_mxfp4", 8), ("cfg5_tp2_mxfp4_norm", 8)])
+def test_activation_codes_bitexact(workload, rows):
+    """The kernel's quantized x (and normed x) equal the oracle's bit for bit."""
+    from oracle import formats as fm
+
+    c = _case(workload, rows)
+    run = _runner(c)
+    run.moe(c.w, c.x)
+    torch.cuda.synchronize()
+    h = c.p["hidden"]
+    if c.p["norm_eps"] is not None:
+        xn = run.region("x_normed")[: rows * h * 2].view(torch.bfloat16).cpu().reshape(rows, h)
+        assert torch.equal(xn.view(torch.int16), c.xin.view(torch.int16)), "normed x"
+    q, s = fm.group_fp8_quant(c.xin, 128)
+    name_q, name_s = ("x_codes_shared", "x_scales_shared") if c.p["routed_fmt"] == "mxfp4" else ("x_codes", "x_scales")
+    assert torch.equal(run.region(name_q)[: rows * h].cpu().reshape(rows, h), q), "group-128 codes"
+    got_s = run.region(name_s)[: rows * (h // 128) * 4].view(torch.float32).cpu().reshape(rows, -1)
+    assert torch.equal(got_s, s), "group-128 scales"
+    if c.p["routed_fmt"] == "mxfp4":
+        q, code = fm.mxfp8_quant(c.xin)
+        assert torch.equal(run.region("x_codes")[: rows * h].cpu().reshape(rows, h), q), "MXFP8 codes"
+        assert torch.equal(run.region("x_scales")[: rows * (h // 32)].cpu().reshape(rows, -1), code), "MXFP8 scales"
+
+
+@pytest.mark.parametrize("workload,rows", [("cfg1_plumbing_fp8", 4), ("cfg2_tp4_fp8", 8), ("cfg3_tp4_mxfp4", 48), ("cfg5_tp2_mxfp4_norm", 8)])
+def test_staged_equals_fused_and_repeats(workload, rows):
+    c = _case(workload, rows)
+    run = _runner(c)
+    a = run.moe(c.w, c.x).clone()
+    b = run.moe(c.w, c.x, staged=True).clone()
+    d = run.moe(c.w, c.x).clone()
+    torch.cuda.synchronize()
+    run.raise_on_device_error()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16)), "staged != fused"
+    assert torch.equal(a.view(torch.int16), d.view(torch.int16)), "repeat differs"
+
+
+def test_graph_replay_bitwise():
+    """Every row count of one preset in one graph, replayed with eager work between replays."""
+    c = _case("cfg2_tp4_fp8", 8)
+    run = _runner(c)
+    xs = [c.x[:r].contiguous() for r in (1, 3, 8)]
+    outs = [torch.empty(r, c.p["hidden"], dtype=torch.bfloat16, device="cuda") for r in (1, 3, 8)]
+    for x, o in zip(xs, outs):
+        run.moe(c.w, x, out=o)
+    torch.cuda.synchronize()
+    ref = [o.clone() for o in outs]
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for x, o in zip(xs, outs):
+                run.moe(c.w, x, out=o)
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(6):
+        for o in outs:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, r in zip(outs, ref):
+            assert torch.equal(o.view(torch.int16), r.view(torch.int16)), f"replay {i}"
+        run.moe(c.w, xs[1], out=outs[1])  # eager work between replays
+        torch.cuda.synchronize()
+    run.raise_on_device_error()
+
+
+def test_host_validation_errors():
+    c = _case("cfg1_plumbing_fp8", 4)
+    run = _runner(c)
+    with pytest.raises(RuntimeError, match="rows"):
+        run.moe(c.w, torch.zeros(49, c.p["hidden"], dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(RuntimeError, match="out"):
+        run.moe(c.w, c.x, out=torch.zeros(4, 8, dtype=torch.bfloat16, device="cuda"))
+    bad = type(c.w)(**{**c.w.__dict__, "gate_w": c.w.gate_w.float()})
+    with pytest.raises(RuntimeError, match="gate_w"):
+        run.moe(bad, c.x)

@@ -1,0 +1,182 @@
+"""Pin the oracle's routing (``oracle/routing.py``) and the kernel's host-built sigmoid and top-k.
+
+Pins: fixed-order logits against an fp64 matmul and an index-by-index scalar
+restatement; the fp64 sigmoid against math.exp and the C build of the
+kernel's steps (bit for bit); the grouped top-k against exhaustive search of
+group and expert subsets at E = 16, its invariants, and the C build (bit for
+bit, ties included); the fixed-order RMSNorm against an fp64 RMSNorm.
+"""
+
+import itertools
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import routing as rt
+
+
+def test_router_logits_close_to_fp64():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(3, 7168, generator=g).to(torch.bfloat16)
+    w = (torch.randn(16, 7168, generator=g) / math.sqrt(7168)).to(torch.bfloat16)
+    got = rt.router_logits(x, w, 7)
+    ref = x.double() @ w.double().T
+    assert np.abs(got - ref.numpy()).max() < 2e-5
+
+
+def test_router_logits_scalar_restatement():
+    """Index by index: lane l of chunk c holds elements 512 c + 8 l + j; parts of C / P chunks."""
+    g = torch.Generator().manual_seed(1)
+    h, parts = 1024, 2
+    x = torch.randn(2, h, generator=g).to(torch.bfloat16)
+    w = torch.randn(3, h, generator=g).to(torch.bfloat16)
+    got = rt.router_logits(x, w, parts)
+    xs, ws = x.float().numpy(), w.float().numpy()
+    f = np.float32
+    per = (h // 512) // parts
+    for r in range(2):
+        for e in range(3):
+            logit = f(0)
+            for p in range(parts):
+                lanes = []
+                for lane in range(64):
+                    a = f(0)
+                    for c in range(p * per, (p + 1) * per):
+                        for j in range(8):
+                            k = 512 * c + 8 * lane + j
+                            a = f(a + f(xs[r, k] * ws[e, k]))
+                    lanes.append(a)
+                d = 32
+                while d >= 1:
+                    lanes = [f(lanes[i] + lanes[i + d]) for i in range(d)]
+                    d //= 2
+                logit = f(logit + lanes[0])
+            assert got[r, e] == logit
+
+
+def test_sigmoid_exact_accuracy():
+    rng = np.random.default_rng(2)
+    x = np.concatenate([rng.standard_normal(20000) * 4, np.linspace(-70, 70, 2001)]).astype(np.float32)
+    got = rt.sigmoid_exact(x)
+    xc = np.clip(x.astype(np.float64), -60, 60)
+    ref = np.array([1 / (1 + math.exp(-v)) for v in xc])
+    # within half an fp32 ulp of the true value, plus fp64 slack
+    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(got.astype(np.float64) - ref) <= 0.5 * ulp + 1e-15)
+    assert np.mean(got == ref.astype(np.float32)) > 0.9999
+
+
+def test_host_sigmoid_bitexact():
+    from sgl_amd_mono.moe import _lib
+
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.standard_normal(100000) * 3, rng.uniform(-80, 80, 20000),
+                        [0.0, -0.0, 60.0, -60.0, 1e-30, -1e-30]]).astype(np.float32)  # fmt: skip
+    out = np.zeros_like(x)
+    _lib.lib().mkmoe_host_sigmoid(x.ctypes.data, out.ctypes.data, x.size)
+    assert np.array_equal(out.view(np.uint32), rt.sigmoid_exact(x).view(np.uint32))
+
+
+def _brute_topk(choice, scores, k, n_group, topk_group, scale):
+    """Exhaustive: the group subset with the largest scores in (score desc, index asc) order,
+    then the expert subset likewise, then the weights."""
+    e = len(choice)
+    per = e // n_group
+    gs = []
+    for g in range(n_group):
+        top = sorted(choice[g * per : (g + 1) * per], reverse=True)
+        gs.append(np.float32(top[0] + top[1]) if per > 1 else np.float32(top[0]))
+
+    def rank_key(vals, idxs):
+        return sorted(((-float(vals[i]), i) for i in idxs))
+
+    best_groups = None
+    for sub in itertools.combinations(range(n_group), topk_group):
+        key = rank_key(gs, sub)
+        # a subset is the top set iff every outside group ranks below every member
+        outside = [g for g in range(n_group) if g not in sub]
+        if all((-float(gs[o]), o) > key[-1] for o in outside):
+            best_groups = sub
+    allowed = [x for g in best_groups for x in range(g * per, (g + 1) * per)]
+    order = [i for _, i in rank_key(choice, allowed)][:k]
+    w = scores[order]
+    total = np.float32(0)
+    for v in w:
+        total = np.float32(total + v)
+    f = np.float32(np.float32(scale) / total)
+    return np.array(order), (w * f).astype(np.float32)
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_grouped_topk_exhaustive(seed):
+    rng = np.random.default_rng(seed)
+    e, k, ng, tg = 16, 4, 4, 2
+    scores = rt.sigmoid_exact(rng.standard_normal((1, e)).astype(np.float32))
+    bias = (rng.standard_normal(e) * 0.02).astype(np.float32)
+    if seed % 3 == 0:  # plant ties
+        scores[0, 5] = scores[0, 9]
+        bias[5] = bias[9]
+    ids, wts = rt.grouped_topk(scores, bias, k, ng, tg, 2.5)
+    choice = (scores[0] + bias).astype(np.float32)
+    bid, bw = _brute_topk(choice, scores[0], k, ng, tg, 2.5)
+    assert ids[0].tolist() == bid.tolist()
+    assert np.array_equal(wts[0].view(np.uint32), bw.view(np.uint32))
+
+
+def test_grouped_topk_invariants():
+    rng = np.random.default_rng(7)
+    scores = rt.sigmoid_exact(rng.standard_normal((64, 256)).astype(np.float32))
+    bias = (rng.standard_normal(256) * 0.02).astype(np.float32)
+    ids, wts = rt.grouped_topk(scores, bias, 8, 8, 4, 2.5)
+    choice = scores + bias
+    for r in range(64):
+        assert len(set(ids[r].tolist())) == 8
+        assert len({int(i) // 32 for i in ids[r]}) <= 4
+        c = choice[r, ids[r]]
+        assert np.all(c[:-1] >= c[1:])
+        assert abs(float(wts[r].sum()) - 2.5) < 1e-5
+
+
+def _host_topk(preset, scores, bias):
+    from sgl_amd_mono.moe import _lib
+
+    shape = _lib.shape_of(preset)
+    ids = np.zeros(preset.topk, np.int32)
+    w = np.zeros(preset.topk, np.float32)
+    _lib.lib().mkmoe_host_topk(
+        __import__("ctypes").byref(shape), scores.ctypes.data, bias.ctypes.data, ids.ctypes.data, w.ctypes.data
+    )
+    return ids, w
+
+
+@pytest.mark.parametrize("name", ["plumbing_fp8", "dsv3_tp4_fp8"])
+def test_host_topk_bitexact(name):
+    from sgl_amd_mono.moe.presets import PRESETS
+
+    p = PRESETS[name]
+    rng = np.random.default_rng(11)
+    bias = np.ascontiguousarray((rng.standard_normal(p.experts) * 0.02).astype(np.float32))
+    for t in range(200):
+        scores = rt.sigmoid_exact(rng.standard_normal((1, p.experts)).astype(np.float32))
+        if t % 4 == 0:  # ties across groups and within
+            scores[0, : p.experts // 2] = scores[0, p.experts // 2 :]
+        if t % 4 == 1:
+            scores[0, :] = scores[0, 0]
+        scores = np.ascontiguousarray(scores[0])
+        ids, w = _host_topk(p, scores, bias)
+        rid, rw = rt.grouped_topk(scores[None], bias, p.topk, p.n_group, p.topk_group, p.routed_scale)
+        assert ids.tolist() == rid[0].tolist()
+        assert np.array_equal(w.view(np.uint32), rw[0].view(np.uint32))
+
+
+def test_rmsnorm_close_to_fp64():
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(4, 7168, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(7168, generator=g)).to(torch.bfloat16)
+    got = rt.rmsnorm_exact(x, w, 1e-6).float()
+    xd = x.double()
+    ref = xd * torch.rsqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-6) * w.double()
+    ulp = torch.ldexp(torch.ones_like(ref), torch.frexp(ref.abs())[1] - 8)
+    assert float(((got.double() - ref).abs() / ulp).max()) <= 1.0
