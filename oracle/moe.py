@@ -5,7 +5,11 @@ TEST INFRASTRUCTURE ONLY (the oracle): imported by ``tests/``,
 product path.
 
 It restates ``golden_partial`` of ``test/kernels/deepseek_v41/check_ffn.py:209-232``
-generalised over the presets (weight format, activation rule, routing, widths):
+generalised over the presets (weight format, activation rule, routing, widths).
+With ``exact=True`` (the default) every GEMV and SwiGLU follows the kernel's
+fixed arithmetic order (``oracle.exact``), so the kernel's output must match
+bit for bit; ``exact=False`` keeps the golden's fp32 matmuls and torch's silu
+(the CPU baseline, and a cross-check within tolerance):
 
 - routed experts, per expert e of the step's union (ascending id), its picks'
   rows: h = xr @ W13(e)^T in fp32; gate = h[:, :I], up = h[:, I:];
@@ -83,20 +87,41 @@ class ExpertSource:
         return self.w13[e], self.w13_s[e], self.w2[e], self.w2_s[e]
 
 
-def moe_partial(x: torch.Tensor, w: dict, p: dict, experts=None):
+def _qdq_codes(x: torch.Tensor, fmt: str):
+    """(codes, scales) of the activation rule feeding weight format ``fmt``."""
+    if fmt == MXFP4:
+        return fm.mxfp8_quant(x)
+    return fm.group_fp8_quant(x, 128)
+
+
+def _gemv(wq, ws, xq, xs, fmt) -> np.ndarray:
+    from . import exact as ex
+
+    if fmt == MXFP4:
+        return ex.gemv_mxfp4(wq, ws, xq, xs)
+    return ex.gemv_fp8_b128(wq, ws, xq, xs)
+
+
+def moe_partial(x: torch.Tensor, w: dict, p: dict, experts=None, exact: bool = True):
     """This rank's MoE partial of bf16 rows ``x`` [R, H].
 
     ``w`` holds CPU tensors: gate_w bf16 [E, H], bias fp32 [E], norm bf16 [H]
     (fused-norm preset only), sgu / sgu_s / sw2 / sw2_s (FP8 128 x 128 shared
     expert), and either the per-expert tensors w13 / w13_s / w2 / w2_s or an
-    ``experts`` source with ``get(e)``. Returns a dict with ids, weights,
-    logits, the normed rows (if any) and the bf16 output.
+    ``experts`` source with ``get(e)``. ``exact``: the kernel's GEMV and SwiGLU
+    arithmetic (``oracle.exact``), bit for bit; otherwise the golden's fp32
+    matmuls and torch's silu. Returns ids, weights, logits, the normed rows (if
+    any), the per-pick contributions and the bf16 output.
     """
+    from . import exact as ex
+
     lim = float(p["swiglu_limit"])
     r = x.shape[0]
     h = p["hidden"]
     inter = p["inter"]
+    ish = p["shared_inter"]
     fmt = p["routed_fmt"]
+    topk = p["topk"]
     if experts is None:
         experts = ExpertSource(w["w13"], w["w13_s"], w["w2"], w["w2_s"])
     xin = x
@@ -105,24 +130,39 @@ def moe_partial(x: torch.Tensor, w: dict, p: dict, experts=None):
     logit, ids_np, wts_np = rt.route(xin, w["gate_w"], w["bias"], p)
     ids = torch.from_numpy(ids_np.astype(np.int64))
     wts = torch.from_numpy(wts_np)
-    xr = act_qdq(xin, fmt)
-    xs = act_qdq(xin, FP8_B128)
-    topk = p["topk"]
     per_k = torch.zeros(r, topk, h)
-    for e in ids.unique().tolist():
-        rows, ks = (ids == e).nonzero(as_tuple=True)
-        w13, w13_s, w2, w2_s = experts.get(e)
-        hh = xr[rows] @ deq_weight(w13, w13_s, fmt).T
-        gate, up = hh[:, :inter], hh[:, inter:]
-        mid = fm.bf(silu(gate.clamp(max=lim)) * up.clamp(-lim, lim))
-        y = act_qdq(mid, fmt) @ deq_weight(w2, w2_s, fmt).T
-        per_k[rows, ks] = fm.bf(y * wts[rows, ks, None])
+    if exact:
+        xq, xs = _qdq_codes(xin, fmt)
+        xq2, xs2 = fm.group_fp8_quant(xin, 128)
+        for e in ids.unique().tolist():
+            rows, ks = (ids == e).nonzero(as_tuple=True)
+            w13, w13_s, w2, w2_s = experts.get(e)
+            hh = _gemv(w13, w13_s, xq[rows], xs[rows], fmt)
+            mid = ex.swiglu_routed(hh[:, :inter], hh[:, inter:], lim)
+            mq, ms = _qdq_codes(torch.from_numpy(mid), fmt)
+            y = _gemv(w2, w2_s, mq, ms, fmt)
+            per_k[rows, ks] = fm.bf(torch.from_numpy(y) * wts[rows, ks, None])
+    else:
+        xr = act_qdq(xin, fmt)
+        for e in ids.unique().tolist():
+            rows, ks = (ids == e).nonzero(as_tuple=True)
+            w13, w13_s, w2, w2_s = experts.get(e)
+            hh = xr[rows] @ deq_weight(w13, w13_s, fmt).T
+            gate, up = hh[:, :inter], hh[:, inter:]
+            mid = fm.bf(silu(gate.clamp(max=lim)) * up.clamp(-lim, lim))
+            y = act_qdq(mid, fmt) @ deq_weight(w2, w2_s, fmt).T
+            per_k[rows, ks] = fm.bf(y * wts[rows, ks, None])
     routed = torch.zeros(r, h)
     for k in range(topk):
         routed = fm.bf(routed + per_k[:, k])
-    ish = p["shared_inter"]
-    if ish > 0:
-        hs = xs @ fm.deq_fp8_b128(w["sgu"], w["sgu_s"]).T
+    if ish > 0 and exact:
+        hs = ex.gemv_fp8_b128(w["sgu"], w["sgu_s"], xq2, xs2)
+        smid = ex.swiglu_shared(hs[:, :ish], hs[:, ish:], lim)
+        smq, sms = fm.group_fp8_quant(torch.from_numpy(smid), 128)
+        shared = fm.bf(torch.from_numpy(ex.gemv_fp8_b128(w["sw2"], w["sw2_s"], smq, sms)))
+    elif ish > 0:
+        xs_ = act_qdq(xin, FP8_B128)
+        hs = xs_ @ fm.deq_fp8_b128(w["sgu"], w["sgu_s"]).T
         smid = fm.bf(silu(fm.bf(hs[:, :ish].clamp(max=lim))) * fm.bf(hs[:, ish:].clamp(-lim, lim)))
         shared = fm.bf(act_qdq(smid, FP8_B128) @ fm.deq_fp8_b128(w["sw2"], w["sw2_s"]).T)
     else:

@@ -7,9 +7,14 @@
 //   A  router GEMV part sums (fixed order) + activation quantization
 //                                                              wave per (expert, K part) / (row, 512 cols)
 //   B  routing (sigmoid, grouped top-k, weights)               wave per row
-//      + shared expert gate_up, SwiGLU                         wave per 2 intermediate columns
-//   C  routed gate_up + SwiGLU for the step's union of experts wave per (expert, 2 columns)
+//      + shared expert gate_up + SwiGLU                        wave per (column, 8 rows)
+//   C  routed gate_up + SwiGLU for the step's union of experts wave per (expert, column, 8 picks)
 //   D  down GEMVs (shared + routed) and the weighted combine   workgroup per tile of output rows
+// Every GEMV runs on the vector ALUs in one fixed fp32 order (see WRows), so the
+// output is reproducible bit for bit by a CPU restatement; the gfx950 scaled MFMA
+// accumulates with an internal precision that no restatement can follow.
+// Hand-off data between workgroups is written and read with device-coherent
+// (sc1) buffer accesses, so the counters need no L2 write-back / invalidate.
 // The staged entry point runs the same stage functions as one launch each.
 //
 // Reference: the stages of sgl_amd_mono/deepseek_v41/gfx950/stages/moe.py
@@ -24,8 +29,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
-#include <atomic>
 #include <mutex>
+#include <type_traits>
 
 #include "../../include/mkmoe.h"
 #include "mkmoe_numerics.h"
@@ -34,10 +39,11 @@ namespace mkmoe {
 
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
-constexpr int kRowsMax = 48;  // rows a launch takes at most
-constexpr int kTileMax = 32;  // output rows of a down tile, at most
+constexpr int kRowsMax = 48;   // rows a launch takes at most
+constexpr int kTileMax = 32;   // output rows of a down tile, at most
 constexpr int kFp8 = MKMOE_FMT_FP8_B128;
 constexpr int kFp4 = MKMOE_FMT_MXFP4;
+constexpr int kAuxDev = 16;  // sc1: device-coherent access
 
 // control words at the start of the workspace
 constexpr int kCtlNorm = 0, kCtlA = 1, kCtlB = 2, kCtlC = 3, kCtlExit = 5;
@@ -53,12 +59,14 @@ struct Cfg {
                        P = P_;
   static constexpr bool NORM = NORM_;
   static constexpr int CH512 = H / 512;  // router / quantize chunks of a row
-  static_assert(H % 512 == 0 && CH512 % P == 0, "router chunks");
+  static_assert(H % 1024 == 0 && CH512 % P == 0, "router chunks, K split over 8 waves");
   static_assert(I % 128 == 0 && S % 128 == 0, "widths");
   static_assert(E <= 1024 && (NG == 1 || (E % NG == 0)), "experts");
-  // down-stage mid batch: picks whose quantized rows fit 32 KB of LDS
+  // down-stage mid batch: picks whose quantized rows fit ~32 KB of LDS
   static constexpr int PB = 32768 / I;
-  static constexpr int SCB = FMT == kFp4 ? I / 32 : (I / 128) * 4;  // scale bytes a mid row
+  static constexpr int MQS = I + 16;  // LDS row stride of quantized mid (bank spread)
+  static constexpr int SQS = S + 16;
+  static constexpr int MSC = FMT == kFp4 ? I / 32 : I / 128;  // mid scales a pick
 };
 
 using CfgPlumbing = Cfg<1024, 16, 4, 1, 1, 512, 512, kFp8, 2, false>;
@@ -116,6 +124,7 @@ struct Params {
   const uint8_t* sw2;
   const float* sw2_s;
   uint8_t* ws;
+  uint32_t ws_bytes;
   int rows;
   int rmax;
   int renorm;
@@ -124,21 +133,49 @@ struct Params {
   float limit;
   float eps;
   unsigned long long deadline;  // s_memrealtime ticks (100 MHz)
-  size_t off[10];
+  uint32_t off[10];
 };
 
 // ---------------------------------------------------------------- small device helpers
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; }
 __device__ __forceinline__ u32x4 ld16_nt(const void* p) {
   return __builtin_nontemporal_load((const u32x4*)p);
 }
 
-template <class T>
-__device__ __forceinline__ T* wsp(const Params& p, int region) {
-  return (T*)(p.ws + p.off[region]);
+// the workspace as a buffer resource: hand-off data goes through sc1 (device-coherent) accesses
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(const Params& p) {
+  return __builtin_amdgcn_make_buffer_rsrc(p.ws, (short)0, (int)p.ws_bytes, 0x00020000);
 }
+__device__ __forceinline__ u32x4 dld128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kAuxDev);
+}
+__device__ __forceinline__ uint32_t dld32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kAuxDev);
+}
+__device__ __forceinline__ uint32_t dld8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, kAuxDev);
+}
+__device__ __forceinline__ void dst128(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kAuxDev);
+}
+__device__ __forceinline__ void dst64(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, kAuxDev);
+}
+__device__ __forceinline__ void dst32(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, kAuxDev);
+}
+__device__ __forceinline__ void dst16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint16_t v) {
+  __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, kAuxDev);
+}
+__device__ __forceinline__ void dst8(__amdgpu_buffer_rsrc_t r, uint32_t off, uint8_t v) {
+  __builtin_amdgcn_raw_buffer_store_b8(v, r, off, 0, kAuxDev);
+}
+
 __device__ __forceinline__ uint32_t* ctl(const Params& p) { return (uint32_t*)p.ws; }
 
 __device__ __forceinline__ float bf_lo(uint32_t w) { return u2f(w << 16); }
@@ -168,6 +205,7 @@ __device__ __forceinline__ float group_max(float v) {
 }
 
 __device__ __forceinline__ float silu(float z) { return z / (1.0f + __expf(-z)); }
+__device__ __forceinline__ float clampf(float v, float lim) { return fminf(fmaxf(v, -lim), lim); }
 
 // 16 e4m3 weights . 16 e4m3 activations, unscaled
 __device__ __forceinline__ float dot16_fp8(u32x4 w, u32x4 x) {
@@ -224,15 +262,16 @@ __device__ void record_error(const Params& p, int stage) {
   atomicAdd(&e[MKMOE_ERRW_COUNT], 1u);
 }
 
-// this workgroup is done with a stage: its stores before the count (device scope)
+// this workgroup is done with a stage: its sc1 stores acknowledged, then the count
 __device__ __forceinline__ void arrive(const Params& p, int which) {
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    __hip_atomic_fetch_add(ctl(p) + which, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(ctl(p) + which, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// wait until ``target`` workgroups arrived at ``which`` (or the deadline passed)
+// wait until ``target`` workgroups arrived at ``which`` (or the deadline passed); the data
+// behind the count is read with sc1 loads afterwards
 __device__ __forceinline__ void await_all(const Params& p, int which, uint32_t target, int stage) {
   if (threadIdx.x == 0) {
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
@@ -243,7 +282,6 @@ __device__ __forceinline__ void await_all(const Params& p, int which, uint32_t t
         break;
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
 }
@@ -252,7 +290,7 @@ __device__ __forceinline__ void await_all(const Params& p, int which, uint32_t t
 __device__ void leave(const Params& p) {
   __syncthreads();
   if (threadIdx.x == 0) {
-    uint32_t n = __hip_atomic_fetch_add(ctl(p) + kCtlExit, 1u, __ATOMIC_ACQ_REL,
+    uint32_t n = __hip_atomic_fetch_add(ctl(p) + kCtlExit, 1u, __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_AGENT);
     if (n == gridDim.x - 1) {
       for (int i = 0; i < kCtlCounters; ++i)
@@ -260,6 +298,9 @@ __device__ void leave(const Params& p) {
     }
   }
 }
+
+// wave units spread over workgroups first: this wave is slot b + nwg * wave
+__device__ __forceinline__ int wave_slot(int b, int nwg) { return b + nwg * (int)(threadIdx.x >> 6); }
 
 // ---------------------------------------------------------------- stage N: RMSNorm
 template <class C>
@@ -283,7 +324,8 @@ __device__ void norm_row(const Params& p, int r, int lane) {
   float ss = wave_sum(acc);
   float mean = ss / (float)C::H;
   float rstd = 1.0f / sqrtf(mean + p.eps);
-  uint16_t* y = wsp<uint16_t>(p, 0) + (size_t)r * C::H;
+  const auto rs = ws_rsrc(p);
+  const uint32_t base = p.off[0] + (uint32_t)r * C::H * 2;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const uint32_t w4[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
@@ -297,19 +339,21 @@ __device__ void norm_row(const Params& p, int r, int lane) {
       b = b * bf_hi(n4[q]);
       o[q] = (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
     }
-    *(u32x4*)(y + c * 512 + lane * 8) = u32x4{o[0], o[1], o[2], o[3]};
+    dst128(rs, base + (c * 512 + lane * 8) * 2, u32x4{o[0], o[1], o[2], o[3]});
   }
 }
 
 template <class C>
 __device__ void stage_norm(const Params& p, int b, int nwg) {
-  const int lane = threadIdx.x & 63, gw = b * kWaves + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, gw = wave_slot(b, nwg);
   for (int r = gw; r < p.rows; r += nwg * kWaves) norm_row<C>(p, r, lane);
 }
 
+// 8 bf16 of row r from element col: the normed rows (sc1) or the input
 template <class C>
-__device__ __forceinline__ const uint16_t* x_in(const Params& p) {
-  return C::NORM ? wsp<const uint16_t>(p, 0) : p.x;
+__device__ __forceinline__ u32x4 x_load(const Params& p, __amdgpu_buffer_rsrc_t rs, int r, int col) {
+  if constexpr (C::NORM) return dld128(rs, p.off[0] + ((uint32_t)r * C::H + col) * 2);
+  return ld16(p.x + (size_t)r * C::H + col);
 }
 
 // ---------------------------------------------------------------- stage A
@@ -318,17 +362,16 @@ template <class C>
 __device__ void router_unit(const Params& p, int e, int part, int lane) {
 #pragma clang fp contract(off)
   constexpr int CPP = C::CH512 / C::P;
-  const uint16_t* x = x_in<C>(p);
+  const auto rs = ws_rsrc(p);
   u32x4 wv[CPP];
 #pragma unroll
   for (int i = 0; i < CPP; ++i)
     wv[i] = ld16_nt(p.gate_w + (size_t)e * C::H + (part * CPP + i) * 512 + lane * 8);
-  float* out = wsp<float>(p, 5);
   for (int r = 0; r < p.rows; ++r) {
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < CPP; ++i) {
-      u32x4 xv = ld16(x + (size_t)r * C::H + (part * CPP + i) * 512 + lane * 8);
+      u32x4 xv = x_load<C>(p, rs, r, (part * CPP + i) * 512 + lane * 8);
       const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
       const uint32_t ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
 #pragma unroll
@@ -338,7 +381,7 @@ __device__ void router_unit(const Params& p, int e, int part, int lane) {
       }
     }
     float s = wave_sum(acc);
-    if (lane == 0) out[((size_t)r * C::E + e) * C::P + part] = s;
+    if (lane == 0) dst32(rs, p.off[5] + (((uint32_t)r * C::E + e) * C::P + part) * 4, f2u(s));
   }
 }
 
@@ -347,8 +390,8 @@ __device__ void router_unit(const Params& p, int e, int part, int lane) {
 template <class C>
 __device__ void quant_unit(const Params& p, int r, int c, int lane) {
 #pragma clang fp contract(off)
-  const uint16_t* x = x_in<C>(p) + (size_t)r * C::H + c * 512 + lane * 8;
-  u32x4 xv = ld16(x);
+  const auto rs = ws_rsrc(p);
+  u32x4 xv = x_load<C>(p, rs, r, c * 512 + lane * 8);
   const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
   float v[8];
   float am = 0.0f;
@@ -359,7 +402,7 @@ __device__ void quant_unit(const Params& p, int r, int c, int lane) {
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) am = fabsf(v[j]) > am ? fabsf(v[j]) : am;
-  const size_t col = (size_t)r * C::H + c * 512 + lane * 8;
+  const uint32_t col = (uint32_t)r * C::H + c * 512 + lane * 8;
   // group-128 fp8: 16 lanes a group
   {
     float g = group_max<16>(am);
@@ -369,9 +412,10 @@ __device__ void quant_unit(const Params& p, int r, int c, int lane) {
     for (int j = 0; j < 4; ++j) lo |= e4m3_encode(v[j] / s) << (8 * j);
 #pragma unroll
     for (int j = 0; j < 4; ++j) hi |= e4m3_encode(v[4 + j] / s) << (8 * j);
-    const int rq = C::FMT == kFp4 ? 3 : 1, rs = C::FMT == kFp4 ? 4 : 2;
-    *(u32x2*)(wsp<uint8_t>(p, rq) + col) = u32x2{lo, hi};
-    if ((lane & 15) == 0) wsp<float>(p, rs)[(size_t)r * (C::H / 128) + c * 4 + lane / 16] = s;
+    const int rq = C::FMT == kFp4 ? 3 : 1, rsc = C::FMT == kFp4 ? 4 : 2;
+    dst64(rs, p.off[rq] + col, u32x2{lo, hi});
+    if ((lane & 15) == 0)
+      dst32(rs, p.off[rsc] + ((uint32_t)r * (C::H / 128) + c * 4 + lane / 16) * 4, f2u(s));
   }
   if constexpr (C::FMT == kFp4) {
     float g = group_max<4>(am);
@@ -382,14 +426,15 @@ __device__ void quant_unit(const Params& p, int r, int c, int lane) {
     for (int j = 0; j < 4; ++j) lo |= e4m3_encode(v[j] * inv) << (8 * j);
 #pragma unroll
     for (int j = 0; j < 4; ++j) hi |= e4m3_encode(v[4 + j] * inv) << (8 * j);
-    *(u32x2*)(wsp<uint8_t>(p, 1) + col) = u32x2{lo, hi};
-    if ((lane & 3) == 0) wsp<uint8_t>(p, 2)[(size_t)r * (C::H / 32) + c * 16 + lane / 4] = (uint8_t)code;
+    dst64(rs, p.off[1] + col, u32x2{lo, hi});
+    if ((lane & 3) == 0)
+      dst8(rs, p.off[2] + (uint32_t)r * (C::H / 32) + c * 16 + lane / 4, (uint8_t)code);
   }
 }
 
 template <class C>
 __device__ void stage_a(const Params& p, int b, int nwg) {
-  const int lane = threadIdx.x & 63, gw = b * kWaves + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, gw = wave_slot(b, nwg);
   const int n_router = C::E * C::P, n_quant = p.rows * C::CH512;
   for (int u = gw; u < n_router + n_quant; u += nwg * kWaves) {
     if (u < n_router)
@@ -404,7 +449,8 @@ template <class C>
 __device__ void route_row(const Params& p, int r, int lane) {
 #pragma clang fp contract(off)
   constexpr int EPL = (C::E + 63) / 64;
-  const float* part = wsp<const float>(p, 5) + (size_t)r * C::E * C::P;
+  const auto rs = ws_rsrc(p);
+  const uint32_t part0 = p.off[5] + (uint32_t)r * C::E * C::P * 4;
   float sc[EPL], ch[EPL];
   bool alive[EPL];
 #pragma unroll
@@ -413,7 +459,7 @@ __device__ void route_row(const Params& p, int r, int lane) {
     if (e < C::E) {
       float logit = 0.0f;
 #pragma unroll
-      for (int q = 0; q < C::P; ++q) logit = logit + part[e * C::P + q];
+      for (int q = 0; q < C::P; ++q) logit = logit + u2f(dld32(rs, part0 + (e * C::P + q) * 4));
       // a NaN score weighs 0 and its choice never wins (as the reference's route)
       const float sg = sigmoid_exact(logit);
       sc[i] = sg != sg ? 0.0f : sg;
@@ -522,32 +568,31 @@ __device__ void route_row(const Params& p, int r, int lane) {
   if (p.renorm) f = p.scale / (total > 1e-20f ? total : 1e-20f);
   if (lane < C::K) {
     const float w = my_w * f;
-    wsp<int32_t>(p, 6)[r * C::K + lane] = my_id;
-    wsp<float>(p, 7)[r * C::K + lane] = w;
+    dst32(rs, p.off[6] + (r * C::K + lane) * 4, (uint32_t)my_id);
+    dst32(rs, p.off[7] + (r * C::K + lane) * 4, f2u(w));
     if (p.ids_out) p.ids_out[r * C::K + lane] = my_id;
     if (p.w_out) p.w_out[r * C::K + lane] = w;
   }
 }
 
-// ---------------------------------------------------------------- GEMV of weight rows
-// A unit of NR weight rows of length KD elements is streamed by one wave; the
-// wave's lanes split into G sub-groups of LPR = 64 / G lanes, sub-group g
-// taking rows g, g + G, ...; each lane loads CPL 16-byte chunks of a row.
-// ``acts(t)`` -> activation pointers of token t. Results per (row, token) are
-// summed over the sub-group's lanes.
+// ---------------------------------------------------------------- VALU GEMV of weight rows
+// Every expert GEMV runs in one fixed order (the oracle restates it): a row of KD
+// elements is cut into 16-element (FP8) / 32-element (FP4) chunks; a chunk's unscaled
+// sum runs in element order (the products are exact in fp32); it is scaled (FP8:
+// d * fp32(s_w * s_x); FP4: d * 2^(e_w + e_x - 254)); chunk c goes to lane c % LPR,
+// each lane sums its chunks in order, and the LPR lanes add as a halving tree.
+// A unit of NR rows is streamed by one wave whose lanes split into G = 64 / LPR
+// sub-groups, sub-group g taking rows g, g + G, ...
 template <int FMT, int KD>
 struct RowShape {
-  static constexpr int CPR = FMT == kFp4 ? KD / 32 : KD / 16;  // 16-byte chunks a row
-  // sub-groups: the fewest that split a row evenly over a sub-group's lanes
+  static constexpr int CPR = FMT == kFp4 ? KD / 32 : KD / 16;  // chunks a row
+  // lanes a row: 64, or the largest power of two below it that divides the chunks
   static constexpr int G = CPR % 64 == 0 ? 1 : CPR % 32 == 0 ? 2 : CPR % 16 == 0 ? 4 : 8;
   static constexpr int LPR = 64 / G;
-  static constexpr int CPL = CPR / LPR;                          // chunks a lane a row
-  static constexpr int RB = FMT == kFp4 ? KD / 2 : KD;           // bytes a row
+  static constexpr int CPL = CPR / LPR;  // chunks a lane a row
   static_assert(CPR % LPR == 0, "row chunks");
 };
 
-// fp8 rows with fp32 128 x 128 scales: ``srow[q]`` points at row q's scales
-// (one per 128 K), activations e4m3 with a fp32 scale per 128
 // rows[q * G + g] for this lane's sub-group g, without indexing a register array
 template <int G, class T>
 __device__ __forceinline__ T sub_pick(const T* arr, int q, int g) {
@@ -558,147 +603,172 @@ __device__ __forceinline__ T sub_pick(const T* arr, int q, int g) {
   return v;
 }
 
-template <int KD, int NR>
-struct Fp8Rows {
-  using S = RowShape<kFp8, KD>;
-  static constexpr int RPG = NR / S::G;  // rows a sub-group
-  u32x4 w[RPG][S::CPL];
-  float s[RPG][S::CPL];
+// activations of one row: e4m3 codes and their scales (fp32 per 128, or E8M0 per 32)
+struct DevAct {  // in the workspace (sc1 loads)
+  __amdgpu_buffer_rsrc_t rs;
+  uint32_t q;  // byte offset of the row's codes
+  uint32_t s;  // byte offset of the row's scales
+  __device__ __forceinline__ u32x4 q16(int off) const { return dld128(rs, q + off); }
+  __device__ __forceinline__ float sf(int i) const { return u2f(dld32(rs, s + i * 4)); }
+  __device__ __forceinline__ int se(int i) const { return (int)dld8(rs, s + i); }
+};
+struct LdsAct {  // in LDS
+  const uint8_t* q;
+  const void* s;
+  __device__ __forceinline__ u32x4 q16(int off) const { return *(const u32x4*)(q + off); }
+  __device__ __forceinline__ float sf(int i) const { return ((const float*)s)[i]; }
+  __device__ __forceinline__ int se(int i) const { return ((const uint8_t*)s)[i]; }
+};
 
-  __device__ __forceinline__ void load(const uint8_t* const* rows, const float* const* srow,
-                                       int lane) {
+// NR weight rows (FP8 with fp32 128 x 128 scales, or MXFP4 with E8M0 per 32) in registers:
+// ``rows[r]`` is row r's first byte, ``srow[r]`` its scales (FP8: the row block's fp32
+// scales, one per 128 K; FP4: the row's E8M0 bytes)
+template <int FMT, int KD, int NR>
+struct WRows {
+  using S = RowShape<FMT, KD>;
+  static constexpr int RPG = NR / S::G;  // rows a sub-group
+  static_assert(RPG * S::G == NR, "rows split over sub-groups");
+  u32x4 w[RPG][S::CPL];
+  float sf[RPG][S::CPL];
+  int se[RPG][S::CPL];
+
+  __device__ __forceinline__ void load(const uint8_t* const* rows, const void* const* srow, int lane) {
     const int g = lane / S::LPR, l = lane % S::LPR;
 #pragma unroll
     for (int q = 0; q < RPG; ++q) {
+      const uint8_t* r = sub_pick<S::G>(rows, q, g);
 #pragma unroll
-      for (int i = 0; i < S::CPL; ++i) {
-        const int c = l + S::LPR * i;
-        w[q][i] = ld16_nt(sub_pick<S::G>(rows, q, g) + c * 16);
-      }
+      for (int i = 0; i < S::CPL; ++i) w[q][i] = ld16_nt(r + (l + S::LPR * i) * 16);
     }
 #pragma unroll
     for (int q = 0; q < RPG; ++q) {
-      const float* sr = sub_pick<S::G>(srow, q, g);
+      const void* sr = sub_pick<S::G>(srow, q, g);
 #pragma unroll
-      for (int i = 0; i < S::CPL; ++i) s[q][i] = sr[(l + S::LPR * i) / 8];
+      for (int i = 0; i < S::CPL; ++i) {
+        const int c = l + S::LPR * i;
+        if constexpr (FMT == kFp8) sf[q][i] = ((const float*)sr)[c / 8];
+        else se[q][i] = ((const uint8_t*)sr)[c];
+      }
     }
   }
-  // row partial sums (this lane) against one token's activations
-  __device__ __forceinline__ void dot(const uint8_t* xq, const float* xs, int lane,
-                                      float (&acc)[RPG]) const {
+
+  // this lane's sums of its rows against one activation row
+  template <class Act>
+  __device__ __forceinline__ void dot(const Act& x, int lane, float (&acc)[RPG]) const {
+#pragma clang fp contract(off)
     const int l = lane % S::LPR;
 #pragma unroll
     for (int q = 0; q < RPG; ++q) acc[q] = 0.0f;
 #pragma unroll
     for (int i = 0; i < S::CPL; ++i) {
       const int c = l + S::LPR * i;
-      const u32x4 xv = ld16(xq + c * 16);
-      const float sx = xs[c / 8];
+      if constexpr (FMT == kFp8) {
+        const u32x4 xv = x.q16(c * 16);
+        const float sx = x.sf(c / 8);
 #pragma unroll
-      for (int q = 0; q < RPG; ++q) {
-        // opaque to the optimiser: the weight conversions stay inside the token loop
-        // (hoisted, the unit's weights as fp32 would not fit the register file)
-        u32x4 wq = w[q][i];
-        asm volatile("" : "+v"(wq));
-        acc[q] = fmaf(dot16_fp8(wq, xv), s[q][i] * sx, acc[q]);
+        for (int q = 0; q < RPG; ++q) {
+          // opaque to the optimiser: the weight conversions stay inside the token loop
+          // (hoisted, the unit's weights as fp32 would not fit the register file)
+          u32x4 wq = w[q][i];
+          asm volatile("" : "+v"(wq));
+          const float f = sf[q][i] * sx;
+          acc[q] = acc[q] + dot16_fp8(wq, xv) * f;
+        }
+      } else {
+        const u32x4 xa = x.q16(c * 32), xb = x.q16(c * 32 + 16);
+        const int ex = x.se(c);
+#pragma unroll
+        for (int q = 0; q < RPG; ++q) {
+          u32x4 wq = w[q][i];
+          asm volatile("" : "+v"(wq));
+          acc[q] = acc[q] + ldexpf(dot32_fp4(wq, xa, xb), se[q][i] + ex - 254);
+        }
       }
     }
   }
 };
 
-// MXFP4 rows (E8M0 per 32 K): ``srow[q]`` points at row q's scale bytes;
-// activations MXFP8 (E8M0 per 32)
-template <int KD, int NR>
-struct Fp4Rows {
-  using S = RowShape<kFp4, KD>;
-  static constexpr int RPG = NR / S::G;
-  u32x4 w[RPG][S::CPL];
-  int s[RPG][S::CPL];
+// silu(z) = z * sigmoid(z) with the exact fp64 sigmoid; the SwiGLU of a gate_up pair: the
+// routed rule (check_ffn.py:220) or the shared rule, which rounds gate and up to bf16
+// first (check_ffn.py:227-230)
+__device__ __forceinline__ float silu_exact(float z) {
+#pragma clang fp contract(off)
+  return z * sigmoid_exact(z);
+}
+__device__ __forceinline__ float swiglu_routed(float g, float u, float lim) {
+#pragma clang fp contract(off)
+  return bf_round(silu_exact(fminf(g, lim)) * clampf(u, lim));
+}
+__device__ __forceinline__ float swiglu_shared(float g, float u, float lim) {
+#pragma clang fp contract(off)
+  return bf_round(silu_exact(bf_round(fminf(g, lim))) * bf_round(clampf(u, lim)));
+}
 
-  __device__ __forceinline__ void load(const uint8_t* const* rows, const uint8_t* const* srow,
-                                       int lane) {
-    const int g = lane / S::LPR, l = lane % S::LPR;
+constexpr int kTokGroup = 8;  // picks a gate_up unit takes at most
+
+// gate_up of one intermediate column j (rows j and W + j of a [2W][H] weight) for up to
+// kTokGroup activation rows; emit(i, mid) stores pick i's SwiGLU output
+template <int FMT, int H>
+struct GateUp {
+  using R = WRows<FMT, H, 2>;
+  R wr;
+  __device__ __forceinline__ void load(const uint8_t* w, const void* s, int W, int j, int lane) {
+    const uint8_t* rows[2];
+    const void* srow[2];
+    const int rid[2] = {j, W + j};
 #pragma unroll
-    for (int q = 0; q < RPG; ++q) {
-#pragma unroll
-      for (int i = 0; i < S::CPL; ++i)
-        w[q][i] = ld16_nt(sub_pick<S::G>(rows, q, g) + (l + S::LPR * i) * 16);
-    }
-#pragma unroll
-    for (int q = 0; q < RPG; ++q) {
-      const uint8_t* sr = sub_pick<S::G>(srow, q, g);
-#pragma unroll
-      for (int i = 0; i < S::CPL; ++i) s[q][i] = sr[l + S::LPR * i];
-    }
-  }
-  __device__ __forceinline__ void dot(const uint8_t* xq, const uint8_t* xs, int lane,
-                                      float (&acc)[RPG]) const {
-    const int l = lane % S::LPR;
-#pragma unroll
-    for (int q = 0; q < RPG; ++q) acc[q] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < S::CPL; ++i) {
-      const int c = l + S::LPR * i;
-      const u32x4 xa = ld16(xq + c * 32), xb = ld16(xq + c * 32 + 16);
-      const int sx = xs[c];
-#pragma unroll
-      for (int q = 0; q < RPG; ++q) {
-        u32x4 wq = w[q][i];
-        asm volatile("" : "+v"(wq));
-        acc[q] = acc[q] + ldexpf(dot32_fp4(wq, xa, xb), s[q][i] + sx - 254);
+    for (int q = 0; q < 2; ++q) {
+      if constexpr (FMT == kFp8) {
+        rows[q] = w + (size_t)rid[q] * H;
+        srow[q] = (const float*)s + (size_t)(rid[q] / 128) * (H / 128);
+      } else {
+        rows[q] = w + (size_t)rid[q] * (H / 2);
+        srow[q] = (const uint8_t*)s + (size_t)rid[q] * (H / 32);
       }
+    }
+    wr.load(rows, srow, lane);
+  }
+  // (gate, up) sums of one activation row, valid in every lane
+  template <class Act>
+  __device__ __forceinline__ void run(const Act& x, int lane, float& g, float& u) const {
+    float acc[R::RPG];
+    wr.dot(x, lane, acc);
+#pragma unroll
+    for (int q = 0; q < R::RPG; ++q) acc[q] = group_sum<R::S::LPR>(acc[q]);
+    if constexpr (R::S::G == 1) {
+      g = acc[0];
+      u = acc[1];
+    } else {
+      static_assert(R::S::G == 2, "gate and up on two sub-groups");
+      g = __shfl(acc[0], 0);
+      u = __shfl(acc[0], 32);
     }
   }
 };
 
 // ---------------------------------------------------------------- stage B: shared gate_up
-// unit u: intermediate columns 2u, 2u + 1 of the shared expert for every row
+// unit u: shared column j = u % S for rows of token group u / S
 template <class C>
 __device__ void shared_gu_unit(const Params& p, int u, int lane) {
-  using R = Fp8Rows<C::H, 4>;
-  const int j0 = 2 * u;
-  // rows in sub-group order: (gate j0, gate j0+1, up j0, up j0+1) so that a
-  // sub-group holds a (gate, up) pair when G = 2 and all four when G = 1
-  const int rid[4] = {j0, j0 + 1, C::S + j0, C::S + j0 + 1};
-  const uint8_t* rows[4];
-  const float* srow[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    rows[q] = p.sgu + (size_t)rid[q] * C::H;
-    srow[q] = p.sgu_s + (size_t)(rid[q] / 128) * (C::H / 128);
-  }
-  R wr;
-  wr.load(rows, srow, lane);
-  const uint8_t* xq = wsp<uint8_t>(p, C::FMT == kFp4 ? 3 : 1);
-  const float* xs = wsp<float>(p, C::FMT == kFp4 ? 4 : 2);
-  uint16_t* smid = wsp<uint16_t>(p, 8);
-  const float lim = p.limit;
-  for (int t = 0; t < p.rows; ++t) {
-    float acc[R::RPG];
-    wr.dot(xq + (size_t)t * C::H, xs + (size_t)t * (C::H / 128), lane, acc);
-#pragma unroll
-    for (int q = 0; q < R::RPG; ++q) acc[q] = group_sum<R::S::LPR>(acc[q]);
-    // G = 1: acc = (g0, g1, u0, u1); G = 2: sub-group g holds (g_g, u_g)
-    if constexpr (R::S::G == 1) {
-      if (lane == 0) {
-        float m0 = bf_round(silu(bf_round(fminf(acc[0], lim))) * bf_round(fminf(fmaxf(acc[2], -lim), lim)));
-        float m1 = bf_round(silu(bf_round(fminf(acc[1], lim))) * bf_round(fminf(fmaxf(acc[3], -lim), lim)));
-        *(uint32_t*)(smid + (size_t)t * C::S + j0) = (uint32_t)f2bf(m0) | ((uint32_t)f2bf(m1) << 16);
-      }
-    } else {
-      if ((lane % R::S::LPR) == 0) {
-        const int g = lane / R::S::LPR;
-        float m = bf_round(silu(bf_round(fminf(acc[0], lim))) * bf_round(fminf(fmaxf(acc[1], -lim), lim)));
-        smid[(size_t)t * C::S + j0 + g] = f2bf(m);
-      }
-    }
+  const int j = u % C::S, tg = u / C::S;
+  GateUp<kFp8, C::H> gu;
+  gu.load(p.sgu, p.sgu_s, C::S, j, lane);
+  const auto rs = ws_rsrc(p);
+  const int rq = C::FMT == kFp4 ? 3 : 1, rsc = C::FMT == kFp4 ? 4 : 2;
+  const int t1 = min(p.rows, (tg + 1) * kTokGroup);
+  for (int t = tg * kTokGroup; t < t1; ++t) {
+    float g, up;
+    gu.run(DevAct{rs, p.off[rq] + (uint32_t)t * C::H, p.off[rsc] + (uint32_t)t * (C::H / 128) * 4},
+           lane, g, up);
+    if (lane == 0) dst16(rs, p.off[8] + ((uint32_t)t * C::S + j) * 2, f2bf(swiglu_shared(g, up, p.limit)));
   }
 }
 
 template <class C>
 __device__ void stage_b(const Params& p, int b, int nwg) {
-  const int lane = threadIdx.x & 63, gw = b * kWaves + (threadIdx.x >> 6);
-  const int n_route = p.rows, n_sh = C::S / 2;
+  const int lane = threadIdx.x & 63, gw = wave_slot(b, nwg);
+  const int n_route = p.rows;
+  const int n_sh = C::S * ((p.rows + kTokGroup - 1) / kTokGroup);
   for (int u = gw; u < n_route + n_sh; u += nwg * kWaves) {
     if (u < n_route)
       route_row<C>(p, u, lane);
@@ -714,69 +784,79 @@ struct Union {
   int slot_of[C::E];
   int slot_e[C::E];
   int slot_start[C::E + 1];
+  int tg_start[C::E + 1];       // a slot's first token group (groups of kTokGroup picks)
+  int tg_slot[kRowsMax * C::K];  // a token group's slot
   int picks[kRowsMax * C::K];
   float wts[kRowsMax * C::K];
   int n;
+  int ntg;
 };
 
-// experts picked by any row (ascending id) and their picks (pick = row * K + k)
+// experts picked by any row (ascending id), their picks (pick = row * K + k) and token groups
 template <class C>
 __device__ void build_union(const Params& p, Union<C>& un) {
   const int tid = threadIdx.x;
   const int npk = p.rows * C::K;
-  const int32_t* rid = wsp<const int32_t>(p, 6);
-  const float* rw = wsp<const float>(p, 7);
+  const auto rs = ws_rsrc(p);
   __syncthreads();
   for (int e = tid; e < C::E; e += kThreads) un.cnt[e] = 0;
   __syncthreads();
   for (int t = tid; t < npk; t += kThreads) {
-    const int e = min(max((int)rid[t], 0), C::E - 1);
+    const int e = min(max((int)dld32(rs, p.off[6] + t * 4), 0), C::E - 1);
     atomicAdd(&un.cnt[e], 1);
-    un.wts[t] = rw[t];
+    un.wts[t] = u2f(dld32(rs, p.off[7] + t * 4));
   }
   __syncthreads();
   if (tid < 64) {
     constexpr int EPL = (C::E + 63) / 64;
     const int e0 = tid * EPL;
-    int ns = 0, np = 0;
+    int ns = 0, np = 0, ng = 0;
     for (int i = 0; i < EPL; ++i) {
       const int e = e0 + i;
       if (e < C::E && un.cnt[e] > 0) {
         ns += 1;
         np += un.cnt[e];
+        ng += (un.cnt[e] + kTokGroup - 1) / kTokGroup;
       }
     }
     // exclusive prefix over lanes
-    int is = ns, ip = np;
+    int is = ns, ip = np, ig = ng;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
-      int os = __shfl_up(is, d), op = __shfl_up(ip, d);
+      int os = __shfl_up(is, d), op = __shfl_up(ip, d), og = __shfl_up(ig, d);
       if (tid >= d) {
         is += os;
         ip += op;
+        ig += og;
       }
     }
-    int s = is - ns, pk = ip - np;
+    int s = is - ns, pk = ip - np, gq = ig - ng;
     for (int i = 0; i < EPL; ++i) {
       const int e = e0 + i;
       if (e < C::E && un.cnt[e] > 0) {
+        const int c = un.cnt[e];
+        const int groups = (c + kTokGroup - 1) / kTokGroup;
         un.slot_of[e] = s;
         un.slot_e[s] = e;
         un.slot_start[s] = pk;
-        const int c = un.cnt[e];
+        un.tg_start[s] = gq;
+        for (int q = 0; q < groups; ++q) un.tg_slot[gq + q] = s;
         un.cnt[e] = pk;  // fill cursor
         s += 1;
         pk += c;
+        gq += groups;
       }
     }
     if (tid == 63) {
       un.n = is;
       un.slot_start[is] = ip;
+      un.tg_start[is] = ig;
+      un.ntg = ig;
     }
   }
   __syncthreads();
   for (int t = tid; t < npk; t += kThreads) {
-    const int e = min(max((int)rid[t], 0), C::E - 1);
+    const int e = min(max((int)dld32(rs, p.off[6] + t * 4), 0), C::E - 1);
     const int pos = atomicAdd(&un.cnt[e], 1);
     un.picks[pos] = t;
   }
@@ -784,88 +864,53 @@ __device__ void build_union(const Params& p, Union<C>& un) {
 }
 
 // ---------------------------------------------------------------- stage C: routed gate_up
-template <class C>
-__device__ void routed_gu_unit(const Params& p, const Union<C>& un, int slot, int jp, int lane) {
-  const int e = un.slot_e[slot];
-  const int j0 = 2 * jp;
-  const int rid[4] = {j0, j0 + 1, C::I + j0, C::I + j0 + 1};
-  const int first = un.slot_start[slot], last = un.slot_start[slot + 1];
-  uint16_t* mid = wsp<uint16_t>(p, 9);
-  const float lim = p.limit;
-  if constexpr (C::FMT == kFp8) {
-    using R = Fp8Rows<C::H, 4>;
-    const uint8_t* rows[4];
-    const float* srow[4];
-    const float* s13 = (const float*)p.w13_s + (size_t)e * (2 * C::I / 128) * (C::H / 128);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      rows[q] = p.w13 + ((size_t)e * 2 * C::I + rid[q]) * C::H;
-      srow[q] = s13 + (size_t)(rid[q] / 128) * (C::H / 128);
-    }
-    R wr;
-    wr.load(rows, srow, lane);
-    const uint8_t* xq = wsp<uint8_t>(p, 1);
-    const float* xs = wsp<float>(p, 2);
-    for (int j = first; j < last; ++j) {
-      const int pk = un.picks[j], t = pk / C::K;
-      float acc[R::RPG];
-      wr.dot(xq + (size_t)t * C::H, xs + (size_t)t * (C::H / 128), lane, acc);
-#pragma unroll
-      for (int q = 0; q < R::RPG; ++q) acc[q] = group_sum<R::S::LPR>(acc[q]);
-      if constexpr (R::S::G == 1) {
-        if (lane == 0) {
-          float m0 = bf_round(silu(fminf(acc[0], lim)) * fminf(fmaxf(acc[2], -lim), lim));
-          float m1 = bf_round(silu(fminf(acc[1], lim)) * fminf(fmaxf(acc[3], -lim), lim));
-          *(uint32_t*)(mid + (size_t)pk * C::I + j0) = (uint32_t)f2bf(m0) | ((uint32_t)f2bf(m1) << 16);
-        }
-      } else if ((lane % R::S::LPR) == 0) {
-        const int g = lane / R::S::LPR;
-        float m = bf_round(silu(fminf(acc[0], lim)) * fminf(fmaxf(acc[1], -lim), lim));
-        mid[(size_t)pk * C::I + j0 + g] = f2bf(m);
-      }
-    }
-  } else {
-    using R = Fp4Rows<C::H, 4>;
-    const uint8_t* rows[4];
-    const uint8_t* srow[4];
-    const uint8_t* s13 = (const uint8_t*)p.w13_s;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const size_t row = (size_t)e * 2 * C::I + rid[q];
-      rows[q] = p.w13 + row * (C::H / 2);
-      srow[q] = s13 + row * (C::H / 32);
-    }
-    R wr;
-    wr.load(rows, srow, lane);
-    const uint8_t* xq = wsp<uint8_t>(p, 1);
-    const uint8_t* xs = wsp<uint8_t>(p, 2);
-    for (int j = first; j < last; ++j) {
-      const int pk = un.picks[j], t = pk / C::K;
-      float acc[R::RPG];
-      wr.dot(xq + (size_t)t * C::H, xs + (size_t)t * (C::H / 32), lane, acc);
-#pragma unroll
-      for (int q = 0; q < R::RPG; ++q) acc[q] = group_sum<R::S::LPR>(acc[q]);
-      if constexpr (R::S::G == 1) {
-        if (lane == 0) {
-          float m0 = bf_round(silu(fminf(acc[0], lim)) * fminf(fmaxf(acc[2], -lim), lim));
-          float m1 = bf_round(silu(fminf(acc[1], lim)) * fminf(fmaxf(acc[3], -lim), lim));
-          *(uint32_t*)(mid + (size_t)pk * C::I + j0) = (uint32_t)f2bf(m0) | ((uint32_t)f2bf(m1) << 16);
-        }
-      } else if ((lane % R::S::LPR) == 0) {
-        const int g = lane / R::S::LPR;
-        float m = bf_round(silu(fminf(acc[0], lim)) * fminf(fmaxf(acc[1], -lim), lim));
-        mid[(size_t)pk * C::I + j0 + g] = f2bf(m);
-      }
-    }
-  }
-}
-
+// unit u: column j = u % I of the token group u / I (a slot's picks, kTokGroup at a time);
+// a wave's next unit's weights load while it computes the current one
 template <class C>
 __device__ void stage_c(const Params& p, const Union<C>& un, int b, int nwg) {
-  const int lane = threadIdx.x & 63, gw = b * kWaves + (threadIdx.x >> 6);
-  const int per = C::I / 2;
-  const int n = un.n * per;
-  for (int u = gw; u < n; u += nwg * kWaves) routed_gu_unit<C>(p, un, u / per, u % per, lane);
+  const int lane = threadIdx.x & 63, gw = wave_slot(b, nwg);
+  const int stride = nwg * kWaves;
+  const int n = un.ntg * C::I;
+  const auto rs = ws_rsrc(p);
+  using GU = GateUp<C::FMT, C::H>;
+  auto load = [&](GU& gu, int u) {
+    const int tgg = u / C::I, j = u % C::I;
+    const int e = un.slot_e[un.tg_slot[tgg]];
+    if constexpr (C::FMT == kFp8)
+      gu.load(p.w13 + (size_t)e * 2 * C::I * C::H,
+              (const float*)p.w13_s + (size_t)e * (2 * C::I / 128) * (C::H / 128), C::I, j, lane);
+    else
+      gu.load(p.w13 + (size_t)e * 2 * C::I * (C::H / 2),
+              (const uint8_t*)p.w13_s + (size_t)e * 2 * C::I * (C::H / 32), C::I, j, lane);
+  };
+  auto compute = [&](const GU& gu, int u) {
+    const int tgg = u / C::I, j = u % C::I;
+    const int slot = un.tg_slot[tgg];
+    const int j0 = un.slot_start[slot] + (tgg - un.tg_start[slot]) * kTokGroup;
+    const int j1 = min(j0 + kTokGroup, un.slot_start[slot + 1]);
+    for (int jj = j0; jj < j1; ++jj) {
+      const int pk = un.picks[jj], t = pk / C::K;
+      float g, up;
+      if constexpr (C::FMT == kFp8)
+        gu.run(DevAct{rs, p.off[1] + (uint32_t)t * C::H, p.off[2] + (uint32_t)t * (C::H / 128) * 4}, lane, g, up);
+      else
+        gu.run(DevAct{rs, p.off[1] + (uint32_t)t * C::H, p.off[2] + (uint32_t)t * (C::H / 32)}, lane, g, up);
+      if (lane == 0) dst16(rs, p.off[9] + ((uint32_t)pk * C::I + j) * 2, f2bf(swiglu_routed(g, up, p.limit)));
+    }
+  };
+  int u = gw;
+  if (u >= n) return;
+  GU cur;
+  load(cur, u);
+  while (true) {
+    const int un_next = u + stride;
+    GU nxt;
+    if (un_next < n) load(nxt, un_next);
+    compute(cur, u);
+    if (un_next >= n) break;
+    cur = nxt;
+    u = un_next;
+  }
 }
 
 // ---------------------------------------------------------------- stage D: down + combine
@@ -875,23 +920,24 @@ struct DownSmem {
   float ysh[kRowsMax * kTileMax];
   union {
     struct {
-      uint8_t q[kRowsMax * C::S];
+      uint8_t q[kRowsMax * C::SQS];
       float s[kRowsMax * (C::S / 128)];
     } sh;
     struct {
-      uint8_t q[C::PB * C::I];
-      uint8_t s[C::PB * C::SCB];
+      uint8_t q[C::PB * C::MQS];
+      uint8_t s[C::PB * C::MSC * 4];
     } mid;
   } u;
 };
 
-// quantize bf16 rows [n][W] (global) into LDS codes [n][W] and scales: group-128 fp8 (fp32
-// scales) or MXFP8 (E8M0 bytes); row i of the source is ``src_row(i)``
-template <int FMT, int W, class RowFn>
-__device__ void quant_rows_lds(RowFn src_row, int n, uint8_t* q, void* s) {
+// quantize bf16 rows [n][W] (workspace, sc1) into LDS codes [n][QS] and scales: group-128 fp8
+// (fp32 scales) or MXFP8 (E8M0 bytes); row i of the source starts at byte ``src_row(i)``
+template <int FMT, int W, int QS, class RowFn>
+__device__ void quant_rows_lds(const Params& p, RowFn src_row, int n, uint8_t* q, void* s) {
 #pragma clang fp contract(off)
   constexpr int PER = W / 8;  // 8-value chunks a row
   const int tid = threadIdx.x;
+  const auto rs = ws_rsrc(p);
   // a wave's lanes cover consecutive chunks so that a group's lanes are adjacent
   const int total = n * PER;
   for (int base = 0; base < total; base += kThreads) {
@@ -901,7 +947,7 @@ __device__ void quant_rows_lds(RowFn src_row, int n, uint8_t* q, void* s) {
     float v[8];
     float am = 0.0f;
     if (ok) {
-      u32x4 xv = ld16(src_row(i) + c * 8);
+      u32x4 xv = dld128(rs, src_row(i) + c * 16);
       const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -923,7 +969,7 @@ __device__ void quant_rows_lds(RowFn src_row, int n, uint8_t* q, void* s) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) hi |= e4m3_encode(v[4 + k] / sc) << (8 * k);
       if (ok) {
-        *(u32x2*)(q + (size_t)i * W + c * 8) = u32x2{lo, hi};
+        *(u32x2*)(q + (size_t)i * QS + c * 8) = u32x2{lo, hi};
         if ((c & 15) == 0) ((float*)s)[i * (W / 128) + c / 16] = sc;
       }
     } else {
@@ -936,122 +982,128 @@ __device__ void quant_rows_lds(RowFn src_row, int n, uint8_t* q, void* s) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) hi |= e4m3_encode(v[4 + k] * inv) << (8 * k);
       if (ok) {
-        *(u32x2*)(q + (size_t)i * W + c * 8) = u32x2{lo, hi};
+        *(u32x2*)(q + (size_t)i * QS + c * 8) = u32x2{lo, hi};
         if ((c & 3) == 0) ((uint8_t*)s)[i * (W / 32) + c / 4] = (uint8_t)code;
       }
     }
   }
 }
 
+constexpr int kDownBatch = 4;  // down units a wave holds in flight
+
+// the down rows of a tile: units of G rows (one wave load); a wave takes units v = wave,
+// wave + 8, ... in batches of kDownBatch, issuing the batch's loads before computing it.
+// rows_of(v, ptrs, sptrs) fills the unit's G row / scale pointers; work(v, rows) runs it.
+template <int FMT, int KD, class RowsFn, class WorkFn>
+__device__ __forceinline__ void down_units(int n_units, RowsFn rows_of, WorkFn work) {
+  using S = RowShape<FMT, KD>;
+  using W = WRows<FMT, KD, S::G>;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int v0 = wave; v0 < n_units; v0 += kWaves * kDownBatch) {
+    W wr[kDownBatch];
+#pragma unroll
+    for (int b = 0; b < kDownBatch; ++b) {
+      const int v = v0 + kWaves * b;
+      if (v < n_units) {
+        const uint8_t* rows[S::G];
+        const void* srow[S::G];
+        rows_of(v, rows, srow);
+        wr[b].load(rows, srow, lane);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kDownBatch; ++b) {
+      const int v = v0 + kWaves * b;
+      if (v < n_units) work(v, wr[b]);
+    }
+  }
+}
+
 template <class C>
 __device__ void down_tile(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int R = p.rows;
   // ---- shared expert: quantize SMID (every row) into LDS, then its down rows
+  quant_rows_lds<kFp8, C::S, C::SQS>(
+      p, [&](int i) { return p.off[8] + (uint32_t)i * C::S * 2; }, R, sm.u.sh.q, sm.u.sh.s);
+  __syncthreads();
   {
-    const uint16_t* smid = wsp<const uint16_t>(p, 8);
-    quant_rows_lds<kFp8, C::S>([&](int i) { return smid + (size_t)i * C::S; }, R, sm.u.sh.q,
-                               sm.u.sh.s);
-    __syncthreads();
-    using RS = RowShape<kFp8, C::S>;
-    using W = Fp8Rows<C::S, RS::G>;
-    // a unit: G consecutive rows (one per sub-group)
-    const int n_units = hn / RS::G;
-    for (int v = wave; v < n_units; v += kWaves) {
-      const uint8_t* rows[RS::G];
-      const float* srow[RS::G];
+    using SS = RowShape<kFp8, C::S>;
+    using W = WRows<kFp8, C::S, SS::G>;
+    const int g = lane / SS::LPR;
+    down_units<kFp8, C::S>(
+        hn / SS::G,
+        [&](int v, const uint8_t** rows, const void** srow) {
 #pragma unroll
-      for (int g = 0; g < RS::G; ++g) {
-        const int h = h0 + v * RS::G + g;
-        rows[g] = p.sw2 + (size_t)h * C::S;
-        srow[g] = p.sw2_s + (size_t)(h / 128) * (C::S / 128);
-      }
-      W wr;
-      wr.load(rows, srow, lane);
-      const int g = lane / RS::LPR;
-      for (int t = 0; t < R; ++t) {
-        float acc[1];
-        wr.dot(sm.u.sh.q + (size_t)t * C::S, sm.u.sh.s + t * (C::S / 128), lane, acc);
-        float y = group_sum<RS::LPR>(acc[0]);
-        if ((lane % RS::LPR) == 0) sm.ysh[t * kTileMax + v * RS::G + g] = bf_round(y);
-      }
-    }
-    __syncthreads();
+          for (int q = 0; q < SS::G; ++q) {
+            const int h = h0 + v * SS::G + q;
+            rows[q] = p.sw2 + (size_t)h * C::S;
+            srow[q] = p.sw2_s + (size_t)(h / 128) * (C::S / 128);
+          }
+        },
+        [&](int v, const W& wr) {
+          for (int t = 0; t < R; ++t) {
+            float acc[1];
+            wr.dot(LdsAct{sm.u.sh.q + (size_t)t * C::SQS, sm.u.sh.s + t * (C::S / 128)}, lane, acc);
+            const float y = group_sum<SS::LPR>(acc[0]);
+            if ((lane % SS::LPR) == 0) sm.ysh[t * kTileMax + v * SS::G + g] = bf_round(y);
+          }
+        });
   }
+  __syncthreads();
   // ---- routed experts, in batches of PB picks (slot order)
-  const int npk = R * C::K;
   using RD = RowShape<C::FMT, C::I>;
+  using WD = WRows<C::FMT, C::I, RD::G>;
   const int rg = hn / RD::G;  // row groups of the tile
+  const int npk = R * C::K;
+  const int gsub = lane / RD::LPR;
   for (int pb0 = 0; pb0 < npk; pb0 += C::PB) {
     const int pbn = min(C::PB, npk - pb0);
-    {
-      const uint16_t* mid = wsp<const uint16_t>(p, 9);
-      quant_rows_lds<C::FMT, C::I>(
-          [&](int i) { return mid + (size_t)un.picks[pb0 + i] * C::I; }, pbn, sm.u.mid.q,
-          sm.u.mid.s);
-    }
+    quant_rows_lds<C::FMT, C::I, C::MQS>(
+        p, [&](int i) { return p.off[9] + (uint32_t)un.picks[pb0 + i] * C::I * 2; }, pbn,
+        sm.u.mid.q, sm.u.mid.s);
     __syncthreads();
     // slots with picks in [pb0, pb0 + pbn)
-    int s_lo = 0;
-    {
-      // the slot of pick position pb0 (binary search over slot_start)
-      int lo = 0, hi = un.n - 1;
-      while (lo < hi) {
-        int mid = (lo + hi + 1) >> 1;
-        if (un.slot_start[mid] <= pb0) lo = mid; else hi = mid - 1;
-      }
-      s_lo = lo;
+    int lo = 0, hi = un.n - 1;
+    while (lo < hi) {
+      int mid = (lo + hi + 1) >> 1;
+      if (un.slot_start[mid] <= pb0) lo = mid; else hi = mid - 1;
     }
+    const int s_lo = lo;
     int s_hi = s_lo;
     while (s_hi + 1 < un.n && un.slot_start[s_hi + 1] < pb0 + pbn) ++s_hi;
-    const int n_units = (s_hi - s_lo + 1) * rg;
-    for (int v = wave; v < n_units; v += kWaves) {
-      const int slot = s_lo + v / rg, r0 = (v % rg) * RD::G;
-      const int e = un.slot_e[slot];
-      const int j0 = max(un.slot_start[slot], pb0), j1 = min(un.slot_start[slot + 1], pb0 + pbn);
-      const int g = lane / RD::LPR;
-      if constexpr (C::FMT == kFp8) {
-        using W = Fp8Rows<C::I, RD::G>;
-        const uint8_t* rows[RD::G];
-        const float* srow[RD::G];
-        const float* s2 = (const float*)p.w2_s + (size_t)e * (C::H / 128) * (C::I / 128);
+    down_units<C::FMT, C::I>(
+        (s_hi - s_lo + 1) * rg,
+        [&](int v, const uint8_t** rows, const void** srow) {
+          const int e = un.slot_e[s_lo + v / rg];
+          const int r0 = h0 + (v % rg) * RD::G;
 #pragma unroll
-        for (int q = 0; q < RD::G; ++q) {
-          const int h = h0 + r0 + q;
-          rows[q] = p.w2 + ((size_t)e * C::H + h) * C::I;
-          srow[q] = s2 + (size_t)(h / 128) * (C::I / 128);
-        }
-        W wr;
-        wr.load(rows, srow, lane);
-        for (int j = j0; j < j1; ++j) {
-          const int lp = j - pb0;
-          float acc[1];
-          wr.dot(sm.u.mid.q + (size_t)lp * C::I, (const float*)(sm.u.mid.s) + lp * (C::I / 128),
-                 lane, acc);
-          float y = group_sum<RD::LPR>(acc[0]);
-          if ((lane % RD::LPR) == 0) sm.contrib[un.picks[j] * kTileMax + r0 + g] = y;
-        }
-      } else {
-        using W = Fp4Rows<C::I, RD::G>;
-        const uint8_t* rows[RD::G];
-        const uint8_t* srow[RD::G];
-#pragma unroll
-        for (int q = 0; q < RD::G; ++q) {
-          const size_t row = (size_t)e * C::H + h0 + r0 + q;
-          rows[q] = p.w2 + row * (C::I / 2);
-          srow[q] = (const uint8_t*)p.w2_s + row * (C::I / 32);
-        }
-        W wr;
-        wr.load(rows, srow, lane);
-        for (int j = j0; j < j1; ++j) {
-          const int lp = j - pb0;
-          float acc[1];
-          wr.dot(sm.u.mid.q + (size_t)lp * C::I, sm.u.mid.s + lp * (C::I / 32), lane, acc);
-          float y = group_sum<RD::LPR>(acc[0]);
-          if ((lane % RD::LPR) == 0) sm.contrib[un.picks[j] * kTileMax + r0 + g] = y;
-        }
-      }
-    }
+          for (int q = 0; q < RD::G; ++q) {
+            const size_t row = (size_t)e * C::H + r0 + q;
+            if constexpr (C::FMT == kFp8) {
+              rows[q] = p.w2 + row * C::I;
+              srow[q] = (const float*)p.w2_s + (size_t)e * (C::H / 128) * (C::I / 128) +
+                        (size_t)((r0 + q) / 128) * (C::I / 128);
+            } else {
+              rows[q] = p.w2 + row * (C::I / 2);
+              srow[q] = (const uint8_t*)p.w2_s + row * (C::I / 32);
+            }
+          }
+        },
+        [&](int v, const WD& wr) {
+          const int slot = s_lo + v / rg, r0 = (v % rg) * RD::G;
+          const int j0 = max(un.slot_start[slot], pb0), j1 = min(un.slot_start[slot + 1], pb0 + pbn);
+          for (int jj = j0; jj < j1; ++jj) {
+            const int lp = jj - pb0;
+            float acc[1];
+            if constexpr (C::FMT == kFp8)
+              wr.dot(LdsAct{sm.u.mid.q + (size_t)lp * C::MQS, (const float*)sm.u.mid.s + lp * (C::I / 128)}, lane, acc);
+            else
+              wr.dot(LdsAct{sm.u.mid.q + (size_t)lp * C::MQS, sm.u.mid.s + lp * (C::I / 32)}, lane, acc);
+            const float y = group_sum<RD::LPR>(acc[0]);
+            if ((lane % RD::LPR) == 0) sm.contrib[un.picks[jj] * kTileMax + r0 + gsub] = y;
+          }
+        });
     __syncthreads();
   }
   // ---- combine: top-k order, bf16 at every add, then + shared
@@ -1242,7 +1294,7 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
     if (!aligned16(q)) return MKMOE_ERR_ALIGN;
   if (s->use_norm && !aligned16(w->norm)) return MKMOE_ERR_ALIGN;
   Layout L = layout_of(s);
-  if (ws_bytes < L.total) return MKMOE_ERR_WORKSPACE;
+  if (ws_bytes < L.total || L.total >= (1ull << 31)) return MKMOE_ERR_WORKSPACE;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return MKMOE_ERR_HIP;
   DevInfo di;
@@ -1267,6 +1319,7 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
   p.sw2 = (const uint8_t*)w->sw2;
   p.sw2_s = (const float*)w->sw2_s;
   p.ws = (uint8_t*)ws;
+  p.ws_bytes = (uint32_t)L.total;
   p.rows = rows;
   p.rmax = s->max_rows;
   p.renorm = s->renorm;
@@ -1283,7 +1336,7 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
     dl = g_deadline_s;
   }
   p.deadline = (unsigned long long)(dl * 1e8);
-  for (int i = 0; i < 10; ++i) p.off[i] = L.off[i];
+  for (int i = 0; i < 10; ++i) p.off[i] = (uint32_t)L.off[i];
   hipStream_t st = (hipStream_t)stream;
   switch (cfg_id(s)) {
     case kIdPlumbing:

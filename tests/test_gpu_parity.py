@@ -1,9 +1,10 @@
 """Parity of the HIP MoE block (through the C ABI) with the CPU oracle, on an MI355X.
 
-Bars: router part sums, activation codes, expert ids and routing weights bit
-for bit; the bf16 output within max-abs 2e-2 and relative L2 1e-2 of the
-oracle; the persistent and the staged launches bit for bit alike; repeated and
-graph-replayed launches bit for bit alike.
+Bars: router part sums, activation codes, expert ids, routing weights and the
+bf16 output bit for bit (the oracle restates the kernel's arithmetic order);
+the output also within max-abs 2e-2 and relative L2 1e-2; the persistent and
+the staged launches bit for bit alike; repeated and graph-replayed launches
+bit for bit alike.
 """
 
 import numpy as np
@@ -85,11 +86,14 @@ def test_parity(workload, rows):
     # routing, bit for bit
     assert np.array_equal(ids.cpu().numpy(), c.ids), "expert ids"
     assert np.array_equal(wts.cpu().numpy().view(np.uint32), c.wts.view(np.uint32)), "routing weights"
-    e = errors(out[torch.from_numpy(c.check).cuda()], c.ref)
+    got = out[torch.from_numpy(c.check).cuda()].cpu()
+    e = errors(got, c.ref)
     print(f"  out vs oracle: {e}", flush=True)
     assert not e["nan"] and not torch.isnan(out).any()
     assert e["rel_l2"] <= REL_L2, e
     assert e["max_abs"] <= MAX_ABS, e
+    n_diff = int((got.view(torch.int16) != c.ref.view(torch.int16)).sum())
+    assert n_diff == 0, f"{n_diff} output elements differ from the oracle's bits"
 
 
 @pytest.mark.parametrize("workload,rows", [("cfg2_tp4_fp8", 8), ("cfg3_tp4_mxfp4", 8), ("cfg5_tp2_mxfp4_norm", 8)])
