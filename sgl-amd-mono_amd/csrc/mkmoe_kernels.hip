@@ -62,8 +62,8 @@ struct Cfg {
   static_assert(H % 1024 == 0 && CH512 % P == 0, "router chunks, K split over 8 waves");
   static_assert(I % 128 == 0 && S % 128 == 0, "widths");
   static_assert(E <= 1024 && (NG == 1 || (E % NG == 0)), "experts");
-  // down-stage mid batch: picks whose quantized rows fit ~32 KB of LDS
-  static constexpr int PB = 32768 / I;
+  // down-stage mid batch: picks whose quantized rows fit ~64 KB of LDS
+  static constexpr int PB = 65536 / I;
   static constexpr int MQS = I + 16;  // LDS row stride of quantized mid (bank spread)
   static constexpr int SQS = S + 16;
   static constexpr int MSC = FMT == kFp4 ? I / 32 : I / 128;  // mid scales a pick
@@ -181,26 +181,56 @@ __device__ __forceinline__ uint32_t* ctl(const Params& p) { return (uint32_t*)p.
 __device__ __forceinline__ float bf_lo(uint32_t w) { return u2f(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return u2f(w & 0xffff0000u); }
 
-__device__ __forceinline__ float wave_sum(float v) {
-  // halving tree: lanes l and l + d, d = 32 .. 1 (every lane ends with the sum)
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) v = v + __shfl_xor(v, d);
-  return v;
+// lane l < D receives lane l + D's value (what other lanes receive is unspecified):
+// DPP row_shl within a 16-lane row; the gfx950 lane swaps across rows (second result of
+// permlane16_swap(v, v): rows 0 and 2 get rows 1 and 3; of permlane32_swap(v, v): lanes
+// 0-31 get lanes 32-63)
+template <int D>
+__device__ __forceinline__ float from_lane_above(float v) {
+  const int iv = __float_as_int(v);
+  if constexpr (D == 32) {
+    return __int_as_float((int)__builtin_amdgcn_permlane32_swap(iv, iv, false, false)[1]);
+  } else if constexpr (D == 16) {
+    return __int_as_float((int)__builtin_amdgcn_permlane16_swap(iv, iv, false, false)[1]);
+  } else {
+    static_assert(D >= 1 && D <= 8, "row shift");
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0x100 + D, 0xF, 0xF, true));
+  }
 }
-// sum over groups of G lanes (G a power of two)
+
+// halving-tree sum over groups of G lanes (G a power of two): lanes l and l + d added for
+// d = G/2 .. 1; the first lane of each group ends with the group's sum
 template <int G>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int d = G / 2; d >= 1; d >>= 1) v = v + __shfl_xor(v, d);
+__device__ __forceinline__ float tree_sum(float v) {
+  if constexpr (G >= 64) v = v + from_lane_above<32>(v);
+  if constexpr (G >= 32) v = v + from_lane_above<16>(v);
+  if constexpr (G >= 16) v = v + from_lane_above<8>(v);
+  if constexpr (G >= 8) v = v + from_lane_above<4>(v);
+  if constexpr (G >= 4) v = v + from_lane_above<2>(v);
+  if constexpr (G >= 2) v = v + from_lane_above<1>(v);
   return v;
 }
+
+// lane l's value, uniform over the wave
+__device__ __forceinline__ float lane_value(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// the halving-tree sum of the wave, in every lane
+__device__ __forceinline__ float wave_sum(float v) { return lane_value(tree_sum<64>(v), 0); }
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+// max over aligned groups of G lanes (G <= 16), in every lane of the group; the inputs are
+// never NaN, and a max of non-NaN values does not depend on the exchange pattern
 template <int G>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int d = G / 2; d >= 1; d >>= 1) {
-    float o = __shfl_xor(v, d);
-    v = o > v ? o : v;
-  }
+  static_assert(G >= 1 && G <= 16, "within a 16-lane row");
+  if constexpr (G >= 2) { const float o = dpp_mov<0xB1>(v); v = o > v ? o : v; }   // quad_perm 1,0,3,2
+  if constexpr (G >= 4) { const float o = dpp_mov<0x4E>(v); v = o > v ? o : v; }   // quad_perm 2,3,0,1
+  if constexpr (G >= 8) { const float o = dpp_mov<0x141>(v); v = o > v ? o : v; }  // row_half_mirror
+  if constexpr (G >= 16) { const float o = dpp_mov<0x140>(v); v = o > v ? o : v; } // row_mirror
   return v;
 }
 
@@ -357,21 +387,45 @@ __device__ __forceinline__ u32x4 x_load(const Params& p, __amdgpu_buffer_rsrc_t 
 }
 
 // ---------------------------------------------------------------- stage A
-// router part sums: logit part (e, part) of every row, in the fixed order
+// the columns of one router K part for every row, staged in LDS
 template <class C>
-__device__ void router_unit(const Params& p, int e, int part, int lane) {
+struct RouterSmem {
+  static constexpr int PW = C::H / C::P;
+  uint16_t x[kRowsMax * PW];
+};
+
+// router part sums of one workgroup unit: K part ``part`` of experts eb * 8 .. eb * 8 + 7
+// (one a wave) for every row, in the fixed order: lane l sums its 8 columns of each
+// 512-column chunk of the part in order (products rounded, then added), then the
+// wave's halving tree
+template <class C>
+__device__ void router_unit(const Params& p, RouterSmem<C>& sm, int part, int eb, int lane, int wave) {
 #pragma clang fp contract(off)
   constexpr int CPP = C::CH512 / C::P;
+  constexpr int PW = RouterSmem<C>::PW;
+  static_assert(PW == CPP * 512, "part width");
+  const int e = eb * kWaves + wave;
   const auto rs = ws_rsrc(p);
   u32x4 wv[CPP];
+  if (e < C::E) {
 #pragma unroll
-  for (int i = 0; i < CPP; ++i)
-    wv[i] = ld16_nt(p.gate_w + (size_t)e * C::H + (part * CPP + i) * 512 + lane * 8);
+    for (int i = 0; i < CPP; ++i)
+      wv[i] = ld16_nt(p.gate_w + (size_t)e * C::H + (part * CPP + i) * 512 + lane * 8);
+  }
+  __syncthreads();  // the previous unit is done with the tile
+  const int n = p.rows * (PW / 8);
+#pragma unroll 4
+  for (int i = threadIdx.x; i < n; i += kThreads) {
+    const int r = i / (PW / 8), c = i % (PW / 8);
+    *(u32x4*)(sm.x + r * PW + c * 8) = x_load<C>(p, rs, r, part * PW + c * 8);
+  }
+  __syncthreads();
+  if (e >= C::E) return;
   for (int r = 0; r < p.rows; ++r) {
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < CPP; ++i) {
-      u32x4 xv = x_load<C>(p, rs, r, (part * CPP + i) * 512 + lane * 8);
+      const u32x4 xv = *(const u32x4*)(sm.x + r * PW + i * 512 + lane * 8);
       const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
       const uint32_t ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
 #pragma unroll
@@ -380,7 +434,7 @@ __device__ void router_unit(const Params& p, int e, int part, int lane) {
         acc = acc + bf_hi(xw[q]) * bf_hi(ww[q]);
       }
     }
-    float s = wave_sum(acc);
+    const float s = tree_sum<64>(acc);
     if (lane == 0) dst32(rs, p.off[5] + (((uint32_t)r * C::E + e) * C::P + part) * 4, f2u(s));
   }
 }
@@ -432,15 +486,19 @@ __device__ void quant_unit(const Params& p, int r, int c, int lane) {
   }
 }
 
+// workgroup units: (router K part, block of 8 experts), then one unit a row to quantize
 template <class C>
-__device__ void stage_a(const Params& p, int b, int nwg) {
-  const int lane = threadIdx.x & 63, gw = wave_slot(b, nwg);
-  const int n_router = C::E * C::P, n_quant = p.rows * C::CH512;
-  for (int u = gw; u < n_router + n_quant; u += nwg * kWaves) {
-    if (u < n_router)
-      router_unit<C>(p, u / C::P, u % C::P, lane);
-    else
-      quant_unit<C>(p, (u - n_router) / C::CH512, (u - n_router) % C::CH512, lane);
+__device__ void stage_a(const Params& p, RouterSmem<C>& sm, int b, int nwg) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int EB = (C::E + kWaves - 1) / kWaves;
+  constexpr int n_router = C::P * EB;
+  const int n = n_router + p.rows;
+  for (int u = b; u < n; u += nwg) {
+    if (u < n_router) {
+      router_unit<C>(p, sm, u % C::P, u / C::P, lane, wave);
+    } else {
+      for (int c = wave; c < C::CH512; c += kWaves) quant_unit<C>(p, u - n_router, c, lane);
+    }
   }
 }
 
@@ -593,16 +651,6 @@ struct RowShape {
   static_assert(CPR % LPR == 0, "row chunks");
 };
 
-// rows[q * G + g] for this lane's sub-group g, without indexing a register array
-template <int G, class T>
-__device__ __forceinline__ T sub_pick(const T* arr, int q, int g) {
-  T v = arr[q * G];
-#pragma unroll
-  for (int k = 1; k < G; ++k)
-    if (g == k) v = arr[q * G + k];
-  return v;
-}
-
 // activations of one row: e4m3 codes and their scales (fp32 per 128, or E8M0 per 32)
 struct DevAct {  // in the workspace (sc1 loads)
   __amdgpu_buffer_rsrc_t rs;
@@ -632,17 +680,18 @@ struct WRows {
   float sf[RPG][S::CPL];
   int se[RPG][S::CPL];
 
-  __device__ __forceinline__ void load(const uint8_t* const* rows, const void* const* srow, int lane) {
+  // row(i, w, s) sets row i's first byte and its scales (i < NR; this lane's sub-group g
+  // takes rows g, g + G, ...)
+  template <class RowFn>
+  __device__ __forceinline__ void load(RowFn row, int lane) {
     const int g = lane / S::LPR, l = lane % S::LPR;
 #pragma unroll
     for (int q = 0; q < RPG; ++q) {
-      const uint8_t* r = sub_pick<S::G>(rows, q, g);
+      const uint8_t* r;
+      const void* sr;
+      row(q * S::G + g, r, sr);
 #pragma unroll
       for (int i = 0; i < S::CPL; ++i) w[q][i] = ld16_nt(r + (l + S::LPR * i) * 16);
-    }
-#pragma unroll
-    for (int q = 0; q < RPG; ++q) {
-      const void* sr = sub_pick<S::G>(srow, q, g);
 #pragma unroll
       for (int i = 0; i < S::CPL; ++i) {
         const int c = l + S::LPR * i;
@@ -706,80 +755,279 @@ __device__ __forceinline__ float swiglu_shared(float g, float u, float lim) {
 
 constexpr int kTokGroup = 8;  // picks a gate_up unit takes at most
 
-// gate_up of one intermediate column j (rows j and W + j of a [2W][H] weight) for up to
-// kTokGroup activation rows; emit(i, mid) stores pick i's SwiGLU output
+// activation rows of a unit staged in LDS: kTokGroup rows of codes and their scales
+template <class C>
+struct XTile {
+  static constexpr int QS = C::H + 16;  // row stride (bank spread)
+  uint8_t q[kTokGroup * QS];
+  uint8_t s[kTokGroup * (C::H / 32)];  // E8M0 per 32, or fp32 per 128 (the same bytes)
+};
+
+// copy activation rows tok(p), p < np (codes at qoff + t H, scales at soff + t * sbytes)
+// from the workspace (sc1) into the tile; every thread of the workgroup takes part
+template <class C, class TokFn>
+__device__ void load_xtile(const Params& p, XTile<C>& xt, int np, uint32_t qoff, uint32_t soff,
+                           int sbytes, TokFn tok) {
+  const auto rs = ws_rsrc(p);
+  const int tid = threadIdx.x;
+  constexpr int QC = C::H / 16;  // 16-byte chunks a row
+  for (int i = tid; i < np * QC; i += kThreads) {
+    const int r = i / QC, c = i % QC;
+    *(u32x4*)(xt.q + r * XTile<C>::QS + c * 16) = dld128(rs, qoff + (uint32_t)tok(r) * C::H + c * 16);
+  }
+  const int sc = sbytes / 4;  // 4-byte words of a row's scales
+  for (int i = tid; i < np * sc; i += kThreads) {
+    const int r = i / sc, c = i % sc;
+    ((uint32_t*)xt.s)[r * sc + c] = dld32(rs, soff + (uint32_t)tok(r) * sbytes + c * 4);
+  }
+}
+
+// gate_up of one intermediate column (rows j and W + j of a [2W][H] weight) against the np
+// activation rows of an XTile: chunk-outer, pick-inner (the weights convert once a chunk);
+// the per-(row, pick) arithmetic is the canonical order of WRows. -> g[p], u[p] in every lane
 template <int FMT, int H>
-struct GateUp {
+struct GateUpCol {
   using R = WRows<FMT, H, 2>;
+  using S = typename R::S;
   R wr;
+
   __device__ __forceinline__ void load(const uint8_t* w, const void* s, int W, int j, int lane) {
-    const uint8_t* rows[2];
-    const void* srow[2];
-    const int rid[2] = {j, W + j};
+    wr.load(
+        [&](int i, const uint8_t*& r, const void*& sr) {
+          const int rid = i == 0 ? j : W + j;
+          if constexpr (FMT == kFp8) {
+            r = w + (size_t)rid * H;
+            sr = (const float*)s + (size_t)(rid / 128) * (H / 128);
+          } else {
+            r = w + (size_t)rid * (H / 2);
+            sr = (const uint8_t*)s + (size_t)rid * (H / 32);
+          }
+        },
+        lane);
+  }
+
+  template <int QS>
+  __device__ __forceinline__ void run(const uint8_t* xq, const uint8_t* xs, int np, int lane,
+                                      float (&g)[kTokGroup], float (&u)[kTokGroup]) const {
+#pragma clang fp contract(off)
+    const int l = lane % S::LPR;
+    float acc[R::RPG][kTokGroup];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < R::RPG; ++q)
+#pragma unroll
+      for (int p = 0; p < kTokGroup; ++p) acc[q][p] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < S::CPL; ++i) {
+      const int c = l + S::LPR * i;
       if constexpr (FMT == kFp8) {
-        rows[q] = w + (size_t)rid[q] * H;
-        srow[q] = (const float*)s + (size_t)(rid[q] / 128) * (H / 128);
+        float wf[R::RPG][16];
+#pragma unroll
+        for (int q = 0; q < R::RPG; ++q) {
+          u32x4 wq = wr.w[q][i];
+          asm volatile("" : "+v"(wq));
+          const uint32_t wv[4] = {wq.x, wq.y, wq.z, wq.w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)wv[k], false);
+            auto b = __builtin_amdgcn_cvt_pk_f32_fp8((int)wv[k], true);
+            wf[q][4 * k] = a[0];
+            wf[q][4 * k + 1] = a[1];
+            wf[q][4 * k + 2] = b[0];
+            wf[q][4 * k + 3] = b[1];
+          }
+        }
+#pragma unroll
+        for (int p = 0; p < kTokGroup; ++p) {
+          if (p < np) {
+            const u32x4 xv = *(const u32x4*)(xq + p * QS + c * 16);
+            const float sx = ((const float*)xs)[p * (H / 128) + c / 8];
+            const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+            float xf[16];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)xw[k], false);
+              auto b = __builtin_amdgcn_cvt_pk_f32_fp8((int)xw[k], true);
+              xf[4 * k] = a[0];
+              xf[4 * k + 1] = a[1];
+              xf[4 * k + 2] = b[0];
+              xf[4 * k + 3] = b[1];
+            }
+#pragma unroll
+            for (int q = 0; q < R::RPG; ++q) {
+              float d = 0.0f;
+#pragma unroll
+              for (int k = 0; k < 16; ++k) d = fmaf(wf[q][k], xf[k], d);
+              const float f = wr.sf[q][i] * sx;
+              acc[q][p] = acc[q][p] + d * f;
+            }
+          }
+        }
       } else {
-        rows[q] = w + (size_t)rid[q] * (H / 2);
-        srow[q] = (const uint8_t*)s + (size_t)rid[q] * (H / 32);
+        float wf[R::RPG][32];
+#pragma unroll
+        for (int q = 0; q < R::RPG; ++q) {
+          u32x4 wq = wr.w[q][i];
+          asm volatile("" : "+v"(wq));
+          const uint32_t wv[4] = {wq.x, wq.y, wq.z, wq.w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            auto a = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wv[k], 1.0f, 0);
+            auto b = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wv[k], 1.0f, 1);
+            auto c2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wv[k], 1.0f, 2);
+            auto d2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wv[k], 1.0f, 3);
+            wf[q][8 * k] = a[0];
+            wf[q][8 * k + 1] = a[1];
+            wf[q][8 * k + 2] = b[0];
+            wf[q][8 * k + 3] = b[1];
+            wf[q][8 * k + 4] = c2[0];
+            wf[q][8 * k + 5] = c2[1];
+            wf[q][8 * k + 6] = d2[0];
+            wf[q][8 * k + 7] = d2[1];
+          }
+        }
+#pragma unroll
+        for (int p = 0; p < kTokGroup; ++p) {
+          if (p < np) {
+            const u32x4 xa = *(const u32x4*)(xq + p * QS + c * 32);
+            const u32x4 xb = *(const u32x4*)(xq + p * QS + c * 32 + 16);
+            const int ex = xs[p * (H / 32) + c];
+            const uint32_t xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+            float xf[32];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)xw[k], false);
+              auto b = __builtin_amdgcn_cvt_pk_f32_fp8((int)xw[k], true);
+              xf[4 * k] = a[0];
+              xf[4 * k + 1] = a[1];
+              xf[4 * k + 2] = b[0];
+              xf[4 * k + 3] = b[1];
+            }
+#pragma unroll
+            for (int q = 0; q < R::RPG; ++q) {
+              float d = 0.0f;
+#pragma unroll
+              for (int k = 0; k < 32; ++k) d = fmaf(wf[q][k], xf[k], d);
+              acc[q][p] = acc[q][p] + ldexpf(d, wr.se[q][i] + ex - 254);
+            }
+          }
+        }
       }
     }
-    wr.load(rows, srow, lane);
-  }
-  // (gate, up) sums of one activation row, valid in every lane
-  template <class Act>
-  __device__ __forceinline__ void run(const Act& x, int lane, float& g, float& u) const {
-    float acc[R::RPG];
-    wr.dot(x, lane, acc);
 #pragma unroll
-    for (int q = 0; q < R::RPG; ++q) acc[q] = group_sum<R::S::LPR>(acc[q]);
-    if constexpr (R::S::G == 1) {
-      g = acc[0];
-      u = acc[1];
-    } else {
-      static_assert(R::S::G == 2, "gate and up on two sub-groups");
-      g = __shfl(acc[0], 0);
-      u = __shfl(acc[0], 32);
+    for (int p = 0; p < kTokGroup; ++p) {
+      if (p < np) {
+        if constexpr (S::G == 1) {
+          g[p] = lane_value(tree_sum<64>(acc[0][p]), 0);
+          u[p] = lane_value(tree_sum<64>(acc[1][p]), 0);
+        } else {
+          static_assert(S::G == 2, "gate and up on two sub-groups");
+          const float t = tree_sum<32>(acc[0][p]);
+          g[p] = lane_value(t, 0);
+          u[p] = lane_value(t, 32);
+        }
+      }
     }
   }
 };
 
-// ---------------------------------------------------------------- stage B: shared gate_up
-// unit u: shared column j = u % S for rows of token group u / S
-template <class C>
-__device__ void shared_gu_unit(const Params& p, int u, int lane) {
-  const int j = u % C::S, tg = u / C::S;
-  GateUp<kFp8, C::H> gu;
-  gu.load(p.sgu, p.sgu_s, C::S, j, lane);
-  const auto rs = ws_rsrc(p);
-  const int rq = C::FMT == kFp4 ? 3 : 1, rsc = C::FMT == kFp4 ? 4 : 2;
-  const int t1 = min(p.rows, (tg + 1) * kTokGroup);
-  for (int t = tg * kTokGroup; t < t1; ++t) {
-    float g, up;
-    gu.run(DevAct{rs, p.off[rq] + (uint32_t)t * C::H, p.off[rsc] + (uint32_t)t * (C::H / 128) * 4},
-           lane, g, up);
-    if (lane == 0) dst16(rs, p.off[8] + ((uint32_t)t * C::S + j) * 2, f2bf(swiglu_shared(g, up, p.limit)));
+// lane k (k < kTokGroup) receives a[k] of a wave-uniform array (lane writes, no indexing)
+template <int K>
+__device__ __forceinline__ void write_lane(float& v, float s) {
+  const int u = __builtin_amdgcn_readfirstlane(__float_as_int(s));
+  asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(v) : "s"(u), "i"(K));
+}
+__device__ __forceinline__ float lane_pick(const float (&a)[kTokGroup]) {
+  static_assert(kTokGroup == 8, "lanes written");
+  float v = 0.0f;
+  write_lane<0>(v, a[0]);
+  write_lane<1>(v, a[1]);
+  write_lane<2>(v, a[2]);
+  write_lane<3>(v, a[3]);
+  write_lane<4>(v, a[4]);
+  write_lane<5>(v, a[5]);
+  write_lane<6>(v, a[6]);
+  write_lane<7>(v, a[7]);
+  return v;
+}
+
+// columns per gate_up workgroup unit: the smallest power of two >= 8 that still leaves
+// about two units a workgroup
+__device__ __forceinline__ int gu_block(int groups, int width, int nwg) {
+  int cb = 8;
+  while (cb < 64 && groups * (width / (2 * cb)) >= 2 * nwg) cb *= 2;
+  return cb;
+}
+
+// one workgroup unit: columns [c0, c0 + cb) of a [2W][H] weight for np activation rows;
+// wave w takes columns c0 + w, c0 + w + 8, ...: its first column's weights are requested
+// before load_x() stages the rows in the tile, and every next column's weights load while
+// it computes the current one; emit(p, column, g, u) runs in lane p (p < np)
+template <class C, int FMT, class WFn, class XFn, class EmitFn>
+__device__ void gu_unit(const Params& p, XTile<C>& xt, int np, int W, int c0, int cb, WFn weights,
+                        XFn load_x, EmitFn emit) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  using GU = GateUpCol<FMT, C::H>;
+  const uint8_t* wb;
+  const void* sb;
+  weights(wb, sb);
+  int col = c0 + wave;
+  const int end = c0 + cb;
+  GU cur;
+  if (col < end) cur.load(wb, sb, W, col, lane);
+  __syncthreads();  // the previous unit is done with the tile
+  load_x();
+  __syncthreads();
+  if (col >= end) return;
+  while (true) {
+    const int nxt_col = col + kWaves;
+    GU nxt;
+    if (nxt_col < end) nxt.load(wb, sb, W, nxt_col, lane);
+    float g[kTokGroup] = {}, u[kTokGroup] = {};
+    cur.template run<XTile<C>::QS>(xt.q, xt.s, np, lane, g, u);
+    {
+      const float gl = lane_pick(g), ul = lane_pick(u);
+      if (lane < np) emit(lane, col, gl, ul);
+    }
+    if (nxt_col >= end) break;
+    cur = nxt;
+    col = nxt_col;
   }
 }
 
+// ---------------------------------------------------------------- stage B: routing + shared gate_up
 template <class C>
-__device__ void stage_b(const Params& p, int b, int nwg) {
+__device__ void stage_b(const Params& p, XTile<C>& xt, int b, int nwg) {
   const int lane = threadIdx.x & 63, gw = wave_slot(b, nwg);
-  const int n_route = p.rows;
-  const int n_sh = C::S * ((p.rows + kTokGroup - 1) / kTokGroup);
-  for (int u = gw; u < n_route + n_sh; u += nwg * kWaves) {
-    if (u < n_route)
-      route_row<C>(p, u, lane);
-    else
-      shared_gu_unit<C>(p, u - n_route, lane);
+  for (int u = gw; u < p.rows; u += nwg * kWaves) route_row<C>(p, u, lane);
+  // shared expert: workgroup units (token group, column block), placed after the routing rows
+  const int groups = (p.rows + kTokGroup - 1) / kTokGroup;
+  const int cb = gu_block(groups, C::S, nwg);
+  const int nblk = C::S / cb;
+  const int n = groups * nblk;
+  const int first = (b - min(p.rows, nwg) % nwg + nwg) % nwg;  // routing workgroups go last
+  const auto rs = ws_rsrc(p);
+  const uint32_t qoff = C::FMT == kFp4 ? p.off[3] : p.off[1];
+  const uint32_t soff = C::FMT == kFp4 ? p.off[4] : p.off[2];
+  for (int wu = first; wu < n; wu += nwg) {
+    const int tg = wu / nblk, blk = wu % nblk;
+    const int t0 = tg * kTokGroup, np = min(kTokGroup, p.rows - t0);
+    gu_unit<C, kFp8>(
+        p, xt, np, C::S, blk * cb, cb,
+        [&](const uint8_t*& w, const void*& s) {
+          w = p.sgu;
+          s = p.sgu_s;
+        },
+        [&]() { load_xtile<C>(p, xt, np, qoff, soff, (C::H / 128) * 4, [&](int r) { return t0 + r; }); },
+        [&](int q, int col, float g, float u) {
+          dst16(rs, p.off[8] + ((uint32_t)(t0 + q) * C::S + col) * 2, f2bf(swiglu_shared(g, u, p.limit)));
+        });
   }
 }
 
 // ---------------------------------------------------------------- the step's union (LDS)
 template <class C>
 struct Union {
+  uint32_t rows_of[C::E][2];  // rows (bit r) that picked expert e
   int cnt[C::E];
   int slot_of[C::E];
   int slot_e[C::E];
@@ -792,20 +1040,26 @@ struct Union {
   int ntg;
 };
 
-// experts picked by any row (ascending id), their picks (pick = row * K + k) and token groups
+// experts picked by any row (ascending id), their picks (pick = row * K + k; a slot's picks
+// in row order, the same in every workgroup) and token groups
 template <class C>
 __device__ void build_union(const Params& p, Union<C>& un) {
+  static_assert(kRowsMax <= 64, "row bitmaps");
   const int tid = threadIdx.x;
   const int npk = p.rows * C::K;
   const auto rs = ws_rsrc(p);
   __syncthreads();
-  for (int e = tid; e < C::E; e += kThreads) un.cnt[e] = 0;
+  for (int e = tid; e < C::E; e += kThreads) un.rows_of[e][0] = un.rows_of[e][1] = 0u;
   __syncthreads();
   for (int t = tid; t < npk; t += kThreads) {
     const int e = min(max((int)dld32(rs, p.off[6] + t * 4), 0), C::E - 1);
-    atomicAdd(&un.cnt[e], 1);
+    const int r = t / C::K;
+    atomicOr(&un.rows_of[e][r >> 5], 1u << (r & 31));
     un.wts[t] = u2f(dld32(rs, p.off[7] + t * 4));
   }
+  __syncthreads();
+  for (int e = tid; e < C::E; e += kThreads)
+    un.cnt[e] = __popc(un.rows_of[e][0]) + __popc(un.rows_of[e][1]);
   __syncthreads();
   if (tid < 64) {
     constexpr int EPL = (C::E + 63) / 64;
@@ -855,61 +1109,50 @@ __device__ void build_union(const Params& p, Union<C>& un) {
     }
   }
   __syncthreads();
+  // a pick's place: its slot's start + the rows below its own that picked the same expert
   for (int t = tid; t < npk; t += kThreads) {
     const int e = min(max((int)dld32(rs, p.off[6] + t * 4), 0), C::E - 1);
-    const int pos = atomicAdd(&un.cnt[e], 1);
-    un.picks[pos] = t;
+    const int r = t / C::K;
+    const uint32_t below0 = r >= 32 ? 0xffffffffu : (1u << r) - 1u;
+    const uint32_t below1 = r >= 32 ? (1u << (r - 32)) - 1u : 0u;
+    const int pos = un.cnt[e] + __popc(un.rows_of[e][0] & below0) + __popc(un.rows_of[e][1] & below1);
+    un.picks[min(pos, npk - 1)] = t;
   }
   __syncthreads();
 }
 
 // ---------------------------------------------------------------- stage C: routed gate_up
-// unit u: column j = u % I of the token group u / I (a slot's picks, kTokGroup at a time);
-// a wave's next unit's weights load while it computes the current one
+// workgroup units (token group, column block): a slot's picks, kTokGroup at a time, against
+// a block of intermediate columns; the picks' activation rows are staged in LDS once a unit
 template <class C>
-__device__ void stage_c(const Params& p, const Union<C>& un, int b, int nwg) {
-  const int lane = threadIdx.x & 63, gw = wave_slot(b, nwg);
-  const int stride = nwg * kWaves;
-  const int n = un.ntg * C::I;
+__device__ void stage_c(const Params& p, const Union<C>& un, XTile<C>& xt, int b, int nwg) {
+  const int cb = gu_block(un.ntg, C::I, nwg);
+  const int nblk = C::I / cb;
+  const int n = un.ntg * nblk;
   const auto rs = ws_rsrc(p);
-  using GU = GateUp<C::FMT, C::H>;
-  auto load = [&](GU& gu, int u) {
-    const int tgg = u / C::I, j = u % C::I;
-    const int e = un.slot_e[un.tg_slot[tgg]];
-    if constexpr (C::FMT == kFp8)
-      gu.load(p.w13 + (size_t)e * 2 * C::I * C::H,
-              (const float*)p.w13_s + (size_t)e * (2 * C::I / 128) * (C::H / 128), C::I, j, lane);
-    else
-      gu.load(p.w13 + (size_t)e * 2 * C::I * (C::H / 2),
-              (const uint8_t*)p.w13_s + (size_t)e * 2 * C::I * (C::H / 32), C::I, j, lane);
-  };
-  auto compute = [&](const GU& gu, int u) {
-    const int tgg = u / C::I, j = u % C::I;
+  constexpr int SB = C::FMT == kFp4 ? C::H / 32 : (C::H / 128) * 4;  // scale bytes of a row
+  for (int wu = b; wu < n; wu += nwg) {
+    const int tgg = wu / nblk, blk = wu % nblk;
     const int slot = un.tg_slot[tgg];
+    const int e = un.slot_e[slot];
     const int j0 = un.slot_start[slot] + (tgg - un.tg_start[slot]) * kTokGroup;
-    const int j1 = min(j0 + kTokGroup, un.slot_start[slot + 1]);
-    for (int jj = j0; jj < j1; ++jj) {
-      const int pk = un.picks[jj], t = pk / C::K;
-      float g, up;
-      if constexpr (C::FMT == kFp8)
-        gu.run(DevAct{rs, p.off[1] + (uint32_t)t * C::H, p.off[2] + (uint32_t)t * (C::H / 128) * 4}, lane, g, up);
-      else
-        gu.run(DevAct{rs, p.off[1] + (uint32_t)t * C::H, p.off[2] + (uint32_t)t * (C::H / 32)}, lane, g, up);
-      if (lane == 0) dst16(rs, p.off[9] + ((uint32_t)pk * C::I + j) * 2, f2bf(swiglu_routed(g, up, p.limit)));
-    }
-  };
-  int u = gw;
-  if (u >= n) return;
-  GU cur;
-  load(cur, u);
-  while (true) {
-    const int un_next = u + stride;
-    GU nxt;
-    if (un_next < n) load(nxt, un_next);
-    compute(cur, u);
-    if (un_next >= n) break;
-    cur = nxt;
-    u = un_next;
+    const int np = min(kTokGroup, un.slot_start[slot + 1] - j0);
+    gu_unit<C, C::FMT>(
+        p, xt, np, C::I, blk * cb, cb,
+        [&](const uint8_t*& w, const void*& s) {
+          if constexpr (C::FMT == kFp8) {
+            w = p.w13 + (size_t)e * 2 * C::I * C::H;
+            s = (const float*)p.w13_s + (size_t)e * (2 * C::I / 128) * (C::H / 128);
+          } else {
+            w = p.w13 + (size_t)e * 2 * C::I * (C::H / 2);
+            s = (const uint8_t*)p.w13_s + (size_t)e * 2 * C::I * (C::H / 32);
+          }
+        },
+        [&]() { load_xtile<C>(p, xt, np, p.off[1], p.off[2], SB, [&](int r) { return un.picks[j0 + r] / C::K; }); },
+        [&](int q, int col, float g, float u) {
+          const int pk = un.picks[j0 + q];
+          dst16(rs, p.off[9] + ((uint32_t)pk * C::I + col) * 2, f2bf(swiglu_routed(g, u, p.limit)));
+        });
   }
 }
 
@@ -989,33 +1232,43 @@ __device__ void quant_rows_lds(const Params& p, RowFn src_row, int n, uint8_t* q
   }
 }
 
-constexpr int kDownBatch = 4;  // down units a wave holds in flight
+constexpr int kDownBatch = 8;  // down units a wave requests at once
 
 // the down rows of a tile: units of G rows (one wave load); a wave takes units v = wave,
-// wave + 8, ... in batches of kDownBatch, issuing the batch's loads before computing it.
-// rows_of(v, ptrs, sptrs) fills the unit's G row / scale pointers; work(v, rows) runs it.
-template <int FMT, int KD, class RowsFn, class WorkFn>
-__device__ __forceinline__ void down_units(int n_units, RowsFn rows_of, WorkFn work) {
+// wave + 8, ... in batches of kDownBatch, the next batch's loads in flight while it
+// computes the current one. row_of(v, i, w, s) sets row i's (i < G) first byte and scales
+// for unit v; work(v, rows) runs it.
+template <int FMT, int KD, class RowFn, class WorkFn>
+__device__ __forceinline__ void down_units(int n_units, RowFn row_of, WorkFn work) {
   using S = RowShape<FMT, KD>;
   using W = WRows<FMT, KD, S::G>;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int v0 = wave; v0 < n_units; v0 += kWaves * kDownBatch) {
-    W wr[kDownBatch];
+  constexpr int kStep = kWaves * kDownBatch;
+  auto load = [&](W (&wr)[kDownBatch], int v0) {
 #pragma unroll
     for (int b = 0; b < kDownBatch; ++b) {
       const int v = v0 + kWaves * b;
-      if (v < n_units) {
-        const uint8_t* rows[S::G];
-        const void* srow[S::G];
-        rows_of(v, rows, srow);
-        wr[b].load(rows, srow, lane);
-      }
+      if (v < n_units)
+        wr[b].load([&](int i, const uint8_t*& r, const void*& sr) { row_of(v, i, r, sr); }, lane);
     }
+  };
+  int v0 = wave;
+  if (v0 >= n_units) return;
+  W cur[kDownBatch];
+  load(cur, v0);
+  while (true) {
+    const int v1 = v0 + kStep;
+    W nxt[kDownBatch];
+    if (v1 < n_units) load(nxt, v1);
 #pragma unroll
     for (int b = 0; b < kDownBatch; ++b) {
       const int v = v0 + kWaves * b;
-      if (v < n_units) work(v, wr[b]);
+      if (v < n_units) work(v, cur[b]);
     }
+    if (v1 >= n_units) break;
+#pragma unroll
+    for (int b = 0; b < kDownBatch; ++b) cur[b] = nxt[b];
+    v0 = v1;
   }
 }
 
@@ -1033,19 +1286,16 @@ __device__ void down_tile(const Params& p, const Union<C>& un, DownSmem<C>& sm, 
     const int g = lane / SS::LPR;
     down_units<kFp8, C::S>(
         hn / SS::G,
-        [&](int v, const uint8_t** rows, const void** srow) {
-#pragma unroll
-          for (int q = 0; q < SS::G; ++q) {
-            const int h = h0 + v * SS::G + q;
-            rows[q] = p.sw2 + (size_t)h * C::S;
-            srow[q] = p.sw2_s + (size_t)(h / 128) * (C::S / 128);
-          }
+        [&](int v, int i, const uint8_t*& r, const void*& sr) {
+          const int h = h0 + v * SS::G + i;
+          r = p.sw2 + (size_t)h * C::S;
+          sr = p.sw2_s + (size_t)(h / 128) * (C::S / 128);
         },
         [&](int v, const W& wr) {
           for (int t = 0; t < R; ++t) {
             float acc[1];
             wr.dot(LdsAct{sm.u.sh.q + (size_t)t * C::SQS, sm.u.sh.s + t * (C::S / 128)}, lane, acc);
-            const float y = group_sum<SS::LPR>(acc[0]);
+            const float y = tree_sum<SS::LPR>(acc[0]);
             if ((lane % SS::LPR) == 0) sm.ysh[t * kTileMax + v * SS::G + g] = bf_round(y);
           }
         });
@@ -1074,20 +1324,16 @@ __device__ void down_tile(const Params& p, const Union<C>& un, DownSmem<C>& sm, 
     while (s_hi + 1 < un.n && un.slot_start[s_hi + 1] < pb0 + pbn) ++s_hi;
     down_units<C::FMT, C::I>(
         (s_hi - s_lo + 1) * rg,
-        [&](int v, const uint8_t** rows, const void** srow) {
+        [&](int v, int i, const uint8_t*& r, const void*& sr) {
           const int e = un.slot_e[s_lo + v / rg];
-          const int r0 = h0 + (v % rg) * RD::G;
-#pragma unroll
-          for (int q = 0; q < RD::G; ++q) {
-            const size_t row = (size_t)e * C::H + r0 + q;
-            if constexpr (C::FMT == kFp8) {
-              rows[q] = p.w2 + row * C::I;
-              srow[q] = (const float*)p.w2_s + (size_t)e * (C::H / 128) * (C::I / 128) +
-                        (size_t)((r0 + q) / 128) * (C::I / 128);
-            } else {
-              rows[q] = p.w2 + row * (C::I / 2);
-              srow[q] = (const uint8_t*)p.w2_s + row * (C::I / 32);
-            }
+          const int h = h0 + (v % rg) * RD::G + i;
+          const size_t row = (size_t)e * C::H + h;
+          if constexpr (C::FMT == kFp8) {
+            r = p.w2 + row * C::I;
+            sr = (const float*)p.w2_s + (size_t)e * (C::H / 128) * (C::I / 128) + (size_t)(h / 128) * (C::I / 128);
+          } else {
+            r = p.w2 + row * (C::I / 2);
+            sr = (const uint8_t*)p.w2_s + row * (C::I / 32);
           }
         },
         [&](int v, const WD& wr) {
@@ -1100,7 +1346,7 @@ __device__ void down_tile(const Params& p, const Union<C>& un, DownSmem<C>& sm, 
               wr.dot(LdsAct{sm.u.mid.q + (size_t)lp * C::MQS, (const float*)sm.u.mid.s + lp * (C::I / 128)}, lane, acc);
             else
               wr.dot(LdsAct{sm.u.mid.q + (size_t)lp * C::MQS, sm.u.mid.s + lp * (C::I / 32)}, lane, acc);
-            const float y = group_sum<RD::LPR>(acc[0]);
+            const float y = tree_sum<RD::LPR>(acc[0]);
             if ((lane % RD::LPR) == 0) sm.contrib[un.picks[jj] * kTileMax + r0 + gsub] = y;
           }
         });
@@ -1131,27 +1377,36 @@ __device__ void stage_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, in
 }
 
 // ---------------------------------------------------------------- kernels
+// the LDS of the stages: the union lives from stage C to the end; the stage buffers share
+template <class C>
+union StageSmem {
+  RouterSmem<C> a;
+  XTile<C> x;
+  DownSmem<C> d;
+};
+
 template <class C>
 __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   __shared__ Union<C> un;
-  __shared__ DownSmem<C> sm;
+  __shared__ StageSmem<C> sm;
   const int b = blockIdx.x, nwg = gridDim.x;
   if constexpr (C::NORM) {
     stage_norm<C>(p, b, nwg);
     arrive(p, kCtlNorm);
     await_all(p, kCtlNorm, nwg, kStageNorm);
   }
-  stage_a<C>(p, b, nwg);
+  stage_a<C>(p, sm.a, b, nwg);
   arrive(p, kCtlA);
   await_all(p, kCtlA, nwg, kStageA);
-  stage_b<C>(p, b, nwg);
+  stage_b<C>(p, sm.x, b, nwg);
   arrive(p, kCtlB);
   await_all(p, kCtlB, nwg, kStageB);
   build_union<C>(p, un);
-  stage_c<C>(p, un, b, nwg);
+  stage_c<C>(p, un, sm.x, b, nwg);
   arrive(p, kCtlC);
   await_all(p, kCtlC, nwg, kStageC);
-  stage_d<C>(p, un, sm, b, nwg);
+  __syncthreads();  // the tile's readers are done before the down stage reuses its LDS
+  stage_d<C>(p, un, sm.d, b, nwg);
   leave(p);
 }
 
@@ -1161,17 +1416,20 @@ __global__ __launch_bounds__(kThreads) void k_norm(Params p) {
 }
 template <class C>
 __global__ __launch_bounds__(kThreads) void k_a(Params p) {
-  stage_a<C>(p, blockIdx.x, gridDim.x);
+  __shared__ RouterSmem<C> sm;
+  stage_a<C>(p, sm, blockIdx.x, gridDim.x);
 }
 template <class C>
 __global__ __launch_bounds__(kThreads) void k_b(Params p) {
-  stage_b<C>(p, blockIdx.x, gridDim.x);
+  __shared__ XTile<C> xt;
+  stage_b<C>(p, xt, blockIdx.x, gridDim.x);
 }
 template <class C>
 __global__ __launch_bounds__(kThreads) void k_c(Params p) {
   __shared__ Union<C> un;
+  __shared__ XTile<C> xt;
   build_union<C>(p, un);
-  stage_c<C>(p, un, blockIdx.x, gridDim.x);
+  stage_c<C>(p, un, xt, blockIdx.x, gridDim.x);
 }
 template <class C>
 __global__ __launch_bounds__(kThreads) void k_d(Params p) {

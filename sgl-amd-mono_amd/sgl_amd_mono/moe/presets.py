@@ -109,6 +109,10 @@ WORKLOADS = {
     "cfg3_tp4_mxfp4": dict(preset="dsv3_tp4_mxfp4", rows=(1, 8, 48)),
     "cfg4_tp4_mxfp4_zipf": dict(preset="dsv3_tp4_mxfp4", rows=(48,), zipf_s=1.2),
     "cfg5_tp2_mxfp4_norm": dict(preset="dsv3_tp2_mxfp4_norm", rows=(1, 8, 48)),
+    # parity stress cases: the Zipf skew on the other weight formats (experts picked by
+    # more rows than one gate_up token group holds)
+    "tp4_fp8_zipf": dict(preset="dsv3_tp4_fp8", rows=(16, 48), zipf_s=1.2),
+    "tp2_mxfp4_norm_zipf": dict(preset="dsv3_tp2_mxfp4_norm", rows=(48,), zipf_s=1.2),
 }
 
 

@@ -26,6 +26,9 @@ CASES = [
     ("cfg5_tp2_mxfp4_norm", 1),
     ("cfg5_tp2_mxfp4_norm", 8),
     ("cfg5_tp2_mxfp4_norm", 48),
+    ("tp4_fp8_zipf", 16),
+    ("tp4_fp8_zipf", 48),
+    ("tp2_mxfp4_norm_zipf", 48),
 ]
 _cache = {}
 
