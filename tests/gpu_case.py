@@ -34,7 +34,8 @@ class Case:
     parts: np.ndarray  # oracle router part sums [R, E, P]
     xin: torch.Tensor  # oracle normed (or raw) x, CPU bf16
     check: np.ndarray  # rows whose output the oracle computed
-    ref: torch.Tensor  # oracle output bf16 [len(check), H]
+    ref: torch.Tensor  # oracle output bf16 [len(check), H] (the kernel's arithmetic order)
+    golden: torch.Tensor  # the golden's fp32-matmul output bf16 [len(check), H]
 
 
 def _random_fill(shape, dtype, fmt, kind, device, g):
@@ -67,6 +68,7 @@ def build(workload: str, rows: int, seed: int = 0, device="cuda") -> Case:
     ex = gen.LazyExperts(p, seed)
     res = om.moe_partial(x[torch.from_numpy(check)], dense, p, experts=ex)
     assert np.array_equal(res["ids"], ids[check])
+    golden = om.moe_partial(x[torch.from_numpy(check)], dense, p, experts=ex, exact=False)["out"]
     g = torch.Generator(device=device).manual_seed(1234 + seed)
     dev = {}
     for name, (shape, dtype) in gen.expert_shapes(p).items():
@@ -87,7 +89,7 @@ def build(workload: str, rows: int, seed: int = 0, device="cuda") -> Case:
         norm=dense["norm"].to(device) if "norm" in dense else None,
         **dev,
     )
-    return Case(workload, preset, p, rows, x.to(device), w, ids, wts, parts, xin, check, res["out"])
+    return Case(workload, preset, p, rows, x.to(device), w, ids, wts, parts, xin, check, res["out"], golden)
 
 
 def errors(out: torch.Tensor, ref: torch.Tensor) -> dict:

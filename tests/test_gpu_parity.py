@@ -2,7 +2,8 @@
 
 Bars: router part sums, activation codes, expert ids, routing weights and the
 bf16 output bit for bit (the oracle restates the kernel's arithmetic order);
-the output also within max-abs 2e-2 and relative L2 1e-2; the persistent and
+the output also within max-abs 2e-2 and relative L2 1e-2 of both the oracle and
+the golden's fp32-matmul form (the reference's PyTorch path); the persistent and
 the staged launches bit for bit alike; repeated and graph-replayed launches
 bit for bit alike.
 """
@@ -97,6 +98,10 @@ def test_parity(workload, rows):
     assert e["max_abs"] <= MAX_ABS, e
     n_diff = int((got.view(torch.int16) != c.ref.view(torch.int16)).sum())
     assert n_diff == 0, f"{n_diff} output elements differ from the oracle's bits"
+    # and against the golden's own fp32 matmuls (the reference's PyTorch path, check_ffn.py:209-232)
+    g = errors(got, c.golden)
+    print(f"  out vs fp32-matmul golden: {g}", flush=True)
+    assert g["max_abs"] <= MAX_ABS and g["rel_l2"] <= REL_L2, g
 
 
 @pytest.mark.parametrize("workload,rows", [("cfg2_tp4_fp8", 8), ("cfg3_tp4_mxfp4", 8), ("cfg5_tp2_mxfp4_norm", 8)])
@@ -176,3 +181,27 @@ def test_host_validation_errors():
     bad = type(c.w)(**{**c.w.__dict__, "gate_w": c.w.gate_w.float()})
     with pytest.raises(RuntimeError, match="gate_w"):
         run.moe(bad, c.x)
+
+
+def test_golden_fixtures():
+    """The kernel against the committed golden vectors (tests/golden/), bit for bit."""
+    import sys
+    from pathlib import Path
+
+    sys.path.insert(0, str(Path(__file__).resolve().parent / "golden"))
+    import make_golden as mg
+
+    for workload, rows in mg.CASES:
+        f = np.load(mg.case_file(workload, rows))
+        c = _case(workload, rows)
+        assert np.array_equal(c.x.view(torch.int16).cpu().numpy(), f["x_bits"]), "seeded x"
+        run = _runner(c)
+        ids = torch.zeros(rows, c.p["topk"], dtype=torch.int32, device="cuda")
+        wts = torch.zeros(rows, c.p["topk"], dtype=torch.float32, device="cuda")
+        out = run.moe(c.w, c.x, topk_ids=ids, topk_w=wts)
+        torch.cuda.synchronize()
+        run.raise_on_device_error()
+        print(f"\n{workload} R={rows} golden", flush=True)
+        assert np.array_equal(ids.cpu().numpy(), f["ids"]), "expert ids"
+        assert np.array_equal(wts.cpu().numpy().view(np.uint32), f["weights_bits"]), "routing weights"
+        assert np.array_equal(out.view(torch.int16).cpu().numpy(), f["out_bits"]), "output bits"
