@@ -174,6 +174,30 @@ def cpu_baseline(workload: str, rows: int, budget_s: float = 25.0):
     }
 
 
+def calibrate_copy(mib: int, reps: int = 4) -> dict:
+    """A plain device-to-device copy of known size (torch's copy kernel), for scaling the
+    FETCH_SIZE / WRITE_SIZE counters of the MoE launch to bytes."""
+    import torch
+
+    n = mib << 20
+    src = torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"copy_bytes_read": n, "copy_bytes_written": n, "reps": reps}
+
+
+def measured_traffic(workload: str, rows: int):
+    """HBM bytes per launch from the committed counter passes (profiles/), or None."""
+    f = ROOT / "profiles" / f"traffic_{workload}_r{rows}.json"
+    if not f.exists():
+        return None, None
+    d = json.loads(f.read_text())
+    return d.get("hbm_bytes_per_launch"), f"profiles/{f.name}"
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -184,6 +208,8 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--staged", action="store_true", help="time the one-launch-per-stage variant")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain copy of MIB MiB (counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
@@ -197,6 +223,10 @@ def main() -> int:
 
     from sgl_amd_mono.moe.presets import PRESETS, WORKLOADS
     from sgl_amd_mono.moe.runner import MoeRunner
+
+    if args.calibrate_copy:
+        print(json.dumps(calibrate_copy(args.calibrate_copy)), flush=True)
+        return 0
 
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
@@ -257,6 +287,11 @@ def main() -> int:
             "traffic": None,
         },
     }
+    traffic, source = measured_traffic(args.workload, head)
+    if traffic is not None and not args.staged:
+        out["roofline"]["traffic"] = traffic
+        out["roofline"]["traffic_source"] = source
+        out["roofline"]["alg_bytes_per_launch"] = round(h["alg_MB_per_layer"] * 1e6)
     if not args.no_cpu:
         log("CPU baseline (oracle on the host cores)")
         out["cpu_baseline"] = cpu_baseline(args.workload, head)
