@@ -20,8 +20,9 @@ fixed order below, and this module restates it. A GEMV of a weight row w
    v = d * 2^(e_w + e_x - 254) (exact) with the E8M0 codes of the chunk.
 3. the row's chunks are dealt to LPR lanes, chunk c to lane c mod LPR; each
    lane sums its chunks in order from 0; the LPR lane sums are added as a
-   halving tree (lanes l and l + d, d = LPR/2 .. 1). LPR is 64 when the row
-   has a multiple of 64 chunks, else 32, 16 or 8 (the largest that divides).
+   halving tree (lanes l and l + d, d = LPR/2 .. 1). For the gate_up GEMVs
+   LPR is 64 when the row has a multiple of 64 chunks, else 32, 16 or 8 (the
+   largest that divides); the down GEMVs (routed and shared) use LPR = 8.
 
 SwiGLU uses silu(z) = fp32(z * sigmoid(z)) with the exact fp64 sigmoid of
 ``oracle.routing`` (the same steps as the routing's scores), not torch's silu.
@@ -40,7 +41,12 @@ from . import formats as fm
 from . import routing as rt
 
 
+# lanes a row of the down GEMVs (routed and shared): chunk c to lane c mod 8
+DOWN_LANES = 8
+
+
 def lanes_per_row(chunks: int) -> int:
+    """Lanes a row of the gate_up GEMVs: the largest of 64, 32, 16, 8 that divides the chunks."""
     for lpr in (64, 32, 16, 8):
         if chunks % lpr == 0:
             return lpr
@@ -68,10 +74,13 @@ def _chunk_sums(wv: np.ndarray, xv: np.ndarray, ce: int) -> np.ndarray:
     return d
 
 
-def _lanes(v: np.ndarray) -> np.ndarray:
-    """Deal chunks to lanes, sum each lane in order, then the halving tree -> [T, N]."""
+def _lanes(v: np.ndarray, lpr: int | None = None) -> np.ndarray:
+    """Deal chunks to lanes (lpr lanes a row, by default ``lanes_per_row``), sum each lane
+    in order, then the halving tree -> [T, N]."""
     t, n, c = v.shape
-    lpr = lanes_per_row(c)
+    lpr = lanes_per_row(c) if lpr is None else lpr
+    if c % lpr:
+        raise ValueError((c, lpr))
     v4 = v.reshape(t, n, c // lpr, lpr)
     a = np.zeros((t, n, lpr), np.float32)
     for i in range(c // lpr):
@@ -79,7 +88,7 @@ def _lanes(v: np.ndarray) -> np.ndarray:
     return _tree(a)
 
 
-def gemv_fp8_b128(wq: torch.Tensor, ws: torch.Tensor, xq: torch.Tensor, xs: torch.Tensor) -> np.ndarray:
+def gemv_fp8_b128(wq: torch.Tensor, ws: torch.Tensor, xq: torch.Tensor, xs: torch.Tensor, lpr: int | None = None) -> np.ndarray:
     """[N, K] e4m3 codes with fp32 [N/128, K/128] scales . [T, K] e4m3 codes with fp32 [T, K/128] -> [T, N]."""
     wv = fm.e4m3_to_f32(wq).numpy().astype(np.float32)
     xv = fm.e4m3_to_f32(xq).numpy().astype(np.float32)
@@ -90,16 +99,16 @@ def gemv_fp8_b128(wq: torch.Tensor, ws: torch.Tensor, xq: torch.Tensor, xs: torc
     blk = np.arange(k // 16) // 8  # the chunk's 128-wide K block
     rowblk = np.arange(n) // 128
     f = ws_[rowblk][:, blk][None, :, :] * xs_[:, blk][:, None, :]  # fp32(s_w * s_x)
-    return _lanes((d * f).astype(np.float32))
+    return _lanes((d * f).astype(np.float32), lpr)
 
 
-def gemv_mxfp4(wq: torch.Tensor, ws: torch.Tensor, xq: torch.Tensor, xs: torch.Tensor) -> np.ndarray:
+def gemv_mxfp4(wq: torch.Tensor, ws: torch.Tensor, xq: torch.Tensor, xs: torch.Tensor, lpr: int | None = None) -> np.ndarray:
     """[N, K/2] e2m1 with E8M0 [N, K/32] . [T, K] e4m3 codes with E8M0 [T, K/32] -> [T, N]."""
     wv = fm.fp4_unpack(wq).numpy().astype(np.float32)
     xv = fm.e4m3_to_f32(xq).numpy().astype(np.float32)
     d = _chunk_sums(wv, xv, 32)
     e = ws.view(torch.uint8).numpy().astype(np.int32)[None, :, :] + xs.view(torch.uint8).numpy().astype(np.int32)[:, None, :] - 254
-    return _lanes(np.ldexp(d, e).astype(np.float32))
+    return _lanes(np.ldexp(d, e).astype(np.float32), lpr)
 
 
 def silu_exact(z: np.ndarray) -> np.ndarray:

@@ -94,12 +94,12 @@ def _qdq_codes(x: torch.Tensor, fmt: str):
     return fm.group_fp8_quant(x, 128)
 
 
-def _gemv(wq, ws, xq, xs, fmt) -> np.ndarray:
+def _gemv(wq, ws, xq, xs, fmt, lpr=None) -> np.ndarray:
     from . import exact as ex
 
     if fmt == MXFP4:
-        return ex.gemv_mxfp4(wq, ws, xq, xs)
-    return ex.gemv_fp8_b128(wq, ws, xq, xs)
+        return ex.gemv_mxfp4(wq, ws, xq, xs, lpr)
+    return ex.gemv_fp8_b128(wq, ws, xq, xs, lpr)
 
 
 def moe_partial(x: torch.Tensor, w: dict, p: dict, experts=None, exact: bool = True):
@@ -140,7 +140,7 @@ def moe_partial(x: torch.Tensor, w: dict, p: dict, experts=None, exact: bool = T
             hh = _gemv(w13, w13_s, xq[rows], xs[rows], fmt)
             mid = ex.swiglu_routed(hh[:, :inter], hh[:, inter:], lim)
             mq, ms = _qdq_codes(torch.from_numpy(mid), fmt)
-            y = _gemv(w2, w2_s, mq, ms, fmt)
+            y = _gemv(w2, w2_s, mq, ms, fmt, ex.DOWN_LANES)
             per_k[rows, ks] = fm.bf(torch.from_numpy(y) * wts[rows, ks, None])
     else:
         xr = act_qdq(xin, fmt)
@@ -159,7 +159,7 @@ def moe_partial(x: torch.Tensor, w: dict, p: dict, experts=None, exact: bool = T
         hs = ex.gemv_fp8_b128(w["sgu"], w["sgu_s"], xq2, xs2)
         smid = ex.swiglu_shared(hs[:, :ish], hs[:, ish:], lim)
         smq, sms = fm.group_fp8_quant(torch.from_numpy(smid), 128)
-        shared = fm.bf(torch.from_numpy(ex.gemv_fp8_b128(w["sw2"], w["sw2_s"], smq, sms)))
+        shared = fm.bf(torch.from_numpy(ex.gemv_fp8_b128(w["sw2"], w["sw2_s"], smq, sms, ex.DOWN_LANES)))
     elif ish > 0:
         xs_ = act_qdq(xin, FP8_B128)
         hs = xs_ @ fm.deq_fp8_b128(w["sgu"], w["sgu_s"]).T

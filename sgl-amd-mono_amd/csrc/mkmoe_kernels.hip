@@ -75,9 +75,11 @@ using CfgTp4Fp4 = Cfg<7168, 256, 8, 8, 4, 512, 512, kFp4, 7, false>;
 using CfgTp2Fp4Norm = Cfg<7168, 256, 8, 8, 4, 1024, 1024, kFp4, 7, true>;
 
 // ---------------------------------------------------------------- workspace layout
+constexpr int kRegions = 11;
+
 struct Layout {
-  size_t off[10];
-  size_t size[10];
+  size_t off[kRegions];
+  size_t size[kRegions];
   size_t total;
 };
 
@@ -86,7 +88,7 @@ MKMOE_HD inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 MKMOE_HD inline Layout make_layout(int H, int E, int K, int I, int S, int fmt, int P, int norm,
                                    int rm) {
   Layout L;
-  size_t sz[10];
+  size_t sz[kRegions];
   sz[0] = norm ? (size_t)rm * H * 2 : 0;                              // x normed, bf16
   sz[1] = (size_t)rm * H;                                             // x codes, routed rule
   sz[2] = fmt == kFp4 ? (size_t)rm * (H / 32) : (size_t)rm * (H / 128) * 4;  // its scales
@@ -97,8 +99,9 @@ MKMOE_HD inline Layout make_layout(int H, int E, int K, int I, int S, int fmt, i
   sz[7] = (size_t)rm * K * 4;                                         // weights
   sz[8] = (size_t)rm * S * 2;                                         // shared mid, bf16
   sz[9] = (size_t)rm * K * I * 2;                                     // routed mid, bf16
+  sz[10] = (size_t)rm * H * 2;                                        // shared expert out, bf16
   size_t off = kCtlBytes;
-  for (int i = 0; i < 10; ++i) {
+  for (int i = 0; i < kRegions; ++i) {
     L.off[i] = off;
     L.size[i] = sz[i];
     off = align256(off + sz[i]);
@@ -133,7 +136,7 @@ struct Params {
   float limit;
   float eps;
   unsigned long long deadline;  // s_memrealtime ticks (100 MHz)
-  uint32_t off[10];
+  uint32_t off[kRegions];
 };
 
 // ---------------------------------------------------------------- small device helpers
@@ -156,6 +159,9 @@ __device__ __forceinline__ u32x4 dld128(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 }
 __device__ __forceinline__ uint32_t dld32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kAuxDev);
+}
+__device__ __forceinline__ uint32_t dld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, kAuxDev);
 }
 __device__ __forceinline__ uint32_t dld8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, kAuxDev);
@@ -234,8 +240,17 @@ __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
-__device__ __forceinline__ float silu(float z) { return z / (1.0f + __expf(-z)); }
 __device__ __forceinline__ float clampf(float v, float lim) { return fminf(fmaxf(v, -lim), lim); }
+
+// four e4m3 codes (a in the low byte) by the gfx950 convert after the clamp to +-448: for
+// every finite input the convert's nearest-even code equals e4m3_encode's (checked over all
+// finite fp32 on the device)
+__device__ __forceinline__ float clamp448(float v) { return v > kFp8Max ? kFp8Max : (v < -kFp8Max ? -kFp8Max : v); }
+__device__ __forceinline__ uint32_t e4m3_pack4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(clamp448(a), clamp448(b), 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(clamp448(c), clamp448(d), w, true);
+  return (uint32_t)w;
+}
 
 // 16 e4m3 weights . 16 e4m3 activations, unscaled
 __device__ __forceinline__ float dot16_fp8(u32x4 w, u32x4 x) {
@@ -282,7 +297,7 @@ __device__ __forceinline__ float dot32_fp4(u32x4 w, u32x4 xa, u32x4 xb) {
 }
 
 // ---------------------------------------------------------------- hand-offs
-__device__ void record_error(const Params& p, int stage) {
+__device__ __forceinline__ void record_error(const Params& p, int stage) {
   uint32_t* e = ctl(p) + kCtlErr;
   uint32_t prev = atomicCAS(&e[MKMOE_ERRW_CODE], 0u, (uint32_t)MKMOE_DEVERR_DEADLINE);
   if (prev == 0u) {
@@ -317,7 +332,7 @@ __device__ __forceinline__ void await_all(const Params& p, int which, uint32_t t
 }
 
 // the last workgroup out zeroes the counters for the next launch (graph replay safe)
-__device__ void leave(const Params& p) {
+__device__ __forceinline__ void leave(const Params& p) {
   __syncthreads();
   if (threadIdx.x == 0) {
     uint32_t n = __hip_atomic_fetch_add(ctl(p) + kCtlExit, 1u, __ATOMIC_RELAXED,
@@ -334,7 +349,7 @@ __device__ __forceinline__ int wave_slot(int b, int nwg) { return b + nwg * (int
 
 // ---------------------------------------------------------------- stage N: RMSNorm
 template <class C>
-__device__ void norm_row(const Params& p, int r, int lane) {
+__device__ __forceinline__ void norm_row(const Params& p, int r, int lane) {
 #pragma clang fp contract(off)
   constexpr int CH = C::CH512;
   const uint16_t* x = p.x + (size_t)r * C::H;
@@ -374,7 +389,7 @@ __device__ void norm_row(const Params& p, int r, int lane) {
 }
 
 template <class C>
-__device__ void stage_norm(const Params& p, int b, int nwg) {
+__device__ __forceinline__ void stage_norm(const Params& p, int b, int nwg) {
   const int lane = threadIdx.x & 63, gw = wave_slot(b, nwg);
   for (int r = gw; r < p.rows; r += nwg * kWaves) norm_row<C>(p, r, lane);
 }
@@ -399,7 +414,7 @@ struct RouterSmem {
 // 512-column chunk of the part in order (products rounded, then added), then the
 // wave's halving tree
 template <class C>
-__device__ void router_unit(const Params& p, RouterSmem<C>& sm, int part, int eb, int lane, int wave) {
+__device__ __forceinline__ void router_unit(const Params& p, RouterSmem<C>& sm, int part, int eb, int lane, int wave) {
 #pragma clang fp contract(off)
   constexpr int CPP = C::CH512 / C::P;
   constexpr int PW = RouterSmem<C>::PW;
@@ -442,7 +457,7 @@ __device__ void router_unit(const Params& p, RouterSmem<C>& sm, int part, int eb
 // quantize 512 columns of row r: group-128 fp8 (fp32 scale) and, for MXFP4
 // experts, MXFP8 per 32 ("aiter" rule)
 template <class C>
-__device__ void quant_unit(const Params& p, int r, int c, int lane) {
+__device__ __forceinline__ void quant_unit(const Params& p, int r, int c, int lane) {
 #pragma clang fp contract(off)
   const auto rs = ws_rsrc(p);
   u32x4 xv = x_load<C>(p, rs, r, c * 512 + lane * 8);
@@ -461,11 +476,8 @@ __device__ void quant_unit(const Params& p, int r, int c, int lane) {
   {
     float g = group_max<16>(am);
     float s = group_scale(g);
-    uint32_t lo = 0, hi = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) lo |= e4m3_encode(v[j] / s) << (8 * j);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) hi |= e4m3_encode(v[4 + j] / s) << (8 * j);
+    const uint32_t lo = e4m3_pack4(v[0] / s, v[1] / s, v[2] / s, v[3] / s);
+    const uint32_t hi = e4m3_pack4(v[4] / s, v[5] / s, v[6] / s, v[7] / s);
     const int rq = C::FMT == kFp4 ? 3 : 1, rsc = C::FMT == kFp4 ? 4 : 2;
     dst64(rs, p.off[rq] + col, u32x2{lo, hi});
     if ((lane & 15) == 0)
@@ -475,11 +487,8 @@ __device__ void quant_unit(const Params& p, int r, int c, int lane) {
     float g = group_max<4>(am);
     int code = mx_code(g);
     float inv = mx_inv(code);
-    uint32_t lo = 0, hi = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) lo |= e4m3_encode(v[j] * inv) << (8 * j);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) hi |= e4m3_encode(v[4 + j] * inv) << (8 * j);
+    const uint32_t lo = e4m3_pack4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+    const uint32_t hi = e4m3_pack4(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
     dst64(rs, p.off[1] + col, u32x2{lo, hi});
     if ((lane & 3) == 0)
       dst8(rs, p.off[2] + (uint32_t)r * (C::H / 32) + c * 16 + lane / 4, (uint8_t)code);
@@ -488,7 +497,7 @@ __device__ void quant_unit(const Params& p, int r, int c, int lane) {
 
 // workgroup units: (router K part, block of 8 experts), then one unit a row to quantize
 template <class C>
-__device__ void stage_a(const Params& p, RouterSmem<C>& sm, int b, int nwg) {
+__device__ __forceinline__ void stage_a(const Params& p, RouterSmem<C>& sm, int b, int nwg) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   constexpr int EB = (C::E + kWaves - 1) / kWaves;
   constexpr int n_router = C::P * EB;
@@ -504,7 +513,7 @@ __device__ void stage_a(const Params& p, RouterSmem<C>& sm, int b, int nwg) {
 
 // ---------------------------------------------------------------- stage B: routing
 template <class C>
-__device__ void route_row(const Params& p, int r, int lane) {
+__device__ __forceinline__ void route_row(const Params& p, int r, int lane) {
 #pragma clang fp contract(off)
   constexpr int EPL = (C::E + 63) / 64;
   const auto rs = ws_rsrc(p);
@@ -651,27 +660,10 @@ struct RowShape {
   static_assert(CPR % LPR == 0, "row chunks");
 };
 
-// activations of one row: e4m3 codes and their scales (fp32 per 128, or E8M0 per 32)
-struct DevAct {  // in the workspace (sc1 loads)
-  __amdgpu_buffer_rsrc_t rs;
-  uint32_t q;  // byte offset of the row's codes
-  uint32_t s;  // byte offset of the row's scales
-  __device__ __forceinline__ u32x4 q16(int off) const { return dld128(rs, q + off); }
-  __device__ __forceinline__ float sf(int i) const { return u2f(dld32(rs, s + i * 4)); }
-  __device__ __forceinline__ int se(int i) const { return (int)dld8(rs, s + i); }
-};
-struct LdsAct {  // in LDS
-  const uint8_t* q;
-  const void* s;
-  __device__ __forceinline__ u32x4 q16(int off) const { return *(const u32x4*)(q + off); }
-  __device__ __forceinline__ float sf(int i) const { return ((const float*)s)[i]; }
-  __device__ __forceinline__ int se(int i) const { return ((const uint8_t*)s)[i]; }
-};
-
 // NR weight rows (FP8 with fp32 128 x 128 scales, or MXFP4 with E8M0 per 32) in registers:
 // ``rows[r]`` is row r's first byte, ``srow[r]`` its scales (FP8: the row block's fp32
 // scales, one per 128 K; FP4: the row's E8M0 bytes)
-template <int FMT, int KD, int NR>
+template <int FMT, int KD, int NR, bool FP8_SCALES = true>
 struct WRows {
   using S = RowShape<FMT, KD>;
   static constexpr int RPG = NR / S::G;  // rows a sub-group
@@ -695,46 +687,15 @@ struct WRows {
 #pragma unroll
       for (int i = 0; i < S::CPL; ++i) {
         const int c = l + S::LPR * i;
-        if constexpr (FMT == kFp8) sf[q][i] = ((const float*)sr)[c / 8];
-        else se[q][i] = ((const uint8_t*)sr)[c];
+        if constexpr (FMT == kFp8) {
+          if constexpr (FP8_SCALES) sf[q][i] = ((const float*)sr)[c / 8];
+        } else {
+          se[q][i] = ((const uint8_t*)sr)[c];
+        }
       }
     }
   }
 
-  // this lane's sums of its rows against one activation row
-  template <class Act>
-  __device__ __forceinline__ void dot(const Act& x, int lane, float (&acc)[RPG]) const {
-#pragma clang fp contract(off)
-    const int l = lane % S::LPR;
-#pragma unroll
-    for (int q = 0; q < RPG; ++q) acc[q] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < S::CPL; ++i) {
-      const int c = l + S::LPR * i;
-      if constexpr (FMT == kFp8) {
-        const u32x4 xv = x.q16(c * 16);
-        const float sx = x.sf(c / 8);
-#pragma unroll
-        for (int q = 0; q < RPG; ++q) {
-          // opaque to the optimiser: the weight conversions stay inside the token loop
-          // (hoisted, the unit's weights as fp32 would not fit the register file)
-          u32x4 wq = w[q][i];
-          asm volatile("" : "+v"(wq));
-          const float f = sf[q][i] * sx;
-          acc[q] = acc[q] + dot16_fp8(wq, xv) * f;
-        }
-      } else {
-        const u32x4 xa = x.q16(c * 32), xb = x.q16(c * 32 + 16);
-        const int ex = x.se(c);
-#pragma unroll
-        for (int q = 0; q < RPG; ++q) {
-          u32x4 wq = w[q][i];
-          asm volatile("" : "+v"(wq));
-          acc[q] = acc[q] + ldexpf(dot32_fp4(wq, xa, xb), se[q][i] + ex - 254);
-        }
-      }
-    }
-  }
 };
 
 // silu(z) = z * sigmoid(z) with the exact fp64 sigmoid; the SwiGLU of a gate_up pair: the
@@ -759,35 +720,76 @@ constexpr int kTokGroup = 8;  // picks a gate_up unit takes at most
 template <class C>
 struct XTile {
   static constexpr int QS = C::H + 16;  // row stride (bank spread)
+  // fp32 block scales of an FP8 [2W][H] weight: (2W / 128) x (H / 128)
+  static constexpr int WSC = 2 * (C::I > C::S ? C::I : C::S) / 128 * (C::H / 128);
   uint8_t q[kTokGroup * QS];
   uint8_t s[kTokGroup * (C::H / 32)];  // E8M0 per 32, or fp32 per 128 (the same bytes)
+  float wsc[WSC];
 };
 
-// copy activation rows tok(p), p < np (codes at qoff + t H, scales at soff + t * sbytes)
-// from the workspace (sc1) into the tile; every thread of the workgroup takes part
-template <class C, class TokFn>
-__device__ void load_xtile(const Params& p, XTile<C>& xt, int np, uint32_t qoff, uint32_t soff,
-                           int sbytes, TokFn tok) {
-  const auto rs = ws_rsrc(p);
-  const int tid = threadIdx.x;
-  constexpr int QC = C::H / 16;  // 16-byte chunks a row
-  for (int i = tid; i < np * QC; i += kThreads) {
-    const int r = i / QC, c = i % QC;
-    *(u32x4*)(xt.q + r * XTile<C>::QS + c * 16) = dld128(rs, qoff + (uint32_t)tok(r) * C::H + c * 16);
+// the activation rows of a unit on their way to the tile: each thread's share of the codes
+// (16-byte chunks) and scale words, loaded (sc1) before the unit's weights so that writing
+// them to LDS waits for these loads alone
+template <class C>
+struct XRegs {
+  static constexpr int QC = C::H / 16;  // 16-byte chunks a row
+  static constexpr int NQ = (kTokGroup * QC + kThreads - 1) / kThreads;
+  static constexpr int SW = C::H / 128;  // 4-byte scale words a row (fp32 per 128, or E8M0 per 32)
+  static_assert(kTokGroup * SW <= kThreads, "one scale word a thread");
+  static constexpr int NW = (XTile<C>::WSC + kThreads - 1) / kThreads;
+  u32x4 q[NQ];
+  uint32_t s;
+  float w[NW];
+  int nw = 0;
+
+  // the FP8 weight's block scales, (2W / 128) x (H / 128) fp32 from ws (read-only input)
+  __device__ __forceinline__ void load_wscales(const float* ws, int W) {
+    nw = 2 * W / 128 * (C::H / 128);
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      const int idx = threadIdx.x + i * kThreads;
+      if (idx < nw) w[i] = ws[idx];
+    }
   }
-  const int sc = sbytes / 4;  // 4-byte words of a row's scales
-  for (int i = tid; i < np * sc; i += kThreads) {
-    const int r = i / sc, c = i % sc;
-    ((uint32_t*)xt.s)[r * sc + c] = dld32(rs, soff + (uint32_t)tok(r) * sbytes + c * 4);
+
+  // rows tok(r), r < np: codes at qoff + t H, scales at soff + t * SW * 4
+  template <class TokFn>
+  __device__ __forceinline__ void load(const Params& p, int np, uint32_t qoff, uint32_t soff, TokFn tok) {
+    const auto rs = ws_rsrc(p);
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int idx = tid + i * kThreads;
+      if (idx < np * QC) {
+        const int r = idx / QC, c = idx % QC;
+        q[i] = dld128(rs, qoff + (uint32_t)tok(r) * C::H + c * 16);
+      }
+    }
+    if (tid < np * SW) s = dld32(rs, soff + (uint32_t)tok(tid / SW) * (SW * 4) + (tid % SW) * 4);
   }
-}
+
+  __device__ __forceinline__ void store(XTile<C>& xt, int np) const {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int idx = tid + i * kThreads;
+      if (idx < np * QC) *(u32x4*)(xt.q + (idx / QC) * XTile<C>::QS + (idx % QC) * 16) = q[i];
+    }
+    if (tid < np * SW) ((uint32_t*)xt.s)[tid] = s;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      const int idx = tid + i * kThreads;
+      if (idx < nw) xt.wsc[idx] = w[i];
+    }
+  }
+};
 
 // gate_up of one intermediate column (rows j and W + j of a [2W][H] weight) against the np
 // activation rows of an XTile: chunk-outer, pick-inner (the weights convert once a chunk);
 // the per-(row, pick) arithmetic is the canonical order of WRows. -> g[p], u[p] in every lane
 template <int FMT, int H>
 struct GateUpCol {
-  using R = WRows<FMT, H, 2>;
+  using R = WRows<FMT, H, 2, false>;
   using S = typename R::S;
   R wr;
 
@@ -806,16 +808,18 @@ struct GateUpCol {
         lane);
   }
 
-  template <int QS>
-  __device__ __forceinline__ void run(const uint8_t* xq, const uint8_t* xs, int np, int lane,
-                                      float (&g)[kTokGroup], float (&u)[kTokGroup]) const {
+  // NPB: the picks the code is unrolled for (np <= NPB)
+  // wsc: the FP8 weight's block scales ((2W / 128) x (H / 128)); j: this column
+  template <int QS, int NPB>
+  __device__ __forceinline__ void run(const uint8_t* xq, const uint8_t* xs, const float* wsc, int W, int j,
+                                      int np, int lane, float (&g)[kTokGroup], float (&u)[kTokGroup]) const {
 #pragma clang fp contract(off)
     const int l = lane % S::LPR;
-    float acc[R::RPG][kTokGroup];
+    float acc[R::RPG][NPB];
 #pragma unroll
     for (int q = 0; q < R::RPG; ++q)
 #pragma unroll
-      for (int p = 0; p < kTokGroup; ++p) acc[q][p] = 0.0f;
+      for (int p = 0; p < NPB; ++p) acc[q][p] = 0.0f;
 #pragma unroll
     for (int i = 0; i < S::CPL; ++i) {
       const int c = l + S::LPR * i;
@@ -837,7 +841,7 @@ struct GateUpCol {
           }
         }
 #pragma unroll
-        for (int p = 0; p < kTokGroup; ++p) {
+        for (int p = 0; p < NPB; ++p) {
           if (p < np) {
             const u32x4 xv = *(const u32x4*)(xq + p * QS + c * 16);
             const float sx = ((const float*)xs)[p * (H / 128) + c / 8];
@@ -857,7 +861,8 @@ struct GateUpCol {
               float d = 0.0f;
 #pragma unroll
               for (int k = 0; k < 16; ++k) d = fmaf(wf[q][k], xf[k], d);
-              const float f = wr.sf[q][i] * sx;
+              static_assert(FMT != kFp8 || S::G == 1, "FP8 gate and up rows in every lane");
+              const float f = wsc[((q == 0 ? j : W + j) / 128) * (H / 128) + c / 8] * sx;
               acc[q][p] = acc[q][p] + d * f;
             }
           }
@@ -886,7 +891,7 @@ struct GateUpCol {
           }
         }
 #pragma unroll
-        for (int p = 0; p < kTokGroup; ++p) {
+        for (int p = 0; p < NPB; ++p) {
           if (p < np) {
             const u32x4 xa = *(const u32x4*)(xq + p * QS + c * 32);
             const u32x4 xb = *(const u32x4*)(xq + p * QS + c * 32 + 16);
@@ -914,7 +919,7 @@ struct GateUpCol {
       }
     }
 #pragma unroll
-    for (int p = 0; p < kTokGroup; ++p) {
+    for (int p = 0; p < NPB; ++p) {
       if (p < np) {
         if constexpr (S::G == 1) {
           g[p] = lane_value(tree_sum<64>(acc[0][p]), 0);
@@ -950,77 +955,83 @@ __device__ __forceinline__ float lane_pick(const float (&a)[kTokGroup]) {
   return v;
 }
 
-// columns per gate_up workgroup unit: the smallest power of two >= 8 that still leaves
-// about two units a workgroup
-__device__ __forceinline__ int gu_block(int groups, int width, int nwg) {
-  int cb = 8;
-  while (cb < 64 && groups * (width / (2 * cb)) >= 2 * nwg) cb *= 2;
-  return cb;
-}
-
 // one workgroup unit: columns [c0, c0 + cb) of a [2W][H] weight for np activation rows;
-// wave w takes columns c0 + w, c0 + w + 8, ...: its first column's weights are requested
-// before load_x() stages the rows in the tile, and every next column's weights load while
-// it computes the current one; emit(p, column, g, u) runs in lane p (p < np)
+// wave w takes columns c0 + w, c0 + w + 8, ... with two column buffers in turn. The
+// activation rows are requested first (load_x fills an XRegs), then both buffers' first
+// columns, so the rows reach the tile without waiting for the weights; a buffer's next
+// column is requested as soon as it is computed, so the other's loads stay in flight
+// while a wave waits; emit(p, column, g, u) runs in lane p (p < np)
 template <class C, int FMT, class WFn, class XFn, class EmitFn>
-__device__ void gu_unit(const Params& p, XTile<C>& xt, int np, int W, int c0, int cb, WFn weights,
+__device__ __forceinline__ void gu_unit(const Params& p, XTile<C>& xt, int np, int W, int c0, int cb, WFn weights,
                         XFn load_x, EmitFn emit) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   using GU = GateUpCol<FMT, C::H>;
   const uint8_t* wb;
   const void* sb;
   weights(wb, sb);
-  int col = c0 + wave;
   const int end = c0 + cb;
-  GU cur;
-  if (col < end) cur.load(wb, sb, W, col, lane);
+  int ca = c0 + wave, cx = ca + kWaves;
+  XRegs<C> xr;
+  load_x(xr);
+  if constexpr (FMT == kFp8) xr.load_wscales((const float*)sb, W);
+  GU a, x;
+  if (ca < end) a.load(wb, sb, W, ca, lane);
+  if (cx < end) x.load(wb, sb, W, cx, lane);
   __syncthreads();  // the previous unit is done with the tile
-  load_x();
+  xr.store(xt, np);
   __syncthreads();
-  if (col >= end) return;
-  while (true) {
-    const int nxt_col = col + kWaves;
-    GU nxt;
-    if (nxt_col < end) nxt.load(wb, sb, W, nxt_col, lane);
+  auto step = [&](GU& buf, int& col) {
     float g[kTokGroup] = {}, u[kTokGroup] = {};
-    cur.template run<XTile<C>::QS>(xt.q, xt.s, np, lane, g, u);
-    {
-      const float gl = lane_pick(g), ul = lane_pick(u);
-      if (lane < np) emit(lane, col, gl, ul);
-    }
-    if (nxt_col >= end) break;
-    cur = nxt;
-    col = nxt_col;
+    buf.template run<XTile<C>::QS, kTokGroup>(xt.q, xt.s, xt.wsc, W, col, np, lane, g, u);
+    const float gl = lane_pick(g), ul = lane_pick(u);
+    if (lane < np) emit(lane, col, gl, ul);
+    col += 2 * kWaves;
+    if (col < end) buf.load(wb, sb, W, col, lane);
+  };
+  while (ca < end) {
+    step(a, ca);
+    if (cx >= end) break;
+    step(x, cx);
   }
 }
 
+// this workgroup's share [lo, hi) of n items dealt evenly over nwg workgroups
+__device__ __forceinline__ void even_share(int n, int b, int nwg, int& lo, int& hi) {
+  lo = (int)((long long)n * b / nwg);
+  hi = (int)((long long)n * (b + 1) / nwg);
+}
+
 // ---------------------------------------------------------------- stage B: routing + shared gate_up
+// routing: a wave per row (wave 0 of workgroups 0 .. R-1); the shared expert's gate_up: its
+// (8-row group, column) pairs dealt evenly over the other workgroups, each share run as one
+// or two units of consecutive columns of one group
 template <class C>
-__device__ void stage_b(const Params& p, XTile<C>& xt, int b, int nwg) {
+__device__ __forceinline__ void stage_b(const Params& p, XTile<C>& xt, int b, int nwg) {
   const int lane = threadIdx.x & 63, gw = wave_slot(b, nwg);
   for (int u = gw; u < p.rows; u += nwg * kWaves) route_row<C>(p, u, lane);
-  // shared expert: workgroup units (token group, column block), placed after the routing rows
   const int groups = (p.rows + kTokGroup - 1) / kTokGroup;
-  const int cb = gu_block(groups, C::S, nwg);
-  const int nblk = C::S / cb;
-  const int n = groups * nblk;
-  const int first = (b - min(p.rows, nwg) % nwg + nwg) % nwg;  // routing workgroups go last
+  const int nr = min(p.rows, nwg / 2);  // workgroups that route a row take no shared columns
+  if (b < nr) return;
+  int lo, hi;
+  even_share(groups * C::S, b - nr, nwg - nr, lo, hi);
   const auto rs = ws_rsrc(p);
   const uint32_t qoff = C::FMT == kFp4 ? p.off[3] : p.off[1];
   const uint32_t soff = C::FMT == kFp4 ? p.off[4] : p.off[2];
-  for (int wu = first; wu < n; wu += nwg) {
-    const int tg = wu / nblk, blk = wu % nblk;
+  for (int pos = lo; pos < hi;) {
+    const int tg = pos / C::S, c0 = pos % C::S;
+    const int c1 = min(C::S, c0 + (hi - pos));
     const int t0 = tg * kTokGroup, np = min(kTokGroup, p.rows - t0);
     gu_unit<C, kFp8>(
-        p, xt, np, C::S, blk * cb, cb,
+        p, xt, np, C::S, c0, c1 - c0,
         [&](const uint8_t*& w, const void*& s) {
           w = p.sgu;
           s = p.sgu_s;
         },
-        [&]() { load_xtile<C>(p, xt, np, qoff, soff, (C::H / 128) * 4, [&](int r) { return t0 + r; }); },
+        [&](XRegs<C>& xr) { xr.load(p, np, qoff, soff, [&](int r) { return t0 + r; }); },
         [&](int q, int col, float g, float u) {
           dst16(rs, p.off[8] + ((uint32_t)(t0 + q) * C::S + col) * 2, f2bf(swiglu_shared(g, u, p.limit)));
         });
+    pos += c1 - c0;
   }
 }
 
@@ -1036,14 +1047,19 @@ struct Union {
   int tg_slot[kRowsMax * C::K];  // a token group's slot
   int picks[kRowsMax * C::K];
   float wts[kRowsMax * C::K];
+  int tg_cost[kRowsMax * C::K + 1];  // gate_up cost of the token groups before g, a column
   int n;
   int ntg;
 };
 
+// a gate_up column's cost: its weight loads plus its picks' arithmetic (one per pick)
+template <class C>
+constexpr int kColCost = C::FMT == kFp4 ? 2 : 3;
+
 // experts picked by any row (ascending id), their picks (pick = row * K + k; a slot's picks
 // in row order, the same in every workgroup) and token groups
 template <class C>
-__device__ void build_union(const Params& p, Union<C>& un) {
+__device__ __forceinline__ void build_union(const Params& p, Union<C>& un) {
   static_assert(kRowsMax <= 64, "row bitmaps");
   const int tid = threadIdx.x;
   const int npk = p.rows * C::K;
@@ -1118,65 +1134,197 @@ __device__ void build_union(const Params& p, Union<C>& un) {
     const int pos = un.cnt[e] + __popc(un.rows_of[e][0] & below0) + __popc(un.rows_of[e][1] & below1);
     un.picks[min(pos, npk - 1)] = t;
   }
+  // each token group's cost a column, prefix-summed over the groups
+  if (tid < 64) {
+    constexpr int GPL = (kRowsMax * C::K + 63) / 64;  // groups a lane
+    const int ntg = un.ntg;
+    int loc[GPL];
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < GPL; ++i) {
+      const int g = tid * GPL + i;
+      int c = 0;
+      if (g < ntg) {
+        const int sl = un.tg_slot[g];
+        const int j0 = un.slot_start[sl] + (g - un.tg_start[sl]) * kTokGroup;
+        c = kColCost<C> + min(kTokGroup, un.slot_start[sl + 1] - j0);
+      }
+      loc[i] = c;
+      sum += c;
+    }
+    int inc = sum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(inc, d);
+      if (tid >= d) inc += o;
+    }
+    int run = inc - sum;
+#pragma unroll
+    for (int i = 0; i < GPL; ++i) {
+      const int g = tid * GPL + i;
+      if (g < ntg) un.tg_cost[g] = run;
+      run += loc[i];
+    }
+    if (tid == 63) un.tg_cost[ntg] = inc;
+  }
   __syncthreads();
 }
 
-// ---------------------------------------------------------------- stage C: routed gate_up
-// workgroup units (token group, column block): a slot's picks, kTokGroup at a time, against
-// a block of intermediate columns; the picks' activation rows are staged in LDS once a unit
-template <class C>
-__device__ void stage_c(const Params& p, const Union<C>& un, XTile<C>& xt, int b, int nwg) {
-  const int cb = gu_block(un.ntg, C::I, nwg);
-  const int nblk = C::I / cb;
-  const int n = un.ntg * nblk;
-  const auto rs = ws_rsrc(p);
-  constexpr int SB = C::FMT == kFp4 ? C::H / 32 : (C::H / 128) * 4;  // scale bytes of a row
-  for (int wu = b; wu < n; wu += nwg) {
-    const int tgg = wu / nblk, blk = wu % nblk;
-    const int slot = un.tg_slot[tgg];
-    const int e = un.slot_e[slot];
-    const int j0 = un.slot_start[slot] + (tgg - un.tg_start[slot]) * kTokGroup;
-    const int np = min(kTokGroup, un.slot_start[slot + 1] - j0);
-    gu_unit<C, C::FMT>(
-        p, xt, np, C::I, blk * cb, cb,
-        [&](const uint8_t*& w, const void*& s) {
-          if constexpr (C::FMT == kFp8) {
-            w = p.w13 + (size_t)e * 2 * C::I * C::H;
-            s = (const float*)p.w13_s + (size_t)e * (2 * C::I / 128) * (C::H / 128);
-          } else {
-            w = p.w13 + (size_t)e * 2 * C::I * (C::H / 2);
-            s = (const uint8_t*)p.w13_s + (size_t)e * 2 * C::I * (C::H / 32);
+// ---------------------------------------------------------------- down GEMVs (8 lanes a row)
+// A down unit is 8 weight rows of KD elements, one a group of 8 lanes: lane l of group g
+// holds chunks l, l + 8, ... of row g (16-byte loads, so every load instruction reads eight
+// 128-byte runs). The order is the fixed GEMV order with 8 lanes a row: each chunk's exact
+// products summed in element order and scaled, a lane's chunks summed in order, then the
+// 8 lanes' halving tree.
+constexpr int kDownLanes = 8;
+constexpr int kPickBlock = 4;  // picks a down unit computes per pass over its chunks
+
+template <int FMT, int KD>
+struct DownRows {
+  static constexpr int CE = FMT == kFp4 ? 32 : 16;  // elements a chunk
+  static constexpr int CPR = KD / CE;
+  static constexpr int CPL = CPR / kDownLanes;
+  static_assert(CPR % kDownLanes == 0, "down row chunks");
+  u32x4 w[CPL];
+  float sf[CPL];
+  int se[CPL];
+
+  // this lane's row (w: its first byte, s: its scales: FP8 the row block's fp32 scales,
+  // one per 128 K; FP4 its E8M0 bytes); ok false: the row is past the tile
+  __device__ __forceinline__ void load(const uint8_t* r, const void* s, bool ok, int l) {
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) w[i] = ok ? ld16_nt(r + (l + kDownLanes * i) * 16) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = l + kDownLanes * i;
+      if constexpr (FMT == kFp8) sf[i] = ok ? ((const float*)s)[c / 8] : 0.0f;
+      else se[i] = ok ? (int)((const uint8_t*)s)[c] : 0;
+    }
+  }
+
+  // acc[q] = this lane's sum for pick q < np of the LDS activation rows xq + q * QS
+  // (codes) and xs + q * SST (scales: fp32 per 128, or E8M0 bytes per 32)
+  template <int QS, int SST>
+  __device__ __forceinline__ void dot(const uint8_t* xq, const uint8_t* xs, int np, int l,
+                                      float (&acc)[kPickBlock]) const {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int q = 0; q < kPickBlock; ++q) acc[q] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = l + kDownLanes * i;
+      u32x4 wq = w[i];
+      asm volatile("" : "+v"(wq));
+      const uint32_t wv[4] = {wq.x, wq.y, wq.z, wq.w};
+      if constexpr (FMT == kFp8) {
+        float wf[16];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)wv[k], false);
+          auto b = __builtin_amdgcn_cvt_pk_f32_fp8((int)wv[k], true);
+          wf[4 * k] = a[0];
+          wf[4 * k + 1] = a[1];
+          wf[4 * k + 2] = b[0];
+          wf[4 * k + 3] = b[1];
+        }
+#pragma unroll
+        for (int q = 0; q < kPickBlock; ++q) {
+          if (q < np) {
+            const u32x4 xv = *(const u32x4*)(xq + q * QS + c * 16);
+            const float sx = ((const float*)(xs + q * SST))[c / 8];
+            const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+            float d = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)xw[k], false);
+              auto b = __builtin_amdgcn_cvt_pk_f32_fp8((int)xw[k], true);
+              d = fmaf(wf[4 * k], a[0], d);
+              d = fmaf(wf[4 * k + 1], a[1], d);
+              d = fmaf(wf[4 * k + 2], b[0], d);
+              d = fmaf(wf[4 * k + 3], b[1], d);
+            }
+            acc[q] = acc[q] + d * (sf[i] * sx);
           }
-        },
-        [&]() { load_xtile<C>(p, xt, np, p.off[1], p.off[2], SB, [&](int r) { return un.picks[j0 + r] / C::K; }); },
-        [&](int q, int col, float g, float u) {
-          const int pk = un.picks[j0 + q];
-          dst16(rs, p.off[9] + ((uint32_t)pk * C::I + col) * 2, f2bf(swiglu_routed(g, u, p.limit)));
-        });
+        }
+      } else {
+        float wf[32];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          auto a = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wv[k], 1.0f, 0);
+          auto b = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wv[k], 1.0f, 1);
+          auto c2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wv[k], 1.0f, 2);
+          auto d2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wv[k], 1.0f, 3);
+          wf[8 * k] = a[0];
+          wf[8 * k + 1] = a[1];
+          wf[8 * k + 2] = b[0];
+          wf[8 * k + 3] = b[1];
+          wf[8 * k + 4] = c2[0];
+          wf[8 * k + 5] = c2[1];
+          wf[8 * k + 6] = d2[0];
+          wf[8 * k + 7] = d2[1];
+        }
+#pragma unroll
+        for (int q = 0; q < kPickBlock; ++q) {
+          if (q < np) {
+            const u32x4 xa = *(const u32x4*)(xq + q * QS + c * 32);
+            const u32x4 xb = *(const u32x4*)(xq + q * QS + c * 32 + 16);
+            const int ex = xs[q * SST + c];
+            const uint32_t xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+            float d = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)xw[k], false);
+              auto b = __builtin_amdgcn_cvt_pk_f32_fp8((int)xw[k], true);
+              d = fmaf(wf[4 * k], a[0], d);
+              d = fmaf(wf[4 * k + 1], a[1], d);
+              d = fmaf(wf[4 * k + 2], b[0], d);
+              d = fmaf(wf[4 * k + 3], b[1], d);
+            }
+            acc[q] = acc[q] + ldexpf(d, se[i] + ex - 254);
+          }
+        }
+      }
+    }
+  }
+};
+
+// units v = wave, wave + 8, ... < n in batches of B (32 KB of an 8-row unit's weights a
+// wave a batch at most): a batch's loads are issued together and computed once all have
+// arrived, then the next batch is requested. (Two batches in flight per wave stream the
+// down rows at half the rate: measured on this pattern, 3.1 against 6.5 TB/s.) The first
+// batch may be requested ahead by the caller (first(rows)) before other work.
+template <class Rows>
+struct DownBatch {
+  static constexpr int B = Rows::CPL >= 8 ? 4 : 8;
+  Rows r[B];
+  int v0;
+  template <class LoadFn>
+  __device__ __forceinline__ void load(int v, int n, LoadFn load_unit) {
+    v0 = v;
+#pragma unroll
+    for (int k = 0; k < B; ++k)
+      if (v + kWaves * k < n) load_unit(v + kWaves * k, r[k]);
+  }
+};
+
+// run units v = wave, wave + 8, ... < n from a batch already requested for v = wave
+template <class Rows, class LoadFn, class WorkFn>
+__device__ __forceinline__ void down_pipeline(DownBatch<Rows>& bt, int n, LoadFn load, WorkFn work) {
+  constexpr int B = DownBatch<Rows>::B;
+  while (bt.v0 < n) {
+#pragma unroll
+    for (int k = 0; k < B; ++k)
+      if (bt.v0 + kWaves * k < n) work(bt.v0 + kWaves * k, bt.r[k]);
+    const int v1 = bt.v0 + kWaves * B;
+    if (v1 >= n) break;
+    bt.load(v1, n, load);
   }
 }
-
-// ---------------------------------------------------------------- stage D: down + combine
-template <class C>
-struct DownSmem {
-  float contrib[kRowsMax * C::K * kTileMax];
-  float ysh[kRowsMax * kTileMax];
-  union {
-    struct {
-      uint8_t q[kRowsMax * C::SQS];
-      float s[kRowsMax * (C::S / 128)];
-    } sh;
-    struct {
-      uint8_t q[C::PB * C::MQS];
-      uint8_t s[C::PB * C::MSC * 4];
-    } mid;
-  } u;
-};
 
 // quantize bf16 rows [n][W] (workspace, sc1) into LDS codes [n][QS] and scales: group-128 fp8
 // (fp32 scales) or MXFP8 (E8M0 bytes); row i of the source starts at byte ``src_row(i)``
 template <int FMT, int W, int QS, class RowFn>
-__device__ void quant_rows_lds(const Params& p, RowFn src_row, int n, uint8_t* q, void* s) {
+__device__ __forceinline__ void quant_rows_lds(const Params& p, RowFn src_row, int n, uint8_t* q, void* s) {
 #pragma clang fp contract(off)
   constexpr int PER = W / 8;  // 8-value chunks a row
   const int tid = threadIdx.x;
@@ -1206,11 +1354,8 @@ __device__ void quant_rows_lds(const Params& p, RowFn src_row, int n, uint8_t* q
     if constexpr (FMT == kFp8) {
       float g = group_max<16>(am);
       float sc = group_scale(g);
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) lo |= e4m3_encode(v[k] / sc) << (8 * k);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) hi |= e4m3_encode(v[4 + k] / sc) << (8 * k);
+      const uint32_t lo = e4m3_pack4(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
+      const uint32_t hi = e4m3_pack4(v[4] / sc, v[5] / sc, v[6] / sc, v[7] / sc);
       if (ok) {
         *(u32x2*)(q + (size_t)i * QS + c * 8) = u32x2{lo, hi};
         if ((c & 15) == 0) ((float*)s)[i * (W / 128) + c / 16] = sc;
@@ -1219,11 +1364,8 @@ __device__ void quant_rows_lds(const Params& p, RowFn src_row, int n, uint8_t* q
       float g = group_max<4>(am);
       int code = mx_code(g);
       float inv = mx_inv(code);
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) lo |= e4m3_encode(v[k] * inv) << (8 * k);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) hi |= e4m3_encode(v[4 + k] * inv) << (8 * k);
+      const uint32_t lo = e4m3_pack4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+      const uint32_t hi = e4m3_pack4(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
       if (ok) {
         *(u32x2*)(q + (size_t)i * QS + c * 8) = u32x2{lo, hi};
         if ((c & 3) == 0) ((uint8_t*)s)[i * (W / 32) + c / 4] = (uint8_t)code;
@@ -1232,127 +1374,181 @@ __device__ void quant_rows_lds(const Params& p, RowFn src_row, int n, uint8_t* q
   }
 }
 
-constexpr int kDownBatch = 8;  // down units a wave requests at once
+// row blocks of 8 in a down tile (rows past the tile masked)
+constexpr int kRowBlocks = kTileMax / kDownLanes;
 
-// the down rows of a tile: units of G rows (one wave load); a wave takes units v = wave,
-// wave + 8, ... in batches of kDownBatch, the next batch's loads in flight while it
-// computes the current one. row_of(v, i, w, s) sets row i's (i < G) first byte and scales
-// for unit v; work(v, rows) runs it.
-template <int FMT, int KD, class RowFn, class WorkFn>
-__device__ __forceinline__ void down_units(int n_units, RowFn row_of, WorkFn work) {
-  using S = RowShape<FMT, KD>;
-  using W = WRows<FMT, KD, S::G>;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  constexpr int kStep = kWaves * kDownBatch;
-  auto load = [&](W (&wr)[kDownBatch], int v0) {
-#pragma unroll
-    for (int b = 0; b < kDownBatch; ++b) {
-      const int v = v0 + kWaves * b;
-      if (v < n_units)
-        wr[b].load([&](int i, const uint8_t*& r, const void*& sr) { row_of(v, i, r, sr); }, lane);
-    }
+// ---------------------------------------------------------------- stage C: shared down + routed gate_up
+template <class C>
+struct SharedDownSmem {
+  uint8_t q[kRowsMax * C::SQS];
+  float s[kRowsMax * (C::S / 128)];
+};
+
+// the shared expert's down GEMV for tile rows [h0, h0 + hn) of every row: units (8-row
+// block, block of kPickBlock rows); bf16 results to the workspace
+template <class C>
+__device__ __forceinline__ void shared_down_tile(const Params& p, SharedDownSmem<C>& sm, int h0, int hn) {
+  const int lane = threadIdx.x & 63, g = lane / kDownLanes, l = lane % kDownLanes;
+  const int R = p.rows;
+  const auto rs = ws_rsrc(p);
+  __syncthreads();  // the previous user of the LDS is done
+  quant_rows_lds<kFp8, C::S, C::SQS>(
+      p, [&](int i) { return p.off[8] + (uint32_t)i * C::S * 2; }, R, sm.q, sm.s);
+  __syncthreads();
+  using DR = DownRows<kFp8, C::S>;
+  const int npb = (R + kPickBlock - 1) / kPickBlock;
+  auto load = [&](int v, DR& wr) {
+    const int rb = v % kRowBlocks;
+    const int h = h0 + rb * kDownLanes + g;
+    const bool ok = rb * kDownLanes + g < hn;
+    wr.load(p.sw2 + (size_t)h * C::S, p.sw2_s + (size_t)(h / 128) * (C::S / 128), ok, l);
   };
-  int v0 = wave;
-  if (v0 >= n_units) return;
-  W cur[kDownBatch];
-  load(cur, v0);
-  while (true) {
-    const int v1 = v0 + kStep;
-    W nxt[kDownBatch];
-    if (v1 < n_units) load(nxt, v1);
+  DownBatch<DR> bt;
+  bt.load(threadIdx.x >> 6, kRowBlocks * npb, load);
+  down_pipeline<DR>(bt, kRowBlocks * npb, load, [&](int v, const DR& wr) {
+    const int rb = v % kRowBlocks, pb = v / kRowBlocks;
+    if (rb * kDownLanes >= hn) return;
+    const int t0 = pb * kPickBlock, np = min(kPickBlock, R - t0);
+    float acc[kPickBlock];
+    wr.template dot<C::SQS, (C::S / 128) * 4>(sm.q + (size_t)t0 * C::SQS, (const uint8_t*)(sm.s + t0 * (C::S / 128)), np, l, acc);
+    const int hl = rb * kDownLanes + g;
 #pragma unroll
-    for (int b = 0; b < kDownBatch; ++b) {
-      const int v = v0 + kWaves * b;
-      if (v < n_units) work(v, cur[b]);
+    for (int q = 0; q < kPickBlock; ++q) {
+      const float y = tree_sum<kDownLanes>(acc[q]);
+      if (q < np && l == 0 && hl < hn)
+        dst16(rs, p.off[10] + ((uint32_t)(t0 + q) * C::H + h0 + hl) * 2, f2bf(y));
     }
-    if (v1 >= n_units) break;
-#pragma unroll
-    for (int b = 0; b < kDownBatch; ++b) cur[b] = nxt[b];
-    v0 = v1;
+  });
+}
+
+// routed gate_up: the (token group, column) pairs of the step dealt over the workgroups in
+// equal shares of cost (a column costs its loads plus one per pick: kColCost + picks);
+// column j of group g belongs to the share holding its first cost unit
+template <class C>
+__device__ __forceinline__ void routed_gate_up(const Params& p, const Union<C>& un, XTile<C>& xt, int b, int nwg) {
+  const long long total = (long long)un.tg_cost[un.ntg] * C::I;
+  const long long lo = total * b / nwg, hi = total * (b + 1) / nwg;
+  const auto rs = ws_rsrc(p);
+  // the last group that starts at or before lo
+  int gl = 0, gh = un.ntg - 1;
+  while (gl < gh) {
+    const int mid = (gl + gh + 1) >> 1;
+    if ((long long)un.tg_cost[mid] * C::I <= lo) gl = mid; else gh = mid - 1;
+  }
+  for (int tgg = gl; tgg < un.ntg && (long long)un.tg_cost[tgg] * C::I < hi; ++tgg) {
+    const long long base = (long long)un.tg_cost[tgg] * C::I;
+    const int cg = un.tg_cost[tgg + 1] - un.tg_cost[tgg];
+    const int c0 = lo > base ? (int)min((lo - base + cg - 1) / cg, (long long)C::I) : 0;
+    const int c1 = (int)min((hi - base + cg - 1) / cg, (long long)C::I);
+    if (c1 <= c0) continue;
+    const int slot = un.tg_slot[tgg];
+    const int e = un.slot_e[slot];
+    const int j0 = un.slot_start[slot] + (tgg - un.tg_start[slot]) * kTokGroup;
+    const int np = min(kTokGroup, un.slot_start[slot + 1] - j0);
+    gu_unit<C, C::FMT>(
+        p, xt, np, C::I, c0, c1 - c0,
+        [&](const uint8_t*& w, const void*& s) {
+          if constexpr (C::FMT == kFp8) {
+            w = p.w13 + (size_t)e * 2 * C::I * C::H;
+            s = (const float*)p.w13_s + (size_t)e * (2 * C::I / 128) * (C::H / 128);
+          } else {
+            w = p.w13 + (size_t)e * 2 * C::I * (C::H / 2);
+            s = (const uint8_t*)p.w13_s + (size_t)e * 2 * C::I * (C::H / 32);
+          }
+        },
+        [&](XRegs<C>& xr) { xr.load(p, np, p.off[1], p.off[2], [&](int r) { return un.picks[j0 + r] / C::K; }); },
+        [&](int q, int col, float g, float u) {
+          const int pk = un.picks[j0 + q];
+          dst16(rs, p.off[9] + ((uint32_t)pk * C::I + col) * 2, f2bf(swiglu_routed(g, u, p.limit)));
+        });
   }
 }
 
 template <class C>
-__device__ void down_tile(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn) {
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int R = p.rows;
-  // ---- shared expert: quantize SMID (every row) into LDS, then its down rows
-  quant_rows_lds<kFp8, C::S, C::SQS>(
-      p, [&](int i) { return p.off[8] + (uint32_t)i * C::S * 2; }, R, sm.u.sh.q, sm.u.sh.s);
-  __syncthreads();
-  {
-    using SS = RowShape<kFp8, C::S>;
-    using W = WRows<kFp8, C::S, SS::G>;
-    const int g = lane / SS::LPR;
-    down_units<kFp8, C::S>(
-        hn / SS::G,
-        [&](int v, int i, const uint8_t*& r, const void*& sr) {
-          const int h = h0 + v * SS::G + i;
-          r = p.sw2 + (size_t)h * C::S;
-          sr = p.sw2_s + (size_t)(h / 128) * (C::S / 128);
-        },
-        [&](int v, const W& wr) {
-          for (int t = 0; t < R; ++t) {
-            float acc[1];
-            wr.dot(LdsAct{sm.u.sh.q + (size_t)t * C::SQS, sm.u.sh.s + t * (C::S / 128)}, lane, acc);
-            const float y = tree_sum<SS::LPR>(acc[0]);
-            if ((lane % SS::LPR) == 0) sm.ysh[t * kTileMax + v * SS::G + g] = bf_round(y);
-          }
-        });
+union CSmem {
+  XTile<C> x;
+  SharedDownSmem<C> sd;
+};
+
+template <class C>
+__device__ __forceinline__ void stage_c(const Params& p, const Union<C>& un, CSmem<C>& sm, int b, int nwg) {
+  routed_gate_up<C>(p, un, sm.x, b, nwg);
+  const int tr = p.tile_rows;
+  const int n_tiles = (C::H + tr - 1) / tr;
+  for (int tile = b; tile < n_tiles; tile += nwg) {
+    const int h0 = tile * tr;
+    shared_down_tile<C>(p, sm.sd, h0, min(tr, C::H - h0));
   }
-  __syncthreads();
-  // ---- routed experts, in batches of PB picks (slot order)
-  using RD = RowShape<C::FMT, C::I>;
-  using WD = WRows<C::FMT, C::I, RD::G>;
-  const int rg = hn / RD::G;  // row groups of the tile
+}
+
+// ---------------------------------------------------------------- stage D: routed down + combine
+template <class C>
+struct DownSmem {
+  float contrib[kRowsMax * C::K * kTileMax];
+  uint8_t q[C::PB * C::MQS];
+  uint8_t s[C::PB * C::MSC * 4];
+};
+
+template <class C>
+__device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn) {
+  const int tid = threadIdx.x, lane = tid & 63, g = lane / kDownLanes, l = lane % kDownLanes;
+  const int R = p.rows;
   const int npk = R * C::K;
-  const int gsub = lane / RD::LPR;
+  using DR = DownRows<C::FMT, C::I>;
+  constexpr int SST = C::FMT == kFp4 ? C::I / 32 : (C::I / 128) * 4;  // scale bytes of a pick
   for (int pb0 = 0; pb0 < npk; pb0 += C::PB) {
     const int pbn = min(C::PB, npk - pb0);
-    quant_rows_lds<C::FMT, C::I, C::MQS>(
-        p, [&](int i) { return p.off[9] + (uint32_t)un.picks[pb0 + i] * C::I * 2; }, pbn,
-        sm.u.mid.q, sm.u.mid.s);
-    __syncthreads();
     // slots with picks in [pb0, pb0 + pbn)
     int lo = 0, hi = un.n - 1;
     while (lo < hi) {
-      int mid = (lo + hi + 1) >> 1;
+      const int mid = (lo + hi + 1) >> 1;
       if (un.slot_start[mid] <= pb0) lo = mid; else hi = mid - 1;
     }
     const int s_lo = lo;
     int s_hi = s_lo;
     while (s_hi + 1 < un.n && un.slot_start[s_hi + 1] < pb0 + pbn) ++s_hi;
-    down_units<C::FMT, C::I>(
-        (s_hi - s_lo + 1) * rg,
-        [&](int v, int i, const uint8_t*& r, const void*& sr) {
-          const int e = un.slot_e[s_lo + v / rg];
-          const int h = h0 + (v % rg) * RD::G + i;
-          const size_t row = (size_t)e * C::H + h;
-          if constexpr (C::FMT == kFp8) {
-            r = p.w2 + row * C::I;
-            sr = (const float*)p.w2_s + (size_t)e * (C::H / 128) * (C::I / 128) + (size_t)(h / 128) * (C::I / 128);
-          } else {
-            r = p.w2 + row * (C::I / 2);
-            sr = (const uint8_t*)p.w2_s + row * (C::I / 32);
-          }
-        },
-        [&](int v, const WD& wr) {
-          const int slot = s_lo + v / rg, r0 = (v % rg) * RD::G;
-          const int j0 = max(un.slot_start[slot], pb0), j1 = min(un.slot_start[slot + 1], pb0 + pbn);
-          for (int jj = j0; jj < j1; ++jj) {
-            const int lp = jj - pb0;
-            float acc[1];
-            if constexpr (C::FMT == kFp8)
-              wr.dot(LdsAct{sm.u.mid.q + (size_t)lp * C::MQS, (const float*)sm.u.mid.s + lp * (C::I / 128)}, lane, acc);
-            else
-              wr.dot(LdsAct{sm.u.mid.q + (size_t)lp * C::MQS, sm.u.mid.s + lp * (C::I / 32)}, lane, acc);
-            const float y = tree_sum<RD::LPR>(acc[0]);
-            if ((lane % RD::LPR) == 0) sm.contrib[un.picks[jj] * kTileMax + r0 + gsub] = y;
-          }
-        });
+    const int n_units = (s_hi - s_lo + 1) * kRowBlocks;
+    auto load = [&](int v, DR& wr) {
+      const int slot = s_lo + v / kRowBlocks, rb = v % kRowBlocks;
+      const int e = un.slot_e[slot];
+      const int hl = rb * kDownLanes + g;
+      const int h = h0 + hl;
+      const size_t row = (size_t)e * C::H + h;
+      if constexpr (C::FMT == kFp8)
+        wr.load(p.w2 + row * C::I,
+                (const float*)p.w2_s + (size_t)e * (C::H / 128) * (C::I / 128) + (size_t)(h / 128) * (C::I / 128),
+                hl < hn, l);
+      else
+        wr.load(p.w2 + row * (C::I / 2), (const uint8_t*)p.w2_s + row * (C::I / 32), hl < hn, l);
+    };
+    // the first batch's weights are requested before the picks' rows are quantized
+    DownBatch<DR> bt;
+    bt.load(threadIdx.x >> 6, n_units, load);
+    __syncthreads();  // the previous batch is done with the LDS rows
+    quant_rows_lds<C::FMT, C::I, C::MQS>(
+        p, [&](int i) { return p.off[9] + (uint32_t)un.picks[pb0 + i] * C::I * 2; }, pbn, sm.q, sm.s);
     __syncthreads();
+    down_pipeline<DR>(bt, n_units, load, [&](int v, const DR& wr) {
+      const int slot = s_lo + v / kRowBlocks, rb = v % kRowBlocks;
+      if (rb * kDownLanes >= hn) return;
+      const int hl = rb * kDownLanes + g;
+      const int j0 = max(un.slot_start[slot], pb0), j1 = min(un.slot_start[slot + 1], pb0 + pbn);
+      for (int jj = j0; jj < j1; jj += kPickBlock) {
+        const int np = min(kPickBlock, j1 - jj);
+        const int lp = jj - pb0;
+        float acc[kPickBlock];
+        wr.template dot<C::MQS, SST>(sm.q + (size_t)lp * C::MQS, sm.s + lp * SST, np, l, acc);
+#pragma unroll
+        for (int q = 0; q < kPickBlock; ++q) {
+          const float y = tree_sum<kDownLanes>(acc[q]);
+          if (q < np && l == 0 && hl < hn) sm.contrib[un.picks[jj + q] * kTileMax + hl] = y;
+        }
+      }
+    });
   }
-  // ---- combine: top-k order, bf16 at every add, then + shared
+  __syncthreads();
+  // ---- combine: top-k order, bf16 at every add, then + the shared expert's bf16 result
+  const auto rs = ws_rsrc(p);
   for (int idx = tid; idx < R * hn; idx += kThreads) {
     const int t = idx / hn, hl = idx % hn;
     float routed = 0.0f;
@@ -1361,13 +1557,14 @@ __device__ void down_tile(const Params& p, const Union<C>& un, DownSmem<C>& sm, 
       const int pk = t * C::K + k;
       routed = bf_round(routed + bf_round(sm.contrib[pk * kTileMax + hl] * un.wts[pk]));
     }
-    p.out[(size_t)t * C::H + h0 + hl] = f2bf(routed + sm.ysh[t * kTileMax + hl]);
+    const float sh = bf2f((uint16_t)dld16(rs, p.off[10] + ((uint32_t)t * C::H + h0 + hl) * 2));
+    p.out[(size_t)t * C::H + h0 + hl] = f2bf(routed + sh);
   }
   __syncthreads();
 }
 
 template <class C>
-__device__ void stage_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg) {
+__device__ __forceinline__ void stage_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg) {
   const int tr = p.tile_rows;
   const int n_tiles = (C::H + tr - 1) / tr;
   for (int tile = b; tile < n_tiles; tile += nwg) {
@@ -1382,6 +1579,7 @@ template <class C>
 union StageSmem {
   RouterSmem<C> a;
   XTile<C> x;
+  CSmem<C> c;
   DownSmem<C> d;
 };
 
@@ -1402,7 +1600,7 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   arrive(p, kCtlB);
   await_all(p, kCtlB, nwg, kStageB);
   build_union<C>(p, un);
-  stage_c<C>(p, un, sm.x, b, nwg);
+  stage_c<C>(p, un, sm.c, b, nwg);
   arrive(p, kCtlC);
   await_all(p, kCtlC, nwg, kStageC);
   __syncthreads();  // the tile's readers are done before the down stage reuses its LDS
@@ -1427,9 +1625,9 @@ __global__ __launch_bounds__(kThreads) void k_b(Params p) {
 template <class C>
 __global__ __launch_bounds__(kThreads) void k_c(Params p) {
   __shared__ Union<C> un;
-  __shared__ XTile<C> xt;
+  __shared__ CSmem<C> sm;
   build_union<C>(p, un);
-  stage_c<C>(p, un, xt, blockIdx.x, gridDim.x);
+  stage_c<C>(p, un, sm, blockIdx.x, gridDim.x);
 }
 template <class C>
 __global__ __launch_bounds__(kThreads) void k_d(Params p) {
@@ -1594,7 +1792,7 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
     dl = g_deadline_s;
   }
   p.deadline = (unsigned long long)(dl * 1e8);
-  for (int i = 0; i < 10; ++i) p.off[i] = (uint32_t)L.off[i];
+  for (int i = 0; i < kRegions; ++i) p.off[i] = (uint32_t)L.off[i];
   hipStream_t st = (hipStream_t)stream;
   switch (cfg_id(s)) {
     case kIdPlumbing:
@@ -1634,7 +1832,7 @@ int mkmoe_workspace_region(const mkmoe_shape* shape, int32_t region, size_t* off
   int rc = check_shape(shape);
   if (rc) return rc;
   if (!offset || !bytes) return MKMOE_ERR_NULL;
-  if (region < 0 || region >= 10) return MKMOE_ERR_ARG;
+  if (region < 0 || region >= kRegions) return MKMOE_ERR_ARG;
   Layout L = layout_of(shape);
   *offset = L.off[region];
   *bytes = L.size[region];

@@ -26,8 +26,9 @@ REGIONS = {
     "weights": 7,
     "shared_mid": 8,
     "mid": 9,
+    "shared_out": 10,
 }
-STAGES = {1: "norm", 2: "router + quantize", 3: "route + shared gate_up", 4: "routed gate_up", 5: "down"}
+STAGES = {1: "norm", 2: "router + quantize", 3: "route + shared gate_up", 4: "shared down + routed gate_up", 5: "routed down + combine"}
 
 # every symbol include/mkmoe.h declares
 EXPORTS = (

@@ -46,12 +46,13 @@ def test_fp4_gemv_close_to_fp64(k):
     assert err < 1e-5, err
 
 
-def _scalar_gemv(wv, xv, scale, ce):
+def _scalar_gemv(wv, xv, scale, ce, lpr=None):
     """Index by index: chunk sums in element order, scaled, chunk c to lane c % LPR, lane sums, tree."""
     f = np.float32
     n, k = wv.shape
     c_n = k // ce
-    lpr = 64 if c_n % 64 == 0 else 32 if c_n % 32 == 0 else 16 if c_n % 16 == 0 else 8
+    if lpr is None:
+        lpr = 64 if c_n % 64 == 0 else 32 if c_n % 32 == 0 else 16 if c_n % 16 == 0 else 8
     out = np.zeros((xv.shape[0], n), np.float32)
     for t in range(xv.shape[0]):
         for r in range(n):
@@ -68,7 +69,8 @@ def _scalar_gemv(wv, xv, scale, ce):
     return out
 
 
-def test_fp8_gemv_scalar_restatement():
+@pytest.mark.parametrize("lpr", [None, 8])
+def test_fp8_gemv_scalar_restatement(lpr):
     wq, ws, xq, xs = _fp8_case(3, 512, 2, 11)
     wv = fm.e4m3_to_f32(wq).numpy()
     xv = fm.e4m3_to_f32(xq).numpy()
@@ -78,12 +80,13 @@ def test_fp8_gemv_scalar_restatement():
     def scale(t, r, c, d):
         return f(d * f(wsn[r // 128, c // 8] * xsn[t, c // 8]))
 
-    want = _scalar_gemv(wv, xv, scale, 16)
-    got = ex.gemv_fp8_b128(wq, ws, xq, xs)
+    want = _scalar_gemv(wv, xv, scale, 16, lpr)
+    got = ex.gemv_fp8_b128(wq, ws, xq, xs, lpr)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-def test_fp4_gemv_scalar_restatement():
+@pytest.mark.parametrize("lpr", [None, 8])
+def test_fp4_gemv_scalar_restatement(lpr):
     wq, ws, xq, xs = _fp4_case(3, 1024, 2, 12)
     wv = fm.fp4_unpack(wq).numpy()
     xv = fm.e4m3_to_f32(xq).numpy()
@@ -92,18 +95,28 @@ def test_fp4_gemv_scalar_restatement():
     def scale(t, r, c, d):
         return np.float32(np.ldexp(d, wsn[r, c] + xsn[t, c] - 254))
 
-    want = _scalar_gemv(wv, xv, scale, 32)
-    got = ex.gemv_mxfp4(wq, ws, xq, xs)
+    want = _scalar_gemv(wv, xv, scale, 32, lpr)
+    got = ex.gemv_mxfp4(wq, ws, xq, xs, lpr)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 def test_lanes_per_row_matches_kernel_rule():
-    # the kernel's RowShape: 64 lanes when the chunks divide by 64, else 32, 16, 8
+    # the kernel's gate_up rows: 64 lanes when the chunks divide by 64, else 32, 16, 8
     assert ex.lanes_per_row(7168 // 16) == 64  # FP8 gate_up rows
     assert ex.lanes_per_row(7168 // 32) == 32  # MXFP4 gate_up rows
-    assert ex.lanes_per_row(512 // 16) == 32  # FP8 down rows at I = 512
-    assert ex.lanes_per_row(512 // 32) == 16  # MXFP4 down rows at I = 512
     assert ex.lanes_per_row(1024 // 32) == 32
+    # the down rows: 8 lanes a row, whatever the width
+    assert ex.DOWN_LANES == 8
+
+
+def test_lane_count_changes_the_sum():
+    # the restatement is sensitive to the lane count it is given: a kernel that dealt its
+    # down chunks to 16 or 32 lanes would not match the oracle's 8
+    wq, ws, xq, xs = _fp8_case(64, 512, 4, 13)
+    a = ex.gemv_fp8_b128(wq, ws, xq, xs, 8)
+    for other in (16, 32):
+        b = ex.gemv_fp8_b128(wq, ws, xq, xs, other)
+        assert not np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
 def test_silu_exact_close_to_torch():
