@@ -809,10 +809,11 @@ struct GateUpCol {
   }
 
   // NPB: the picks the code is unrolled for (np <= NPB)
-  // wsc: the FP8 weight's block scales ((2W / 128) x (H / 128)); j: this column
+  // wsc: the FP8 weight's block scales ((2W / 128) x (H / 128)); j: this column;
+  // g[p], u[p] for p < np <= NPB
   template <int QS, int NPB>
   __device__ __forceinline__ void run(const uint8_t* xq, const uint8_t* xs, const float* wsc, int W, int j,
-                                      int np, int lane, float (&g)[kTokGroup], float (&u)[kTokGroup]) const {
+                                      int np, int lane, float* g, float* u) const {
 #pragma clang fp contract(off)
     const int l = lane % S::LPR;
     float acc[R::RPG][NPB];
@@ -955,12 +956,15 @@ __device__ __forceinline__ float lane_pick(const float (&a)[kTokGroup]) {
   return v;
 }
 
-// one workgroup unit: columns [c0, c0 + cb) of a [2W][H] weight for np activation rows;
-// wave w takes columns c0 + w, c0 + w + 8, ... with two column buffers in turn. The
-// activation rows are requested first (load_x fills an XRegs), then both buffers' first
-// columns, so the rows reach the tile without waiting for the weights; a buffer's next
-// column is requested as soon as it is computed, so the other's loads stay in flight
-// while a wave waits; emit(p, column, g, u) runs in lane p (p < np)
+// one workgroup unit: columns [c0, c0 + cb) of a [2W][H] weight for np activation rows.
+// When the unit has fewer columns than waves, its picks split over ps waves a column (each
+// pick's sums are independent, so the split leaves the arithmetic as it is). Wave w takes
+// the picks of part w % ps and columns c0 + w / ps, c0 + w / ps + 8 / ps, ... with two
+// column buffers in turn. The activation rows are requested first (load_x fills an XRegs),
+// then both buffers' first columns, so the rows reach the tile without waiting for the
+// weights; a buffer's next column is requested as soon as it is computed, so the other's
+// loads stay in flight while a wave waits; emit(p, column, g, u) runs in lane q for pick
+// p = q0 + q
 template <class C, int FMT, class WFn, class XFn, class EmitFn>
 __device__ __forceinline__ void gu_unit(const Params& p, XTile<C>& xt, int np, int W, int c0, int cb, WFn weights,
                         XFn load_x, EmitFn emit) {
@@ -969,29 +973,32 @@ __device__ __forceinline__ void gu_unit(const Params& p, XTile<C>& xt, int np, i
   const uint8_t* wb;
   const void* sb;
   weights(wb, sb);
+  int ps = 1;
+  while (ps * 2 <= np && cb * ps < kWaves) ps *= 2;
+  const int ppw = (np + ps - 1) / ps;           // picks a part
+  const int q0 = (wave % ps) * ppw;             // this wave's first pick
+  const int nq = max(0, min(ppw, np - q0));      // and its count
+  const int cstep = kWaves / ps;
   const int end = c0 + cb;
-  int ca = c0 + wave, cx = ca + kWaves;
+  int col = c0 + wave / ps;
+  if (nq == 0) col = end;
   XRegs<C> xr;
   load_x(xr);
   if constexpr (FMT == kFp8) xr.load_wscales((const float*)sb, W);
-  GU a, x;
-  if (ca < end) a.load(wb, sb, W, ca, lane);
-  if (cx < end) x.load(wb, sb, W, cx, lane);
+  GU a;
+  if (col < end) a.load(wb, sb, W, col, lane);
   __syncthreads();  // the previous unit is done with the tile
   xr.store(xt, np);
   __syncthreads();
-  auto step = [&](GU& buf, int& col) {
+  const uint8_t* xq = xt.q + q0 * XTile<C>::QS;
+  const uint8_t* xs = xt.s + q0 * (C::H / 32);
+  while (col < end) {
     float g[kTokGroup] = {}, u[kTokGroup] = {};
-    buf.template run<XTile<C>::QS, kTokGroup>(xt.q, xt.s, xt.wsc, W, col, np, lane, g, u);
+    a.template run<XTile<C>::QS, kTokGroup>(xq, xs, xt.wsc, W, col, nq, lane, g, u);
     const float gl = lane_pick(g), ul = lane_pick(u);
-    if (lane < np) emit(lane, col, gl, ul);
-    col += 2 * kWaves;
-    if (col < end) buf.load(wb, sb, W, col, lane);
-  };
-  while (ca < end) {
-    step(a, ca);
-    if (cx >= end) break;
-    step(x, cx);
+    if (lane < nq) emit(q0 + lane, col, gl, ul);
+    col += cstep;
+    if (col < end) a.load(wb, sb, W, col, lane);
   }
 }
 
