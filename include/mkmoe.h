@@ -139,6 +139,13 @@ int mkmoe_forward_staged(const mkmoe_shape* shape, const mkmoe_weights* w, const
  * (default 2.0). A wait past it sets the error words and the launch ends. */
 int mkmoe_set_deadline(double seconds);
 
+/* Row counts from which launches run the gate_up GEMMs (routed and shared) and the down
+ * GEMMs (routed and shared) on MFMA (defaults: gate_up never, i.e. 49; down 8). Below them
+ * the fixed-order VALU GEMVs run, whose output is bit-identical to the oracle; MFMA launches
+ * are held to the numerics bounds of the spec. No counterpart in the reference, whose kernels
+ * pick their GEMM instruction per width at build time (spec.py:959-967 widths). */
+int mkmoe_set_mfma_rows(int32_t gate_up_rows, int32_t down_rows);
+
 /* Copy the MKMOE_ERRW_WORDS error words to host memory (synchronises stream). */
 int mkmoe_read_errors(const void* ws, int32_t* words, int32_t n, void* stream);
 int mkmoe_clear_errors(void* ws, void* stream);

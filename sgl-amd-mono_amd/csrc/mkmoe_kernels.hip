@@ -132,6 +132,8 @@ struct Params {
   int rmax;
   int renorm;
   int tile_rows;
+  int mfma_gate;  // launches with at least this many rows run the gate_up GEMMs on MFMA
+  int mfma_down;  // ... and the down GEMMs
   float scale;
   float limit;
   float eps;
@@ -714,31 +716,34 @@ __device__ __forceinline__ float swiglu_shared(float g, float u, float lim) {
   return bf_round(silu_exact(bf_round(fminf(g, lim))) * bf_round(clampf(u, lim)));
 }
 
-constexpr int kTokGroup = 8;  // picks a gate_up unit takes at most
+constexpr int kTokGroup = 8;    // picks a VALU gate_up unit takes at most
+constexpr int kMfmaPicks = 16;  // picks an MFMA unit takes at most (the MFMA's 16 columns)
 
-// activation rows of a unit staged in LDS: kTokGroup rows of codes and their scales
+// activation rows of a unit staged in LDS: up to kMfmaPicks rows of codes and their scales
 template <class C>
 struct XTile {
   static constexpr int QS = C::H + 16;  // row stride (bank spread)
-  // fp32 block scales of an FP8 [2W][H] weight: (2W / 128) x (H / 128)
-  static constexpr int WSC = 2 * (C::I > C::S ? C::I : C::S) / 128 * (C::H / 128);
-  uint8_t q[kTokGroup * QS];
-  uint8_t s[kTokGroup * (C::H / 32)];  // E8M0 per 32, or fp32 per 128 (the same bytes)
+  // fp32 block scales of an FP8 [2W][H] weight: (2W / 128) x (H / 128), padded to 1 KB
+  static constexpr int WSC = (2 * (C::I > C::S ? C::I : C::S) / 128 * (C::H / 128) + 255) / 256 * 256;
+  static constexpr int SB = (kMfmaPicks * (C::H / 32) + 1023) / 1024 * 1024;  // scale bytes, padded
+  uint8_t q[kMfmaPicks * QS];
+  uint8_t s[SB];  // E8M0 per 32, or fp32 per 128 (the same bytes), C::H / 32 bytes a row
   float wsc[WSC];
 };
 
-// the activation rows of a unit on their way to the tile: each thread's share of the codes
-// (16-byte chunks) and scale words, loaded (sc1) before the unit's weights so that writing
-// them to LDS waits for these loads alone
-template <class C>
+// the (at most NR) activation rows of a unit on their way to the tile: each thread's share of
+// the codes (16-byte chunks) and scale words, loaded (sc1) before the unit's weights so that
+// writing them to LDS waits for these loads alone
+template <class C, int NR>
 struct XRegs {
   static constexpr int QC = C::H / 16;  // 16-byte chunks a row
-  static constexpr int NQ = (kTokGroup * QC + kThreads - 1) / kThreads;
+  static constexpr int NQ = (NR * QC + kThreads - 1) / kThreads;
   static constexpr int SW = C::H / 128;  // 4-byte scale words a row (fp32 per 128, or E8M0 per 32)
-  static_assert(kTokGroup * SW <= kThreads, "one scale word a thread");
+  static constexpr int NS = (NR * SW + kThreads - 1) / kThreads;
+  static_assert(NR <= kMfmaPicks, "rows of the tile");
   static constexpr int NW = (XTile<C>::WSC + kThreads - 1) / kThreads;
   u32x4 q[NQ];
-  uint32_t s;
+  uint32_t s[NS];
   float w[NW];
   int nw = 0;
 
@@ -765,7 +770,11 @@ struct XRegs {
         q[i] = dld128(rs, qoff + (uint32_t)tok(r) * C::H + c * 16);
       }
     }
-    if (tid < np * SW) s = dld32(rs, soff + (uint32_t)tok(tid / SW) * (SW * 4) + (tid % SW) * 4);
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      const int idx = tid + i * kThreads;
+      if (idx < np * SW) s[i] = dld32(rs, soff + (uint32_t)tok(idx / SW) * (SW * 4) + (idx % SW) * 4);
+    }
   }
 
   __device__ __forceinline__ void store(XTile<C>& xt, int np) const {
@@ -775,7 +784,11 @@ struct XRegs {
       const int idx = tid + i * kThreads;
       if (idx < np * QC) *(u32x4*)(xt.q + (idx / QC) * XTile<C>::QS + (idx % QC) * 16) = q[i];
     }
-    if (tid < np * SW) ((uint32_t*)xt.s)[tid] = s;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      const int idx = tid + i * kThreads;
+      if (idx < np * SW) ((uint32_t*)xt.s)[idx] = s[i];
+    }
 #pragma unroll
     for (int i = 0; i < NW; ++i) {
       const int idx = tid + i * kThreads;
@@ -959,12 +972,11 @@ __device__ __forceinline__ float lane_pick(const float (&a)[kTokGroup]) {
 // one workgroup unit: columns [c0, c0 + cb) of a [2W][H] weight for np activation rows.
 // When the unit has fewer columns than waves, its picks split over ps waves a column (each
 // pick's sums are independent, so the split leaves the arithmetic as it is). Wave w takes
-// the picks of part w % ps and columns c0 + w / ps, c0 + w / ps + 8 / ps, ... with two
-// column buffers in turn. The activation rows are requested first (load_x fills an XRegs),
-// then both buffers' first columns, so the rows reach the tile without waiting for the
-// weights; a buffer's next column is requested as soon as it is computed, so the other's
-// loads stay in flight while a wave waits; emit(p, column, g, u) runs in lane q for pick
-// p = q0 + q
+// the picks of part w % ps and columns c0 + w / ps, c0 + w / ps + 8 / ps, ..., one column
+// in registers at a time (a wave's next column is requested as soon as its current one is
+// computed). The activation rows are requested first (load_x fills an XRegs), then the
+// first column, so the rows reach the tile without waiting for the weights;
+// emit(p, column, g, u) runs in lane q for pick p = q0 + q
 template <class C, int FMT, class WFn, class XFn, class EmitFn>
 __device__ __forceinline__ void gu_unit(const Params& p, XTile<C>& xt, int np, int W, int c0, int cb, WFn weights,
                         XFn load_x, EmitFn emit) {
@@ -982,7 +994,7 @@ __device__ __forceinline__ void gu_unit(const Params& p, XTile<C>& xt, int np, i
   const int end = c0 + cb;
   int col = c0 + wave / ps;
   if (nq == 0) col = end;
-  XRegs<C> xr;
+  XRegs<C, kTokGroup> xr;
   load_x(xr);
   if constexpr (FMT == kFp8) xr.load_wscales((const float*)sb, W);
   GU a;
@@ -1008,22 +1020,373 @@ __device__ __forceinline__ void even_share(int n, int b, int nwg, int& lo, int& 
   hi = (int)((long long)n * (b + 1) / nwg);
 }
 
+// ---------------------------------------------------------------- MFMA expert GEMMs
+// Launches with at least mfma_gate (gate_up) / mfma_down (down) rows run those expert GEMMs on
+// v_mfma_f32_16x16x32_bf16 (fewer rows keep the fixed-order VALU GEMVs above). The gate_up
+// default keeps the VALU GEMVs at every row count: the MFMA operand layout reads 16 rows x 64
+// bytes a load, which streams a [2W][H] weight at 5.1-5.3 TB/s against 6.8 TB/s for the 1 KB
+// row loads of the VALU GEMVs (load-only measurement, 57 experts at 8 rows). The e4m3 and e2m1 codes convert to bf16
+// exactly (with an E8M0 scale folded in, still exact), every bf16 x bf16 product is exact in
+// fp32 and the instruction sums them like an fp32 chain (measured on gfx950: within 0.42 x
+// 2^-24 x sum |products| of the exact sum). The fp8 MFMAs are not used: their sums drift by
+// up to 267 x 2^-24 x sum |products|, enough to move bf16 outputs by two units in the last place.
+// Lane l supplies row (A) / column (B) l % 16 and, as lane group j = l / 16, 8 of the 32 K of a
+// step (A and B take the same K from the same places, so which 8 the hardware assigns them
+// does not matter); C[m][n] lands in lane n + 16 (m / 4), element m % 4. Weights are the A
+// operand (16 rows), picks the B operand (16 columns).
+// FP8 weights: a 128-K step is four MFMAs on the raw codes (lane group j: K 16j .. 16j + 15
+// and 64 + 16j .. 64 + 16j + 15 of the step, so that each 16-byte load reads 64 contiguous
+// bytes of a row), then scaled by the weight's 128 x 128 block scale times the pick's
+// group-128 scale as it is added to the sum. MXFP4 weights with MXFP8 activations: lane group
+// j holds the step's 32-K block j and converts it with its row's and its column's E8M0 scales
+// folded in, so every product is exactly scaled whichever block it came from; the four MFMAs
+// accumulate across steps.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+// 8 e4m3 codes (bytes of w0 then w1) times s, as bf16
+__device__ __forceinline__ bf16x8 fp8x8(uint32_t w0, uint32_t w1, float s) {
+  const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, s, false);
+  const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, s, true);
+  const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, s, false);
+  const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, s, true);
+  return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+// 8 e2m1 codes (the nibbles of w, low first) times s, as bf16
+__device__ __forceinline__ bf16x8 fp4x8(uint32_t w, float s) {
+  const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 0);
+  const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 1);
+  const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 2);
+  const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 3);
+  return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+// an E8M0 scale as a float (2^(e - 127))
+__device__ __forceinline__ float e8m0(uint32_t e) { return e == 0u ? 0x1p-127f : __uint_as_float(e << 23); }
+// an FP8 128-K step on MFMA: A and B 32 raw code bytes a lane each (lo then hi 16 bytes)
+__device__ __forceinline__ f32x4 mma_fp8_step(u32x4 alo, u32x4 ahi, u32x4 blo, u32x4 bhi) {
+  f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+  c = mfma_bf16(fp8x8(alo.x, alo.y, 1.0f), fp8x8(blo.x, blo.y, 1.0f), c);
+  c = mfma_bf16(fp8x8(alo.z, alo.w, 1.0f), fp8x8(blo.z, blo.w, 1.0f), c);
+  c = mfma_bf16(fp8x8(ahi.x, ahi.y, 1.0f), fp8x8(bhi.x, bhi.y, 1.0f), c);
+  c = mfma_bf16(fp8x8(ahi.z, ahi.w, 1.0f), fp8x8(bhi.z, bhi.w, 1.0f), c);
+  return c;
+}
+// an MXFP4 x MXFP8 128-K step, accumulated into c: a holds the lane's 32 e2m1 codes of its
+// block (8 a word), sw its row's scale; blo / bhi the column's 32 code bytes of the same
+// block, sx the column's scale
+__device__ __forceinline__ f32x4 mma_fp4_step(u32x4 a, float sw, u32x4 blo, u32x4 bhi, float sx, f32x4 c) {
+  c = mfma_bf16(fp4x8(a.x, sw), fp8x8(blo.x, blo.y, sx), c);
+  c = mfma_bf16(fp4x8(a.y, sw), fp8x8(blo.z, blo.w, sx), c);
+  c = mfma_bf16(fp4x8(a.z, sw), fp8x8(bhi.x, bhi.y, sx), c);
+  c = mfma_bf16(fp4x8(a.w, sw), fp8x8(bhi.z, bhi.w, sx), c);
+  return c;
+}
+
+// 16 bytes a lane from a buffer straight into LDS: lane l's bytes land at lds + 16 l (lds
+// the same in every lane of the wave)
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, void* lds, uint32_t voff, int aux) {
+  if (aux)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, kAuxDev);
+  else
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+}
+
+// stage np activation rows into the tile: codes (qoff + t H) and scale bytes (soff + t H / 32)
+// of rows t = tok(r) from the workspace, and, for an FP8 weight, its nw fp32 block scales
+// (wsc, a read-only input); 1 KB LDS-direct loads spread over the waves, so no registers hold
+// the rows on their way. Ends with the tile complete and visible to the workgroup.
+template <class C, class TokFn>
+__device__ __forceinline__ void stage_x_lds(const Params& p, XTile<C>& xt, int np, uint32_t qoff, uint32_t soff, TokFn tok,
+                                            const float* wsc, int nw) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const auto rs = ws_rsrc(p);
+  constexpr int IPR = C::H / 1024;  // 1 KB loads a row of codes
+  constexpr int RB = C::H / 32;     // scale bytes a row
+  static_assert(C::H % 1024 == 0 && RB % 16 == 0, "1 KB code loads, 16-byte scale pieces");
+  __syncthreads();  // the previous user of the tile is done
+  for (int k = wave; k < np * IPR; k += kWaves) {
+    const int r = k / IPR, i = k % IPR;
+    lds_load16(rs, xt.q + r * XTile<C>::QS + i * 1024, qoff + (uint32_t)tok(r) * C::H + i * 1024 + lane * 16, 1);
+  }
+  const int sbytes = np * RB;
+  for (int k = wave; k * 1024 < sbytes; k += kWaves) {
+    const int off = k * 1024 + lane * 16;
+    const bool ok = off < sbytes;  // the rest lands in the padding, from row 0
+    const int r = ok ? off / RB : 0, in = ok ? off % RB : 0;
+    lds_load16(rs, xt.s + k * 1024, soff + (uint32_t)tok(r) * RB + in, 1);
+  }
+  if (nw > 0) {
+    const auto wr = __builtin_amdgcn_make_buffer_rsrc((void*)wsc, (short)0, nw * 4, 0x00020000);
+    for (int k = wave; k * 256 < nw; k += kWaves) {
+      const int off = k * 1024 + lane * 16;
+      lds_load16(wr, (uint8_t*)xt.wsc + k * 1024, off < nw * 4 ? off : 0, 0);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
+// LDS of an MFMA gate_up: the activation tile and the waves' partial C tiles (gate, up)
+template <class C>
+struct GuSmem {
+  XTile<C> x;
+  f32x4 red[2][kWaves][64];
+};
+
+// the rows of an MFMA gate_up unit of a [2W][H] weight, this wave's K steps (the 8 waves
+// split the H / 128 steps evenly), in registers: FP8 units are 8 columns (one A operand: gate
+// rows j0 .. j0 + 7 in A rows 0..7, up rows W + j0 .. in A rows 8..15), MXFP4 units 16 columns
+// (A operands of gate rows j0 .. j0 + 15 and of up rows W + j0 ..): 56 registers a wave either way
+template <class C, int WFMT>
+struct GuTile {
+  static constexpr int KS = C::H / 128;
+  static constexpr int SPW = KS / kWaves;
+  static_assert(KS % kWaves == 0, "K steps split evenly over the waves");
+  static constexpr int NA = WFMT == kFp8 ? 1 : 2;   // A operands a K step
+  static constexpr int NC = WFMT == kFp8 ? 8 : 16;  // columns a unit
+  static constexpr int NW = WFMT == kFp8 ? 2 : 1;   // 16-byte words of a lane's step
+  u32x4 a[NA][SPW][NW];
+  uint32_t sa[NA][SPW];  // MXFP4: the E8M0 byte of the lane's row and block
+
+  __device__ __forceinline__ void load(const uint8_t* w, const void* s, int W, int j0, int lane, int wave) {
+    const int m = lane & 15, j = lane >> 4, s0 = wave * SPW;
+    if constexpr (WFMT == kFp8) {
+      const size_t r = (size_t)(m < 8 ? j0 + m : W + j0 + m - 8);
+#pragma unroll
+      for (int i = 0; i < SPW; ++i) {
+        const uint8_t* p = w + r * C::H + (s0 + i) * 128 + 16 * j;
+        a[0][i][0] = ld16_nt(p);
+        a[0][i][1] = ld16_nt(p + 64);
+      }
+    } else {
+      const uint8_t* ss = (const uint8_t*)s;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const size_t r = (size_t)(q * W + j0 + m);
+#pragma unroll
+        for (int i = 0; i < SPW; ++i) {
+          a[q][i][0] = ld16_nt(w + r * (C::H / 2) + (s0 + i) * 64 + 16 * j);
+          sa[q][i] = ss[r * (C::H / 32) + (s0 + i) * 4 + j];
+        }
+      }
+    }
+  }
+
+  // this wave's partial C tiles over its K steps against the np picks of the tile
+  __device__ __forceinline__ void mma(const XTile<C>& xt, int W, int j0, int np, int lane, int wave,
+                                      f32x4 (&acc)[NA]) const {
+    const int n = lane & 15, j = lane >> 4, s0 = wave * SPW;
+    const bool live = n < np;
+    const int row = live ? n : 0;
+    const uint8_t* xr = xt.q + row * XTile<C>::QS;
+#pragma unroll
+    for (int q = 0; q < NA; ++q) acc[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // FP8: this lane's C rows are gate rows (lanes 0..31) or up rows (lanes 32..63)
+    const int sblk = ((lane < 32 ? j0 : W + j0) / 128) * (C::H / 128);
+#pragma unroll
+    for (int i = 0; i < SPW; ++i) {
+      const int ks = s0 + i, k0 = ks * 128;
+      if constexpr (WFMT == kFp8) {
+        u32x4 blo = *(const u32x4*)(xr + k0 + 16 * j), bhi = *(const u32x4*)(xr + k0 + 64 + 16 * j);
+        if (!live) blo = bhi = u32x4{0u, 0u, 0u, 0u};
+        const float f = xt.wsc[sblk + ks] * ((const float*)xt.s)[row * (C::H / 128) + ks];
+        const f32x4 c = mma_fp8_step(a[0][i][0], a[0][i][1], blo, bhi);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[0][v] = fmaf(c[v], f, acc[0][v]);
+      } else {
+        u32x4 blo = *(const u32x4*)(xr + k0 + 32 * j), bhi = *(const u32x4*)(xr + k0 + 32 * j + 16);
+        if (!live) blo = bhi = u32x4{0u, 0u, 0u, 0u};
+        const float sx = e8m0(xt.s[row * (C::H / 32) + k0 / 32 + j]);
+#pragma unroll
+        for (int q = 0; q < NA; ++q) acc[q] = mma_fp4_step(a[q][i][0], e8m0(sa[q][i]), blo, bhi, sx, acc[q]);
+      }
+    }
+  }
+};
+
+// MFMA gate_up of units [lo, hi) of a [2W][H] weight; unit u is token group u / (W / NC) and
+// its NC columns (u % (W / NC)) * NC ... group(tg, w, s, np) gives a group's weight, scales and
+// pick count, stage(tg, np, s) stages its activation rows (and an FP8 weight's block scales s)
+// in the tile, emit(tg, q, col, g, u) takes pick q's gate and up sums of a column. The next
+// unit's weights are requested into the registers of this one as soon as its MFMAs are done
+// (past the barrier of the partial tiles, which add in LDS in wave order). The activation
+// tile is restaged when the group changes. (A second unit in flight streams no faster: the
+// operand layout's 64-byte row pieces, not the requests in flight, set the rate.)
+template <class C, int WFMT, class GroupFn, class StageFn, class EmitFn>
+__device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo, int hi, GroupFn group, StageFn stage, EmitFn emit) {
+  using T = GuTile<C, WFMT>;
+  if (lo >= hi) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nb = W / T::NC;
+  T t;
+  const uint8_t* wb;
+  const void* sb;
+  int tg_w = lo / nb, np_w;  // the group whose weights t holds
+  group(tg_w, wb, sb, np_w);
+  t.load(wb, sb, W, (lo % nb) * T::NC, lane, wave);
+  int tg_x = -1, np_x = 0;   // the group staged in the tile
+  for (int u = lo; u < hi; ++u) {
+    const int j0 = (u % nb) * T::NC;
+    if (tg_w != tg_x) {
+      stage(tg_w, np_w, sb);
+      tg_x = tg_w;
+      np_x = np_w;
+    }
+    f32x4 acc[T::NA];
+    t.mma(sm.x, W, j0, np_x, lane, wave, acc);
+#pragma unroll
+    for (int q = 0; q < T::NA; ++q) sm.red[q][wave][lane] = acc[q];
+    __syncthreads();
+    if (u + 1 < hi) {
+      const int tn = (u + 1) / nb;
+      if (tn != tg_w) {
+        tg_w = tn;
+        group(tg_w, wb, sb, np_w);
+      }
+      t.load(wb, sb, W, ((u + 1) % nb) * T::NC, lane, wave);
+    }
+    if (tid < 16 * T::NC) {
+      // C[m][n] is element m % 4 of lane n + 16 (m / 4); FP8: up row m + 8 is 32 lanes on
+      const int m = tid >> 4, n = tid & 15;
+      const int L = n + 16 * (m >> 2), v = m & 3;
+      const int qu = T::NA - 1, Lu = T::NA == 1 ? L + 32 : L;
+      float g = 0.0f, uu = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        g = g + sm.red[0][w][L][v];
+        uu = uu + sm.red[qu][w][Lu][v];
+      }
+      if (n < np_x) emit(tg_x, n, j0 + m, g, uu);
+    }
+    __syncthreads();
+  }
+}
+
+// MFMA down: rows [hb, hb + 16) of a [H][KD] weight (nv of them real), all K steps, in
+// registers; mma() gives C[m][n] = row hb + m against pick column n of an LDS mid tile
+template <int WFMT, int KD>
+struct DownTile {
+  static constexpr int KS = KD / 128;
+  static constexpr int NW = WFMT == kFp8 ? 2 : 1;  // 16-byte words of a lane's step
+  static constexpr int BYTES = NW * 16 * 64 * KS;  // registers' bytes a unit
+  // units a wave requests at once: 16 KB of codes (MXFP4 rows of 1024 K: one unit, leaving
+  // registers for the conversions)
+  static constexpr int kBatch =
+      (WFMT == kFp4 && KS >= 8) || BYTES >= 16384 ? 1 : (16384 / BYTES > 4 ? 4 : 16384 / BYTES);
+  u32x4 a[KS][NW];
+  uint32_t sa[KS];        // MXFP4: the E8M0 byte of the lane's row and block
+  float s0[KS], s1[KS];   // FP8: block scales of the lane's first and last C row
+  int split;              // FP8: C elements v < split take s0, the rest s1
+
+  // w: row 0 of the weight; s: its scales (FP8 [H / 128][KD / 128] fp32, MXFP4 [H][KD / 32])
+  __device__ __forceinline__ void load(const uint8_t* w, const void* s, int hb, int nv, int lane) {
+    const int m = lane & 15, j = lane >> 4;
+    const bool ok = m < nv;
+    const size_t h = (size_t)hb + (ok ? m : 0);
+    if constexpr (WFMT == kFp8) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const uint8_t* p = w + h * KD + ks * 128 + 16 * j;
+        if (ok) {
+          a[ks][0] = ld16_nt(p);
+          a[ks][1] = ld16_nt(p + 64);
+        } else {
+          a[ks][0] = a[ks][1] = u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+      // this lane's C rows hb + 4j .. hb + 4j + 3 (the real ones) and where a 128-row block ends
+      const int r0 = hb + min(4 * j, nv - 1), r3 = hb + min(4 * j + 3, nv - 1);
+      const float* sp = (const float*)s;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        s0[ks] = sp[(r0 / 128) * (KD / 128) + ks];
+        s1[ks] = sp[(r3 / 128) * (KD / 128) + ks];
+      }
+      split = r0 / 128 == r3 / 128 ? 4 : 128 - (hb + 4 * j) % 128;
+    } else {
+      const uint8_t* ss = (const uint8_t*)s;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        if (ok) {
+          a[ks][0] = ld16_nt(w + h * (KD / 2) + ks * 64 + 16 * j);
+          sa[ks] = ss[h * (KD / 32) + ks * 4 + j];
+        } else {
+          a[ks][0] = u32x4{0u, 0u, 0u, 0u};
+          sa[ks] = 127u;
+        }
+      }
+    }
+  }
+
+  // C tile against picks [lp, lp + np) of the LDS mid rows (codes xq, row stride QS; scales
+  // xs, SST bytes a row: fp32 per 128, or E8M0 per 32)
+  template <int QS, int SST>
+  __device__ __forceinline__ f32x4 mma(const uint8_t* xq, const uint8_t* xs, int lp, int np, int lane) const {
+    const int n = lane & 15, j = lane >> 4;
+    const bool live = n < np;
+    const int row = lp + (live ? n : 0);
+    const uint8_t* xr = xq + (size_t)row * QS;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if constexpr (WFMT == kFp8) {
+        u32x4 blo = *(const u32x4*)(xr + ks * 128 + 16 * j), bhi = *(const u32x4*)(xr + ks * 128 + 64 + 16 * j);
+        if (!live) blo = bhi = u32x4{0u, 0u, 0u, 0u};
+        const float sx = ((const float*)(xs + row * SST))[ks];
+        const f32x4 c = mma_fp8_step(a[ks][0], a[ks][1], blo, bhi);
+        const float f0 = s0[ks] * sx, f1 = s1[ks] * sx;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[v] = fmaf(c[v], v < split ? f0 : f1, acc[v]);
+      } else {
+        u32x4 blo = *(const u32x4*)(xr + ks * 128 + 32 * j), bhi = *(const u32x4*)(xr + ks * 128 + 32 * j + 16);
+        if (!live) blo = bhi = u32x4{0u, 0u, 0u, 0u};
+        acc = mma_fp4_step(a[ks][0], e8m0(sa[ks]), blo, bhi, e8m0(xs[row * SST + ks * 4 + j]), acc);
+      }
+    }
+    return acc;
+  }
+};
+
 // ---------------------------------------------------------------- stage B: routing + shared gate_up
 // routing: a wave per row (wave 0 of workgroups 0 .. R-1); the shared expert's gate_up: its
 // (8-row group, column) pairs dealt evenly over the other workgroups, each share run as one
 // or two units of consecutive columns of one group
 template <class C>
-__device__ __forceinline__ void stage_b(const Params& p, XTile<C>& xt, int b, int nwg) {
+__device__ __forceinline__ void stage_b(const Params& p, GuSmem<C>& sm, int b, int nwg) {
   const int lane = threadIdx.x & 63, gw = wave_slot(b, nwg);
   for (int u = gw; u < p.rows; u += nwg * kWaves) route_row<C>(p, u, lane);
-  const int groups = (p.rows + kTokGroup - 1) / kTokGroup;
   const int nr = min(p.rows, nwg / 2);  // workgroups that route a row take no shared columns
   if (b < nr) return;
-  int lo, hi;
-  even_share(groups * C::S, b - nr, nwg - nr, lo, hi);
   const auto rs = ws_rsrc(p);
   const uint32_t qoff = C::FMT == kFp4 ? p.off[3] : p.off[1];
   const uint32_t soff = C::FMT == kFp4 ? p.off[4] : p.off[2];
+  int lo, hi;
+  if (p.rows >= p.mfma_gate) {
+    // MFMA: (16-row group, 8-column block) units dealt evenly
+    const int groups = (p.rows + kMfmaPicks - 1) / kMfmaPicks;
+    even_share(groups * (C::S / GuTile<C, kFp8>::NC), b - nr, nwg - nr, lo, hi);
+    gu_mfma<C, kFp8>(
+        sm, C::S, lo, hi,
+        [&](int tg, const uint8_t*& w, const void*& s, int& np) {
+          w = p.sgu;
+          s = p.sgu_s;
+          np = min(kMfmaPicks, p.rows - tg * kMfmaPicks);
+        },
+        [&](int tg, int np, const void* s) {
+          stage_x_lds<C>(p, sm.x, np, qoff, soff, [&](int r) { return tg * kMfmaPicks + r; }, (const float*)s,
+                         2 * C::S / 128 * (C::H / 128));
+        },
+        [&](int tg, int q, int col, float g, float u) {
+          dst16(rs, p.off[8] + ((uint32_t)(tg * kMfmaPicks + q) * C::S + col) * 2, f2bf(swiglu_shared(g, u, p.limit)));
+        });
+    return;
+  }
+  XTile<C>& xt = sm.x;
+  const int groups = (p.rows + kTokGroup - 1) / kTokGroup;
+  even_share(groups * C::S, b - nr, nwg - nr, lo, hi);
   for (int pos = lo; pos < hi;) {
     const int tg = pos / C::S, c0 = pos % C::S;
     const int c1 = min(C::S, c0 + (hi - pos));
@@ -1034,7 +1397,7 @@ __device__ __forceinline__ void stage_b(const Params& p, XTile<C>& xt, int b, in
           w = p.sgu;
           s = p.sgu_s;
         },
-        [&](XRegs<C>& xr) { xr.load(p, np, qoff, soff, [&](int r) { return t0 + r; }); },
+        [&](XRegs<C, kTokGroup>& xr) { xr.load(p, np, qoff, soff, [&](int r) { return t0 + r; }); },
         [&](int q, int col, float g, float u) {
           dst16(rs, p.off[8] + ((uint32_t)(t0 + q) * C::S + col) * 2, f2bf(swiglu_shared(g, u, p.limit)));
         });
@@ -1050,7 +1413,7 @@ struct Union {
   int slot_of[C::E];
   int slot_e[C::E];
   int slot_start[C::E + 1];
-  int tg_start[C::E + 1];       // a slot's first token group (groups of kTokGroup picks)
+  int tg_start[C::E + 1];       // a slot's first token group (kTokGroup picks, MFMA: kMfmaPicks)
   int tg_slot[kRowsMax * C::K];  // a token group's slot
   int picks[kRowsMax * C::K];
   float wts[kRowsMax * C::K];
@@ -1070,15 +1433,21 @@ __device__ __forceinline__ void build_union(const Params& p, Union<C>& un) {
   static_assert(kRowsMax <= 64, "row bitmaps");
   const int tid = threadIdx.x;
   const int npk = p.rows * C::K;
+  const int tgs = p.rows >= p.mfma_gate ? kMfmaPicks : kTokGroup;  // picks a token group
   const auto rs = ws_rsrc(p);
   __syncthreads();
   for (int e = tid; e < C::E; e += kThreads) un.rows_of[e][0] = un.rows_of[e][1] = 0u;
   __syncthreads();
-  for (int t = tid; t < npk; t += kThreads) {
-    const int e = min(max((int)dld32(rs, p.off[6] + t * 4), 0), C::E - 1);
+  // one pick a thread; its expert is kept for the placement below
+  static_assert(kRowsMax * C::K <= kThreads, "a pick a thread");
+  const int t = tid;
+  int my_e = 0;
+  if (t < npk) {
+    my_e = min(max((int)dld32(rs, p.off[6] + t * 4), 0), C::E - 1);
+    const float w = u2f(dld32(rs, p.off[7] + t * 4));
     const int r = t / C::K;
-    atomicOr(&un.rows_of[e][r >> 5], 1u << (r & 31));
-    un.wts[t] = u2f(dld32(rs, p.off[7] + t * 4));
+    atomicOr(&un.rows_of[my_e][r >> 5], 1u << (r & 31));
+    un.wts[t] = w;
   }
   __syncthreads();
   for (int e = tid; e < C::E; e += kThreads)
@@ -1093,7 +1462,7 @@ __device__ __forceinline__ void build_union(const Params& p, Union<C>& un) {
       if (e < C::E && un.cnt[e] > 0) {
         ns += 1;
         np += un.cnt[e];
-        ng += (un.cnt[e] + kTokGroup - 1) / kTokGroup;
+        ng += (un.cnt[e] + tgs - 1) / tgs;
       }
     }
     // exclusive prefix over lanes
@@ -1112,7 +1481,7 @@ __device__ __forceinline__ void build_union(const Params& p, Union<C>& un) {
       const int e = e0 + i;
       if (e < C::E && un.cnt[e] > 0) {
         const int c = un.cnt[e];
-        const int groups = (c + kTokGroup - 1) / kTokGroup;
+        const int groups = (c + tgs - 1) / tgs;
         un.slot_of[e] = s;
         un.slot_e[s] = e;
         un.slot_start[s] = pk;
@@ -1133,8 +1502,8 @@ __device__ __forceinline__ void build_union(const Params& p, Union<C>& un) {
   }
   __syncthreads();
   // a pick's place: its slot's start + the rows below its own that picked the same expert
-  for (int t = tid; t < npk; t += kThreads) {
-    const int e = min(max((int)dld32(rs, p.off[6] + t * 4), 0), C::E - 1);
+  if (t < npk) {
+    const int e = my_e;
     const int r = t / C::K;
     const uint32_t below0 = r >= 32 ? 0xffffffffu : (1u << r) - 1u;
     const uint32_t below1 = r >= 32 ? (1u << (r - 32)) - 1u : 0u;
@@ -1153,8 +1522,8 @@ __device__ __forceinline__ void build_union(const Params& p, Union<C>& un) {
       int c = 0;
       if (g < ntg) {
         const int sl = un.tg_slot[g];
-        const int j0 = un.slot_start[sl] + (g - un.tg_start[sl]) * kTokGroup;
-        c = kColCost<C> + min(kTokGroup, un.slot_start[sl + 1] - j0);
+        const int j0 = un.slot_start[sl] + (g - un.tg_start[sl]) * tgs;
+        c = kColCost<C> + min(tgs, un.slot_start[sl + 1] - j0);
       }
       loc[i] = c;
       sum += c;
@@ -1191,6 +1560,8 @@ struct DownRows {
   static constexpr int CE = FMT == kFp4 ? 32 : 16;  // elements a chunk
   static constexpr int CPR = KD / CE;
   static constexpr int CPL = CPR / kDownLanes;
+  // units a wave requests at once (MXFP4 rows of 1024 K: 6, leaving registers for the quant)
+  static constexpr int kBatch = CPL >= 8 ? 4 : (FMT == kFp4 && KD >= 1024 ? 6 : 8);
   static_assert(CPR % kDownLanes == 0, "down row chunks");
   u32x4 w[CPL];
   float sf[CPL];
@@ -1302,7 +1673,7 @@ struct DownRows {
 // batch may be requested ahead by the caller (first(rows)) before other work.
 template <class Rows>
 struct DownBatch {
-  static constexpr int B = Rows::CPL >= 8 ? 4 : 8;
+  static constexpr int B = Rows::kBatch;
   Rows r[B];
   int v0;
   template <class LoadFn>
@@ -1329,53 +1700,66 @@ __device__ __forceinline__ void down_pipeline(DownBatch<Rows>& bt, int n, LoadFn
 }
 
 // quantize bf16 rows [n][W] (workspace, sc1) into LDS codes [n][QS] and scales: group-128 fp8
-// (fp32 scales) or MXFP8 (E8M0 bytes); row i of the source starts at byte ``src_row(i)``
+// (fp32 scales) or MXFP8 (E8M0 bytes); row i of the source starts at byte ``src_row(i)``.
+// A thread's chunks (8 values each) are requested kQuantBatch at a time before any is
+// converted, so a batch costs one trip to memory.
+constexpr int kQuantBatch = 4;
 template <int FMT, int W, int QS, class RowFn>
 __device__ __forceinline__ void quant_rows_lds(const Params& p, RowFn src_row, int n, uint8_t* q, void* s) {
 #pragma clang fp contract(off)
   constexpr int PER = W / 8;  // 8-value chunks a row
+  static_assert(kThreads % PER == 0, "a thread keeps its column chunk");
   const int tid = threadIdx.x;
   const auto rs = ws_rsrc(p);
   // a wave's lanes cover consecutive chunks so that a group's lanes are adjacent
   const int total = n * PER;
-  for (int base = 0; base < total; base += kThreads) {
-    const int idx = base + tid;
-    const bool ok = idx < total;
-    const int i = ok ? idx / PER : 0, c = ok ? idx % PER : 0;
-    float v[8];
-    float am = 0.0f;
-    if (ok) {
-      u32x4 xv = dld128(rs, src_row(i) + c * 16);
-      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+  for (int base = 0; base < total; base += kQuantBatch * kThreads) {
+    u32x4 xv[kQuantBatch];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        v[2 * k] = bf_lo(xw[k]);
-        v[2 * k + 1] = bf_hi(xw[k]);
-      }
-#pragma unroll
-      for (int k = 0; k < 8; ++k) am = fabsf(v[k]) > am ? fabsf(v[k]) : am;
-    } else {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = 0.0f;
+    for (int k = 0; k < kQuantBatch; ++k) {
+      const int idx = base + k * kThreads + tid;
+      if (idx < total) xv[k] = dld128(rs, src_row(idx / PER) + (idx % PER) * 16);
     }
-    if constexpr (FMT == kFp8) {
-      float g = group_max<16>(am);
-      float sc = group_scale(g);
-      const uint32_t lo = e4m3_pack4(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
-      const uint32_t hi = e4m3_pack4(v[4] / sc, v[5] / sc, v[6] / sc, v[7] / sc);
+#pragma unroll
+    for (int k = 0; k < kQuantBatch; ++k) {
+      const int idx = base + k * kThreads + tid;
+      if (base + k * kThreads >= total) break;  // uniform: no chunk of this round is left
+      const bool ok = idx < total;
+      const int i = ok ? idx / PER : 0, c = ok ? idx % PER : 0;
+      float v[8];
+      float am = 0.0f;
       if (ok) {
-        *(u32x2*)(q + (size_t)i * QS + c * 8) = u32x2{lo, hi};
-        if ((c & 15) == 0) ((float*)s)[i * (W / 128) + c / 16] = sc;
+        const uint32_t xw[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[2 * j] = bf_lo(xw[j]);
+          v[2 * j + 1] = bf_hi(xw[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) am = fabsf(v[j]) > am ? fabsf(v[j]) : am;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = 0.0f;
       }
-    } else {
-      float g = group_max<4>(am);
-      int code = mx_code(g);
-      float inv = mx_inv(code);
-      const uint32_t lo = e4m3_pack4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
-      const uint32_t hi = e4m3_pack4(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
-      if (ok) {
-        *(u32x2*)(q + (size_t)i * QS + c * 8) = u32x2{lo, hi};
-        if ((c & 3) == 0) ((uint8_t*)s)[i * (W / 32) + c / 4] = (uint8_t)code;
+      if constexpr (FMT == kFp8) {
+        float g = group_max<16>(am);
+        float sc = group_scale(g);
+        const uint32_t lo = e4m3_pack4(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
+        const uint32_t hi = e4m3_pack4(v[4] / sc, v[5] / sc, v[6] / sc, v[7] / sc);
+        if (ok) {
+          *(u32x2*)(q + (size_t)i * QS + c * 8) = u32x2{lo, hi};
+          if ((c & 15) == 0) ((float*)s)[i * (W / 128) + c / 16] = sc;
+        }
+      } else {
+        float g = group_max<4>(am);
+        int code = mx_code(g);
+        float inv = mx_inv(code);
+        const uint32_t lo = e4m3_pack4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+        const uint32_t hi = e4m3_pack4(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
+        if (ok) {
+          *(u32x2*)(q + (size_t)i * QS + c * 8) = u32x2{lo, hi};
+          if ((c & 3) == 0) ((uint8_t*)s)[i * (W / 32) + c / 4] = (uint8_t)code;
+        }
       }
     }
   }
@@ -1463,7 +1847,7 @@ __device__ __forceinline__ void routed_gate_up(const Params& p, const Union<C>& 
             s = (const uint8_t*)p.w13_s + (size_t)e * 2 * C::I * (C::H / 32);
           }
         },
-        [&](XRegs<C>& xr) { xr.load(p, np, p.off[1], p.off[2], [&](int r) { return un.picks[j0 + r] / C::K; }); },
+        [&](XRegs<C, kTokGroup>& xr) { xr.load(p, np, p.off[1], p.off[2], [&](int r) { return un.picks[j0 + r] / C::K; }); },
         [&](int q, int col, float g, float u) {
           const int pk = un.picks[j0 + q];
           dst16(rs, p.off[9] + ((uint32_t)pk * C::I + col) * 2, f2bf(swiglu_routed(g, u, p.limit)));
@@ -1471,20 +1855,91 @@ __device__ __forceinline__ void routed_gate_up(const Params& p, const Union<C>& 
   }
 }
 
+// MFMA shared down for tile rows [h0, h0 + hn): units (16-row block, 16-row pick tile), one a
+// wave; bf16 results to the workspace
+template <class C>
+__device__ __forceinline__ void shared_down_tile_mfma(const Params& p, SharedDownSmem<C>& sm, int h0, int hn) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int R = p.rows;
+  const auto rs = ws_rsrc(p);
+  using DT = DownTile<kFp8, C::S>;
+  const int nb = (hn + 15) / 16, npt = (R + kMfmaPicks - 1) / kMfmaPicks;
+  DT dt;
+  const int n_units = nb * npt;
+  if (wave < n_units) {
+    const int rb = wave % nb;
+    dt.load(p.sw2, p.sw2_s, h0 + rb * 16, min(16, hn - rb * 16), lane);
+  }
+  __syncthreads();  // the previous user of the LDS is done
+  quant_rows_lds<kFp8, C::S, C::SQS>(
+      p, [&](int i) { return p.off[8] + (uint32_t)i * C::S * 2; }, R, sm.q, sm.s);
+  __syncthreads();
+  for (int v = wave; v < n_units; v += kWaves) {
+    const int rb = v % nb, pt = v / nb;
+    if (v != wave) dt.load(p.sw2, p.sw2_s, h0 + rb * 16, min(16, hn - rb * 16), lane);
+    const int t0 = pt * kMfmaPicks, np = min(kMfmaPicks, R - t0);
+    const f32x4 acc = dt.template mma<C::SQS, (C::S / 128) * 4>(sm.q, (const uint8_t*)sm.s, t0, np, lane);
+    const int n = lane & 15;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int hl = rb * 16 + 4 * (lane >> 4) + k;
+      if (n < np && hl < hn) dst16(rs, p.off[10] + ((uint32_t)(t0 + n) * C::H + h0 + hl) * 2, f2bf(acc[k]));
+    }
+  }
+}
+
+// MFMA routed gate_up: (token group, column block) units dealt evenly over the workgroups
+template <class C>
+__device__ __forceinline__ void routed_gate_up_mfma(const Params& p, const Union<C>& un, GuSmem<C>& sm, int b, int nwg) {
+  const auto rs = ws_rsrc(p);
+  int lo, hi;
+  even_share(un.ntg * (C::I / GuTile<C, C::FMT>::NC), b, nwg, lo, hi);
+  auto first = [&](int tg) {
+    const int slot = un.tg_slot[tg];
+    return un.slot_start[slot] + (tg - un.tg_start[slot]) * kMfmaPicks;
+  };
+  gu_mfma<C, C::FMT>(
+      sm, C::I, lo, hi,
+      [&](int tg, const uint8_t*& w, const void*& s, int& np) {
+        const int slot = un.tg_slot[tg];
+        const int e = un.slot_e[slot];
+        np = min(kMfmaPicks, un.slot_start[slot + 1] - first(tg));
+        if constexpr (C::FMT == kFp8) {
+          w = p.w13 + (size_t)e * 2 * C::I * C::H;
+          s = (const float*)p.w13_s + (size_t)e * (2 * C::I / 128) * (C::H / 128);
+        } else {
+          w = p.w13 + (size_t)e * 2 * C::I * (C::H / 2);
+          s = (const uint8_t*)p.w13_s + (size_t)e * 2 * C::I * (C::H / 32);
+        }
+      },
+      [&](int tg, int np, const void* s) {
+        const int j0 = first(tg);
+        stage_x_lds<C>(p, sm.x, np, p.off[1], p.off[2], [&](int r) { return un.picks[j0 + r] / C::K; },
+                       (const float*)s, C::FMT == kFp8 ? 2 * C::I / 128 * (C::H / 128) : 0);
+      },
+      [&](int tg, int q, int col, float g, float u) {
+        const int pk = un.picks[first(tg) + q];
+        dst16(rs, p.off[9] + ((uint32_t)pk * C::I + col) * 2, f2bf(swiglu_routed(g, u, p.limit)));
+      });
+}
+
 template <class C>
 union CSmem {
-  XTile<C> x;
+  GuSmem<C> g;
   SharedDownSmem<C> sd;
 };
 
 template <class C>
 __device__ __forceinline__ void stage_c(const Params& p, const Union<C>& un, CSmem<C>& sm, int b, int nwg) {
-  routed_gate_up<C>(p, un, sm.x, b, nwg);
+  if (p.rows >= p.mfma_gate) routed_gate_up_mfma<C>(p, un, sm.g, b, nwg);
+  else routed_gate_up<C>(p, un, sm.g.x, b, nwg);
+  const bool mf = p.rows >= p.mfma_down;
   const int tr = p.tile_rows;
   const int n_tiles = (C::H + tr - 1) / tr;
   for (int tile = b; tile < n_tiles; tile += nwg) {
     const int h0 = tile * tr;
-    shared_down_tile<C>(p, sm.sd, h0, min(tr, C::H - h0));
+    if (mf) shared_down_tile_mfma<C>(p, sm.sd, h0, min(tr, C::H - h0));
+    else shared_down_tile<C>(p, sm.sd, h0, min(tr, C::H - h0));
   }
 }
 
@@ -1494,43 +1949,94 @@ struct DownSmem {
   float contrib[kRowsMax * C::K * kTileMax];
   uint8_t q[C::PB * C::MQS];
   uint8_t s[C::PB * C::MSC * 4];
+  uint32_t shv[kRowsMax * kTileMax / 2];  // the shared expert's bf16 results of the tile
 };
 
+// the slots holding picks [pb0, pb0 + pbn) of the step (picks are stored slot by slot)
 template <class C>
-__device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn) {
-  const int tid = threadIdx.x, lane = tid & 63, g = lane / kDownLanes, l = lane % kDownLanes;
-  const int R = p.rows;
-  const int npk = R * C::K;
-  using DR = DownRows<C::FMT, C::I>;
+__device__ __forceinline__ void batch_slots(const Union<C>& un, int pb0, int pbn, int& s_lo, int& s_hi) {
+  int lo = 0, hi = un.n - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (un.slot_start[mid] <= pb0) lo = mid; else hi = mid - 1;
+  }
+  s_lo = lo;
+  s_hi = s_lo;
+  while (s_hi + 1 < un.n && un.slot_start[s_hi + 1] < pb0 + pbn) ++s_hi;
+}
+
+// the routed down GEMVs of tile rows [h0, h0 + hn) for every pick, into sm.contrib
+// (VALU, 8-row units of 8 lanes a row)
+template <class C>
+using DownRowsOf = DownRows<C::FMT, C::I>;
+template <class C>
+using DownTileOf = DownTile<C::FMT, C::I>;
+// the down stage's batch of units: MFMA (MF) or VALU
+template <class C, bool MF>
+using DownBatchOf = DownBatch<typename std::conditional<MF, DownTileOf<C>, DownRowsOf<C>>::type>;
+
+// loaders of the units of tile rows [h0, h0 + hn) for slots from s_lo: VALU units (slot,
+// 8-row block), MFMA units (slot, 16-row block)
+template <class C>
+__device__ __forceinline__ auto valu_down_loader(const Params& p, const Union<C>& un, int h0, int hn, int s_lo) {
+  const int lane = threadIdx.x & 63, g = lane / kDownLanes, l = lane % kDownLanes;
+  return [&p, &un, h0, hn, s_lo, g, l](int v, DownRowsOf<C>& wr) {
+    const int slot = s_lo + v / kRowBlocks, rb = v % kRowBlocks;
+    const int e = un.slot_e[slot];
+    const int hl = rb * kDownLanes + g;
+    const int h = h0 + hl;
+    const size_t row = (size_t)e * C::H + h;
+    if constexpr (C::FMT == kFp8)
+      wr.load(p.w2 + row * C::I,
+              (const float*)p.w2_s + (size_t)e * (C::H / 128) * (C::I / 128) + (size_t)(h / 128) * (C::I / 128), hl < hn,
+              l);
+    else
+      wr.load(p.w2 + row * (C::I / 2), (const uint8_t*)p.w2_s + row * (C::I / 32), hl < hn, l);
+  };
+}
+template <class C>
+__device__ __forceinline__ auto mfma_down_loader(const Params& p, const Union<C>& un, int h0, int hn, int s_lo) {
+  const int lane = threadIdx.x & 63;
+  const int nb = (hn + 15) / 16;
+  return [&p, &un, h0, hn, s_lo, nb, lane](int v, DownTileOf<C>& dt) {
+    const int slot = s_lo + v / nb, rb = v % nb;
+    const int e = un.slot_e[slot];
+    if constexpr (C::FMT == kFp8)
+      dt.load(p.w2 + (size_t)e * C::H * C::I, (const float*)p.w2_s + (size_t)e * (C::H / 128) * (C::I / 128),
+              h0 + rb * 16, min(16, hn - rb * 16), lane);
+    else
+      dt.load(p.w2 + (size_t)e * C::H * (C::I / 2), (const uint8_t*)p.w2_s + (size_t)e * C::H * (C::I / 32),
+              h0 + rb * 16, min(16, hn - rb * 16), lane);
+  };
+}
+
+// request the first pick batch's first units of tile rows [h0, h0 + hn); the down stage goes
+// on from them
+template <class C, bool MF>
+__device__ __forceinline__ void down_first(const Params& p, const Union<C>& un, int h0, int hn, DownBatchOf<C, MF>& bt) {
+  const int npk = p.rows * C::K;
+  int s_lo, s_hi;
+  batch_slots(un, 0, min(C::PB, npk), s_lo, s_hi);
+  const int wave = threadIdx.x >> 6;
+  if constexpr (MF) bt.load(wave, (s_hi - s_lo + 1) * ((hn + 15) / 16), mfma_down_loader<C>(p, un, h0, hn, s_lo));
+  else bt.load(wave, (s_hi - s_lo + 1) * kRowBlocks, valu_down_loader<C>(p, un, h0, hn, s_lo));
+}
+
+template <class C>
+__device__ __forceinline__ void down_valu(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
+                                          DownBatch<DownRowsOf<C>>& bt, bool first_ready) {
+  const int lane = threadIdx.x & 63, l = lane % kDownLanes, g = lane / kDownLanes;
+  const int npk = p.rows * C::K;
+  using DR = DownRowsOf<C>;
   constexpr int SST = C::FMT == kFp4 ? C::I / 32 : (C::I / 128) * 4;  // scale bytes of a pick
   for (int pb0 = 0; pb0 < npk; pb0 += C::PB) {
     const int pbn = min(C::PB, npk - pb0);
-    // slots with picks in [pb0, pb0 + pbn)
-    int lo = 0, hi = un.n - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (un.slot_start[mid] <= pb0) lo = mid; else hi = mid - 1;
-    }
-    const int s_lo = lo;
-    int s_hi = s_lo;
-    while (s_hi + 1 < un.n && un.slot_start[s_hi + 1] < pb0 + pbn) ++s_hi;
+    int s_lo, s_hi;
+    batch_slots(un, pb0, pbn, s_lo, s_hi);
     const int n_units = (s_hi - s_lo + 1) * kRowBlocks;
-    auto load = [&](int v, DR& wr) {
-      const int slot = s_lo + v / kRowBlocks, rb = v % kRowBlocks;
-      const int e = un.slot_e[slot];
-      const int hl = rb * kDownLanes + g;
-      const int h = h0 + hl;
-      const size_t row = (size_t)e * C::H + h;
-      if constexpr (C::FMT == kFp8)
-        wr.load(p.w2 + row * C::I,
-                (const float*)p.w2_s + (size_t)e * (C::H / 128) * (C::I / 128) + (size_t)(h / 128) * (C::I / 128),
-                hl < hn, l);
-      else
-        wr.load(p.w2 + row * (C::I / 2), (const uint8_t*)p.w2_s + row * (C::I / 32), hl < hn, l);
-    };
+    auto load = valu_down_loader<C>(p, un, h0, hn, s_lo);
     // the first batch's weights are requested before the picks' rows are quantized
-    DownBatch<DR> bt;
-    bt.load(threadIdx.x >> 6, n_units, load);
+    if (pb0 > 0 || !first_ready) bt.load(threadIdx.x >> 6, n_units, load);
     __syncthreads();  // the previous batch is done with the LDS rows
     quant_rows_lds<C::FMT, C::I, C::MQS>(
         p, [&](int i) { return p.off[9] + (uint32_t)un.picks[pb0 + i] * C::I * 2; }, pbn, sm.q, sm.s);
@@ -1553,9 +2059,72 @@ __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, D
       }
     });
   }
+}
+
+// the same on MFMA: units (slot, 16-row block), each against its slot's picks 16 at a time
+template <class C>
+__device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
+                                          DownBatch<DownTileOf<C>>& bt, bool first_ready) {
+  const int lane = threadIdx.x & 63;
+  const int npk = p.rows * C::K;
+  using DT = DownTileOf<C>;
+  constexpr int SST = C::FMT == kFp4 ? C::I / 32 : (C::I / 128) * 4;  // scale bytes of a pick
+  const int nb = (hn + 15) / 16;
+  for (int pb0 = 0; pb0 < npk; pb0 += C::PB) {
+    const int pbn = min(C::PB, npk - pb0);
+    int s_lo, s_hi;
+    batch_slots(un, pb0, pbn, s_lo, s_hi);
+    const int n_units = (s_hi - s_lo + 1) * nb;
+    auto load = mfma_down_loader<C>(p, un, h0, hn, s_lo);
+    if (pb0 > 0 || !first_ready) bt.load(threadIdx.x >> 6, n_units, load);
+    __syncthreads();  // the previous batch is done with the LDS rows
+    quant_rows_lds<C::FMT, C::I, C::MQS>(
+        p, [&](int i) { return p.off[9] + (uint32_t)un.picks[pb0 + i] * C::I * 2; }, pbn, sm.q, sm.s);
+    __syncthreads();
+    down_pipeline<DT>(bt, n_units, load, [&](int v, const DT& dt) {
+      const int slot = s_lo + v / nb, rb = v % nb;
+      const int j0 = max(un.slot_start[slot], pb0), j1 = min(un.slot_start[slot + 1], pb0 + pbn);
+      const int n = lane & 15;
+      for (int jj = j0; jj < j1; jj += kMfmaPicks) {
+        const int np = min(kMfmaPicks, j1 - jj);
+        const f32x4 acc = dt.template mma<C::MQS, SST>(sm.q, sm.s, jj - pb0, np, lane);
+        const int pk = n < np ? un.picks[jj + n] : 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int hl = rb * 16 + 4 * (lane >> 4) + k;
+          if (n < np && hl < hn) sm.contrib[pk * kTileMax + hl] = acc[k];
+        }
+      }
+    });
+  }
+}
+
+// tile rows [h0, h0 + hn): routed down GEMVs (MFMA or VALU), then the combine; first_ready:
+// the first pick batch's first units are already requested into bt
+template <class C, bool MF>
+__device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
+                                          DownBatchOf<C, MF>& bt, bool first_ready) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int R = p.rows;
+  // the shared expert's bf16 results of this tile (hn / 2 words a row), requested now straight
+  // into LDS for the combine; a wave's last lanes past the rows refill the padding from row 0
+  static_assert(kRowsMax * kTileMax / 2 % 64 == 0, "whole waves of words");
+  const auto rs = ws_rsrc(p);
+  {
+    const int wpr = hn / 2, total = R * wpr;
+    for (int k = wave; k * 64 < total; k += kWaves) {
+      const int idx = k * 64 + lane;
+      const bool ok = idx < total;
+      const int t = ok ? idx / wpr : 0, d = ok ? idx % wpr : 0;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(sm.shv + k * 64), 4,
+                                               p.off[10] + ((uint32_t)t * C::H + h0) * 2 + d * 4, 0, 0, kAuxDev);
+    }
+  }
+  if constexpr (MF) down_mfma<C>(p, un, sm, h0, hn, bt, first_ready);
+  else down_valu<C>(p, un, sm, h0, hn, bt, first_ready);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the LDS-direct words have landed
   __syncthreads();
   // ---- combine: top-k order, bf16 at every add, then + the shared expert's bf16 result
-  const auto rs = ws_rsrc(p);
   for (int idx = tid; idx < R * hn; idx += kThreads) {
     const int t = idx / hn, hl = idx % hn;
     float routed = 0.0f;
@@ -1564,20 +2133,34 @@ __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, D
       const int pk = t * C::K + k;
       routed = bf_round(routed + bf_round(sm.contrib[pk * kTileMax + hl] * un.wts[pk]));
     }
-    const float sh = bf2f((uint16_t)dld16(rs, p.off[10] + ((uint32_t)t * C::H + h0 + hl) * 2));
-    p.out[(size_t)t * C::H + h0 + hl] = f2bf(routed + sh);
+    p.out[(size_t)t * C::H + h0 + hl] = f2bf(routed + bf2f(((const uint16_t*)sm.shv)[idx]));
   }
   __syncthreads();
 }
 
-template <class C>
-__device__ __forceinline__ void stage_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg) {
+// this workgroup's tiles; first_ready: its first tile's first units are already requested
+template <class C, bool MF>
+__device__ __forceinline__ void stage_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg,
+                                        DownBatchOf<C, MF>& bt, bool first_ready) {
   const int tr = p.tile_rows;
   const int n_tiles = (C::H + tr - 1) / tr;
   for (int tile = b; tile < n_tiles; tile += nwg) {
     const int h0 = tile * tr;
-    down_tile<C>(p, un, sm, h0, min(tr, C::H - h0));
+    down_tile<C, MF>(p, un, sm, h0, min(tr, C::H - h0), bt, first_ready && tile == b);
   }
+}
+
+// the persistent launch past its C arrival: the down stage's first weights depend on the
+// union alone, so they are requested before the wait for the other workgroups' gate_up
+template <class C, bool MF>
+__device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg) {
+  DownBatchOf<C, MF> bt;
+  const int tr = p.tile_rows;
+  const bool first = b * tr < C::H;
+  if (first) down_first<C, MF>(p, un, b * tr, min(tr, C::H - b * tr), bt);
+  await_all(p, kCtlC, nwg, kStageC);
+  __syncthreads();  // the tile's readers are done before the down stage reuses its LDS
+  stage_d<C, MF>(p, un, sm, b, nwg, bt, first);
 }
 
 // ---------------------------------------------------------------- kernels
@@ -1585,7 +2168,7 @@ __device__ __forceinline__ void stage_d(const Params& p, const Union<C>& un, Dow
 template <class C>
 union StageSmem {
   RouterSmem<C> a;
-  XTile<C> x;
+  GuSmem<C> g;
   CSmem<C> c;
   DownSmem<C> d;
 };
@@ -1603,15 +2186,14 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   stage_a<C>(p, sm.a, b, nwg);
   arrive(p, kCtlA);
   await_all(p, kCtlA, nwg, kStageA);
-  stage_b<C>(p, sm.x, b, nwg);
+  stage_b<C>(p, sm.g, b, nwg);
   arrive(p, kCtlB);
   await_all(p, kCtlB, nwg, kStageB);
   build_union<C>(p, un);
   stage_c<C>(p, un, sm.c, b, nwg);
   arrive(p, kCtlC);
-  await_all(p, kCtlC, nwg, kStageC);
-  __syncthreads();  // the tile's readers are done before the down stage reuses its LDS
-  stage_d<C>(p, un, sm.d, b, nwg);
+  if (p.rows >= p.mfma_down) wait_then_d<C, true>(p, un, sm.d, b, nwg);
+  else wait_then_d<C, false>(p, un, sm.d, b, nwg);
   leave(p);
 }
 
@@ -1626,8 +2208,8 @@ __global__ __launch_bounds__(kThreads) void k_a(Params p) {
 }
 template <class C>
 __global__ __launch_bounds__(kThreads) void k_b(Params p) {
-  __shared__ XTile<C> xt;
-  stage_b<C>(p, xt, blockIdx.x, gridDim.x);
+  __shared__ GuSmem<C> sm;
+  stage_b<C>(p, sm, blockIdx.x, gridDim.x);
 }
 template <class C>
 __global__ __launch_bounds__(kThreads) void k_c(Params p) {
@@ -1641,7 +2223,13 @@ __global__ __launch_bounds__(kThreads) void k_d(Params p) {
   __shared__ Union<C> un;
   __shared__ DownSmem<C> sm;
   build_union<C>(p, un);
-  stage_d<C>(p, un, sm, blockIdx.x, gridDim.x);
+  if (p.rows >= p.mfma_down) {
+    DownBatchOf<C, true> bt;
+    stage_d<C, true>(p, un, sm, blockIdx.x, gridDim.x, bt, false);
+  } else {
+    DownBatchOf<C, false> bt;
+    stage_d<C, false>(p, un, sm, blockIdx.x, gridDim.x, bt, false);
+  }
 }
 
 // decode byte i as e4m3 (the fp8 convert the GEMVs use) and as two e2m1 (the fp4 convert)
@@ -1672,6 +2260,8 @@ struct DevInfo {
 std::mutex g_mu;
 DevInfo g_dev[64];
 double g_deadline_s = 2.0;
+int g_mfma_gate = kRowsMax + 1;  // gate_up: VALU at every row count
+int g_mfma_down = 8;
 
 int device_info(int dev, DevInfo* out) {
   std::lock_guard<std::mutex> lk(g_mu);
@@ -1799,6 +2389,11 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
     dl = g_deadline_s;
   }
   p.deadline = (unsigned long long)(dl * 1e8);
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    p.mfma_gate = g_mfma_gate;
+    p.mfma_down = g_mfma_down;
+  }
   for (int i = 0; i < kRegions; ++i) p.off[i] = (uint32_t)L.off[i];
   hipStream_t st = (hipStream_t)stream;
   switch (cfg_id(s)) {
@@ -1871,6 +2466,14 @@ int mkmoe_set_deadline(double seconds) {
   if (!(seconds > 0.0) || seconds > 3600.0) return MKMOE_ERR_ARG;
   std::lock_guard<std::mutex> lk(g_mu);
   g_deadline_s = seconds;
+  return MKMOE_OK;
+}
+
+int mkmoe_set_mfma_rows(int32_t gate_up_rows, int32_t down_rows) {
+  if (gate_up_rows < 1 || down_rows < 1) return MKMOE_ERR_ARG;
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_mfma_gate = gate_up_rows;
+  g_mfma_down = down_rows;
   return MKMOE_OK;
 }
 

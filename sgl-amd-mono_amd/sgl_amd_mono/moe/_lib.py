@@ -39,6 +39,7 @@ EXPORTS = (
     "mkmoe_forward",
     "mkmoe_forward_staged",
     "mkmoe_set_deadline",
+    "mkmoe_set_mfma_rows",
     "mkmoe_read_errors",
     "mkmoe_clear_errors",
     "mkmoe_workspace_region",
@@ -101,6 +102,7 @@ def lib() -> ctypes.CDLL:
         L.mkmoe_forward.argtypes = fwd
         L.mkmoe_forward_staged.argtypes = fwd
         L.mkmoe_set_deadline.argtypes = [ctypes.c_double]
+        L.mkmoe_set_mfma_rows.argtypes = [i32, i32]
         L.mkmoe_read_errors.argtypes = [vp, ctypes.POINTER(i32), i32, vp]
         L.mkmoe_clear_errors.argtypes = [vp, vp]
         L.mkmoe_workspace_region.argtypes = [sp, i32, ctypes.POINTER(sz), ctypes.POINTER(sz)]

@@ -230,3 +230,14 @@ class MoeRunner:
 
 def set_deadline(seconds: float) -> None:
     _lib.check(_lib.lib().mkmoe_set_deadline(seconds), "deadline")
+
+
+# the library's defaults: launches with at least this many rows run the gate_up / down GEMMs
+# on MFMA (gate_up: never; its MFMA operand layout streams weights slower than the VALU GEMVs)
+MFMA_GATE_ROWS, MFMA_DOWN_ROWS = 49, 8
+
+
+def set_mfma_rows(gate_up_rows: int = MFMA_GATE_ROWS, down_rows: int = MFMA_DOWN_ROWS) -> None:
+    """Launches with at least ``gate_up_rows`` (``down_rows``) rows run the gate_up (down) GEMMs
+    on MFMA; fewer rows run the fixed-order VALU GEMVs (bit-identical to the oracle)."""
+    _lib.check(_lib.lib().mkmoe_set_mfma_rows(int(gate_up_rows), int(down_rows)), "mfma rows")

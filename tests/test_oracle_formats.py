@@ -185,8 +185,14 @@ def test_weight_roundtrip_error(fmt):
 def test_host_library_exports():
     from sgl_amd_mono.moe import _lib
 
+    import re
+    from pathlib import Path
+
     L = _lib.lib()
     assert L.mkmoe_abi_version() == 1
+    header = (Path(__file__).resolve().parents[1] / "include" / "mkmoe.h").read_text()
+    declared = set(re.findall(r"^(?:int|void|const char\*)\s+(mkmoe_\w+)\(", header, re.M))
+    assert declared == set(_lib.EXPORTS), declared ^ set(_lib.EXPORTS)
     for name in _lib.EXPORTS:
         assert hasattr(L, name), name
     assert ctypes.c_char_p(L.mkmoe_status_string(-2)).value
