@@ -128,8 +128,8 @@ int mkmoe_forward(const mkmoe_shape* shape, const mkmoe_weights* w, const void* 
                   void* out, int32_t* topk_ids, float* topk_w, void* ws, size_t ws_bytes,
                   void* stream);
 
-/* The same results in one launch per stage (norm, router + quantize, route +
- * shared gate_up, shared down + routed gate_up, routed down + combine); for
+/* The same results in one launch per stage (norm, router + quantize, route,
+ * gate_up (routed and shared), down (shared and routed) + combine); for
  * diagnosis and per-stage profiles. */
 int mkmoe_forward_staged(const mkmoe_shape* shape, const mkmoe_weights* w, const void* x,
                          int32_t rows, void* out, int32_t* topk_ids, float* topk_w, void* ws,
@@ -155,7 +155,7 @@ int mkmoe_clear_errors(void* ws, void* stream);
  * 3 x codes (shared rule), 4 x scales (shared rule), 5 router part sums
  * fp32 [rows][E][parts], 6 ids int32 [rows][topk], 7 weights fp32
  * [rows][topk], 8 shared intermediate bf16 [rows][S], 9 routed intermediate
- * bf16 [rows * topk][I], 10 shared expert output bf16 [rows][H]. */
+ * bf16 [rows * topk][I]. */
 int mkmoe_workspace_region(const mkmoe_shape* shape, int32_t region, size_t* offset,
                            size_t* bytes);
 

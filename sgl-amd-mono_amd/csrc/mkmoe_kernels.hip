@@ -75,7 +75,7 @@ using CfgTp4Fp4 = Cfg<7168, 256, 8, 8, 4, 512, 512, kFp4, 7, false>;
 using CfgTp2Fp4Norm = Cfg<7168, 256, 8, 8, 4, 1024, 1024, kFp4, 7, true>;
 
 // ---------------------------------------------------------------- workspace layout
-constexpr int kRegions = 11;
+constexpr int kRegions = 10;
 
 struct Layout {
   size_t off[kRegions];
@@ -99,7 +99,6 @@ MKMOE_HD inline Layout make_layout(int H, int E, int K, int I, int S, int fmt, i
   sz[7] = (size_t)rm * K * 4;                                         // weights
   sz[8] = (size_t)rm * S * 2;                                         // shared mid, bf16
   sz[9] = (size_t)rm * K * I * 2;                                     // routed mid, bf16
-  sz[10] = (size_t)rm * H * 2;                                        // shared expert out, bf16
   size_t off = kCtlBytes;
   for (int i = 0; i < kRegions; ++i) {
     L.off[i] = off;
@@ -1350,62 +1349,20 @@ struct DownTile {
   }
 };
 
-// ---------------------------------------------------------------- stage B: routing + shared gate_up
-// routing: a wave per row (wave 0 of workgroups 0 .. R-1); the shared expert's gate_up: its
-// (8-row group, column) pairs dealt evenly over the other workgroups, each share run as one
-// or two units of consecutive columns of one group
+// ---------------------------------------------------------------- stage B: routing
+// a wave per row (wave 0 of workgroups 0 .. R-1)
 template <class C>
-__device__ __forceinline__ void stage_b(const Params& p, GuSmem<C>& sm, int b, int nwg) {
+__device__ __forceinline__ void stage_b(const Params& p, int b, int nwg) {
   const int lane = threadIdx.x & 63, gw = wave_slot(b, nwg);
   for (int u = gw; u < p.rows; u += nwg * kWaves) route_row<C>(p, u, lane);
-  const int nr = min(p.rows, nwg / 2);  // workgroups that route a row take no shared columns
-  if (b < nr) return;
-  const auto rs = ws_rsrc(p);
-  const uint32_t qoff = C::FMT == kFp4 ? p.off[3] : p.off[1];
-  const uint32_t soff = C::FMT == kFp4 ? p.off[4] : p.off[2];
-  int lo, hi;
-  if (p.rows >= p.mfma_gate) {
-    // MFMA: (16-row group, 8-column block) units dealt evenly
-    const int groups = (p.rows + kMfmaPicks - 1) / kMfmaPicks;
-    even_share(groups * (C::S / GuTile<C, kFp8>::NC), b - nr, nwg - nr, lo, hi);
-    gu_mfma<C, kFp8>(
-        sm, C::S, lo, hi,
-        [&](int tg, const uint8_t*& w, const void*& s, int& np) {
-          w = p.sgu;
-          s = p.sgu_s;
-          np = min(kMfmaPicks, p.rows - tg * kMfmaPicks);
-        },
-        [&](int tg, int np, const void* s) {
-          stage_x_lds<C>(p, sm.x, np, qoff, soff, [&](int r) { return tg * kMfmaPicks + r; }, (const float*)s,
-                         2 * C::S / 128 * (C::H / 128));
-        },
-        [&](int tg, int q, int col, float g, float u) {
-          dst16(rs, p.off[8] + ((uint32_t)(tg * kMfmaPicks + q) * C::S + col) * 2, f2bf(swiglu_shared(g, u, p.limit)));
-        });
-    return;
-  }
-  XTile<C>& xt = sm.x;
-  const int groups = (p.rows + kTokGroup - 1) / kTokGroup;
-  even_share(groups * C::S, b - nr, nwg - nr, lo, hi);
-  for (int pos = lo; pos < hi;) {
-    const int tg = pos / C::S, c0 = pos % C::S;
-    const int c1 = min(C::S, c0 + (hi - pos));
-    const int t0 = tg * kTokGroup, np = min(kTokGroup, p.rows - t0);
-    gu_unit<C, kFp8>(
-        p, xt, np, C::S, c0, c1 - c0,
-        [&](const uint8_t*& w, const void*& s) {
-          w = p.sgu;
-          s = p.sgu_s;
-        },
-        [&](XRegs<C, kTokGroup>& xr) { xr.load(p, np, qoff, soff, [&](int r) { return t0 + r; }); },
-        [&](int q, int col, float g, float u) {
-          dst16(rs, p.off[8] + ((uint32_t)(t0 + q) * C::S + col) * 2, f2bf(swiglu_shared(g, u, p.limit)));
-        });
-    pos += c1 - c0;
-  }
 }
 
 // ---------------------------------------------------------------- the step's union (LDS)
+// token groups of a step at most: the routed ones (one a pick at most), then the shared
+// expert's (its rows in groups of kTokGroup)
+template <class C>
+constexpr int kMaxGroups = kRowsMax * C::K + kRowsMax / kTokGroup;
+
 template <class C>
 struct Union {
   uint32_t rows_of[C::E][2];  // rows (bit r) that picked expert e
@@ -1413,18 +1370,20 @@ struct Union {
   int slot_of[C::E];
   int slot_e[C::E];
   int slot_start[C::E + 1];
-  int tg_start[C::E + 1];       // a slot's first token group (kTokGroup picks, MFMA: kMfmaPicks)
-  int tg_slot[kRowsMax * C::K];  // a token group's slot
+  int tg_start[C::E + 1];          // a slot's first token group (kTokGroup picks, MFMA: kMfmaPicks)
+  int tg_slot[kMaxGroups<C>];      // a routed token group's slot
   int picks[kRowsMax * C::K];
   float wts[kRowsMax * C::K];
-  int tg_cost[kRowsMax * C::K + 1];  // gate_up cost of the token groups before g, a column
+  int tg_cost[kMaxGroups<C> + 1];  // gate_up cost of the token groups before g, a column
   int n;
+  int ntg_r;  // routed token groups: [0, ntg_r); the shared expert's: [ntg_r, ntg)
   int ntg;
 };
 
-// a gate_up column's cost: its weight loads plus its picks' arithmetic (one per pick)
-template <class C>
-constexpr int kColCost = C::FMT == kFp4 ? 2 : 3;
+// a gate_up column's cost in units of one pick's arithmetic: its weight loads (kColCost) plus
+// one per pick. Fitted to per-workgroup gate_up times at 8 and 48 rows (FP8 and MXFP4 alike:
+// 0.33-0.35 us a column + 0.17-0.19 us a column-pick, i.e. a column costs 1.9 picks)
+constexpr int kColCost = 2;
 
 // experts picked by any row (ascending id), their picks (pick = row * K + k; a slot's picks
 // in row order, the same in every workgroup) and token groups
@@ -1497,7 +1456,8 @@ __device__ __forceinline__ void build_union(const Params& p, Union<C>& un) {
       un.n = is;
       un.slot_start[is] = ip;
       un.tg_start[is] = ig;
-      un.ntg = ig;
+      un.ntg_r = ig;
+      un.ntg = ig + (p.rows + tgs - 1) / tgs;
     }
   }
   __syncthreads();
@@ -1512,18 +1472,20 @@ __device__ __forceinline__ void build_union(const Params& p, Union<C>& un) {
   }
   // each token group's cost a column, prefix-summed over the groups
   if (tid < 64) {
-    constexpr int GPL = (kRowsMax * C::K + 63) / 64;  // groups a lane
-    const int ntg = un.ntg;
+    constexpr int GPL = (kMaxGroups<C> + 63) / 64;  // groups a lane
+    const int ntg = un.ntg, ntg_r = un.ntg_r;
     int loc[GPL];
     int sum = 0;
 #pragma unroll
     for (int i = 0; i < GPL; ++i) {
       const int g = tid * GPL + i;
       int c = 0;
-      if (g < ntg) {
+      if (g < ntg_r) {
         const int sl = un.tg_slot[g];
         const int j0 = un.slot_start[sl] + (g - un.tg_start[sl]) * tgs;
-        c = kColCost<C> + min(tgs, un.slot_start[sl + 1] - j0);
+        c = kColCost + min(tgs, un.slot_start[sl + 1] - j0);
+      } else if (g < ntg) {
+        c = kColCost + min(tgs, p.rows - (g - ntg_r) * tgs);
       }
       loc[i] = c;
       sum += c;
@@ -1768,55 +1730,103 @@ __device__ __forceinline__ void quant_rows_lds(const Params& p, RowFn src_row, i
 // row blocks of 8 in a down tile (rows past the tile masked)
 constexpr int kRowBlocks = kTileMax / kDownLanes;
 
-// ---------------------------------------------------------------- stage C: shared down + routed gate_up
+// ---------------------------------------------------------------- stage C: gate_up
+// the shared expert's down GEMV for tile rows [h0, h0 + hn) of every row (VALU: units of an
+// 8-row block and kPickBlock rows; MFMA: a 16-row block and 16 rows), into the tile's bf16
+// results; the shared intermediate is quantized into LDS first
 template <class C>
 struct SharedDownSmem {
   uint8_t q[kRowsMax * C::SQS];
   float s[kRowsMax * (C::S / 128)];
 };
 
-// the shared expert's down GEMV for tile rows [h0, h0 + hn) of every row: units (8-row
-// block, block of kPickBlock rows); bf16 results to the workspace
-template <class C>
-__device__ __forceinline__ void shared_down_tile(const Params& p, SharedDownSmem<C>& sm, int h0, int hn) {
+// the shared down's units a wave requests at once: up to 8 KB of codes
+template <class Rows>
+struct Batched : Rows {
+  static constexpr int kBatch = Rows::kBatch < 2 ? Rows::kBatch : 2;
+};
+template <class C, bool MF>
+using SharedDownBatch =
+    DownBatch<Batched<typename std::conditional<MF, DownTile<kFp8, C::S>, DownRows<kFp8, C::S>>::type>>;
+
+// loader of the shared down's units of tile rows [h0, h0 + hn)
+template <class C, bool MF>
+__device__ __forceinline__ auto shared_down_loader(const Params& p, int h0, int hn) {
+  const int lane = threadIdx.x & 63, g = lane / kDownLanes, l = lane % kDownLanes;
+  if constexpr (MF) {
+    const int nb = (hn + 15) / 16;
+    return [&p, h0, hn, nb, lane](int v, DownTile<kFp8, C::S>& dt) {
+      const int rb = v % nb;
+      dt.load(p.sw2, p.sw2_s, h0 + rb * 16, min(16, hn - rb * 16), lane);
+    };
+  } else {
+    return [&p, h0, hn, g, l](int v, DownRows<kFp8, C::S>& wr) {
+      const int rb = v % kRowBlocks;
+      const int h = h0 + rb * kDownLanes + g;
+      wr.load(p.sw2 + (size_t)h * C::S, p.sw2_s + (size_t)(h / 128) * (C::S / 128), rb * kDownLanes + g < hn, l);
+    };
+  }
+}
+template <class C, bool MF>
+__device__ __forceinline__ int shared_down_units(int R, int hn) {
+  if constexpr (MF) return ((hn + 15) / 16) * ((R + kMfmaPicks - 1) / kMfmaPicks);
+  else return kRowBlocks * ((R + kPickBlock - 1) / kPickBlock);
+}
+
+// the shared down of tile rows [h0, h0 + hn) into out[t * hn + hl] (bf16); first_ready: the
+// first units are already requested into bt
+template <class C, bool MF>
+__device__ __forceinline__ void shared_down_tile(const Params& p, SharedDownSmem<C>& sm, uint16_t* out, int h0, int hn,
+                                                 SharedDownBatch<C, MF>& bt, bool first_ready) {
   const int lane = threadIdx.x & 63, g = lane / kDownLanes, l = lane % kDownLanes;
   const int R = p.rows;
-  const auto rs = ws_rsrc(p);
+  const int n_units = shared_down_units<C, MF>(R, hn);
+  auto load = shared_down_loader<C, MF>(p, h0, hn);
+  if (!first_ready) bt.load(threadIdx.x >> 6, n_units, load);
   __syncthreads();  // the previous user of the LDS is done
   quant_rows_lds<kFp8, C::S, C::SQS>(
       p, [&](int i) { return p.off[8] + (uint32_t)i * C::S * 2; }, R, sm.q, sm.s);
   __syncthreads();
-  using DR = DownRows<kFp8, C::S>;
-  const int npb = (R + kPickBlock - 1) / kPickBlock;
-  auto load = [&](int v, DR& wr) {
-    const int rb = v % kRowBlocks;
-    const int h = h0 + rb * kDownLanes + g;
-    const bool ok = rb * kDownLanes + g < hn;
-    wr.load(p.sw2 + (size_t)h * C::S, p.sw2_s + (size_t)(h / 128) * (C::S / 128), ok, l);
-  };
-  DownBatch<DR> bt;
-  bt.load(threadIdx.x >> 6, kRowBlocks * npb, load);
-  down_pipeline<DR>(bt, kRowBlocks * npb, load, [&](int v, const DR& wr) {
-    const int rb = v % kRowBlocks, pb = v / kRowBlocks;
-    if (rb * kDownLanes >= hn) return;
-    const int t0 = pb * kPickBlock, np = min(kPickBlock, R - t0);
-    float acc[kPickBlock];
-    wr.template dot<C::SQS, (C::S / 128) * 4>(sm.q + (size_t)t0 * C::SQS, (const uint8_t*)(sm.s + t0 * (C::S / 128)), np, l, acc);
-    const int hl = rb * kDownLanes + g;
+  if constexpr (MF) {
+    using DT = Batched<DownTile<kFp8, C::S>>;
+    const int nb = (hn + 15) / 16;
+    down_pipeline<DT>(bt, n_units, load, [&](int v, const DT& dt) {
+      const int rb = v % nb, pt = v / nb;
+      const int t0 = pt * kMfmaPicks, np = min(kMfmaPicks, R - t0);
+      const f32x4 acc = dt.template mma<C::SQS, (C::S / 128) * 4>(sm.q, (const uint8_t*)sm.s, t0, np, lane);
+      const int n = lane & 15;
 #pragma unroll
-    for (int q = 0; q < kPickBlock; ++q) {
-      const float y = tree_sum<kDownLanes>(acc[q]);
-      if (q < np && l == 0 && hl < hn)
-        dst16(rs, p.off[10] + ((uint32_t)(t0 + q) * C::H + h0 + hl) * 2, f2bf(y));
-    }
-  });
+      for (int k = 0; k < 4; ++k) {
+        const int hl = rb * 16 + 4 * (lane >> 4) + k;
+        if (n < np && hl < hn) out[(t0 + n) * hn + hl] = f2bf(acc[k]);
+      }
+    });
+  } else {
+    using DR = Batched<DownRows<kFp8, C::S>>;
+    down_pipeline<DR>(bt, n_units, load, [&](int v, const DR& wr) {
+      const int rb = v % kRowBlocks, pb = v / kRowBlocks;
+      if (rb * kDownLanes >= hn) return;
+      const int t0 = pb * kPickBlock, np = min(kPickBlock, R - t0);
+      float acc[kPickBlock];
+      wr.template dot<C::SQS, (C::S / 128) * 4>(sm.q + (size_t)t0 * C::SQS, (const uint8_t*)(sm.s + t0 * (C::S / 128)), np, l,
+                                                acc);
+      const int hl = rb * kDownLanes + g;
+#pragma unroll
+      for (int q = 0; q < kPickBlock; ++q) {
+        const float y = tree_sum<kDownLanes>(acc[q]);
+        if (q < np && l == 0 && hl < hn) out[(t0 + q) * hn + hl] = f2bf(y);
+      }
+    });
+  }
 }
 
-// routed gate_up: the (token group, column) pairs of the step dealt over the workgroups in
-// equal shares of cost (a column costs its loads plus one per pick: kColCost + picks);
-// column j of group g belongs to the share holding its first cost unit
+// gate_up of the step's token groups, routed and shared (the shared expert's rows count as
+// groups of their own after the routed ones): the (group, column) pairs dealt over the
+// workgroups in equal shares of cost (a column costs kColCost + its picks); column j of group
+// g belongs to the share holding its first cost unit
 template <class C>
-__device__ __forceinline__ void routed_gate_up(const Params& p, const Union<C>& un, XTile<C>& xt, int b, int nwg) {
+__device__ __forceinline__ void gate_up_valu(const Params& p, const Union<C>& un, XTile<C>& xt, int b, int nwg) {
+  static_assert(C::S == C::I, "shared and routed columns deal alike");
   const long long total = (long long)un.tg_cost[un.ntg] * C::I;
   const long long lo = total * b / nwg, hi = total * (b + 1) / nwg;
   const auto rs = ws_rsrc(p);
@@ -1832,6 +1842,23 @@ __device__ __forceinline__ void routed_gate_up(const Params& p, const Union<C>& 
     const int c0 = lo > base ? (int)min((lo - base + cg - 1) / cg, (long long)C::I) : 0;
     const int c1 = (int)min((hi - base + cg - 1) / cg, (long long)C::I);
     if (c1 <= c0) continue;
+    if (tgg >= un.ntg_r) {
+      // the shared expert (FP8) for rows t0 .. t0 + np - 1
+      const int t0 = (tgg - un.ntg_r) * kTokGroup, np = min(kTokGroup, p.rows - t0);
+      const uint32_t qoff = C::FMT == kFp4 ? p.off[3] : p.off[1];
+      const uint32_t soff = C::FMT == kFp4 ? p.off[4] : p.off[2];
+      gu_unit<C, kFp8>(
+          p, xt, np, C::S, c0, c1 - c0,
+          [&](const uint8_t*& w, const void*& s) {
+            w = p.sgu;
+            s = p.sgu_s;
+          },
+          [&](XRegs<C, kTokGroup>& xr) { xr.load(p, np, qoff, soff, [&](int r) { return t0 + r; }); },
+          [&](int q, int col, float g, float u) {
+            dst16(rs, p.off[8] + ((uint32_t)(t0 + q) * C::S + col) * 2, f2bf(swiglu_shared(g, u, p.limit)));
+          });
+      continue;
+    }
     const int slot = un.tg_slot[tgg];
     const int e = un.slot_e[slot];
     const int j0 = un.slot_start[slot] + (tgg - un.tg_start[slot]) * kTokGroup;
@@ -1855,45 +1882,33 @@ __device__ __forceinline__ void routed_gate_up(const Params& p, const Union<C>& 
   }
 }
 
-// MFMA shared down for tile rows [h0, h0 + hn): units (16-row block, 16-row pick tile), one a
-// wave; bf16 results to the workspace
+// the same on MFMA: the shared expert's (16-row group, column block) units dealt evenly, then
+// the routed ones
 template <class C>
-__device__ __forceinline__ void shared_down_tile_mfma(const Params& p, SharedDownSmem<C>& sm, int h0, int hn) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int R = p.rows;
-  const auto rs = ws_rsrc(p);
-  using DT = DownTile<kFp8, C::S>;
-  const int nb = (hn + 15) / 16, npt = (R + kMfmaPicks - 1) / kMfmaPicks;
-  DT dt;
-  const int n_units = nb * npt;
-  if (wave < n_units) {
-    const int rb = wave % nb;
-    dt.load(p.sw2, p.sw2_s, h0 + rb * 16, min(16, hn - rb * 16), lane);
-  }
-  __syncthreads();  // the previous user of the LDS is done
-  quant_rows_lds<kFp8, C::S, C::SQS>(
-      p, [&](int i) { return p.off[8] + (uint32_t)i * C::S * 2; }, R, sm.q, sm.s);
-  __syncthreads();
-  for (int v = wave; v < n_units; v += kWaves) {
-    const int rb = v % nb, pt = v / nb;
-    if (v != wave) dt.load(p.sw2, p.sw2_s, h0 + rb * 16, min(16, hn - rb * 16), lane);
-    const int t0 = pt * kMfmaPicks, np = min(kMfmaPicks, R - t0);
-    const f32x4 acc = dt.template mma<C::SQS, (C::S / 128) * 4>(sm.q, (const uint8_t*)sm.s, t0, np, lane);
-    const int n = lane & 15;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int hl = rb * 16 + 4 * (lane >> 4) + k;
-      if (n < np && hl < hn) dst16(rs, p.off[10] + ((uint32_t)(t0 + n) * C::H + h0 + hl) * 2, f2bf(acc[k]));
-    }
-  }
-}
-
-// MFMA routed gate_up: (token group, column block) units dealt evenly over the workgroups
-template <class C>
-__device__ __forceinline__ void routed_gate_up_mfma(const Params& p, const Union<C>& un, GuSmem<C>& sm, int b, int nwg) {
+__device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un, GuSmem<C>& sm, int b, int nwg) {
   const auto rs = ws_rsrc(p);
   int lo, hi;
-  even_share(un.ntg * (C::I / GuTile<C, C::FMT>::NC), b, nwg, lo, hi);
+  {
+    const uint32_t qoff = C::FMT == kFp4 ? p.off[3] : p.off[1];
+    const uint32_t soff = C::FMT == kFp4 ? p.off[4] : p.off[2];
+    const int groups = (p.rows + kMfmaPicks - 1) / kMfmaPicks;
+    even_share(groups * (C::S / GuTile<C, kFp8>::NC), b, nwg, lo, hi);
+    gu_mfma<C, kFp8>(
+        sm, C::S, lo, hi,
+        [&](int tg, const uint8_t*& w, const void*& s, int& np) {
+          w = p.sgu;
+          s = p.sgu_s;
+          np = min(kMfmaPicks, p.rows - tg * kMfmaPicks);
+        },
+        [&](int tg, int np, const void* s) {
+          stage_x_lds<C>(p, sm.x, np, qoff, soff, [&](int r) { return tg * kMfmaPicks + r; }, (const float*)s,
+                         2 * C::S / 128 * (C::H / 128));
+        },
+        [&](int tg, int q, int col, float g, float u) {
+          dst16(rs, p.off[8] + ((uint32_t)(tg * kMfmaPicks + q) * C::S + col) * 2, f2bf(swiglu_shared(g, u, p.limit)));
+        });
+  }
+  even_share(un.ntg_r * (C::I / GuTile<C, C::FMT>::NC), b, nwg, lo, hi);
   auto first = [&](int tg) {
     const int slot = un.tg_slot[tg];
     return un.slot_start[slot] + (tg - un.tg_start[slot]) * kMfmaPicks;
@@ -1924,32 +1939,23 @@ __device__ __forceinline__ void routed_gate_up_mfma(const Params& p, const Union
 }
 
 template <class C>
-union CSmem {
-  GuSmem<C> g;
-  SharedDownSmem<C> sd;
-};
-
-template <class C>
-__device__ __forceinline__ void stage_c(const Params& p, const Union<C>& un, CSmem<C>& sm, int b, int nwg) {
-  if (p.rows >= p.mfma_gate) routed_gate_up_mfma<C>(p, un, sm.g, b, nwg);
-  else routed_gate_up<C>(p, un, sm.g.x, b, nwg);
-  const bool mf = p.rows >= p.mfma_down;
-  const int tr = p.tile_rows;
-  const int n_tiles = (C::H + tr - 1) / tr;
-  for (int tile = b; tile < n_tiles; tile += nwg) {
-    const int h0 = tile * tr;
-    if (mf) shared_down_tile_mfma<C>(p, sm.sd, h0, min(tr, C::H - h0));
-    else shared_down_tile<C>(p, sm.sd, h0, min(tr, C::H - h0));
-  }
+__device__ __forceinline__ void stage_c(const Params& p, const Union<C>& un, GuSmem<C>& sm, int b, int nwg) {
+  if (p.rows >= p.mfma_gate) gate_up_mfma<C>(p, un, sm, b, nwg);
+  else gate_up_valu<C>(p, un, sm.x, b, nwg);
 }
 
-// ---------------------------------------------------------------- stage D: routed down + combine
+// ---------------------------------------------------------------- stage D: shared and routed down + combine
 template <class C>
 struct DownSmem {
   float contrib[kRowsMax * C::K * kTileMax];
-  uint8_t q[C::PB * C::MQS];
-  uint8_t s[C::PB * C::MSC * 4];
-  uint32_t shv[kRowsMax * kTileMax / 2];  // the shared expert's bf16 results of the tile
+  union {
+    struct {
+      uint8_t q[C::PB * C::MQS];
+      uint8_t s[C::PB * C::MSC * 4];
+    };
+    SharedDownSmem<C> sd;  // the shared down's quantized rows, done before the routed ones
+  };
+  uint16_t shv[kRowsMax * kTileMax];  // the shared expert's bf16 results of the tile
 };
 
 // the slots holding picks [pb0, pb0 + pbn) of the step (picks are stored slot by slot)
@@ -2008,18 +2014,6 @@ __device__ __forceinline__ auto mfma_down_loader(const Params& p, const Union<C>
       dt.load(p.w2 + (size_t)e * C::H * (C::I / 2), (const uint8_t*)p.w2_s + (size_t)e * C::H * (C::I / 32),
               h0 + rb * 16, min(16, hn - rb * 16), lane);
   };
-}
-
-// request the first pick batch's first units of tile rows [h0, h0 + hn); the down stage goes
-// on from them
-template <class C, bool MF>
-__device__ __forceinline__ void down_first(const Params& p, const Union<C>& un, int h0, int hn, DownBatchOf<C, MF>& bt) {
-  const int npk = p.rows * C::K;
-  int s_lo, s_hi;
-  batch_slots(un, 0, min(C::PB, npk), s_lo, s_hi);
-  const int wave = threadIdx.x >> 6;
-  if constexpr (MF) bt.load(wave, (s_hi - s_lo + 1) * ((hn + 15) / 16), mfma_down_loader<C>(p, un, h0, hn, s_lo));
-  else bt.load(wave, (s_hi - s_lo + 1) * kRowBlocks, valu_down_loader<C>(p, un, h0, hn, s_lo));
 }
 
 template <class C>
@@ -2099,30 +2093,32 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
   }
 }
 
-// tile rows [h0, h0 + hn): routed down GEMVs (MFMA or VALU), then the combine; first_ready:
-// the first pick batch's first units are already requested into bt
+// request the first pick batch's first units of tile rows [h0, h0 + hn); the down stage goes
+// on from them
+template <class C, bool MF>
+__device__ __forceinline__ void down_first(const Params& p, const Union<C>& un, int h0, int hn, DownBatchOf<C, MF>& bt) {
+  const int npk = p.rows * C::K;
+  int s_lo, s_hi;
+  batch_slots(un, 0, min(C::PB, npk), s_lo, s_hi);
+  const int wave = threadIdx.x >> 6;
+  if constexpr (MF) bt.load(wave, (s_hi - s_lo + 1) * ((hn + 15) / 16), mfma_down_loader<C>(p, un, h0, hn, s_lo));
+  else bt.load(wave, (s_hi - s_lo + 1) * kRowBlocks, valu_down_loader<C>(p, un, h0, hn, s_lo));
+}
+
+// tile rows [h0, h0 + hn): the routed down GEMVs (MFMA or VALU, as MF), the shared expert's
+// down, then the combine; first_ready: the routed down's first units are already requested
+// into bt
 template <class C, bool MF>
 __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
                                           DownBatchOf<C, MF>& bt, bool first_ready) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   const int R = p.rows;
-  // the shared expert's bf16 results of this tile (hn / 2 words a row), requested now straight
-  // into LDS for the combine; a wave's last lanes past the rows refill the padding from row 0
-  static_assert(kRowsMax * kTileMax / 2 % 64 == 0, "whole waves of words");
-  const auto rs = ws_rsrc(p);
-  {
-    const int wpr = hn / 2, total = R * wpr;
-    for (int k = wave; k * 64 < total; k += kWaves) {
-      const int idx = k * 64 + lane;
-      const bool ok = idx < total;
-      const int t = ok ? idx / wpr : 0, d = ok ? idx % wpr : 0;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(sm.shv + k * 64), 4,
-                                               p.off[10] + ((uint32_t)t * C::H + h0) * 2 + d * 4, 0, 0, kAuxDev);
-    }
-  }
   if constexpr (MF) down_mfma<C>(p, un, sm, h0, hn, bt, first_ready);
   else down_valu<C>(p, un, sm, h0, hn, bt, first_ready);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the LDS-direct words have landed
+  {
+    SharedDownBatch<C, MF> bs;
+    shared_down_tile<C, MF>(p, sm.sd, sm.shv, h0, hn, bs, false);
+  }
   __syncthreads();
   // ---- combine: top-k order, bf16 at every add, then + the shared expert's bf16 result
   for (int idx = tid; idx < R * hn; idx += kThreads) {
@@ -2133,20 +2129,23 @@ __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, D
       const int pk = t * C::K + k;
       routed = bf_round(routed + bf_round(sm.contrib[pk * kTileMax + hl] * un.wts[pk]));
     }
-    p.out[(size_t)t * C::H + h0 + hl] = f2bf(routed + bf2f(((const uint16_t*)sm.shv)[idx]));
+    p.out[(size_t)t * C::H + h0 + hl] = f2bf(routed + bf2f(sm.shv[idx]));
   }
   __syncthreads();
 }
 
-// this workgroup's tiles; first_ready: its first tile's first units are already requested
+// this workgroup's tiles; first_ready: its first tile's first routed units are already requested
 template <class C, bool MF>
 __device__ __forceinline__ void stage_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg,
                                         DownBatchOf<C, MF>& bt, bool first_ready) {
   const int tr = p.tile_rows;
   const int n_tiles = (C::H + tr - 1) / tr;
-  for (int tile = b; tile < n_tiles; tile += nwg) {
-    const int h0 = tile * tr;
-    down_tile<C, MF>(p, un, sm, h0, min(tr, C::H - h0), bt, first_ready && tile == b);
+  if (b < n_tiles) down_tile<C, MF>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt, first_ready);
+  // further tiles (fewer workgroups than tiles) start from batches of their own, so that bt
+  // is free once the first tile's routed down is done
+  for (int tile = b + nwg; tile < n_tiles; tile += nwg) {
+    DownBatchOf<C, MF> bl;
+    down_tile<C, MF>(p, un, sm, tile * tr, min(tr, C::H - tile * tr), bl, false);
   }
 }
 
@@ -2169,7 +2168,6 @@ template <class C>
 union StageSmem {
   RouterSmem<C> a;
   GuSmem<C> g;
-  CSmem<C> c;
   DownSmem<C> d;
 };
 
@@ -2186,11 +2184,11 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   stage_a<C>(p, sm.a, b, nwg);
   arrive(p, kCtlA);
   await_all(p, kCtlA, nwg, kStageA);
-  stage_b<C>(p, sm.g, b, nwg);
+  stage_b<C>(p, b, nwg);
   arrive(p, kCtlB);
   await_all(p, kCtlB, nwg, kStageB);
   build_union<C>(p, un);
-  stage_c<C>(p, un, sm.c, b, nwg);
+  stage_c<C>(p, un, sm.g, b, nwg);
   arrive(p, kCtlC);
   if (p.rows >= p.mfma_down) wait_then_d<C, true>(p, un, sm.d, b, nwg);
   else wait_then_d<C, false>(p, un, sm.d, b, nwg);
@@ -2208,13 +2206,12 @@ __global__ __launch_bounds__(kThreads) void k_a(Params p) {
 }
 template <class C>
 __global__ __launch_bounds__(kThreads) void k_b(Params p) {
-  __shared__ GuSmem<C> sm;
-  stage_b<C>(p, sm, blockIdx.x, gridDim.x);
+  stage_b<C>(p, blockIdx.x, gridDim.x);
 }
 template <class C>
 __global__ __launch_bounds__(kThreads) void k_c(Params p) {
   __shared__ Union<C> un;
-  __shared__ CSmem<C> sm;
+  __shared__ GuSmem<C> sm;
   build_union<C>(p, un);
   stage_c<C>(p, un, sm, blockIdx.x, gridDim.x);
 }

@@ -26,9 +26,8 @@ REGIONS = {
     "weights": 7,
     "shared_mid": 8,
     "mid": 9,
-    "shared_out": 10,
 }
-STAGES = {1: "norm", 2: "router + quantize", 3: "route + shared gate_up", 4: "shared down + routed gate_up", 5: "routed down + combine"}
+STAGES = {1: "norm", 2: "router + quantize", 3: "route", 4: "gate_up (routed + shared)", 5: "down (shared + routed) + combine"}
 
 # every symbol include/mkmoe.h declares
 EXPORTS = (
