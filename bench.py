@@ -83,11 +83,14 @@ def make_layer(preset, g, device):
     )  # fmt: skip
 
 
-def time_rows(runner, layers, preset, rows, steps, warmup, device, g):
-    """Replay a graph of one step per layer; -> (µs per step, bytes per step, U per step)."""
+def time_rows(runner, layers, preset, rows, steps, warmup, device):
+    """Replay a graph of one step per layer; -> (µs per step, bytes per step, U per step).
+    The rows are seeded by their count alone, so a row count's sample (and its union of
+    experts) is the same whichever other row counts the run times."""
     import torch
 
     L = len(layers)
+    g = torch.Generator(device=device).manual_seed(1000 + rows)
     xs = [torch.randn(rows, preset.hidden, generator=g, device=device).to(torch.bfloat16) for _ in range(L)]
     outs = [torch.empty(rows, preset.hidden, dtype=torch.bfloat16, device=device) for _ in range(L)]
     ids = [torch.empty(rows, preset.topk, dtype=torch.int32, device=device) for _ in range(L)]
@@ -243,7 +246,7 @@ def main() -> int:
         runner.moe = lambda *a, **k: orig(*a, staged=True, **k)
     res = {}
     for r in rows_list:
-        us, b, unions, n = time_rows(runner, layers, preset, r, args.steps, args.warmup, device, g)
+        us, b, unions, n = time_rows(runner, layers, preset, r, args.steps, args.warmup, device)
         gbps = b / (us * 1e-6) / 1e9
         res[r] = {
             "us_per_layer": round(us, 2),

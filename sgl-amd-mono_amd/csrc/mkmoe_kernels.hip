@@ -1663,10 +1663,10 @@ __device__ __forceinline__ void down_pipeline(DownBatch<Rows>& bt, int n, LoadFn
 
 // quantize bf16 rows [n][W] (workspace, sc1) into LDS codes [n][QS] and scales: group-128 fp8
 // (fp32 scales) or MXFP8 (E8M0 bytes); row i of the source starts at byte ``src_row(i)``.
-// A thread's chunks (8 values each) are requested kQuantBatch at a time before any is
+// A thread's chunks (8 values each) are requested NB at a time before any is
 // converted, so a batch costs one trip to memory.
 constexpr int kQuantBatch = 4;
-template <int FMT, int W, int QS, class RowFn>
+template <int FMT, int W, int QS, int NB = kQuantBatch, class RowFn>
 __device__ __forceinline__ void quant_rows_lds(const Params& p, RowFn src_row, int n, uint8_t* q, void* s) {
 #pragma clang fp contract(off)
   constexpr int PER = W / 8;  // 8-value chunks a row
@@ -1675,15 +1675,15 @@ __device__ __forceinline__ void quant_rows_lds(const Params& p, RowFn src_row, i
   const auto rs = ws_rsrc(p);
   // a wave's lanes cover consecutive chunks so that a group's lanes are adjacent
   const int total = n * PER;
-  for (int base = 0; base < total; base += kQuantBatch * kThreads) {
-    u32x4 xv[kQuantBatch];
+  for (int base = 0; base < total; base += NB * kThreads) {
+    u32x4 xv[NB];
 #pragma unroll
-    for (int k = 0; k < kQuantBatch; ++k) {
+    for (int k = 0; k < NB; ++k) {
       const int idx = base + k * kThreads + tid;
       if (idx < total) xv[k] = dld128(rs, src_row(idx / PER) + (idx % PER) * 16);
     }
 #pragma unroll
-    for (int k = 0; k < kQuantBatch; ++k) {
+    for (int k = 0; k < NB; ++k) {
       const int idx = base + k * kThreads + tid;
       if (base + k * kThreads >= total) break;  // uniform: no chunk of this round is left
       const bool ok = idx < total;
@@ -2072,7 +2072,7 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
     auto load = mfma_down_loader<C>(p, un, h0, hn, s_lo);
     if (pb0 > 0 || !first_ready) bt.load(threadIdx.x >> 6, n_units, load);
     __syncthreads();  // the previous batch is done with the LDS rows
-    quant_rows_lds<C::FMT, C::I, C::MQS>(
+    quant_rows_lds<C::FMT, C::I, C::MQS, 2 * kQuantBatch>(
         p, [&](int i) { return p.off[9] + (uint32_t)un.picks[pb0 + i] * C::I * 2; }, pbn, sm.q, sm.s);
     __syncthreads();
     down_pipeline<DT>(bt, n_units, load, [&](int v, const DT& dt) {
