@@ -513,32 +513,43 @@ __device__ __forceinline__ void stage_a(const Params& p, RouterSmem<C>& sm, int 
 }
 
 // ---------------------------------------------------------------- stage B: routing
+// the scores and choices of every expert for one row, spread over the workgroup
 template <class C>
-__device__ __forceinline__ void route_row(const Params& p, int r, int lane) {
+struct RouteSmem {
+  float sc[C::E];
+  float ch[C::E];
+};
+
+// row r's routing by one workgroup: every thread sums an expert's part sums in order and takes
+// its sigmoid score and choice (score + bias) into LDS; wave 0 then selects
+template <class C>
+__device__ __forceinline__ void route_row(const Params& p, RouteSmem<C>& sm, int r) {
 #pragma clang fp contract(off)
   constexpr int EPL = (C::E + 63) / 64;
+  const int tid = threadIdx.x, lane = tid & 63;
   const auto rs = ws_rsrc(p);
   const uint32_t part0 = p.off[5] + (uint32_t)r * C::E * C::P * 4;
+  for (int e = tid; e < C::E; e += kThreads) {
+    float logit = 0.0f;
+#pragma unroll
+    for (int q = 0; q < C::P; ++q) logit = logit + u2f(dld32(rs, part0 + (e * C::P + q) * 4));
+    // a NaN score weighs 0 and its choice never wins (as the reference's route)
+    const float sg = sigmoid_exact(logit);
+    const float s = sg != sg ? 0.0f : sg;
+    const float cv = s + p.bias[e];
+    sm.sc[e] = s;
+    sm.ch[e] = cv != cv ? -INFINITY : cv;
+  }
+  __syncthreads();
+  if (tid >= 64) return;
   float sc[EPL], ch[EPL];
   bool alive[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     const int e = lane + 64 * i;
-    if (e < C::E) {
-      float logit = 0.0f;
-#pragma unroll
-      for (int q = 0; q < C::P; ++q) logit = logit + u2f(dld32(rs, part0 + (e * C::P + q) * 4));
-      // a NaN score weighs 0 and its choice never wins (as the reference's route)
-      const float sg = sigmoid_exact(logit);
-      sc[i] = sg != sg ? 0.0f : sg;
-      const float cv = sc[i] + p.bias[e];
-      ch[i] = cv != cv ? -INFINITY : cv;
-      alive[i] = true;
-    } else {
-      sc[i] = 0.0f;
-      ch[i] = -INFINITY;
-      alive[i] = false;
-    }
+    alive[i] = e < C::E;
+    sc[i] = alive[i] ? sm.sc[e] : 0.0f;
+    ch[i] = alive[i] ? sm.ch[e] : -INFINITY;
   }
   if constexpr (C::NG > 1) {
     constexpr int GS = C::E / C::NG;  // experts a group
@@ -1350,11 +1361,13 @@ struct DownTile {
 };
 
 // ---------------------------------------------------------------- stage B: routing
-// a wave per row (wave 0 of workgroups 0 .. R-1)
+// a workgroup per row (workgroups 0 .. R-1)
 template <class C>
-__device__ __forceinline__ void stage_b(const Params& p, int b, int nwg) {
-  const int lane = threadIdx.x & 63, gw = wave_slot(b, nwg);
-  for (int u = gw; u < p.rows; u += nwg * kWaves) route_row<C>(p, u, lane);
+__device__ __forceinline__ void stage_b(const Params& p, RouteSmem<C>& sm, int b, int nwg) {
+  for (int r = b; r < p.rows; r += nwg) {
+    __syncthreads();  // the previous row's selection is done with the LDS
+    route_row<C>(p, sm, r);
+  }
 }
 
 // ---------------------------------------------------------------- the step's union (LDS)
@@ -1827,20 +1840,20 @@ __device__ __forceinline__ void shared_down_tile(const Params& p, SharedDownSmem
 template <class C>
 __device__ __forceinline__ void gate_up_valu(const Params& p, const Union<C>& un, XTile<C>& xt, int b, int nwg) {
   static_assert(C::S == C::I, "shared and routed columns deal alike");
-  const long long total = (long long)un.tg_cost[un.ntg] * C::I;
-  const long long lo = total * b / nwg, hi = total * (b + 1) / nwg;
+  const int total = un.tg_cost[un.ntg] * C::I;
+  const int lo = (int)((long long)total * b / nwg), hi = (int)((long long)total * (b + 1) / nwg);
   const auto rs = ws_rsrc(p);
   // the last group that starts at or before lo
   int gl = 0, gh = un.ntg - 1;
   while (gl < gh) {
     const int mid = (gl + gh + 1) >> 1;
-    if ((long long)un.tg_cost[mid] * C::I <= lo) gl = mid; else gh = mid - 1;
+    if (un.tg_cost[mid] * C::I <= lo) gl = mid; else gh = mid - 1;
   }
-  for (int tgg = gl; tgg < un.ntg && (long long)un.tg_cost[tgg] * C::I < hi; ++tgg) {
-    const long long base = (long long)un.tg_cost[tgg] * C::I;
+  for (int tgg = gl; tgg < un.ntg && un.tg_cost[tgg] * C::I < hi; ++tgg) {
+    const int base = un.tg_cost[tgg] * C::I;
     const int cg = un.tg_cost[tgg + 1] - un.tg_cost[tgg];
-    const int c0 = lo > base ? (int)min((lo - base + cg - 1) / cg, (long long)C::I) : 0;
-    const int c1 = (int)min((hi - base + cg - 1) / cg, (long long)C::I);
+    const int c0 = lo > base ? min((lo - base + cg - 1) / cg, C::I) : 0;
+    const int c1 = hi > base ? min((hi - base + cg - 1) / cg, C::I) : 0;
     if (c1 <= c0) continue;
     if (tgg >= un.ntg_r) {
       // the shared expert (FP8) for rows t0 .. t0 + np - 1
@@ -2167,6 +2180,7 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
 template <class C>
 union StageSmem {
   RouterSmem<C> a;
+  RouteSmem<C> r;
   GuSmem<C> g;
   DownSmem<C> d;
 };
@@ -2184,7 +2198,7 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   stage_a<C>(p, sm.a, b, nwg);
   arrive(p, kCtlA);
   await_all(p, kCtlA, nwg, kStageA);
-  stage_b<C>(p, b, nwg);
+  stage_b<C>(p, sm.r, b, nwg);
   arrive(p, kCtlB);
   await_all(p, kCtlB, nwg, kStageB);
   build_union<C>(p, un);
@@ -2206,7 +2220,8 @@ __global__ __launch_bounds__(kThreads) void k_a(Params p) {
 }
 template <class C>
 __global__ __launch_bounds__(kThreads) void k_b(Params p) {
-  stage_b<C>(p, blockIdx.x, gridDim.x);
+  __shared__ RouteSmem<C> sm;
+  stage_b<C>(p, sm, blockIdx.x, gridDim.x);
 }
 template <class C>
 __global__ __launch_bounds__(kThreads) void k_c(Params p) {
