@@ -513,145 +513,206 @@ __device__ __forceinline__ void stage_a(const Params& p, RouterSmem<C>& sm, int 
 }
 
 // ---------------------------------------------------------------- stage B: routing
-// the scores and choices of every expert for one row, spread over the workgroup
+// Scores and choices of kRouteRows rows at a time, in LDS
+constexpr int kRouteRows = 16;
+// rows up to which every workgroup routes the whole step itself (no routing hand-off)
+constexpr int kLocalRouteMax = 16;
+
 template <class C>
 struct RouteSmem {
-  float sc[C::E];
-  float ch[C::E];
+  float sc[kRouteRows][C::E];
+  float ch[kRouteRows][C::E];
 };
 
-// row r's routing by one workgroup: every thread sums an expert's part sums in order and takes
-// its sigmoid score and choice (score + bias) into LDS; wave 0 then selects
+// max over aligned groups of G lanes (G a power of two <= 64), in every lane of the group;
+// inputs are never NaN. Across 16-lane rows: permlane16_swap(v, v) returns rows (0, 0, 2, 2)
+// and (1, 1, 3, 3), permlane32_swap(v, v) lanes 0-31 twice and 32-63 twice
+template <int G>
+__device__ __forceinline__ float segment_max(float v) {
+  if constexpr (G <= 16) {
+    return group_max<G>(v);
+  } else {
+    v = group_max<16>(v);
+    const int iv = __float_as_int(v);
+    const auto s = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+    const float a = __int_as_float((int)s[0]), c = __int_as_float((int)s[1]);
+    v = a > c ? a : c;
+    if constexpr (G == 64) {
+      const int jv = __float_as_int(v);
+      const auto t = __builtin_amdgcn_permlane32_swap(jv, jv, false, false);
+      const float d = __int_as_float((int)t[0]), f = __int_as_float((int)t[1]);
+      v = d > f ? d : f;
+    }
+    return v;
+  }
+}
+
+// scores and choices of (row r0 + i, expert e) for i < n, spread over the workgroup: the
+// logit sums the router's part sums in part order; a NaN score weighs 0 and its choice
+// (score + bias) never wins, as in the reference's route
 template <class C>
-__device__ __forceinline__ void route_row(const Params& p, RouteSmem<C>& sm, int r) {
+__device__ __forceinline__ void route_scores(const Params& p, RouteSmem<C>& sm, int r0, int n) {
 #pragma clang fp contract(off)
-  constexpr int EPL = (C::E + 63) / 64;
-  const int tid = threadIdx.x, lane = tid & 63;
   const auto rs = ws_rsrc(p);
-  const uint32_t part0 = p.off[5] + (uint32_t)r * C::E * C::P * 4;
-  for (int e = tid; e < C::E; e += kThreads) {
+  for (int idx = threadIdx.x; idx < n * C::E; idx += kThreads) {
+    const int i = idx / C::E, e = idx - i * C::E;
+    const uint32_t part0 = p.off[5] + ((uint32_t)(r0 + i) * C::E + e) * C::P * 4;
     float logit = 0.0f;
 #pragma unroll
-    for (int q = 0; q < C::P; ++q) logit = logit + u2f(dld32(rs, part0 + (e * C::P + q) * 4));
-    // a NaN score weighs 0 and its choice never wins (as the reference's route)
+    for (int q = 0; q < C::P; ++q) logit = logit + u2f(dld32(rs, part0 + q * 4));
     const float sg = sigmoid_exact(logit);
     const float s = sg != sg ? 0.0f : sg;
     const float cv = s + p.bias[e];
-    sm.sc[e] = s;
-    sm.ch[e] = cv != cv ? -INFINITY : cv;
+    sm.sc[i][e] = s;
+    sm.ch[i][e] = cv != cv ? -INFINITY : cv;
   }
-  __syncthreads();
-  if (tid >= 64) return;
+}
+
+// one row's grouped top-k by one wave, from its scores sc and choices ch in LDS. Lane l holds
+// experts l + 64 i. Group score = top-1 + top-2 choice of the group; the topk_group best groups
+// (larger score, then lower group); then topk experts of those groups, one a round: the largest
+// choice over the wave, and of the experts holding it the lowest id (a ballot), which is the
+// order "larger choice, then lower id". Lane k < topk returns pick k's id and weight.
+template <class C>
+__device__ __forceinline__ void select_row(const Params& p, const float* sc_row, const float* ch_row,
+                                           int lane, int& my_id, float& my_w) {
+#pragma clang fp contract(off)
+  constexpr int EPL = (C::E + 63) / 64;
   float sc[EPL], ch[EPL];
   bool alive[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     const int e = lane + 64 * i;
     alive[i] = e < C::E;
-    sc[i] = alive[i] ? sm.sc[e] : 0.0f;
-    ch[i] = alive[i] ? sm.ch[e] : -INFINITY;
+    sc[i] = alive[i] ? sc_row[e] : 0.0f;
+    ch[i] = alive[i] ? ch_row[e] : -INFINITY;
   }
   if constexpr (C::NG > 1) {
     constexpr int GS = C::E / C::NG;  // experts a group
-    static_assert(GS <= 64 && (64 % GS) == 0, "group size");
+    static_assert(GS >= 2 && GS <= 64 && (64 % GS) == 0, "group size");
     constexpr int GPI = 64 / GS;  // groups a 64-expert slice
+    const uint64_t seg = GS == 64 ? ~0ull : (((1ull << GS) - 1ull) << ((lane / GS) * GS));
     float gsv[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
-      // segmented top-2 over the GS lanes of this group: (value, lowest lane) of the max
-      float v1 = ch[i];
-      int l1 = lane;
-#pragma unroll
-      for (int d = GS / 2; d >= 1; d >>= 1) {
-        float ov = __shfl_xor(v1, d);
-        int ol = __shfl_xor(l1, d);
-        if (ov > v1 || (ov == v1 && ol < l1)) {
-          v1 = ov;
-          l1 = ol;
-        }
-      }
-      float v2 = lane == l1 ? -INFINITY : ch[i];
-#pragma unroll
-      for (int d = GS / 2; d >= 1; d >>= 1) {
-        float ov = __shfl_xor(v2, d);
-        v2 = ov > v2 ? ov : v2;
-      }
-      gsv[i] = v1 + v2;
+      // top-1 of the group, then top-2: top-1 again when two experts hold it, else the max
+      // of the others (the groups never mix live and dead lanes: E is a multiple of GS)
+      const float m1 = segment_max<GS>(ch[i]);
+      const uint64_t eq = __ballot(ch[i] == m1);
+      const float m2 = segment_max<GS>(ch[i] == m1 ? -INFINITY : ch[i]);
+      const float v2 = __popcll(eq & seg) >= 2 ? m1 : m2;
+      gsv[i] = m1 + v2;
     }
-    // every lane: the group scores, then the topk_group best groups
+    // lane g < NG takes group g's score and counts the groups ranked above it
     float gs[C::NG];
 #pragma unroll
-    for (int g = 0; g < C::NG; ++g) gs[g] = __shfl(gsv[g / GPI], (g % GPI) * GS);
-    uint64_t gmask = 0;
+    for (int g = 0; g < C::NG; ++g) gs[g] = lane_value(gsv[g / GPI], (g % GPI) * GS);
+    float mine = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < C::TG; ++t) {
-      int best = -1;
-      float bv = -INFINITY;
+    for (int g = 0; g < C::NG; ++g) mine = lane == g ? gs[g] : mine;
+    int above = 0;
 #pragma unroll
-      for (int g = 0; g < C::NG; ++g) {
-        bool free_g = ((gmask >> g) & 1ull) == 0ull;
-        if (free_g && (best < 0 || better(gs[g], g, bv, best))) {
-          best = g;
-          bv = gs[g];
-        }
-      }
-      gmask |= 1ull << best;
-    }
+    for (int g = 0; g < C::NG; ++g) above += better(gs[g], g, mine, lane) ? 1 : 0;
+    const uint64_t gkeep = __ballot(lane < C::NG && above < C::TG);
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
       const int e = lane + 64 * i;
-      alive[i] = alive[i] && ((gmask >> (e / GS)) & 1ull) != 0ull;
+      alive[i] = alive[i] && ((gkeep >> (e / GS)) & 1ull) != 0ull;
     }
   }
+  float val[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) val[i] = alive[i] ? ch[i] : -INFINITY;
   float total = 0.0f;
-  int my_id = 0;
-  float my_w = 0.0f;
+  my_id = 0;
+  my_w = 0.0f;
   for (int k = 0; k < C::K; ++k) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+    float lm = val[0];
+#pragma unroll
+    for (int i = 1; i < EPL; ++i) lm = val[i] > lm ? val[i] : lm;
+    const float m = lane_value(segment_max<64>(lm), 0);
+    int wi = -1, wl = 0;
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
-      const int e = lane + 64 * i;
-      if (alive[i] && (bi == 0x7fffffff || better(ch[i], e, bv, bi))) {
-        bv = ch[i];
-        bi = e;
+      const uint64_t hit = __ballot(alive[i] && ch[i] == m);
+      if (wi < 0 && hit != 0ull) {
+        wi = i;
+        wl = __builtin_ctzll(hit);
       }
     }
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-      float ov = __shfl_xor(bv, d);
-      int oi = __shfl_xor(bi, d);
-      if (better(ov, oi, bv, bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    bi = bi < 0 || bi >= C::E ? 0 : bi;  // unreachable with >= topk candidates; keeps ids in range
-    // the winner's owner lane retires it and hands out its score
+    wi = wi < 0 ? 0 : wi;  // unreachable with >= topk candidates; keeps ids in range
     float ws = 0.0f;
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
-      if (lane + 64 * i == bi) {
-        alive[i] = false;
-        ws = sc[i];
+      if (i == wi) {
+        ws = lane_value(sc[i], wl);
+        if (lane == wl) {
+          alive[i] = false;
+          val[i] = -INFINITY;
+        }
       }
     }
-    ws = __shfl(ws, bi & 63);
     total = total + ws;
     if (lane == k) {
-      my_id = bi;
+      my_id = min(wl + 64 * wi, C::E - 1);
       my_w = ws;
     }
   }
   float f = p.scale;
   if (p.renorm) f = p.scale / (total > 1e-20f ? total : 1e-20f);
+  my_w = my_w * f;
+}
+
+// row r's routing by one workgroup (stage B), written to the workspace and the outputs
+template <class C>
+__device__ __forceinline__ void route_row(const Params& p, RouteSmem<C>& sm, int r) {
+  const int lane = threadIdx.x & 63;
+  route_scores<C>(p, sm, r, 1);
+  __syncthreads();
+  if (threadIdx.x >= 64) return;
+  int id;
+  float w;
+  select_row<C>(p, sm.sc[0], sm.ch[0], lane, id, w);
   if (lane < C::K) {
-    const float w = my_w * f;
-    dst32(rs, p.off[6] + (r * C::K + lane) * 4, (uint32_t)my_id);
+    const auto rs = ws_rsrc(p);
+    dst32(rs, p.off[6] + (r * C::K + lane) * 4, (uint32_t)id);
     dst32(rs, p.off[7] + (r * C::K + lane) * 4, f2u(w));
-    if (p.ids_out) p.ids_out[r * C::K + lane] = my_id;
+    if (p.ids_out) p.ids_out[r * C::K + lane] = id;
     if (p.w_out) p.w_out[r * C::K + lane] = w;
   }
+}
+
+// every row's routing in this workgroup, into LDS (ids, wts: [rows][topk]); wave w selects
+// rows w, w + 8, ... of each kRouteRows chunk. Workgroup 0 also writes the workspace copies
+// and the outputs.
+template <class C>
+__device__ __forceinline__ void route_all(const Params& p, RouteSmem<C>& sm, int* ids, float* wts,
+                                          int b) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const auto rs = ws_rsrc(p);
+  for (int r0 = 0; r0 < p.rows; r0 += kRouteRows) {
+    const int n = min(kRouteRows, p.rows - r0);
+    __syncthreads();  // the previous chunk's selections are done with the LDS
+    route_scores<C>(p, sm, r0, n);
+    __syncthreads();
+    for (int i = wave; i < n; i += kWaves) {
+      int id;
+      float w;
+      select_row<C>(p, sm.sc[i], sm.ch[i], lane, id, w);
+      const int r = r0 + i;
+      if (lane < C::K) {
+        ids[r * C::K + lane] = id;
+        wts[r * C::K + lane] = w;
+        if (b == 0) {
+          dst32(rs, p.off[6] + (r * C::K + lane) * 4, (uint32_t)id);
+          dst32(rs, p.off[7] + (r * C::K + lane) * 4, f2u(w));
+          if (p.ids_out) p.ids_out[r * C::K + lane] = id;
+          if (p.w_out) p.w_out[r * C::K + lane] = w;
+        }
+      }
+    }
+  }
+  __syncthreads();
 }
 
 // ---------------------------------------------------------------- VALU GEMV of weight rows
@@ -1386,6 +1447,7 @@ struct Union {
   int tg_start[C::E + 1];          // a slot's first token group (kTokGroup picks, MFMA: kMfmaPicks)
   int tg_slot[kMaxGroups<C>];      // a routed token group's slot
   int picks[kRowsMax * C::K];
+  int ids[kRowsMax * C::K];  // pick -> expert (row * topk + k)
   float wts[kRowsMax * C::K];
   int tg_cost[kMaxGroups<C> + 1];  // gate_up cost of the token groups before g, a column
   int n;
@@ -1399,9 +1461,10 @@ struct Union {
 constexpr int kColCost = 2;
 
 // experts picked by any row (ascending id), their picks (pick = row * K + k; a slot's picks
-// in row order, the same in every workgroup) and token groups
+// in row order, the same in every workgroup) and token groups. The routing comes from
+// un.ids / un.wts when this workgroup routed the step itself (local), else from the workspace.
 template <class C>
-__device__ __forceinline__ void build_union(const Params& p, Union<C>& un) {
+__device__ __forceinline__ void build_union(const Params& p, Union<C>& un, bool local) {
   static_assert(kRowsMax <= 64, "row bitmaps");
   const int tid = threadIdx.x;
   const int npk = p.rows * C::K;
@@ -1415,11 +1478,14 @@ __device__ __forceinline__ void build_union(const Params& p, Union<C>& un) {
   const int t = tid;
   int my_e = 0;
   if (t < npk) {
-    my_e = min(max((int)dld32(rs, p.off[6] + t * 4), 0), C::E - 1);
-    const float w = u2f(dld32(rs, p.off[7] + t * 4));
+    if (local) {
+      my_e = un.ids[t];
+    } else {
+      my_e = min(max((int)dld32(rs, p.off[6] + t * 4), 0), C::E - 1);
+      un.wts[t] = u2f(dld32(rs, p.off[7] + t * 4));
+    }
     const int r = t / C::K;
     atomicOr(&un.rows_of[my_e][r >> 5], 1u << (r & 31));
-    un.wts[t] = w;
   }
   __syncthreads();
   for (int e = tid; e < C::E; e += kThreads)
@@ -2198,10 +2264,16 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   stage_a<C>(p, sm.a, b, nwg);
   arrive(p, kCtlA);
   await_all(p, kCtlA, nwg, kStageA);
-  stage_b<C>(p, sm.r, b, nwg);
-  arrive(p, kCtlB);
-  await_all(p, kCtlB, nwg, kStageB);
-  build_union<C>(p, un);
+  if (p.rows <= kLocalRouteMax) {
+    // every workgroup routes the step itself: no routing hand-off
+    route_all<C>(p, sm.r, un.ids, un.wts, b);
+    build_union<C>(p, un, true);
+  } else {
+    stage_b<C>(p, sm.r, b, nwg);
+    arrive(p, kCtlB);
+    await_all(p, kCtlB, nwg, kStageB);
+    build_union<C>(p, un, false);
+  }
   stage_c<C>(p, un, sm.g, b, nwg);
   arrive(p, kCtlC);
   if (p.rows >= p.mfma_down) wait_then_d<C, true>(p, un, sm.d, b, nwg);
@@ -2227,14 +2299,14 @@ template <class C>
 __global__ __launch_bounds__(kThreads) void k_c(Params p) {
   __shared__ Union<C> un;
   __shared__ GuSmem<C> sm;
-  build_union<C>(p, un);
+  build_union<C>(p, un, false);
   stage_c<C>(p, un, sm, blockIdx.x, gridDim.x);
 }
 template <class C>
 __global__ __launch_bounds__(kThreads) void k_d(Params p) {
   __shared__ Union<C> un;
   __shared__ DownSmem<C> sm;
-  build_union<C>(p, un);
+  build_union<C>(p, un, false);
   if (p.rows >= p.mfma_down) {
     DownBatchOf<C, true> bt;
     stage_d<C, true>(p, un, sm, blockIdx.x, gridDim.x, bt, false);
