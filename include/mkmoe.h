@@ -153,7 +153,7 @@ int mkmoe_clear_errors(void* ws, void* stream);
 /* Byte offset and size of a workspace region, for tests that read
  * intermediate results: 0 x normed, 1 x codes (routed rule), 2 x scales,
  * 3 x codes (shared rule), 4 x scales (shared rule), 5 router part sums
- * fp32 [rows][E][parts], 6 ids int32 [rows][topk], 7 weights fp32
+ * fp32 [rows][parts][E], 6 ids int32 [rows][topk], 7 weights fp32
  * [rows][topk], 8 shared intermediate bf16 [rows][S], 9 routed intermediate
  * bf16 [rows * topk][I]. */
 int mkmoe_workspace_region(const mkmoe_shape* shape, int32_t region, size_t* offset,

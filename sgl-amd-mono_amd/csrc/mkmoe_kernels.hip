@@ -241,6 +241,19 @@ __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
+// inclusive prefix sum over the wave: shifts by 1, 2, 4, 8 within each 16-lane row (DPP
+// row_shr, lanes without a source add 0), then row 15's total into rows 1 and 3
+// (row_bcast:15) and lane 31's into rows 2 and 3 (row_bcast:31)
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
+  return v;
+}
+
 __device__ __forceinline__ float clampf(float v, float lim) { return fminf(fmaxf(v, -lim), lim); }
 
 // four e4m3 codes (a in the low byte) by the gfx950 convert after the clamp to +-448: for
@@ -451,7 +464,7 @@ __device__ __forceinline__ void router_unit(const Params& p, RouterSmem<C>& sm, 
       }
     }
     const float s = tree_sum<64>(acc);
-    if (lane == 0) dst32(rs, p.off[5] + (((uint32_t)r * C::E + e) * C::P + part) * 4, f2u(s));
+    if (lane == 0) dst32(rs, p.off[5] + (((uint32_t)r * C::P + part) * C::E + e) * 4, f2u(s));
   }
 }
 
@@ -522,6 +535,10 @@ template <class C>
 struct RouteSmem {
   float sc[kRouteRows][C::E];
   float ch[kRouteRows][C::E];
+  float cv[kWaves][C::E];  // a wave's candidates: choice, id
+  int ce[kWaves][C::E];
+  float ss[kWaves][C::K];  // and its picks: score, id
+  int se[kWaves][C::K];
 };
 
 // max over aligned groups of G lanes (G a power of two <= 64), in every lane of the group;
@@ -553,46 +570,66 @@ __device__ __forceinline__ float segment_max(float v) {
 template <class C>
 __device__ __forceinline__ void route_scores(const Params& p, RouteSmem<C>& sm, int r0, int n) {
 #pragma clang fp contract(off)
+  constexpr int MJ = (kRouteRows * C::E + kThreads - 1) / kThreads;  // (row, expert) a thread
   const auto rs = ws_rsrc(p);
-  for (int idx = threadIdx.x; idx < n * C::E; idx += kThreads) {
-    const int i = idx / C::E, e = idx - i * C::E;
-    const uint32_t part0 = p.off[5] + ((uint32_t)(r0 + i) * C::E + e) * C::P * 4;
-    float logit = 0.0f;
+  const int tid = threadIdx.x;
+  // every part sum ([rows][P][E]) requested before the first is used
+  float part[MJ][C::P];
 #pragma unroll
-    for (int q = 0; q < C::P; ++q) logit = logit + u2f(dld32(rs, part0 + q * 4));
-    const float sg = sigmoid_exact(logit);
-    const float s = sg != sg ? 0.0f : sg;
-    const float cv = s + p.bias[e];
-    sm.sc[i][e] = s;
-    sm.ch[i][e] = cv != cv ? -INFINITY : cv;
+  for (int j = 0; j < MJ; ++j) {
+    const int idx = tid + j * kThreads;
+    const int i = idx / C::E, e = idx - i * C::E;
+    const uint32_t part0 = p.off[5] + ((uint32_t)(r0 + i) * C::P * C::E + e) * 4;
+#pragma unroll
+    for (int q = 0; q < C::P; ++q)
+      part[j][q] = idx < n * C::E ? u2f(dld32(rs, part0 + q * C::E * 4)) : 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < MJ; ++j) {
+    const int idx = tid + j * kThreads;
+    if (idx < n * C::E) {
+      const int i = idx / C::E, e = idx - i * C::E;
+      float logit = 0.0f;
+#pragma unroll
+      for (int q = 0; q < C::P; ++q) logit = logit + part[j][q];
+      const float sg = sigmoid_exact(logit);
+      const float s = sg != sg ? 0.0f : sg;
+      const float cv = s + p.bias[e];
+      sm.sc[i][e] = s;
+      sm.ch[i][e] = cv != cv ? -INFINITY : cv;
+    }
   }
 }
 
-// one row's grouped top-k by one wave, from its scores sc and choices ch in LDS. Lane l holds
-// experts l + 64 i. Group score = top-1 + top-2 choice of the group; the topk_group best groups
-// (larger score, then lower group); then topk experts of those groups, one a round: the largest
-// choice over the wave, and of the experts holding it the lowest id (a ballot), which is the
-// order "larger choice, then lower id". Lane k < topk returns pick k's id and weight.
+// one row's grouped top-k by one wave, from its scores sc and choices ch in LDS; cand is the
+// wave's slice of the LDS scratch. Lane l holds experts l + 64 i. Group score = top-1 + top-2
+// choice of the group; the topk_group best groups are kept (larger score, then lower group);
+// the picks are the topk best experts of the kept groups (larger choice, then lower id), in
+// that order, i.e. the order of a selection that takes the best remaining expert topk times.
+// Every pick's choice is at least L, the smallest top-2 choice of the kept groups (those
+// 2 * topk_group >= topk experts reach it), so only experts with choice >= L are ranked: each
+// against all the others, in parallel. Lane k < topk returns pick k's id and weight.
 template <class C>
 __device__ __forceinline__ void select_row(const Params& p, const float* sc_row, const float* ch_row,
-                                           int lane, int& my_id, float& my_w) {
+                                           float* cv, int* ce, float* ss, int* se, int lane, int& my_id,
+                                           float& my_w) {
 #pragma clang fp contract(off)
   constexpr int EPL = (C::E + 63) / 64;
-  float sc[EPL], ch[EPL];
+  float ch[EPL];
   bool alive[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     const int e = lane + 64 * i;
     alive[i] = e < C::E;
-    sc[i] = alive[i] ? sc_row[e] : 0.0f;
     ch[i] = alive[i] ? ch_row[e] : -INFINITY;
   }
+  float lb = -INFINITY;  // L
   if constexpr (C::NG > 1) {
     constexpr int GS = C::E / C::NG;  // experts a group
     static_assert(GS >= 2 && GS <= 64 && (64 % GS) == 0, "group size");
     constexpr int GPI = 64 / GS;  // groups a 64-expert slice
     const uint64_t seg = GS == 64 ? ~0ull : (((1ull << GS) - 1ull) << ((lane / GS) * GS));
-    float gsv[EPL];
+    float gsv[EPL], gv2[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
       // top-1 of the group, then top-2: top-1 again when two experts hold it, else the max
@@ -602,11 +639,15 @@ __device__ __forceinline__ void select_row(const Params& p, const float* sc_row,
       const float m2 = segment_max<GS>(ch[i] == m1 ? -INFINITY : ch[i]);
       const float v2 = __popcll(eq & seg) >= 2 ? m1 : m2;
       gsv[i] = m1 + v2;
+      gv2[i] = v2;
     }
     // lane g < NG takes group g's score and counts the groups ranked above it
-    float gs[C::NG];
+    float gs[C::NG], g2[C::NG];
 #pragma unroll
-    for (int g = 0; g < C::NG; ++g) gs[g] = lane_value(gsv[g / GPI], (g % GPI) * GS);
+    for (int g = 0; g < C::NG; ++g) {
+      gs[g] = lane_value(gsv[g / GPI], (g % GPI) * GS);
+      g2[g] = lane_value(gv2[g / GPI], (g % GPI) * GS);
+    }
     float mine = -INFINITY;
 #pragma unroll
     for (int g = 0; g < C::NG; ++g) mine = lane == g ? gs[g] : mine;
@@ -619,48 +660,77 @@ __device__ __forceinline__ void select_row(const Params& p, const float* sc_row,
       const int e = lane + 64 * i;
       alive[i] = alive[i] && ((gkeep >> (e / GS)) & 1ull) != 0ull;
     }
-  }
-  float val[EPL];
+    if constexpr (2 * C::TG >= C::K) {
+      lb = INFINITY;
 #pragma unroll
-  for (int i = 0; i < EPL; ++i) val[i] = alive[i] ? ch[i] : -INFINITY;
-  float total = 0.0f;
-  my_id = 0;
-  my_w = 0.0f;
-  for (int k = 0; k < C::K; ++k) {
-    float lm = val[0];
-#pragma unroll
-    for (int i = 1; i < EPL; ++i) lm = val[i] > lm ? val[i] : lm;
-    const float m = lane_value(segment_max<64>(lm), 0);
-    int wi = -1, wl = 0;
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      const uint64_t hit = __ballot(alive[i] && ch[i] == m);
-      if (wi < 0 && hit != 0ull) {
-        wi = i;
-        wl = __builtin_ctzll(hit);
-      }
+      for (int g = 0; g < C::NG; ++g) lb = ((gkeep >> g) & 1ull) && g2[g] < lb ? g2[g] : lb;
     }
-    wi = wi < 0 ? 0 : wi;  // unreachable with >= topk candidates; keeps ids in range
-    float ws = 0.0f;
+  }
+  // candidates to LDS slots 0 .. nc - 1, in id order
+  int nc = 0;
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      if (i == wi) {
-        ws = lane_value(sc[i], wl);
-        if (lane == wl) {
-          alive[i] = false;
-          val[i] = -INFINITY;
+  for (int i = 0; i < EPL; ++i) {
+    const bool cand = alive[i] && ch[i] >= lb;
+    const uint64_t cm = __ballot(cand);
+    if (cand) {
+      const int slot = nc + (int)__popcll(cm & ((1ull << lane) - 1ull));
+      cv[slot] = ch[i];
+      ce[slot] = lane + 64 * i;
+    }
+    nc += (int)__popcll(cm);
+  }
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  // slot c + 64 t to lane c of register t; a candidate's rank is the count of those better
+  // than it: a larger choice, or the same choice at a lower slot (slots ascend with the id)
+  float cvr[EPL];
+#pragma unroll
+  for (int t = 0; t < EPL; ++t) cvr[t] = 64 * t + lane < nc ? cv[64 * t + lane] : -INFINITY;
+  int rank[EPL];
+#pragma unroll
+  for (int t = 0; t < EPL; ++t) rank[t] = 0;
+  if (nc <= 64) {  // the usual case: one register of candidates
+    for (int j = 0; j < nc; ++j) {
+      const float vj = lane_value(cvr[0], j);
+      rank[0] += (vj > cvr[0]) | ((vj == cvr[0]) & (j < lane)) ? 1 : 0;
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < EPL; ++u) {
+      if (64 * u < nc) {
+        const int nj = min(64, nc - 64 * u);
+        for (int j = 0; j < nj; ++j) {
+          const float vj = lane_value(cvr[u], j);
+          const int sj = 64 * u + j;
+#pragma unroll
+          for (int t = 0; t < EPL; ++t) {
+            const int c = 64 * t + lane;
+            rank[t] += (vj > cvr[t]) | ((vj == cvr[t]) & (sj < c)) ? 1 : 0;
+          }
         }
       }
     }
-    total = total + ws;
-    if (lane == k) {
-      my_id = min(wl + 64 * wi, C::E - 1);
-      my_w = ws;
+  }
+#pragma unroll
+  for (int t = 0; t < EPL; ++t) {
+    const int c = 64 * t + lane;
+    if (c < nc && rank[t] < C::K) {
+      const int id = ce[c];
+      ss[rank[t]] = sc_row[id];
+      se[rank[t]] = id;
     }
   }
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  // weights: the picks' scores summed in pick order
+  const float mine_s = lane < C::K ? ss[lane] : 0.0f;
+  my_id = lane < C::K ? min(max(se[lane], 0), C::E - 1) : 0;
+  float total = 0.0f;
+#pragma unroll
+  for (int k = 0; k < C::K; ++k) total = total + lane_value(mine_s, k);
   float f = p.scale;
   if (p.renorm) f = p.scale / (total > 1e-20f ? total : 1e-20f);
-  my_w = my_w * f;
+  my_w = mine_s * f;
 }
 
 // row r's routing by one workgroup (stage B), written to the workspace and the outputs
@@ -672,7 +742,7 @@ __device__ __forceinline__ void route_row(const Params& p, RouteSmem<C>& sm, int
   if (threadIdx.x >= 64) return;
   int id;
   float w;
-  select_row<C>(p, sm.sc[0], sm.ch[0], lane, id, w);
+  select_row<C>(p, sm.sc[0], sm.ch[0], sm.cv[0], sm.ce[0], sm.ss[0], sm.se[0], lane, id, w);
   if (lane < C::K) {
     const auto rs = ws_rsrc(p);
     dst32(rs, p.off[6] + (r * C::K + lane) * 4, (uint32_t)id);
@@ -698,7 +768,7 @@ __device__ __forceinline__ void route_all(const Params& p, RouteSmem<C>& sm, int
     for (int i = wave; i < n; i += kWaves) {
       int id;
       float w;
-      select_row<C>(p, sm.sc[i], sm.ch[i], lane, id, w);
+      select_row<C>(p, sm.sc[i], sm.ch[i], sm.cv[wave], sm.ce[wave], sm.ss[wave], sm.se[wave], lane, id, w);
       const int r = r0 + i;
       if (lane < C::K) {
         ids[r * C::K + lane] = id;
@@ -1504,16 +1574,7 @@ __device__ __forceinline__ void build_union(const Params& p, Union<C>& un, bool 
       }
     }
     // exclusive prefix over lanes
-    int is = ns, ip = np, ig = ng;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      int os = __shfl_up(is, d), op = __shfl_up(ip, d), og = __shfl_up(ig, d);
-      if (tid >= d) {
-        is += os;
-        ip += op;
-        ig += og;
-      }
-    }
+    const int is = wave_incl_scan(ns), ip = wave_incl_scan(np), ig = wave_incl_scan(ng);
     int s = is - ns, pk = ip - np, gq = ig - ng;
     for (int i = 0; i < EPL; ++i) {
       const int e = e0 + i;
@@ -1569,12 +1630,7 @@ __device__ __forceinline__ void build_union(const Params& p, Union<C>& un, bool 
       loc[i] = c;
       sum += c;
     }
-    int inc = sum;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int o = __shfl_up(inc, d);
-      if (tid >= d) inc += o;
-    }
+    const int inc = wave_incl_scan(sum);
     int run = inc - sum;
 #pragma unroll
     for (int i = 0; i < GPL; ++i) {

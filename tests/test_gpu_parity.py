@@ -93,7 +93,8 @@ def _check(c, rows, run, exact):
     run.raise_on_device_error()
     # router part sums, bit for bit
     parts = run.region("router_parts")[: rows * c.p["experts"] * c.p["router_parts"] * 4]
-    parts = parts.view(torch.float32).cpu().numpy().reshape(rows, c.p["experts"], c.p["router_parts"])
+    parts = parts.view(torch.float32).cpu().numpy().reshape(rows, c.p["router_parts"], c.p["experts"])
+    parts = np.ascontiguousarray(parts.transpose(0, 2, 1))
     assert np.array_equal(parts.view(np.uint32), c.parts.view(np.uint32)), "router part sums"
     # routing, bit for bit
     assert np.array_equal(ids.cpu().numpy(), c.ids), "expert ids"
@@ -154,6 +155,37 @@ def test_parity_mfma_forced(workload, rows, mfma_rows):
     mfma_rows(1, 1)
     print(f"\n{workload} R={rows} (MFMA forced)", flush=True)
     _check(c, rows, _runner(c), exact=False)
+
+
+@pytest.mark.parametrize("bias_kind", ["zero", "coarse"])
+@pytest.mark.parametrize("workload,rows", [("cfg1_plumbing_fp8", 4), ("cfg2_tp4_fp8", 1), ("cfg2_tp4_fp8", 16), ("cfg2_tp4_fp8", 24)])
+def test_routing_ties(workload, rows, bias_kind):
+    """Zero rows score 0.5 for every expert, so choices tie wherever the bias does: groups and
+    experts then go by lower index, as in the oracle's stable sorts (16 rows: every workgroup
+    routes the step; 24: a workgroup a row)."""
+    import dataclasses
+
+    from oracle import routing as rt
+
+    c = _case(workload, rows)
+    e = c.p["experts"]
+    if bias_kind == "zero":
+        bias = np.zeros(e, np.float32)
+    else:
+        bias = ((np.arange(e) * 7) % 5).astype(np.float32) * np.float32(0.125)
+    w = dataclasses.replace(c.w, bias=torch.from_numpy(bias).cuda())
+    x = torch.zeros(rows, c.p["hidden"], dtype=torch.bfloat16, device="cuda")
+    scores = rt.sigmoid_exact(np.zeros((rows, e), np.float32))
+    want_ids, want_w = rt.grouped_topk(scores, bias, c.p["topk"], c.p["n_group"], c.p["topk_group"],
+                                       c.p["routed_scale"], renorm=bool(c.p.get("renorm", True)))
+    run = _runner(c)
+    ids = torch.zeros(rows, c.p["topk"], dtype=torch.int32, device="cuda")
+    wts = torch.zeros(rows, c.p["topk"], dtype=torch.float32, device="cuda")
+    run.moe(w, x, topk_ids=ids, topk_w=wts)
+    torch.cuda.synchronize()
+    run.raise_on_device_error()
+    assert np.array_equal(ids.cpu().numpy(), want_ids), "expert ids"
+    assert np.array_equal(wts.cpu().numpy().view(np.uint32), want_w.view(np.uint32)), "routing weights"
 
 
 @pytest.mark.parametrize("workload,rows", [("cfg2_tp4_fp8", 8), ("cfg3_tp4_mxfp4", 8), ("cfg5_tp2_mxfp4_norm", 8)])
