@@ -533,9 +533,12 @@ constexpr int kLocalRouteMax = 16;
 
 template <class C>
 struct RouteSmem {
+  static constexpr int NG = C::NG > 1 ? C::NG : 1;
   float sc[kRouteRows][C::E];
   float ch[kRouteRows][C::E];
-  float cv[kWaves][C::E];  // a wave's candidates: choice, id
+  float gsum[kRouteRows][NG];  // a group's top-1 + top-2 choice
+  float gv2[kRouteRows][NG];   // and its top-2 choice
+  float cv[kWaves][C::E + 8];  // a wave's candidates: choice (8 past the last: -inf), id
   int ce[kWaves][C::E];
   float ss[kWaves][C::K];  // and its picks: score, id
   int se[kWaves][C::K];
@@ -595,8 +598,26 @@ __device__ __forceinline__ void route_scores(const Params& p, RouteSmem<C>& sm, 
       const float sg = sigmoid_exact(logit);
       const float s = sg != sg ? 0.0f : sg;
       const float cv = s + p.bias[e];
+      const float ch = cv != cv ? -INFINITY : cv;
       sm.sc[i][e] = s;
-      sm.ch[i][e] = cv != cv ? -INFINITY : cv;
+      sm.ch[i][e] = ch;
+      if constexpr (C::NG > 1) {
+        // a wave holds 64 consecutive experts of one row (E is a multiple of 64), i.e. whole
+        // groups: top-1 of the group, then top-2: top-1 again when two experts hold it, else
+        // the max of the others
+        constexpr int GS = C::E / C::NG;
+        static_assert(C::E % 64 == 0 && GS >= 2 && GS <= 64 && (64 % GS) == 0, "groups within a wave");
+        const int lane = tid & 63;
+        const uint64_t seg = GS == 64 ? ~0ull : (((1ull << GS) - 1ull) << ((lane / GS) * GS));
+        const float m1 = segment_max<GS>(ch);
+        const uint64_t eq = __ballot(ch == m1);
+        const float m2 = segment_max<GS>(ch == m1 ? -INFINITY : ch);
+        const float v2 = __popcll(eq & seg) >= 2 ? m1 : m2;
+        if (lane % GS == 0) {
+          sm.gsum[i][e / GS] = m1 + v2;
+          sm.gv2[i][e / GS] = v2;
+        }
+      }
     }
   }
 }
@@ -610,11 +631,12 @@ __device__ __forceinline__ void route_scores(const Params& p, RouteSmem<C>& sm, 
 // 2 * topk_group >= topk experts reach it), so only experts with choice >= L are ranked: each
 // against all the others, in parallel. Lane k < topk returns pick k's id and weight.
 template <class C>
-__device__ __forceinline__ void select_row(const Params& p, const float* sc_row, const float* ch_row,
-                                           float* cv, int* ce, float* ss, int* se, int lane, int& my_id,
-                                           float& my_w) {
+__device__ __forceinline__ void select_row(const Params& p, const RouteSmem<C>& sm, int row, float* cv, int* ce,
+                                           float* ss, int* se, int lane, int& my_id, float& my_w) {
 #pragma clang fp contract(off)
   constexpr int EPL = (C::E + 63) / 64;
+  const float* sc_row = sm.sc[row];
+  const float* ch_row = sm.ch[row];
   float ch[EPL];
   bool alive[EPL];
 #pragma unroll
@@ -625,35 +647,12 @@ __device__ __forceinline__ void select_row(const Params& p, const float* sc_row,
   }
   float lb = -INFINITY;  // L
   if constexpr (C::NG > 1) {
-    constexpr int GS = C::E / C::NG;  // experts a group
-    static_assert(GS >= 2 && GS <= 64 && (64 % GS) == 0, "group size");
-    constexpr int GPI = 64 / GS;  // groups a 64-expert slice
-    const uint64_t seg = GS == 64 ? ~0ull : (((1ull << GS) - 1ull) << ((lane / GS) * GS));
-    float gsv[EPL], gv2[EPL];
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      // top-1 of the group, then top-2: top-1 again when two experts hold it, else the max
-      // of the others (the groups never mix live and dead lanes: E is a multiple of GS)
-      const float m1 = segment_max<GS>(ch[i]);
-      const uint64_t eq = __ballot(ch[i] == m1);
-      const float m2 = segment_max<GS>(ch[i] == m1 ? -INFINITY : ch[i]);
-      const float v2 = __popcll(eq & seg) >= 2 ? m1 : m2;
-      gsv[i] = m1 + v2;
-      gv2[i] = v2;
-    }
+    constexpr int GS = C::E / C::NG;
     // lane g < NG takes group g's score and counts the groups ranked above it
-    float gs[C::NG], g2[C::NG];
-#pragma unroll
-    for (int g = 0; g < C::NG; ++g) {
-      gs[g] = lane_value(gsv[g / GPI], (g % GPI) * GS);
-      g2[g] = lane_value(gv2[g / GPI], (g % GPI) * GS);
-    }
-    float mine = -INFINITY;
-#pragma unroll
-    for (int g = 0; g < C::NG; ++g) mine = lane == g ? gs[g] : mine;
+    const float mine = lane < C::NG ? sm.gsum[row][lane] : -INFINITY;
     int above = 0;
 #pragma unroll
-    for (int g = 0; g < C::NG; ++g) above += better(gs[g], g, mine, lane) ? 1 : 0;
+    for (int g = 0; g < C::NG; ++g) above += better(sm.gsum[row][g], g, mine, lane) ? 1 : 0;
     const uint64_t gkeep = __ballot(lane < C::NG && above < C::TG);
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
@@ -663,7 +662,10 @@ __device__ __forceinline__ void select_row(const Params& p, const float* sc_row,
     if constexpr (2 * C::TG >= C::K) {
       lb = INFINITY;
 #pragma unroll
-      for (int g = 0; g < C::NG; ++g) lb = ((gkeep >> g) & 1ull) && g2[g] < lb ? g2[g] : lb;
+      for (int g = 0; g < C::NG; ++g) {
+        const float v2 = sm.gv2[row][g];
+        lb = ((gkeep >> g) & 1ull) && v2 < lb ? v2 : lb;
+      }
     }
   }
   // candidates to LDS slots 0 .. nc - 1, in id order
@@ -679,10 +681,12 @@ __device__ __forceinline__ void select_row(const Params& p, const float* sc_row,
     }
     nc += (int)__popcll(cm);
   }
+  if (lane < 8) cv[nc + lane] = -INFINITY;  // the slots a step of 8 reads past the last
   __builtin_amdgcn_wave_barrier();
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  // slot c + 64 t to lane c of register t; a candidate's rank is the count of those better
-  // than it: a larger choice, or the same choice at a lower slot (slots ascend with the id)
+  // a candidate's rank is the count of those better than it: a larger choice, or the same
+  // choice at a lower slot (slots ascend with the id). Slot c + 64 t is lane c's candidate t;
+  // the candidates are read 8 at a time (LDS broadcasts); the -inf past the last count for none
   float cvr[EPL];
 #pragma unroll
   for (int t = 0; t < EPL; ++t) cvr[t] = 64 * t + lane < nc ? cv[64 * t + lane] : -INFINITY;
@@ -690,25 +694,23 @@ __device__ __forceinline__ void select_row(const Params& p, const float* sc_row,
 #pragma unroll
   for (int t = 0; t < EPL; ++t) rank[t] = 0;
   if (nc <= 64) {  // the usual case: one register of candidates
-    for (int j = 0; j < nc; ++j) {
-      const float vj = lane_value(cvr[0], j);
-      rank[0] += (vj > cvr[0]) | ((vj == cvr[0]) & (j < lane)) ? 1 : 0;
+    for (int j0 = 0; j0 < nc; j0 += 8) {
+      const f32x4 va = *(const f32x4*)(cv + j0);
+      const f32x4 vb = *(const f32x4*)(cv + j0 + 4);
+      const float vj[8] = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) rank[0] += (vj[k] > cvr[0]) | ((vj[k] == cvr[0]) & (j0 + k < lane)) ? 1 : 0;
     }
   } else {
+    for (int j0 = 0; j0 < nc; j0 += 8) {
+      const f32x4 va = *(const f32x4*)(cv + j0);
+      const f32x4 vb = *(const f32x4*)(cv + j0 + 4);
+      const float vj[8] = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
 #pragma unroll
-    for (int u = 0; u < EPL; ++u) {
-      if (64 * u < nc) {
-        const int nj = min(64, nc - 64 * u);
-        for (int j = 0; j < nj; ++j) {
-          const float vj = lane_value(cvr[u], j);
-          const int sj = 64 * u + j;
+      for (int k = 0; k < 8; ++k)
 #pragma unroll
-          for (int t = 0; t < EPL; ++t) {
-            const int c = 64 * t + lane;
-            rank[t] += (vj > cvr[t]) | ((vj == cvr[t]) & (sj < c)) ? 1 : 0;
-          }
-        }
-      }
+        for (int t = 0; t < EPL; ++t)
+          rank[t] += (vj[k] > cvr[t]) | ((vj[k] == cvr[t]) & (j0 + k < 64 * t + lane)) ? 1 : 0;
     }
   }
 #pragma unroll
@@ -742,7 +744,7 @@ __device__ __forceinline__ void route_row(const Params& p, RouteSmem<C>& sm, int
   if (threadIdx.x >= 64) return;
   int id;
   float w;
-  select_row<C>(p, sm.sc[0], sm.ch[0], sm.cv[0], sm.ce[0], sm.ss[0], sm.se[0], lane, id, w);
+  select_row<C>(p, sm, 0, sm.cv[0], sm.ce[0], sm.ss[0], sm.se[0], lane, id, w);
   if (lane < C::K) {
     const auto rs = ws_rsrc(p);
     dst32(rs, p.off[6] + (r * C::K + lane) * 4, (uint32_t)id);
@@ -768,7 +770,7 @@ __device__ __forceinline__ void route_all(const Params& p, RouteSmem<C>& sm, int
     for (int i = wave; i < n; i += kWaves) {
       int id;
       float w;
-      select_row<C>(p, sm.sc[i], sm.ch[i], sm.cv[wave], sm.ce[wave], sm.ss[wave], sm.se[wave], lane, id, w);
+      select_row<C>(p, sm, i, sm.cv[wave], sm.ce[wave], sm.ss[wave], sm.se[wave], lane, id, w);
       const int r = r0 + i;
       if (lane < C::K) {
         ids[r * C::K + lane] = id;
@@ -1558,34 +1560,41 @@ __device__ __forceinline__ void build_union(const Params& p, Union<C>& un, bool 
     atomicOr(&un.rows_of[my_e][r >> 5], 1u << (r & 31));
   }
   __syncthreads();
-  for (int e = tid; e < C::E; e += kThreads)
-    un.cnt[e] = __popc(un.rows_of[e][0]) + __popc(un.rows_of[e][1]);
-  __syncthreads();
+  // wave 0: lane l takes experts l * EPL .. l * EPL + EPL - 1: slots, picks, token groups and
+  // their gate_up costs (a group of c picks costs kColCost + c a column), prefix-summed
   if (tid < 64) {
     constexpr int EPL = (C::E + 63) / 64;
     const int e0 = tid * EPL;
-    int ns = 0, np = 0, ng = 0;
+    int cnt[EPL];
+    int ns = 0, np = 0, ng = 0, nc = 0;
+#pragma unroll
     for (int i = 0; i < EPL; ++i) {
       const int e = e0 + i;
-      if (e < C::E && un.cnt[e] > 0) {
-        ns += 1;
-        np += un.cnt[e];
-        ng += (un.cnt[e] + tgs - 1) / tgs;
-      }
+      cnt[i] = e < C::E ? __popc(un.rows_of[e][0]) + __popc(un.rows_of[e][1]) : 0;
+      const int groups = (cnt[i] + tgs - 1) / tgs;
+      ns += cnt[i] > 0 ? 1 : 0;
+      np += cnt[i];
+      ng += groups;
+      nc += groups * kColCost + cnt[i];
     }
-    // exclusive prefix over lanes
-    const int is = wave_incl_scan(ns), ip = wave_incl_scan(np), ig = wave_incl_scan(ng);
-    int s = is - ns, pk = ip - np, gq = ig - ng;
+    // exclusive prefixes over lanes
+    const int is = wave_incl_scan(ns), ip = wave_incl_scan(np), ig = wave_incl_scan(ng), ic = wave_incl_scan(nc);
+    int s = is - ns, pk = ip - np, gq = ig - ng, run = ic - nc;
+#pragma unroll
     for (int i = 0; i < EPL; ++i) {
       const int e = e0 + i;
-      if (e < C::E && un.cnt[e] > 0) {
-        const int c = un.cnt[e];
+      const int c = cnt[i];
+      if (c > 0) {
         const int groups = (c + tgs - 1) / tgs;
         un.slot_of[e] = s;
         un.slot_e[s] = e;
         un.slot_start[s] = pk;
         un.tg_start[s] = gq;
-        for (int q = 0; q < groups; ++q) un.tg_slot[gq + q] = s;
+        for (int q = 0; q < groups; ++q) {
+          un.tg_slot[gq + q] = s;
+          un.tg_cost[gq + q] = run;
+          run += kColCost + min(tgs, c - q * tgs);
+        }
         un.cnt[e] = pk;  // fill cursor
         s += 1;
         pk += c;
@@ -1593,11 +1602,18 @@ __device__ __forceinline__ void build_union(const Params& p, Union<C>& un, bool 
       }
     }
     if (tid == 63) {
+      // then the shared expert's groups of its rows
+      const int ntg = ig + (p.rows + tgs - 1) / tgs;
       un.n = is;
       un.slot_start[is] = ip;
       un.tg_start[is] = ig;
       un.ntg_r = ig;
-      un.ntg = ig + (p.rows + tgs - 1) / tgs;
+      un.ntg = ntg;
+      for (int g = ig; g < ntg; ++g) {
+        un.tg_cost[g] = run;
+        run += kColCost + min(tgs, p.rows - (g - ig) * tgs);
+      }
+      un.tg_cost[ntg] = run;
     }
   }
   __syncthreads();
@@ -1609,36 +1625,6 @@ __device__ __forceinline__ void build_union(const Params& p, Union<C>& un, bool 
     const uint32_t below1 = r >= 32 ? (1u << (r - 32)) - 1u : 0u;
     const int pos = un.cnt[e] + __popc(un.rows_of[e][0] & below0) + __popc(un.rows_of[e][1] & below1);
     un.picks[min(pos, npk - 1)] = t;
-  }
-  // each token group's cost a column, prefix-summed over the groups
-  if (tid < 64) {
-    constexpr int GPL = (kMaxGroups<C> + 63) / 64;  // groups a lane
-    const int ntg = un.ntg, ntg_r = un.ntg_r;
-    int loc[GPL];
-    int sum = 0;
-#pragma unroll
-    for (int i = 0; i < GPL; ++i) {
-      const int g = tid * GPL + i;
-      int c = 0;
-      if (g < ntg_r) {
-        const int sl = un.tg_slot[g];
-        const int j0 = un.slot_start[sl] + (g - un.tg_start[sl]) * tgs;
-        c = kColCost + min(tgs, un.slot_start[sl + 1] - j0);
-      } else if (g < ntg) {
-        c = kColCost + min(tgs, p.rows - (g - ntg_r) * tgs);
-      }
-      loc[i] = c;
-      sum += c;
-    }
-    const int inc = wave_incl_scan(sum);
-    int run = inc - sum;
-#pragma unroll
-    for (int i = 0; i < GPL; ++i) {
-      const int g = tid * GPL + i;
-      if (g < ntg) un.tg_cost[g] = run;
-      run += loc[i];
-    }
-    if (tid == 63) un.tg_cost[ntg] = inc;
   }
   __syncthreads();
 }
