@@ -44,6 +44,7 @@ constexpr int kTileMax = 32;   // output rows of a down tile, at most
 constexpr int kFp8 = MKMOE_FMT_FP8_B128;
 constexpr int kFp4 = MKMOE_FMT_MXFP4;
 constexpr int kAuxDev = 16;  // sc1: device-coherent access
+constexpr int kAuxNt = 2;    // nt: streamed once
 
 // control words at the start of the workspace
 constexpr int kCtlNorm = 0, kCtlA = 1, kCtlB = 2, kCtlC = 3, kCtlExit = 5;
@@ -62,8 +63,8 @@ struct Cfg {
   static_assert(H % 1024 == 0 && CH512 % P == 0, "router chunks, K split over 8 waves");
   static_assert(I % 128 == 0 && S % 128 == 0, "widths");
   static_assert(E <= 1024 && (NG == 1 || (E % NG == 0)), "experts");
-  // down-stage mid batch: picks whose quantized rows fit ~64 KB of LDS
-  static constexpr int PB = 65536 / I;
+  // down-stage mid batch: picks whose quantized rows fit ~32 KB of LDS
+  static constexpr int PB = 32768 / I;
   static constexpr int MQS = I + 16;  // LDS row stride of quantized mid (bank spread)
   static constexpr int SQS = S + 16;
   static constexpr int MSC = FMT == kFp4 ? I / 32 : I / 128;  // mid scales a pick
@@ -150,6 +151,13 @@ __device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; 
 __device__ __forceinline__ u32x4 ld16_nt(const void* p) {
   return __builtin_nontemporal_load((const u32x4*)p);
 }
+
+// a weight of n bytes as a buffer resource; a load at an offset past n returns zeros without a
+// memory access
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t weight_rsrc(const void* w, uint32_t n) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(w), (short)0, (int)n, 0x00020000);
+}
+constexpr uint32_t kNoLoad = 0xF0000000u;  // an offset past every weight resource
 
 // the workspace as a buffer resource: hand-off data goes through sc1 (device-coherent) accesses
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(const Params& p) {
@@ -1424,6 +1432,69 @@ struct DownTile {
   float s0[KS], s1[KS];   // FP8: block scales of the lane's first and last C row
   int split;              // FP8: C elements v < split take s0, the rest s1
 
+  // The unit through LDS. issue() requests its 16 rows into a wave's slot by LDS-direct
+  // 16-byte loads, each load a contiguous KB of the weight (the operand layout's own loads read
+  // 64-byte runs, which stream at about 5.1 against 6.6 TB/s: measured, loads alone). Chunk c
+  // (16 bytes) of row r sits at slot position r * CPR + (c ^ r), so that the 16 rows' reads of
+  // one chunk fall in distinct banks. Rows past nv are requested past the resource (zeros, no
+  // memory access). fetch() reads the slot into a[][] in the operand layout.
+  static constexpr int RB = WFMT == kFp8 ? KD : KD / 2;  // bytes a row
+  static constexpr int CPR = RB / 16;                   // chunks a row
+  static constexpr int SLOT = 16 * RB;                  // bytes a unit
+  static_assert(CPR >= 16 && (CPR & (CPR - 1)) == 0 && SLOT % 1024 == 0, "slot layout");
+  // wr: a resource over the weight from row 0 (H x RB bytes a matrix); wrow: the unit's first
+  // row's byte offset in it
+  __device__ __forceinline__ static void issue(__amdgpu_buffer_rsrc_t wr, uint32_t wrow, int nv, uint8_t* slot,
+                                               int lane) {
+#pragma unroll
+    for (int i = 0; i < SLOT / 1024; ++i) {
+      const int pos = i * 64 + lane;
+      const int r = pos / CPR, c = (pos % CPR) ^ r;
+      const uint32_t off = r < nv ? wrow + (uint32_t)r * RB + c * 16 : kNoLoad;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(slot + i * 1024), 16,
+                                               off, 0, 0, kAuxNt);
+    }
+  }
+  __device__ __forceinline__ void fetch(const uint8_t* slot, int lane) {
+    const int m = lane & 15, j = lane >> 4;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const int c = WFMT == kFp8 ? ks * 8 + j + 4 * w : ks * 4 + j;
+        a[ks][w] = *(const u32x4*)(slot + (m * CPR + (c ^ m)) * 16);
+      }
+  }
+  // the unit's scales alone (as load() sets them)
+  __device__ __forceinline__ void load_scales(const void* s, int hb, int nv, int lane) {
+    const int m = lane & 15, j = lane >> 4;
+    if constexpr (WFMT == kFp8) {
+      const int r0 = hb + min(4 * j, nv - 1), r3 = hb + min(4 * j + 3, nv - 1);
+      const float* sp = (const float*)s;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        s0[ks] = sp[(r0 / 128) * (KD / 128) + ks];
+        s1[ks] = sp[(r3 / 128) * (KD / 128) + ks];
+      }
+      split = r0 / 128 == r3 / 128 ? 4 : 128 - (hb + 4 * j) % 128;
+    } else {
+      const bool ok = m < nv;
+      const size_t h = (size_t)hb + (ok ? m : 0);
+      const uint8_t* ss = (const uint8_t*)s;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) sa[ks] = ok ? ss[h * (KD / 32) + ks * 4 + j] : 127u;
+    }
+  }
+  __device__ __forceinline__ void take_scales(const DownTile& o) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      sa[ks] = o.sa[ks];
+      s0[ks] = o.s0[ks];
+      s1[ks] = o.s1[ks];
+    }
+    split = o.split;
+  }
+
   // w: row 0 of the weight; s: its scales (FP8 [H / 128][KD / 128] fp32, MXFP4 [H][KD / 32])
   __device__ __forceinline__ void load(const uint8_t* w, const void* s, int hb, int nv, int lane) {
     const int m = lane & 15, j = lane >> 4;
@@ -2068,7 +2139,7 @@ __device__ __forceinline__ void stage_c(const Params& p, const Union<C>& un, GuS
 // ---------------------------------------------------------------- stage D: shared and routed down + combine
 template <class C>
 struct DownSmem {
-  float contrib[kRowsMax * C::K * kTileMax];
+  uint16_t contrib[kRowsMax * C::K * kTileMax];  // bf16 of a pick's down output x its weight
   union {
     struct {
       uint8_t q[C::PB * C::MQS];
@@ -2077,6 +2148,8 @@ struct DownSmem {
     SharedDownSmem<C> sd;  // the shared down's quantized rows, done before the routed ones
   };
   uint16_t shv[kRowsMax * kTileMax];  // the shared expert's bf16 results of the tile
+  // MFMA down: a wave's slot of weight rows (one unit)
+  uint8_t wslot[kWaves][DownTile<C::FMT, C::I>::SLOT] __attribute__((aligned(16)));
 };
 
 // the slots holding picks [pb0, pb0 + pbn) of the step (picks are stored slot by slot)
@@ -2099,8 +2172,13 @@ using DownRowsOf = DownRows<C::FMT, C::I>;
 template <class C>
 using DownTileOf = DownTile<C::FMT, C::I>;
 // the down stage's batch of units: MFMA (MF) or VALU
+// the MFMA down's unit in flight: its rows in the wave's LDS slot, its scales in nxt
+template <class C>
+struct LdsUnit {
+  DownTileOf<C> nxt;
+};
 template <class C, bool MF>
-using DownBatchOf = DownBatch<typename std::conditional<MF, DownTileOf<C>, DownRowsOf<C>>::type>;
+using DownBatchOf = typename std::conditional<MF, LdsUnit<C>, DownBatch<DownRowsOf<C>>>::type;
 
 // loaders of the units of tile rows [h0, h0 + hn) for slots from s_lo: VALU units (slot,
 // 8-row block), MFMA units (slot, 16-row block)
@@ -2121,20 +2199,22 @@ __device__ __forceinline__ auto valu_down_loader(const Params& p, const Union<C>
       wr.load(p.w2 + row * (C::I / 2), (const uint8_t*)p.w2_s + row * (C::I / 32), hl < hn, l);
   };
 }
+// request MFMA unit v (slot, 16-row block) of tile rows [h0, h0 + hn), slots from s_lo: its
+// rows into the wave's LDS slot, its scales into nx
 template <class C>
-__device__ __forceinline__ auto mfma_down_loader(const Params& p, const Union<C>& un, int h0, int hn, int s_lo) {
-  const int lane = threadIdx.x & 63;
+__device__ __forceinline__ void mfma_issue(const Params& p, const Union<C>& un, int h0, int hn, int s_lo, int v,
+                                           uint8_t* slot, DownTileOf<C>& nx, int lane) {
+  using DT = DownTileOf<C>;
   const int nb = (hn + 15) / 16;
-  return [&p, &un, h0, hn, s_lo, nb, lane](int v, DownTileOf<C>& dt) {
-    const int slot = s_lo + v / nb, rb = v % nb;
-    const int e = un.slot_e[slot];
-    if constexpr (C::FMT == kFp8)
-      dt.load(p.w2 + (size_t)e * C::H * C::I, (const float*)p.w2_s + (size_t)e * (C::H / 128) * (C::I / 128),
-              h0 + rb * 16, min(16, hn - rb * 16), lane);
-    else
-      dt.load(p.w2 + (size_t)e * C::H * (C::I / 2), (const uint8_t*)p.w2_s + (size_t)e * C::H * (C::I / 32),
-              h0 + rb * 16, min(16, hn - rb * 16), lane);
-  };
+  const int e = un.slot_e[s_lo + v / nb], rb = v % nb;
+  const int hb = h0 + rb * 16, nv = min(16, hn - rb * 16);
+  static_assert((long long)C::E * C::H * DT::RB < (1ll << 31), "offsets within a 32-bit resource");
+  const auto wr = weight_rsrc(p.w2, (uint32_t)(C::E * C::H * DT::RB));
+  DT::issue(wr, (uint32_t)(e * C::H + hb) * DT::RB, nv, slot, lane);
+  if constexpr (C::FMT == kFp8)
+    nx.load_scales((const float*)p.w2_s + (size_t)e * (C::H / 128) * (C::I / 128), hb, nv, lane);
+  else
+    nx.load_scales((const uint8_t*)p.w2_s + (size_t)e * C::H * (C::I / 32), hb, nv, lane);
 }
 
 template <class C>
@@ -2169,61 +2249,77 @@ __device__ __forceinline__ void down_valu(const Params& p, const Union<C>& un, D
 #pragma unroll
         for (int q = 0; q < kPickBlock; ++q) {
           const float y = tree_sum<kDownLanes>(acc[q]);
-          if (q < np && l == 0 && hl < hn) sm.contrib[un.picks[jj + q] * kTileMax + hl] = y;
+          if (q < np && l == 0 && hl < hn) {
+            const int pk = un.picks[jj + q];
+            sm.contrib[pk * kTileMax + hl] = f2bf(y * un.wts[pk]);
+          }
         }
       }
     });
   }
 }
 
-// the same on MFMA: units (slot, 16-row block), each against its slot's picks 16 at a time
+// the same on MFMA: units (slot, 16-row block), each against its slot's picks 16 at a time. A
+// wave keeps one unit in flight: once a unit's rows are read out of its LDS slot, the wave's
+// next unit is requested into the slot, and the unit is computed while those rows stream in.
 template <class C>
 __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
-                                          DownBatch<DownTileOf<C>>& bt, bool first_ready) {
-  const int lane = threadIdx.x & 63;
+                                          LdsUnit<C>& bt, bool first_ready) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int npk = p.rows * C::K;
   using DT = DownTileOf<C>;
   constexpr int SST = C::FMT == kFp4 ? C::I / 32 : (C::I / 128) * 4;  // scale bytes of a pick
   const int nb = (hn + 15) / 16;
+  uint8_t* slot = sm.wslot[wave];
   for (int pb0 = 0; pb0 < npk; pb0 += C::PB) {
     const int pbn = min(C::PB, npk - pb0);
     int s_lo, s_hi;
     batch_slots(un, pb0, pbn, s_lo, s_hi);
     const int n_units = (s_hi - s_lo + 1) * nb;
-    auto load = mfma_down_loader<C>(p, un, h0, hn, s_lo);
-    if (pb0 > 0 || !first_ready) bt.load(threadIdx.x >> 6, n_units, load);
+    if ((pb0 > 0 || !first_ready) && wave < n_units) mfma_issue<C>(p, un, h0, hn, s_lo, wave, slot, bt.nxt, lane);
     __syncthreads();  // the previous batch is done with the LDS rows
     quant_rows_lds<C::FMT, C::I, C::MQS, 2 * kQuantBatch>(
         p, [&](int i) { return p.off[9] + (uint32_t)un.picks[pb0 + i] * C::I * 2; }, pbn, sm.q, sm.s);
     __syncthreads();
-    down_pipeline<DT>(bt, n_units, load, [&](int v, const DT& dt) {
-      const int slot = s_lo + v / nb, rb = v % nb;
-      const int j0 = max(un.slot_start[slot], pb0), j1 = min(un.slot_start[slot + 1], pb0 + pbn);
+    DT cur;
+    for (int v = wave; v < n_units; v += kWaves) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the unit's rows are in the slot
+      cur.fetch(slot, lane);
+      cur.take_scales(bt.nxt);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // and read out of it
+      if (v + kWaves < n_units) mfma_issue<C>(p, un, h0, hn, s_lo, v + kWaves, slot, bt.nxt, lane);
+      const int slot_i = s_lo + v / nb, rb = v % nb;
+      const int j0 = max(un.slot_start[slot_i], pb0), j1 = min(un.slot_start[slot_i + 1], pb0 + pbn);
       const int n = lane & 15;
       for (int jj = j0; jj < j1; jj += kMfmaPicks) {
         const int np = min(kMfmaPicks, j1 - jj);
-        const f32x4 acc = dt.template mma<C::MQS, SST>(sm.q, sm.s, jj - pb0, np, lane);
+        const f32x4 acc = cur.template mma<C::MQS, SST>(sm.q, sm.s, jj - pb0, np, lane);
         const int pk = n < np ? un.picks[jj + n] : 0;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const int hl = rb * 16 + 4 * (lane >> 4) + k;
-          if (n < np && hl < hn) sm.contrib[pk * kTileMax + hl] = acc[k];
+          if (n < np && hl < hn) sm.contrib[pk * kTileMax + hl] = f2bf(acc[k] * un.wts[pk]);
         }
       }
-    });
+    }
   }
 }
 
 // request the first pick batch's first units of tile rows [h0, h0 + hn); the down stage goes
 // on from them
 template <class C, bool MF>
-__device__ __forceinline__ void down_first(const Params& p, const Union<C>& un, int h0, int hn, DownBatchOf<C, MF>& bt) {
+__device__ __forceinline__ void down_first(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
+                                           DownBatchOf<C, MF>& bt) {
   const int npk = p.rows * C::K;
   int s_lo, s_hi;
   batch_slots(un, 0, min(C::PB, npk), s_lo, s_hi);
   const int wave = threadIdx.x >> 6;
-  if constexpr (MF) bt.load(wave, (s_hi - s_lo + 1) * ((hn + 15) / 16), mfma_down_loader<C>(p, un, h0, hn, s_lo));
-  else bt.load(wave, (s_hi - s_lo + 1) * kRowBlocks, valu_down_loader<C>(p, un, h0, hn, s_lo));
+  if constexpr (MF) {
+    if (wave < (s_hi - s_lo + 1) * ((hn + 15) / 16))
+      mfma_issue<C>(p, un, h0, hn, s_lo, wave, sm.wslot[wave], bt.nxt, threadIdx.x & 63);
+  } else {
+    bt.load(wave, (s_hi - s_lo + 1) * kRowBlocks, valu_down_loader<C>(p, un, h0, hn, s_lo));
+  }
 }
 
 // tile rows [h0, h0 + hn): the routed down GEMVs (MFMA or VALU, as MF), the shared expert's
@@ -2248,7 +2344,7 @@ __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, D
 #pragma unroll
     for (int k = 0; k < C::K; ++k) {
       const int pk = t * C::K + k;
-      routed = bf_round(routed + bf_round(sm.contrib[pk * kTileMax + hl] * un.wts[pk]));
+      routed = bf_round(routed + bf2f(sm.contrib[pk * kTileMax + hl]));
     }
     p.out[(size_t)t * C::H + h0 + hl] = f2bf(routed + bf2f(sm.shv[idx]));
   }
@@ -2277,7 +2373,7 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
   DownBatchOf<C, MF> bt;
   const int tr = p.tile_rows;
   const bool first = b * tr < C::H;
-  if (first) down_first<C, MF>(p, un, b * tr, min(tr, C::H - b * tr), bt);
+  if (first) down_first<C, MF>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt);
   await_all(p, kCtlC, nwg, kStageC);
   __syncthreads();  // the tile's readers are done before the down stage reuses its LDS
   stage_d<C, MF>(p, un, sm, b, nwg, bt, first);
