@@ -158,6 +158,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t weight_rsrc(const void* w, uin
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(w), (short)0, (int)n, 0x00020000);
 }
 constexpr uint32_t kNoLoad = 0xF0000000u;  // an offset past every weight resource
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+// a weight of n bytes as the four scalar words of a buffer resource (for lds_dma16)
+__device__ __forceinline__ i32x4 weight_rsrc_words(const void* w, uint32_t n) {
+  const unsigned long long a = (unsigned long long)w;
+  return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)a), __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xffffu)),
+               __builtin_amdgcn_readfirstlane((int)n), 0x00020000};
+}
+// LDS-direct 16-byte load: lane l's 16 bytes at byte voff of the resource land at lds + 16 l
+// (lds wave-uniform). One asm statement, so that the compiler's wait insertion (which waits
+// for every LDS-direct load before any later access of LDS it cannot tell apart) leaves it
+// in flight while the wave computes; the caller waits (vmcnt) before it reads what it wrote.
+__device__ __forceinline__ void lds_dma16(i32x4 rs, void* lds, uint32_t voff) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(uint8_t*)lds);
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen nt lds" ::"v"(voff), "s"(m0), "s"(rs)
+               : "memory", "m0");
+}
 
 // the workspace as a buffer resource: hand-off data goes through sc1 (device-coherent) accesses
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(const Params& p) {
@@ -1280,10 +1297,18 @@ __device__ __forceinline__ void stage_x_lds(const Params& p, XTile<C>& xt, int n
   __syncthreads();
 }
 
-// LDS of an MFMA gate_up: the activation tile and the waves' partial C tiles (gate, up)
+// LDS of the gate_up stage: the VALU GEMVs' activation tile, or the MFMA units' weight slots
+// (a wave's K slice of one unit: 2 H bytes) and the FP8 weight's block scales; and the waves'
+// partial C tiles (gate, up)
 template <class C>
 struct GuSmem {
-  XTile<C> x;
+  union {
+    XTile<C> x;
+    struct {
+      uint8_t wslot[kWaves][2 * C::H];
+      float wsc[XTile<C>::WSC];
+    } m;
+  };
   f32x4 red[2][kWaves][64];
 };
 
@@ -1300,105 +1325,181 @@ struct GuTile {
   static constexpr int NC = WFMT == kFp8 ? 8 : 16;  // columns a unit
   static constexpr int NW = WFMT == kFp8 ? 2 : 1;   // 16-byte words of a lane's step
   u32x4 a[NA][SPW][NW];
-  uint32_t sa[NA][SPW];  // MXFP4: the E8M0 byte of the lane's row and block
+  uint32_t sa[NA][SPW];   // MXFP4: the E8M0 byte of the lane's row and block
+  uint32_t nsa[NA][SPW];  // and the next unit's, requested with its rows
 
-  __device__ __forceinline__ void load(const uint8_t* w, const void* s, int W, int j0, int lane, int wave) {
-    const int m = lane & 15, j = lane >> 4, s0 = wave * SPW;
-    if constexpr (WFMT == kFp8) {
-      const size_t r = (size_t)(m < 8 ? j0 + m : W + j0 + m - 8);
+  // A unit's weight rows (FP8: gate rows j0 .. j0 + 7 then up rows W + j0 ..; MXFP4: 16 gate
+  // rows then 16 up rows), this wave's K steps, go through the wave's LDS slot: LDS-direct
+  // loads read them as runs of RB bytes a row (the operand layout's own loads read 64-byte
+  // runs, which stream at about 5.1 against 6.6 TB/s: measured, loads alone). Chunk c (16 bytes)
+  // of slot row r sits at position r * CPW + (c ^ key(r)), so that the 16 rows' reads of one
+  // chunk fall in distinct banks.
+  static constexpr int RW = WFMT == kFp8 ? 16 : 32;              // slot rows
+  static constexpr int RB = WFMT == kFp8 ? SPW * 128 : SPW * 64;  // bytes a slot row
+  static constexpr int CPW = RB / 16;
+  static constexpr int SLOT = RW * RB;
+  static_assert(SLOT == 2 * C::H && SLOT % 1024 == 0 && CPW % (WFMT == kFp8 ? 8 : 4) == 0, "slot layout");
+  __device__ __forceinline__ static int key(int r) { return WFMT == kFp8 ? (r >> 1) : ((r & 15) >> 2); }
+  __device__ __forceinline__ static int wrow(int W, int j0, int r) {
+    return WFMT == kFp8 ? (r < 8 ? j0 + r : W + j0 + r - 8) : (r >> 4) * W + j0 + (r & 15);
+  }
+  // w: the [2W][H] weight (wr: its resource words), s: its scales
+  __device__ __forceinline__ void issue(i32x4 wr, const void* s, int W, int j0, uint8_t* slot, int lane, int wave) {
+    const int s0 = wave * SPW;
+    constexpr int ROWB = WFMT == kFp8 ? C::H : C::H / 2;  // bytes a weight row
 #pragma unroll
-      for (int i = 0; i < SPW; ++i) {
-        const uint8_t* p = w + r * C::H + (s0 + i) * 128 + 16 * j;
-        a[0][i][0] = ld16_nt(p);
-        a[0][i][1] = ld16_nt(p + 64);
-      }
-    } else {
+    for (int i = 0; i < SLOT / 1024; ++i) {
+      const int pos = i * 64 + lane, r = pos / CPW, c = (pos % CPW) ^ key(r);
+      lds_dma16(wr, slot + i * 1024, (uint32_t)wrow(W, j0, r) * ROWB + s0 * (RB / SPW) + c * 16);
+    }
+    if constexpr (WFMT == kFp4) {
+      const int m = lane & 15, j = lane >> 4;
       const uint8_t* ss = (const uint8_t*)s;
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const size_t r = (size_t)(q * W + j0 + m);
+      for (int q = 0; q < 2; ++q)
 #pragma unroll
-        for (int i = 0; i < SPW; ++i) {
-          a[q][i][0] = ld16_nt(w + r * (C::H / 2) + (s0 + i) * 64 + 16 * j);
-          sa[q][i] = ss[r * (C::H / 32) + (s0 + i) * 4 + j];
-        }
-      }
+        for (int i = 0; i < SPW; ++i) nsa[q][i] = ss[(size_t)(q * W + j0 + m) * (C::H / 32) + (s0 + i) * 4 + j];
     }
   }
-
-  // this wave's partial C tiles over its K steps against the np picks of the tile
-  __device__ __forceinline__ void mma(const XTile<C>& xt, int W, int j0, int np, int lane, int wave,
-                                      f32x4 (&acc)[NA]) const {
-    const int n = lane & 15, j = lane >> 4, s0 = wave * SPW;
-    const bool live = n < np;
-    const int row = live ? n : 0;
-    const uint8_t* xr = xt.q + row * XTile<C>::QS;
+  __device__ __forceinline__ void fetch(const uint8_t* slot, int lane) {
+    const int m = lane & 15, j = lane >> 4;
 #pragma unroll
-    for (int q = 0; q < NA; ++q) acc[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    // FP8: this lane's C rows are gate rows (lanes 0..31) or up rows (lanes 32..63)
-    const int sblk = ((lane < 32 ? j0 : W + j0) / 128) * (C::H / 128);
+    for (int q = 0; q < NA; ++q)
 #pragma unroll
-    for (int i = 0; i < SPW; ++i) {
-      const int ks = s0 + i, k0 = ks * 128;
-      if constexpr (WFMT == kFp8) {
-        u32x4 blo = *(const u32x4*)(xr + k0 + 16 * j), bhi = *(const u32x4*)(xr + k0 + 64 + 16 * j);
-        if (!live) blo = bhi = u32x4{0u, 0u, 0u, 0u};
-        const float f = xt.wsc[sblk + ks] * ((const float*)xt.s)[row * (C::H / 128) + ks];
-        const f32x4 c = mma_fp8_step(a[0][i][0], a[0][i][1], blo, bhi);
+      for (int i = 0; i < SPW; ++i)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[0][v] = fmaf(c[v], f, acc[0][v]);
-      } else {
-        u32x4 blo = *(const u32x4*)(xr + k0 + 32 * j), bhi = *(const u32x4*)(xr + k0 + 32 * j + 16);
-        if (!live) blo = bhi = u32x4{0u, 0u, 0u, 0u};
-        const float sx = e8m0(xt.s[row * (C::H / 32) + k0 / 32 + j]);
-#pragma unroll
-        for (int q = 0; q < NA; ++q) acc[q] = mma_fp4_step(a[q][i][0], e8m0(sa[q][i]), blo, bhi, sx, acc[q]);
-      }
-    }
+        for (int w = 0; w < NW; ++w) {
+          const int r = q * 16 + m;
+          const int c = WFMT == kFp8 ? i * 8 + j + 4 * w : i * 4 + j;
+          a[q][i][w] = *(const u32x4*)(slot + (r * CPW + (c ^ key(r))) * 16);
+          if (WFMT == kFp4 && w == 0) sa[q][i] = nsa[q][i];
+        }
   }
 };
 
+// a token group's activations for an MFMA gate_up, this wave's K steps, in registers: lane
+// (n, j) holds pick n's codes of its K places (FP8: bytes 16 j .. and 64 + 16 j .. of each
+// 128; MXFP8: 32 j .. 32 j + 31) and the scales; picks past np are zero
+template <class C, int WFMT>
+struct GuX {
+  static constexpr int SPW = C::H / 128 / kWaves;
+  u32x4 lo[SPW], hi[SPW];
+  float sx[SPW];     // FP8: the pick's fp32 scale of the 128-block
+  uint32_t ex[SPW];  // MXFP8: the E8M0 byte of the lane's 32-block
+  template <class TokFn>
+  __device__ __forceinline__ void load(const Params& p, int np, uint32_t qoff, uint32_t soff, TokFn tok, int lane,
+                                       int wave) {
+    const int n = lane & 15, j = lane >> 4, s0 = wave * SPW;
+    const bool live = n < np;
+    const uint32_t t = (uint32_t)tok(live ? n : 0);
+    const auto rs = ws_rsrc(p);
+#pragma unroll
+    for (int i = 0; i < SPW; ++i) {
+      const uint32_t k0 = (s0 + i) * 128;
+      if constexpr (WFMT == kFp8) {
+        lo[i] = dld128(rs, qoff + t * C::H + k0 + 16 * j);
+        hi[i] = dld128(rs, qoff + t * C::H + k0 + 64 + 16 * j);
+        sx[i] = u2f(dld32(rs, soff + (t * (C::H / 128) + s0 + i) * 4));
+      } else {
+        lo[i] = dld128(rs, qoff + t * C::H + k0 + 32 * j);
+        hi[i] = dld128(rs, qoff + t * C::H + k0 + 32 * j + 16);
+        ex[i] = dld8(rs, soff + t * (C::H / 32) + k0 / 32 + j);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < SPW; ++i)
+      if (!live) lo[i] = hi[i] = u32x4{0u, 0u, 0u, 0u};
+  }
+};
+
+// this wave's partial C tiles of unit j0 over its K steps: t's weights against x's picks;
+// wsc the FP8 weight's block scales in LDS
+template <class C, int WFMT>
+__device__ __forceinline__ void gu_mma(const GuTile<C, WFMT>& t, const GuX<C, WFMT>& x, const float* wsc, int W, int j0,
+                                       int lane, int wave, f32x4 (&acc)[GuTile<C, WFMT>::NA]) {
+  using T = GuTile<C, WFMT>;
+  const int s0 = wave * T::SPW;
+#pragma unroll
+  for (int q = 0; q < T::NA; ++q) acc[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  // FP8: this lane's C rows are gate rows (lanes 0..31) or up rows (lanes 32..63)
+  const int sblk = ((lane < 32 ? j0 : W + j0) / 128) * (C::H / 128);
+#pragma unroll
+  for (int i = 0; i < T::SPW; ++i) {
+    const int ks = s0 + i;
+    if constexpr (WFMT == kFp8) {
+      const float f = wsc[sblk + ks] * x.sx[i];
+      const f32x4 c = mma_fp8_step(t.a[0][i][0], t.a[0][i][1], x.lo[i], x.hi[i]);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[0][v] = fmaf(c[v], f, acc[0][v]);
+    } else {
+      const float sx = e8m0(x.ex[i]);
+#pragma unroll
+      for (int q = 0; q < T::NA; ++q) acc[q] = mma_fp4_step(t.a[q][i][0], e8m0(t.sa[q][i]), x.lo[i], x.hi[i], sx, acc[q]);
+    }
+  }
+}
+
 // MFMA gate_up of units [lo, hi) of a [2W][H] weight; unit u is token group u / (W / NC) and
 // its NC columns (u % (W / NC)) * NC ... group(tg, w, s, np) gives a group's weight, scales and
-// pick count, stage(tg, np, s) stages its activation rows (and an FP8 weight's block scales s)
-// in the tile, emit(tg, q, col, g, u) takes pick q's gate and up sums of a column. The next
-// unit's weights are requested into the registers of this one as soon as its MFMAs are done
-// (past the barrier of the partial tiles, which add in LDS in wave order). The activation
-// tile is restaged when the group changes. (A second unit in flight streams no faster: the
-// operand layout's 64-byte row pieces, not the requests in flight, set the rate.)
-template <class C, int WFMT, class GroupFn, class StageFn, class EmitFn>
-__device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo, int hi, GroupFn group, StageFn stage, EmitFn emit) {
+// pick count, xload(tg, np, x) loads its activations into x, emit(tg, q, col, g, u) takes pick
+// q's gate and up sums of a column. A wave's K slice of the next unit is requested into its
+// LDS slot as soon as the current one is read out of it, so it streams while the current
+// unit's MFMAs run and its partial tiles add in LDS (in wave order). An FP8 weight's block
+// scales go to LDS when the group changes.
+template <class C, int WFMT, class GroupFn, class XFn, class EmitFn>
+__device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo, int hi, GroupFn group, XFn xload, EmitFn emit) {
   using T = GuTile<C, WFMT>;
   if (lo >= hi) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nb = W / T::NC;
+  constexpr uint32_t WB = WFMT == kFp8 ? C::H : C::H / 2;  // bytes a weight row
+  uint8_t* slot = sm.m.wslot[wave];
   T t;
+  GuX<C, WFMT> x;
   const uint8_t* wb;
   const void* sb;
-  int tg_w = lo / nb, np_w;  // the group whose weights t holds
+  int tg_w = lo / nb, np_w;  // the group whose unit is in flight
   group(tg_w, wb, sb, np_w);
-  t.load(wb, sb, W, (lo % nb) * T::NC, lane, wave);
-  int tg_x = -1, np_x = 0;   // the group staged in the tile
+  __syncthreads();  // the LDS's previous users are done
+  t.issue(weight_rsrc_words(wb, 2u * W * WB), sb, W, (lo % nb) * T::NC, slot, lane, wave);
+  int tg_x = -1, np_x = 0;  // the group in x
+  const void* sb_x = sb;
   for (int u = lo; u < hi; ++u) {
     const int j0 = (u % nb) * T::NC;
-    if (tg_w != tg_x) {
-      stage(tg_w, np_w, sb);
+    const bool fresh = tg_w != tg_x;
+    if (fresh) {
+      xload(tg_w, np_w, x);
       tg_x = tg_w;
       np_x = np_w;
+      sb_x = sb;
+      if constexpr (WFMT == kFp8) {
+        constexpr int nw = 2 * (C::I > C::S ? C::I : C::S) / 128 * (C::H / 128);
+        const int nws = 2 * W / 128 * (C::H / 128);
+        static_assert(nw <= XTile<C>::WSC, "block scales fit");
+        const auto wr = __builtin_amdgcn_make_buffer_rsrc((void*)sb_x, (short)0, nws * 4, 0x00020000);
+        for (int k = wave; k * 256 < nws; k += kWaves) {
+          const int off = k * 1024 + lane * 16;
+          lds_load16(wr, (uint8_t*)sm.m.wsc + k * 1024, off < nws * 4 ? off : 0, 0);
+        }
+      }
     }
-    f32x4 acc[T::NA];
-    t.mma(sm.x, W, j0, np_x, lane, wave, acc);
-#pragma unroll
-    for (int q = 0; q < T::NA; ++q) sm.red[q][wave][lane] = acc[q];
-    __syncthreads();
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the unit's slot, the activations, the scales
+    if (fresh) __syncthreads();                       // every wave's block scales are in LDS
+    t.fetch(slot, lane);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // read out of the slot
     if (u + 1 < hi) {
       const int tn = (u + 1) / nb;
       if (tn != tg_w) {
         tg_w = tn;
         group(tg_w, wb, sb, np_w);
       }
-      t.load(wb, sb, W, ((u + 1) % nb) * T::NC, lane, wave);
+      t.issue(weight_rsrc_words(wb, 2u * W * WB), sb, W, ((u + 1) % nb) * T::NC, slot, lane, wave);
     }
+    f32x4 acc[T::NA];
+    gu_mma<C, WFMT>(t, x, sm.m.wsc, W, j0, lane, wave, acc);
+#pragma unroll
+    for (int q = 0; q < T::NA; ++q) sm.red[q][wave][lane] = acc[q];
+    __syncthreads();
     if (tid < 16 * T::NC) {
       // C[m][n] is element m % 4 of lane n + 16 (m / 4); FP8: up row m + 8 is 32 lanes on
       const int m = tid >> 4, n = tid & 15;
@@ -2092,9 +2193,8 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
           s = p.sgu_s;
           np = min(kMfmaPicks, p.rows - tg * kMfmaPicks);
         },
-        [&](int tg, int np, const void* s) {
-          stage_x_lds<C>(p, sm.x, np, qoff, soff, [&](int r) { return tg * kMfmaPicks + r; }, (const float*)s,
-                         2 * C::S / 128 * (C::H / 128));
+        [&](int tg, int np, GuX<C, kFp8>& x) {
+          x.load(p, np, qoff, soff, [&](int r) { return tg * kMfmaPicks + r; }, threadIdx.x & 63, threadIdx.x >> 6);
         },
         [&](int tg, int q, int col, float g, float u) {
           dst16(rs, p.off[8] + ((uint32_t)(tg * kMfmaPicks + q) * C::S + col) * 2, f2bf(swiglu_shared(g, u, p.limit)));
@@ -2119,10 +2219,10 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
           s = (const uint8_t*)p.w13_s + (size_t)e * 2 * C::I * (C::H / 32);
         }
       },
-      [&](int tg, int np, const void* s) {
+      [&](int tg, int np, GuX<C, C::FMT>& x) {
         const int j0 = first(tg);
-        stage_x_lds<C>(p, sm.x, np, p.off[1], p.off[2], [&](int r) { return un.picks[j0 + r] / C::K; },
-                       (const float*)s, C::FMT == kFp8 ? 2 * C::I / 128 * (C::H / 128) : 0);
+        x.load(p, np, p.off[1], p.off[2], [&](int r) { return un.picks[j0 + r] / C::K; }, threadIdx.x & 63,
+               threadIdx.x >> 6);
       },
       [&](int tg, int q, int col, float g, float u) {
         const int pk = un.picks[first(tg) + q];
@@ -2482,7 +2582,7 @@ struct DevInfo {
 std::mutex g_mu;
 DevInfo g_dev[64];
 double g_deadline_s = 2.0;
-int g_mfma_gate = kRowsMax + 1;  // gate_up: VALU at every row count
+int g_mfma_gate = 8;
 int g_mfma_down = 8;
 
 int device_info(int dev, DevInfo* out) {

@@ -233,8 +233,8 @@ def set_deadline(seconds: float) -> None:
 
 
 # the library's defaults: launches with at least this many rows run the gate_up / down GEMMs
-# on MFMA (gate_up: never; its MFMA operand layout streams weights slower than the VALU GEMVs)
-MFMA_GATE_ROWS, MFMA_DOWN_ROWS = 49, 8
+# on MFMA; fewer rows run the fixed-order VALU GEMVs
+MFMA_GATE_ROWS, MFMA_DOWN_ROWS = 8, 8
 
 
 def set_mfma_rows(gate_up_rows: int = MFMA_GATE_ROWS, down_rows: int = MFMA_DOWN_ROWS) -> None:
