@@ -2175,19 +2175,20 @@ __device__ __forceinline__ void gate_up_valu(const Params& p, const Union<C>& un
   }
 }
 
-// the same on MFMA: the shared expert's (16-row group, column block) units dealt evenly, then
-// the routed ones
+// the same on MFMA: the shared expert's (16-row group, column block) units, then the routed
+// ones, dealt evenly as one list
 template <class C>
 __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un, GuSmem<C>& sm, int b, int nwg) {
   const auto rs = ws_rsrc(p);
+  const int n_sh = (p.rows + kMfmaPicks - 1) / kMfmaPicks * (C::S / GuTile<C, kFp8>::NC);
+  const int n_rt = un.ntg_r * (C::I / GuTile<C, C::FMT>::NC);
   int lo, hi;
+  even_share(n_sh + n_rt, b, nwg, lo, hi);
   {
     const uint32_t qoff = C::FMT == kFp4 ? p.off[3] : p.off[1];
     const uint32_t soff = C::FMT == kFp4 ? p.off[4] : p.off[2];
-    const int groups = (p.rows + kMfmaPicks - 1) / kMfmaPicks;
-    even_share(groups * (C::S / GuTile<C, kFp8>::NC), b, nwg, lo, hi);
     gu_mfma<C, kFp8>(
-        sm, C::S, lo, hi,
+        sm, C::S, lo, min(hi, n_sh),
         [&](int tg, const uint8_t*& w, const void*& s, int& np) {
           w = p.sgu;
           s = p.sgu_s;
@@ -2200,13 +2201,12 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
           dst16(rs, p.off[8] + ((uint32_t)(tg * kMfmaPicks + q) * C::S + col) * 2, f2bf(swiglu_shared(g, u, p.limit)));
         });
   }
-  even_share(un.ntg_r * (C::I / GuTile<C, C::FMT>::NC), b, nwg, lo, hi);
   auto first = [&](int tg) {
     const int slot = un.tg_slot[tg];
     return un.slot_start[slot] + (tg - un.tg_start[slot]) * kMfmaPicks;
   };
   gu_mfma<C, C::FMT>(
-      sm, C::I, lo, hi,
+      sm, C::I, max(lo, n_sh) - n_sh, hi - n_sh,
       [&](int tg, const uint8_t*& w, const void*& s, int& np) {
         const int slot = un.tg_slot[tg];
         const int e = un.slot_e[slot];
