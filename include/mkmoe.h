@@ -140,7 +140,7 @@ int mkmoe_forward_staged(const mkmoe_shape* shape, const mkmoe_weights* w, const
 int mkmoe_set_deadline(double seconds);
 
 /* Row counts from which launches run the gate_up GEMMs (routed and shared) and the down
- * GEMMs (routed and shared) on MFMA (defaults: 8 and 8). Below them
+ * GEMMs (routed and shared) on MFMA (defaults: 1 and 1, i.e. always). Below them
  * the fixed-order VALU GEMVs run, whose output is bit-identical to the oracle; MFMA launches
  * are held to the numerics bounds of the spec. No counterpart in the reference, whose kernels
  * pick their GEMM instruction per width at build time (spec.py:959-967 widths). */

@@ -2582,8 +2582,8 @@ struct DevInfo {
 std::mutex g_mu;
 DevInfo g_dev[64];
 double g_deadline_s = 2.0;
-int g_mfma_gate = 8;
-int g_mfma_down = 8;
+int g_mfma_gate = 1;  // gate_up and down on MFMA at every row count
+int g_mfma_down = 1;
 
 int device_info(int dev, DevInfo* out) {
   std::lock_guard<std::mutex> lk(g_mu);

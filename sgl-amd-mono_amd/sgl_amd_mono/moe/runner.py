@@ -233,8 +233,9 @@ def set_deadline(seconds: float) -> None:
 
 
 # the library's defaults: launches with at least this many rows run the gate_up / down GEMMs
-# on MFMA; fewer rows run the fixed-order VALU GEMVs
-MFMA_GATE_ROWS, MFMA_DOWN_ROWS = 8, 8
+# on MFMA (every launch); fewer rows run the fixed-order VALU GEMVs, bit-identical to the
+# oracle (set_mfma_rows(49, 49) selects them at every row count)
+MFMA_GATE_ROWS, MFMA_DOWN_ROWS = 1, 1
 
 
 def set_mfma_rows(gate_up_rows: int = MFMA_GATE_ROWS, down_rows: int = MFMA_DOWN_ROWS) -> None:

@@ -3,11 +3,10 @@
 Bars: router part sums, activation codes, expert ids and routing weights bit for
 bit at every row count; the bf16 output within max-abs 2e-2 and relative L2 1e-2
 of both the oracle and the golden's fp32-matmul form (the reference's PyTorch
-path); launches below the down GEMMs' MFMA row count (every GEMM on the
-fixed-order VALU GEMVs, which the oracle restates) also bit for bit against the
-oracle, and so do large launches forced onto the VALU GEMVs; launches with every
-expert GEMM forced onto MFMA within the bounds; the persistent and the staged launches bit for bit
-alike; repeated and graph-replayed launches bit for bit alike.
+path). The default launch runs the expert GEMMs on MFMA; launches forced onto the
+fixed-order VALU GEMVs (which the oracle restates) are also bit for bit against the oracle
+and the golden vectors, at small and large row counts. The persistent and the staged
+launches bit for bit alike; repeated and graph-replayed launches bit for bit alike.
 """
 
 import numpy as np
@@ -117,7 +116,7 @@ def _check(c, rows, run, exact):
 
 @pytest.mark.parametrize("workload,rows", CASES)
 def test_parity(workload, rows):
-    """The default launch: VALU GEMVs below the down MFMA row count (bit for bit), MFMA down from it."""
+    """The default launch (MFMA expert GEMMs from MFMA_*_ROWS rows; VALU GEMVs, bit for bit, below)."""
     from sgl_amd_mono.moe.runner import MFMA_DOWN_ROWS, MFMA_GATE_ROWS
 
     c = _case(workload, rows)
@@ -127,7 +126,17 @@ def test_parity(workload, rows):
 
 
 @pytest.mark.parametrize(
-    "workload,rows", [("cfg2_tp4_fp8", 48), ("cfg3_tp4_mxfp4", 8), ("cfg5_tp2_mxfp4_norm", 48), ("cfg4_tp4_mxfp4_zipf", 48)]
+    "workload,rows",
+    [
+        ("cfg1_plumbing_fp8", 4),
+        ("cfg2_tp4_fp8", 1),
+        ("cfg2_tp4_fp8", 8),
+        ("cfg2_tp4_fp8", 48),
+        ("cfg3_tp4_mxfp4", 8),
+        ("cfg5_tp2_mxfp4_norm", 1),
+        ("cfg5_tp2_mxfp4_norm", 48),
+        ("cfg4_tp4_mxfp4_zipf", 48),
+    ],
 )
 def test_parity_valu_forced(workload, rows, mfma_rows):
     """Large launches held on the VALU GEMVs: bit for bit against the oracle."""
@@ -267,8 +276,9 @@ def test_host_validation_errors():
         run.moe(bad, c.x)
 
 
-def test_golden_fixtures():
-    """The kernel against the committed golden vectors (tests/golden/), bit for bit."""
+def test_golden_fixtures(mfma_rows):
+    """The kernel (its fixed-order VALU GEMVs) against the committed golden vectors
+    (tests/golden/), bit for bit."""
     import sys
     from pathlib import Path
 
@@ -278,6 +288,7 @@ def test_golden_fixtures():
     for workload, rows in mg.CASES:
         f = np.load(mg.case_file(workload, rows))
         c = _case(workload, rows)
+        mfma_rows(rows + 1, rows + 1)
         assert np.array_equal(c.x.view(torch.int16).cpu().numpy(), f["x_bits"]), "seeded x"
         run = _runner(c)
         ids = torch.zeros(rows, c.p["topk"], dtype=torch.int32, device="cuda")
