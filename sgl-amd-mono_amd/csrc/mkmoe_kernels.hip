@@ -46,11 +46,15 @@ constexpr int kFp4 = MKMOE_FMT_MXFP4;
 constexpr int kAuxDev = 16;  // sc1: device-coherent access
 constexpr int kAuxNt = 2;    // nt: streamed once
 
-// control words at the start of the workspace
-constexpr int kCtlNorm = 0, kCtlA = 1, kCtlB = 2, kCtlC = 3, kCtlExit = 5;
-constexpr int kCtlCounters = 8;
+// control words at the start of the workspace: the exit count, the launch epoch, the error
+// words; then, from byte kCtlFlags, a flag array per hand-off (a word per workgroup: the epoch
+// of the launch in which the workgroup last arrived there)
+constexpr int kCtlNorm = 0, kCtlA = 1, kCtlB = 2, kCtlC = 3;  // hand-offs (flag arrays)
+constexpr int kCtlExit = 5, kCtlEpoch = 6;
 constexpr int kCtlErr = 8;  // MKMOE_ERRW_WORDS error words from here
-constexpr int kCtlBytes = 256;
+constexpr int kFlagWgs = 256;  // workgroups a persistent launch has at most
+constexpr int kCtlFlags = 256;
+constexpr int kCtlBytes = kCtlFlags + 4 * kFlagWgs * 4;
 
 enum Stage { kStageNorm = 1, kStageA = 2, kStageB = 3, kStageC = 4, kStageD = 5 };
 
@@ -346,23 +350,38 @@ __device__ __forceinline__ void record_error(const Params& p, int stage) {
   atomicAdd(&e[MKMOE_ERRW_COUNT], 1u);
 }
 
-// this workgroup is done with a stage: its sc1 stores acknowledged, then the count
-__device__ __forceinline__ void arrive(const Params& p, int which) {
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0)
-    __hip_atomic_fetch_add(ctl(p) + which, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// this launch's epoch: one past the word the previous launch's last workgroup left (every
+// workgroup reads the same word, which no workgroup changes before all have passed the last
+// hand-off)
+__device__ __forceinline__ uint32_t launch_epoch(const Params& p) {
+  return __builtin_amdgcn_readfirstlane(dld32(ws_rsrc(p), kCtlEpoch * 4)) + 1u;
 }
 
-// wait until ``target`` workgroups arrived at ``which`` (or the deadline passed); the data
-// behind the count is read with sc1 loads afterwards
-__device__ __forceinline__ void await_all(const Params& p, int which, uint32_t target, int stage) {
-  if (threadIdx.x == 0) {
+// this workgroup is done with a stage: its sc1 stores acknowledged, then its flag (an sc1
+// store of the epoch: cheaper to see than a device-scope atomic count, by about 1 µs)
+__device__ __forceinline__ void arrive(const Params& p, int which, uint32_t epoch) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) dst32(ws_rsrc(p), kCtlFlags + (which * kFlagWgs + blockIdx.x) * 4, epoch);
+}
+
+// wait until the first ``nwg`` workgroups' flags at ``which`` hold the epoch (or the deadline
+// passed): wave 0 reads all of them at once (a lane four); the data behind them is read with
+// sc1 loads afterwards
+__device__ __forceinline__ void await_all(const Params& p, int which, int nwg, int stage, uint32_t epoch) {
+  static_assert(kFlagWgs == 64 * 4, "a lane reads four flags");
+  if (threadIdx.x < 64) {
+    const auto rs = ws_rsrc(p);
+    const int lane = threadIdx.x;
+    const uint32_t off = kCtlFlags + (which * kFlagWgs + 4 * lane) * 4;
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
-    while (__hip_atomic_load(ctl(p) + which, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      __builtin_amdgcn_s_sleep(1);
+    while (true) {
+      const u32x4 f = dld128(rs, off);
+      const bool ok = (f.x == epoch || 4 * lane >= nwg) && (f.y == epoch || 4 * lane + 1 >= nwg) &&
+                      (f.z == epoch || 4 * lane + 2 >= nwg) && (f.w == epoch || 4 * lane + 3 >= nwg);
+      if (__ballot(!ok) == 0ull) break;
       if (__builtin_amdgcn_s_memrealtime() - t0 > p.deadline) {
-        record_error(p, stage);
+        if (lane == 0) record_error(p, stage);
         break;
       }
     }
@@ -370,15 +389,16 @@ __device__ __forceinline__ void await_all(const Params& p, int which, uint32_t t
   __syncthreads();
 }
 
-// the last workgroup out zeroes the counters for the next launch (graph replay safe)
-__device__ __forceinline__ void leave(const Params& p) {
+// the last workgroup out zeroes the exit count and leaves this launch's epoch for the next
+// launch (graph replay safe: the flags need no reset)
+__device__ __forceinline__ void leave(const Params& p, uint32_t epoch) {
   __syncthreads();
   if (threadIdx.x == 0) {
     uint32_t n = __hip_atomic_fetch_add(ctl(p) + kCtlExit, 1u, __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_AGENT);
     if (n == gridDim.x - 1) {
-      for (int i = 0; i < kCtlCounters; ++i)
-        __hip_atomic_store(ctl(p) + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ctl(p) + kCtlExit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ctl(p) + kCtlEpoch, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -2469,12 +2489,13 @@ __device__ __forceinline__ void stage_d(const Params& p, const Union<C>& un, Dow
 // the persistent launch past its C arrival: the down stage's first weights depend on the
 // union alone, so they are requested before the wait for the other workgroups' gate_up
 template <class C, bool MF>
-__device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg) {
+__device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg,
+                                            uint32_t epoch) {
   DownBatchOf<C, MF> bt;
   const int tr = p.tile_rows;
   const bool first = b * tr < C::H;
   if (first) down_first<C, MF>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt);
-  await_all(p, kCtlC, nwg, kStageC);
+  await_all(p, kCtlC, nwg, kStageC, epoch);
   __syncthreads();  // the tile's readers are done before the down stage reuses its LDS
   stage_d<C, MF>(p, un, sm, b, nwg, bt, first);
 }
@@ -2494,29 +2515,30 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   __shared__ Union<C> un;
   __shared__ StageSmem<C> sm;
   const int b = blockIdx.x, nwg = gridDim.x;
+  const uint32_t epoch = launch_epoch(p);
   if constexpr (C::NORM) {
     stage_norm<C>(p, b, nwg);
-    arrive(p, kCtlNorm);
-    await_all(p, kCtlNorm, nwg, kStageNorm);
+    arrive(p, kCtlNorm, epoch);
+    await_all(p, kCtlNorm, nwg, kStageNorm, epoch);
   }
   stage_a<C>(p, sm.a, b, nwg);
-  arrive(p, kCtlA);
-  await_all(p, kCtlA, nwg, kStageA);
+  arrive(p, kCtlA, epoch);
+  await_all(p, kCtlA, nwg, kStageA, epoch);
   if (p.rows <= kLocalRouteMax) {
     // every workgroup routes the step itself: no routing hand-off
     route_all<C>(p, sm.r, un.ids, un.wts, b);
     build_union<C>(p, un, true);
   } else {
     stage_b<C>(p, sm.r, b, nwg);
-    arrive(p, kCtlB);
-    await_all(p, kCtlB, nwg, kStageB);
+    arrive(p, kCtlB, epoch);
+    await_all(p, kCtlB, nwg, kStageB, epoch);
     build_union<C>(p, un, false);
   }
   stage_c<C>(p, un, sm.g, b, nwg);
-  arrive(p, kCtlC);
-  if (p.rows >= p.mfma_down) wait_then_d<C, true>(p, un, sm.d, b, nwg);
-  else wait_then_d<C, false>(p, un, sm.d, b, nwg);
-  leave(p);
+  arrive(p, kCtlC, epoch);
+  if (p.rows >= p.mfma_down) wait_then_d<C, true>(p, un, sm.d, b, nwg, epoch);
+  else wait_then_d<C, false>(p, un, sm.d, b, nwg, epoch);
+  leave(p, epoch);
 }
 
 template <class C>
@@ -2675,7 +2697,7 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
   DevInfo di;
   rc = device_info(dev, &di);
   if (rc) return rc;
-  const int nwg = di.cus;
+  const int nwg = di.cus < kFlagWgs ? di.cus : kFlagWgs;  // the persistent grid: a workgroup a CU
 
   Params p;
   p.x = (const uint16_t*)x;
