@@ -114,7 +114,7 @@ int mkmoe_shape_supported(const mkmoe_shape* shape);
 /* Bytes of workspace one stream needs for calls of up to shape->max_rows rows. */
 int mkmoe_workspace_bytes(const mkmoe_shape* shape, size_t* bytes);
 
-/* Zero the workspace's hand-off words (exit count, launch epoch, arrival flags)
+/* Zero the workspace's hand-off words (exit count, arrival flags)
  * and error words (enqueued on stream; not for use inside graph capture).
  * Required once before the first forward. */
 int mkmoe_init_workspace(const mkmoe_shape* shape, void* ws, size_t ws_bytes, void* stream);
@@ -123,7 +123,7 @@ int mkmoe_init_workspace(const mkmoe_shape* shape, void* ws, size_t ws_bytes, vo
  * rank's partial, before the all-reduce). topk_ids int32 [rows][topk] and
  * topk_w fp32 [rows][topk] receive the routing when not NULL. Enqueues exactly
  * one kernel on stream: no allocation, no host synchronisation, safe to
- * capture in a graph (a launch leaves the next its epoch; no reset). Calls that may
+ * capture in a graph (a launch clears its own hand-off flags). Calls that may
  * overlap need distinct workspaces. */
 int mkmoe_forward(const mkmoe_shape* shape, const mkmoe_weights* w, const void* x, int32_t rows,
                   void* out, int32_t* topk_ids, float* topk_w, void* ws, size_t ws_bytes,

@@ -46,11 +46,11 @@ constexpr int kFp4 = MKMOE_FMT_MXFP4;
 constexpr int kAuxDev = 16;  // sc1: device-coherent access
 constexpr int kAuxNt = 2;    // nt: streamed once
 
-// control words at the start of the workspace: the exit count, the launch epoch, the error
-// words; then, from byte kCtlFlags, a flag array per hand-off (a word per workgroup: the epoch
-// of the launch in which the workgroup last arrived there)
-constexpr int kCtlNorm = 0, kCtlA = 1, kCtlB = 2, kCtlC = 3;  // hand-offs (flag arrays)
-constexpr int kCtlExit = 5, kCtlEpoch = 6;
+// control words at the start of the workspace: the exit count, the error words; then, from
+// byte kCtlFlags, a flag array per hand-off (a word per workgroup: set on arrival, clear
+// between launches)
+constexpr int kCtlNorm = 0, kCtlA = 1, kCtlB = 2, kCtlC = 3;  // hand-offs (flag arrays; C last)
+constexpr int kCtlExit = 5;
 constexpr int kCtlErr = 8;  // MKMOE_ERRW_WORDS error words from here
 constexpr int kFlagWgs = 256;  // workgroups a persistent launch has at most
 constexpr int kCtlFlags = 256;
@@ -350,25 +350,18 @@ __device__ __forceinline__ void record_error(const Params& p, int stage) {
   atomicAdd(&e[MKMOE_ERRW_COUNT], 1u);
 }
 
-// this launch's epoch: one past the word the previous launch's last workgroup left (every
-// workgroup reads the same word, which no workgroup changes before all have passed the last
-// hand-off)
-__device__ __forceinline__ uint32_t launch_epoch(const Params& p) {
-  return __builtin_amdgcn_readfirstlane(dld32(ws_rsrc(p), kCtlEpoch * 4)) + 1u;
-}
-
-// this workgroup is done with a stage: its sc1 stores acknowledged, then its flag (an sc1
-// store of the epoch: cheaper to see than a device-scope atomic count, by about 1 µs)
-__device__ __forceinline__ void arrive(const Params& p, int which, uint32_t epoch) {
+// this workgroup is done with a stage: its sc1 stores acknowledged, then its flag set (an
+// sc1 store: cheaper to see than a device-scope atomic count, by about 1 µs)
+__device__ __forceinline__ void arrive(const Params& p, int which) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) dst32(ws_rsrc(p), kCtlFlags + (which * kFlagWgs + blockIdx.x) * 4, epoch);
+  if (threadIdx.x == 0) dst32(ws_rsrc(p), kCtlFlags + (which * kFlagWgs + blockIdx.x) * 4, 1u);
 }
 
-// wait until the first ``nwg`` workgroups' flags at ``which`` hold the epoch (or the deadline
+// wait until the first ``nwg`` workgroups' flags at ``which`` are set (or the deadline
 // passed): wave 0 reads all of them at once (a lane four); the data behind them is read with
 // sc1 loads afterwards
-__device__ __forceinline__ void await_all(const Params& p, int which, int nwg, int stage, uint32_t epoch) {
+__device__ __forceinline__ void await_all(const Params& p, int which, int nwg, int stage) {
   static_assert(kFlagWgs == 64 * 4, "a lane reads four flags");
   if (threadIdx.x < 64) {
     const auto rs = ws_rsrc(p);
@@ -377,8 +370,8 @@ __device__ __forceinline__ void await_all(const Params& p, int which, int nwg, i
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
     while (true) {
       const u32x4 f = dld128(rs, off);
-      const bool ok = (f.x == epoch || 4 * lane >= nwg) && (f.y == epoch || 4 * lane + 1 >= nwg) &&
-                      (f.z == epoch || 4 * lane + 2 >= nwg) && (f.w == epoch || 4 * lane + 3 >= nwg);
+      const bool ok = (f.x != 0u || 4 * lane >= nwg) && (f.y != 0u || 4 * lane + 1 >= nwg) &&
+                      (f.z != 0u || 4 * lane + 2 >= nwg) && (f.w != 0u || 4 * lane + 3 >= nwg);
       if (__ballot(!ok) == 0ull) break;
       if (__builtin_amdgcn_s_memrealtime() - t0 > p.deadline) {
         if (lane == 0) record_error(p, stage);
@@ -389,16 +382,23 @@ __device__ __forceinline__ void await_all(const Params& p, int which, int nwg, i
   __syncthreads();
 }
 
-// the last workgroup out zeroes the exit count and leaves this launch's epoch for the next
-// launch (graph replay safe: the flags need no reset)
-__device__ __forceinline__ void leave(const Params& p, uint32_t epoch) {
+// leave the launch with its flags clear for the next (graph replay safe): every workgroup
+// here has passed the C hand-off, so every workgroup has passed the earlier ones and a
+// workgroup clears its own flags of those; the last workgroup out clears the C flags (all
+// have passed that wait) and the exit count
+__device__ __forceinline__ void leave(const Params& p) {
   __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t n = __hip_atomic_fetch_add(ctl(p) + kCtlExit, 1u, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x < 64) {
+    const auto rs = ws_rsrc(p);
+    const int lane = threadIdx.x;
+    if (lane < kCtlC) dst32(rs, kCtlFlags + (lane * kFlagWgs + blockIdx.x) * 4, 0u);
+    uint32_t n = 0;
+    if (lane == 0)
+      n = __hip_atomic_fetch_add(ctl(p) + kCtlExit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    n = __builtin_amdgcn_readfirstlane(n);
     if (n == gridDim.x - 1) {
-      __hip_atomic_store(ctl(p) + kCtlExit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(ctl(p) + kCtlEpoch, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      dst128(rs, kCtlFlags + (kCtlC * kFlagWgs + 4 * lane) * 4, u32x4{0u, 0u, 0u, 0u});
+      if (lane == 0) __hip_atomic_store(ctl(p) + kCtlExit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -2489,13 +2489,12 @@ __device__ __forceinline__ void stage_d(const Params& p, const Union<C>& un, Dow
 // the persistent launch past its C arrival: the down stage's first weights depend on the
 // union alone, so they are requested before the wait for the other workgroups' gate_up
 template <class C, bool MF>
-__device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg,
-                                            uint32_t epoch) {
+__device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg) {
   DownBatchOf<C, MF> bt;
   const int tr = p.tile_rows;
   const bool first = b * tr < C::H;
   if (first) down_first<C, MF>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt);
-  await_all(p, kCtlC, nwg, kStageC, epoch);
+  await_all(p, kCtlC, nwg, kStageC);
   __syncthreads();  // the tile's readers are done before the down stage reuses its LDS
   stage_d<C, MF>(p, un, sm, b, nwg, bt, first);
 }
@@ -2515,30 +2514,29 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   __shared__ Union<C> un;
   __shared__ StageSmem<C> sm;
   const int b = blockIdx.x, nwg = gridDim.x;
-  const uint32_t epoch = launch_epoch(p);
   if constexpr (C::NORM) {
     stage_norm<C>(p, b, nwg);
-    arrive(p, kCtlNorm, epoch);
-    await_all(p, kCtlNorm, nwg, kStageNorm, epoch);
+    arrive(p, kCtlNorm);
+    await_all(p, kCtlNorm, nwg, kStageNorm);
   }
   stage_a<C>(p, sm.a, b, nwg);
-  arrive(p, kCtlA, epoch);
-  await_all(p, kCtlA, nwg, kStageA, epoch);
+  arrive(p, kCtlA);
+  await_all(p, kCtlA, nwg, kStageA);
   if (p.rows <= kLocalRouteMax) {
     // every workgroup routes the step itself: no routing hand-off
     route_all<C>(p, sm.r, un.ids, un.wts, b);
     build_union<C>(p, un, true);
   } else {
     stage_b<C>(p, sm.r, b, nwg);
-    arrive(p, kCtlB, epoch);
-    await_all(p, kCtlB, nwg, kStageB, epoch);
+    arrive(p, kCtlB);
+    await_all(p, kCtlB, nwg, kStageB);
     build_union<C>(p, un, false);
   }
   stage_c<C>(p, un, sm.g, b, nwg);
-  arrive(p, kCtlC, epoch);
-  if (p.rows >= p.mfma_down) wait_then_d<C, true>(p, un, sm.d, b, nwg, epoch);
-  else wait_then_d<C, false>(p, un, sm.d, b, nwg, epoch);
-  leave(p, epoch);
+  arrive(p, kCtlC);
+  if (p.rows >= p.mfma_down) wait_then_d<C, true>(p, un, sm.d, b, nwg);
+  else wait_then_d<C, false>(p, un, sm.d, b, nwg);
+  leave(p);
 }
 
 template <class C>
