@@ -114,9 +114,10 @@ int mkmoe_shape_supported(const mkmoe_shape* shape);
 /* Bytes of workspace one stream needs for calls of up to shape->max_rows rows. */
 int mkmoe_workspace_bytes(const mkmoe_shape* shape, size_t* bytes);
 
-/* Zero the workspace's hand-off words (exit count, arrival flags)
- * and error words (enqueued on stream; not for use inside graph capture).
- * Required once before the first forward. */
+/* Zero the workspace's hand-off words (exit count, arrival flags) and error
+ * words, and mark the polled router part sums (region 10) unset (enqueued on
+ * stream; not for use inside graph capture). Required once before the first
+ * forward. */
 int mkmoe_init_workspace(const mkmoe_shape* shape, void* ws, size_t ws_bytes, void* stream);
 
 /* One MoE block for rows bf16 rows x [rows][H] -> out bf16 [rows][H] (this
@@ -156,7 +157,8 @@ int mkmoe_clear_errors(void* ws, void* stream);
  * 3 x codes (shared rule), 4 x scales (shared rule), 5 router part sums
  * fp32 [rows][parts][E], 6 ids int32 [rows][topk], 7 weights fp32
  * [rows][topk], 8 shared intermediate bf16 [rows][S], 9 routed intermediate
- * bf16 [rows * topk][I]. */
+ * bf16 [rows * topk][I], 10 the router part sums as routing polls them (every
+ * word 0xFFFFFFFF between launches). */
 int mkmoe_workspace_region(const mkmoe_shape* shape, int32_t region, size_t* offset,
                            size_t* bytes);
 

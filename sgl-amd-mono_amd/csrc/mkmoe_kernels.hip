@@ -80,7 +80,7 @@ using CfgTp4Fp4 = Cfg<7168, 256, 8, 8, 4, 512, 512, kFp4, 7, false>;
 using CfgTp2Fp4Norm = Cfg<7168, 256, 8, 8, 4, 1024, 1024, kFp4, 7, true>;
 
 // ---------------------------------------------------------------- workspace layout
-constexpr int kRegions = 10;
+constexpr int kRegions = 11;
 
 struct Layout {
   size_t off[kRegions];
@@ -104,6 +104,7 @@ MKMOE_HD inline Layout make_layout(int H, int E, int K, int I, int S, int fmt, i
   sz[7] = (size_t)rm * K * 4;                                         // weights
   sz[8] = (size_t)rm * S * 2;                                         // shared mid, bf16
   sz[9] = (size_t)rm * K * I * 2;                                     // routed mid, bf16
+  sz[10] = sz[5];  // the part sums as routing polls them (kPartUnset between launches)
   size_t off = kCtlBytes;
   for (int i = 0; i < kRegions; ++i) {
     L.off[i] = off;
@@ -509,7 +510,11 @@ __device__ __forceinline__ void router_unit(const Params& p, RouterSmem<C>& sm, 
       }
     }
     const float s = tree_sum<64>(acc);
-    if (lane == 0) dst32(rs, p.off[5] + (((uint32_t)r * C::P + part) * C::E + e) * 4, f2u(s));
+    if (lane == 0) {
+      const uint32_t at = (((uint32_t)r * C::P + part) * C::E + e) * 4;
+      dst32(rs, p.off[5] + at, f2u(s));   // kept for inspection
+      dst32(rs, p.off[10] + at, f2u(s));  // polled, cleared once routed
+    }
   }
 }
 
@@ -555,6 +560,21 @@ __device__ __forceinline__ void quant_unit(const Params& p, int r, int c, int la
 }
 
 // workgroup units: (router K part, block of 8 experts), then one unit a row to quantize
+// The router's part sums are also stored into region 10, which holds kPartUnset between
+// launches, so that routing can read them as they land. It is a NaN that no part sum takes: a NaN propagated from a bf16 input keeps a
+// payload whose low 16 bits are zero, and a NaN the arithmetic generates is the default one.
+constexpr uint32_t kPartUnset = 0xFFFFFFFFu;
+// region 10's part sums of the step's rows back to kPartUnset, spread over the grid (once
+// every workgroup is past its routing)
+template <class C>
+__device__ __forceinline__ void reset_parts(const Params& p, int b, int nwg) {
+  static_assert(C::E % 4 == 0, "16-byte stores");
+  const auto rs = ws_rsrc(p);
+  const int chunks = p.rows * C::P * C::E / 4;
+  for (int i = b * kThreads + (int)threadIdx.x; i < chunks; i += nwg * kThreads)
+    dst128(rs, p.off[10] + (uint32_t)i * 16, u32x4{kPartUnset, kPartUnset, kPartUnset, kPartUnset});
+}
+
 template <class C>
 __device__ __forceinline__ void stage_a(const Params& p, RouterSmem<C>& sm, int b, int nwg) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -615,7 +635,9 @@ __device__ __forceinline__ float segment_max(float v) {
 // scores and choices of (row r0 + i, expert e) for i < n, spread over the workgroup: the
 // logit sums the router's part sums in part order; a NaN score weighs 0 and its choice
 // (score + bias) never wins, as in the reference's route
-template <class C>
+// POLL: the part sums are read before the router's hand-off, each reread until it holds a
+// value (kPartUnset marks a part sum not yet written in this launch)
+template <class C, bool POLL = false>
 __device__ __forceinline__ void route_scores(const Params& p, RouteSmem<C>& sm, int r0, int n) {
 #pragma clang fp contract(off)
   constexpr int MJ = (kRouteRows * C::E + kThreads - 1) / kThreads;  // (row, expert) a thread
@@ -623,14 +645,36 @@ __device__ __forceinline__ void route_scores(const Params& p, RouteSmem<C>& sm, 
   const int tid = threadIdx.x;
   // every part sum ([rows][P][E]) requested before the first is used
   float part[MJ][C::P];
+  auto part_off = [&](int j, int q) {
+    const int idx = tid + j * kThreads;
+    const int i = idx / C::E, e = idx - i * C::E;
+    return p.off[POLL ? 10 : 5] + ((uint32_t)(r0 + i) * C::P * C::E + e) * 4 + q * C::E * 4;
+  };
 #pragma unroll
   for (int j = 0; j < MJ; ++j) {
     const int idx = tid + j * kThreads;
-    const int i = idx / C::E, e = idx - i * C::E;
-    const uint32_t part0 = p.off[5] + ((uint32_t)(r0 + i) * C::P * C::E + e) * 4;
 #pragma unroll
-    for (int q = 0; q < C::P; ++q)
-      part[j][q] = idx < n * C::E ? u2f(dld32(rs, part0 + q * C::E * 4)) : 0.0f;
+    for (int q = 0; q < C::P; ++q) part[j][q] = idx < n * C::E ? u2f(dld32(rs, part_off(j, q))) : 0.0f;
+  }
+  if constexpr (POLL) {
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    while (true) {
+      bool unset = false;
+#pragma unroll
+      for (int j = 0; j < MJ; ++j)
+#pragma unroll
+        for (int q = 0; q < C::P; ++q) unset |= f2u(part[j][q]) == kPartUnset;
+      if (!unset) break;
+      if (__builtin_amdgcn_s_memrealtime() - t0 > p.deadline) {
+        record_error(p, kStageA);
+        break;
+      }
+#pragma unroll
+      for (int j = 0; j < MJ; ++j)
+#pragma unroll
+        for (int q = 0; q < C::P; ++q)
+          if (f2u(part[j][q]) == kPartUnset) part[j][q] = u2f(dld32(rs, part_off(j, q)));
+    }
   }
 #pragma unroll
   for (int j = 0; j < MJ; ++j) {
@@ -810,7 +854,7 @@ __device__ __forceinline__ void route_all(const Params& p, RouteSmem<C>& sm, int
   for (int r0 = 0; r0 < p.rows; r0 += kRouteRows) {
     const int n = min(kRouteRows, p.rows - r0);
     __syncthreads();  // the previous chunk's selections are done with the LDS
-    route_scores<C>(p, sm, r0, n);
+    route_scores<C, true>(p, sm, r0, n);
     __syncthreads();
     for (int i = wave; i < n; i += kWaves) {
       int id;
@@ -2495,6 +2539,7 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
   const bool first = b * tr < C::H;
   if (first) down_first<C, MF>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt);
   await_all(p, kCtlC, nwg, kStageC);
+  reset_parts<C>(p, b, nwg);  // every workgroup is past its routing
   __syncthreads();  // the tile's readers are done before the down stage reuses its LDS
   stage_d<C, MF>(p, un, sm, b, nwg, bt, first);
 }
@@ -2521,12 +2566,14 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   }
   stage_a<C>(p, sm.a, b, nwg);
   arrive(p, kCtlA);
-  await_all(p, kCtlA, nwg, kStageA);
   if (p.rows <= kLocalRouteMax) {
-    // every workgroup routes the step itself: no routing hand-off
+    // every workgroup routes the step itself, reading the router's part sums as they land:
+    // no routing hand-off; the A hand-off (the x codes) is awaited before the gate_up
     route_all<C>(p, sm.r, un.ids, un.wts, b);
     build_union<C>(p, un, true);
+    await_all(p, kCtlA, nwg, kStageA);
   } else {
+    await_all(p, kCtlA, nwg, kStageA);
     stage_b<C>(p, sm.r, b, nwg);
     arrive(p, kCtlB);
     await_all(p, kCtlB, nwg, kStageB);
@@ -2557,6 +2604,7 @@ template <class C>
 __global__ __launch_bounds__(kThreads) void k_c(Params p) {
   __shared__ Union<C> un;
   __shared__ GuSmem<C> sm;
+  reset_parts<C>(p, blockIdx.x, gridDim.x);  // the routing launch is done with them
   build_union<C>(p, un, false);
   stage_c<C>(p, un, sm, blockIdx.x, gridDim.x);
 }
@@ -2789,6 +2837,10 @@ int mkmoe_init_workspace(const mkmoe_shape* shape, void* ws, size_t ws_bytes, vo
   if (!ws) return MKMOE_ERR_NULL;
   if (ws_bytes < layout_of(shape).total) return MKMOE_ERR_WORKSPACE;
   if (hipMemsetAsync(ws, 0, kCtlBytes, (hipStream_t)stream) != hipSuccess) return MKMOE_ERR_HIP;
+  // the polled copy of the router's part sums starts unset (kPartUnset: every byte 0xFF)
+  const Layout L = layout_of(shape);
+  if (hipMemsetAsync((uint8_t*)ws + L.off[10], 0xFF, L.size[10], (hipStream_t)stream) != hipSuccess)
+    return MKMOE_ERR_HIP;
   return MKMOE_OK;
 }
 

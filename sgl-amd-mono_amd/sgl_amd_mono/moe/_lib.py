@@ -26,6 +26,7 @@ REGIONS = {
     "weights": 7,
     "shared_mid": 8,
     "mid": 9,
+    "router_parts_polled": 10,
 }
 STAGES = {1: "norm", 2: "router + quantize", 3: "route", 4: "gate_up (routed + shared)", 5: "down (shared + routed) + combine"}
 

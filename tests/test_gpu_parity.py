@@ -95,6 +95,8 @@ def _check(c, rows, run, exact):
     parts = parts.view(torch.float32).cpu().numpy().reshape(rows, c.p["router_parts"], c.p["experts"])
     parts = np.ascontiguousarray(parts.transpose(0, 2, 1))
     assert np.array_equal(parts.view(np.uint32), c.parts.view(np.uint32)), "router part sums"
+    # the polled copy is back to unset (every byte 0xFF) for the next launch
+    assert bool((run.region("router_parts_polled") == 0xFF).all()), "polled part sums left unset"
     # routing, bit for bit
     assert np.array_equal(ids.cpu().numpy(), c.ids), "expert ids"
     assert np.array_equal(wts.cpu().numpy().view(np.uint32), c.wts.view(np.uint32)), "routing weights"
