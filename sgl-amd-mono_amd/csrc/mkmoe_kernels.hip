@@ -2395,7 +2395,7 @@ __device__ __forceinline__ void down_valu(const Params& p, const Union<C>& un, D
     const int n_units = (s_hi - s_lo + 1) * kRowBlocks;
     auto load = valu_down_loader<C>(p, un, h0, hn, s_lo);
     // the first batch's weights are requested before the picks' rows are quantized
-    if (pb0 > 0 || !first_ready) bt.load(threadIdx.x >> 6, n_units, load);
+    if (pb0 > 0 || !first_ready || threadIdx.x < 64) bt.load(threadIdx.x >> 6, n_units, load);
     __syncthreads();  // the previous batch is done with the LDS rows
     quant_rows_lds<C::FMT, C::I, C::MQS>(
         p, [&](int i) { return p.off[9] + (uint32_t)un.picks[pb0 + i] * C::I * 2; }, pbn, sm.q, sm.s);
@@ -2440,7 +2440,8 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
     int s_lo, s_hi;
     batch_slots(un, pb0, pbn, s_lo, s_hi);
     const int n_units = (s_hi - s_lo + 1) * nb;
-    if ((pb0 > 0 || !first_ready) && wave < n_units) mfma_issue<C>(p, un, h0, hn, s_lo, wave, slot, bt.nxt, lane);
+    if ((pb0 > 0 || !first_ready || wave == 0) && wave < n_units)
+      mfma_issue<C>(p, un, h0, hn, s_lo, wave, slot, bt.nxt, lane);
     __syncthreads();  // the previous batch is done with the LDS rows
     quant_rows_lds<C::FMT, C::I, C::MQS, 2 * kQuantBatch>(
         p, [&](int i) { return p.off[9] + (uint32_t)un.picks[pb0 + i] * C::I * 2; }, pbn, sm.q, sm.s);
@@ -2469,8 +2470,8 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
   }
 }
 
-// request the first pick batch's first units of tile rows [h0, h0 + hn); the down stage goes
-// on from them
+// request the first pick batch's first units of tile rows [h0, h0 + hn) (waves 1-7); the down
+// stage goes on from them
 template <class C, bool MF>
 __device__ __forceinline__ void down_first(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
                                            DownBatchOf<C, MF>& bt) {
@@ -2478,6 +2479,9 @@ __device__ __forceinline__ void down_first(const Params& p, const Union<C>& un, 
   int s_lo, s_hi;
   batch_slots(un, 0, min(C::PB, npk), s_lo, s_hi);
   const int wave = threadIdx.x >> 6;
+  // not wave 0, which polls the hand-off next: its flag reads would return only after
+  // these weights (a wave's loads return in order)
+  if (wave == 0) return;
   if constexpr (MF) {
     if (wave < (s_hi - s_lo + 1) * ((hn + 15) / 16))
       mfma_issue<C>(p, un, h0, hn, s_lo, wave, sm.wslot[wave], bt.nxt, threadIdx.x & 63);
@@ -2488,7 +2492,7 @@ __device__ __forceinline__ void down_first(const Params& p, const Union<C>& un, 
 
 // tile rows [h0, h0 + hn): the routed down GEMVs (MFMA or VALU, as MF), the shared expert's
 // down, then the combine; first_ready: the routed down's first units are already requested
-// into bt
+// into bt (waves 1-7)
 template <class C, bool MF>
 __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
                                           DownBatchOf<C, MF>& bt, bool first_ready) {
