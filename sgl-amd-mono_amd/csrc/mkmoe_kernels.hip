@@ -1407,14 +1407,18 @@ struct GuTile {
   __device__ __forceinline__ static int wrow(int W, int j0, int r) {
     return WFMT == kFp8 ? (r < 8 ? j0 + r : W + j0 + r - 8) : (r >> 4) * W + j0 + (r & 15);
   }
-  // w: the [2W][H] weight (wr: its resource words), s: its scales
-  __device__ __forceinline__ void issue(i32x4 wr, const void* s, int W, int j0, uint8_t* slot, int lane, int wave) {
+  // w: the [2W][H] weight (wr: its resource words), s: its scales; the unit's columns
+  // j0 .. j0 + nc - 1 (nc = NC, or NC / 2 at a share's ends: the other rows are requested
+  // past the resource, so the slot holds zeros there and no memory is read)
+  __device__ __forceinline__ void issue(i32x4 wr, const void* s, int W, int j0, int nc, uint8_t* slot, int lane,
+                                        int wave) {
     const int s0 = wave * SPW;
     constexpr int ROWB = WFMT == kFp8 ? C::H : C::H / 2;  // bytes a weight row
 #pragma unroll
     for (int i = 0; i < SLOT / 1024; ++i) {
       const int pos = i * 64 + lane, r = pos / CPW, c = (pos % CPW) ^ key(r);
-      lds_dma16(wr, slot + i * 1024, (uint32_t)wrow(W, j0, r) * ROWB + s0 * (RB / SPW) + c * 16);
+      const bool live = (WFMT == kFp8 ? (r & 7) : (r & 15)) < nc;
+      lds_dma16(wr, slot + i * 1024, live ? (uint32_t)wrow(W, j0, r) * ROWB + s0 * (RB / SPW) + c * 16 : kNoLoad);
     }
     if constexpr (WFMT == kFp4) {
       const int m = lane & 15, j = lane >> 4;
@@ -1510,10 +1514,23 @@ __device__ __forceinline__ void gu_mma(const GuTile<C, WFMT>& t, const GuX<C, WF
 // LDS slot as soon as the current one is read out of it, so it streams while the current
 // unit's MFMAs run and its partial tiles add in LDS (in wave order). An FP8 weight's block
 // scales go to LDS when the group changes.
-template <class C, int WFMT, class GroupFn, class XFn, class EmitFn>
-__device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo, int hi, GroupFn group, XFn xload, EmitFn emit) {
+template <class C, int WFMT, bool HALF, class GroupFn, class XFn, class EmitFn>
+__device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h, GroupFn group, XFn xload,
+                                        EmitFn emit) {
   using T = GuTile<C, WFMT>;
-  if (lo >= hi) return;
+  if (lo_h >= hi_h) return;
+  // HALF: the share is half-units [lo_h, hi_h): whole units, but at either end possibly one
+  // half; else units [lo_h, hi_h)
+  const int lo = HALF ? lo_h >> 1 : lo_h, hi = HALF ? (hi_h + 1) >> 1 : hi_h;
+  auto half = [&](int u, int& c0, int& nc) {
+    if constexpr (HALF) {
+      c0 = u == lo && (lo_h & 1) ? T::NC / 2 : 0;
+      nc = (u == hi - 1 && (hi_h & 1) ? T::NC / 2 : T::NC) - c0;
+    } else {
+      c0 = 0;
+      nc = T::NC;
+    }
+  };
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nb = W / T::NC;
   constexpr uint32_t WB = WFMT == kFp8 ? C::H : C::H / 2;  // bytes a weight row
@@ -1525,11 +1542,17 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo, int hi, Gr
   int tg_w = lo / nb, np_w;  // the group whose unit is in flight
   group(tg_w, wb, sb, np_w);
   __syncthreads();  // the LDS's previous users are done
-  t.issue(weight_rsrc_words(wb, 2u * W * WB), sb, W, (lo % nb) * T::NC, slot, lane, wave);
+  {
+    int c0, nc;
+    half(lo, c0, nc);
+    t.issue(weight_rsrc_words(wb, 2u * W * WB), sb, W, (lo % nb) * T::NC + c0, nc, slot, lane, wave);
+  }
   int tg_x = -1, np_x = 0;  // the group in x
   const void* sb_x = sb;
   for (int u = lo; u < hi; ++u) {
-    const int j0 = (u % nb) * T::NC;
+    int c0, ncu;
+    half(u, c0, ncu);
+    const int j0 = (u % nb) * T::NC + c0;
     const bool fresh = tg_w != tg_x;
     if (fresh) {
       xload(tg_w, np_w, x);
@@ -1557,14 +1580,16 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo, int hi, Gr
         tg_w = tn;
         group(tg_w, wb, sb, np_w);
       }
-      t.issue(weight_rsrc_words(wb, 2u * W * WB), sb, W, ((u + 1) % nb) * T::NC, slot, lane, wave);
+      int c1, nc1;
+      half(u + 1, c1, nc1);
+      t.issue(weight_rsrc_words(wb, 2u * W * WB), sb, W, ((u + 1) % nb) * T::NC + c1, nc1, slot, lane, wave);
     }
     f32x4 acc[T::NA];
     gu_mma<C, WFMT>(t, x, sm.m.wsc, W, j0, lane, wave, acc);
 #pragma unroll
     for (int q = 0; q < T::NA; ++q) sm.red[q][wave][lane] = acc[q];
     __syncthreads();
-    if (tid < 16 * T::NC) {
+    if (tid < 16 * ncu) {
       // C[m][n] is element m % 4 of lane n + 16 (m / 4); FP8: up row m + 8 is 32 lanes on
       const int m = tid >> 4, n = tid & 15;
       const int L = n + 16 * (m >> 2), v = m & 3;
@@ -2246,13 +2271,18 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
   const auto rs = ws_rsrc(p);
   const int n_sh = (p.rows + kMfmaPicks - 1) / kMfmaPicks * (C::S / GuTile<C, kFp8>::NC);
   const int n_rt = un.ntg_r * (C::I / GuTile<C, C::FMT>::NC);
+  // FP8: the share in half-units (a unit's first or last NC / 2 columns), so that shares
+  // differ by half a unit at most (with MXFP4 weights the extra bookkeeping crowds the
+  // registers of the gate_up loop: whole units)
+  constexpr bool HALF = C::FMT == kFp8;
+  constexpr int HU = HALF ? 2 : 1;  // deal steps a unit
   int lo, hi;
-  even_share(n_sh + n_rt, b, nwg, lo, hi);
+  even_share(HU * (n_sh + n_rt), b, nwg, lo, hi);
   {
     const uint32_t qoff = C::FMT == kFp4 ? p.off[3] : p.off[1];
     const uint32_t soff = C::FMT == kFp4 ? p.off[4] : p.off[2];
-    gu_mfma<C, kFp8>(
-        sm, C::S, lo, min(hi, n_sh),
+    gu_mfma<C, kFp8, HALF>(
+        sm, C::S, lo, min(hi, HU * n_sh),
         [&](int tg, const uint8_t*& w, const void*& s, int& np) {
           w = p.sgu;
           s = p.sgu_s;
@@ -2269,8 +2299,8 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
     const int slot = un.tg_slot[tg];
     return un.slot_start[slot] + (tg - un.tg_start[slot]) * kMfmaPicks;
   };
-  gu_mfma<C, C::FMT>(
-      sm, C::I, max(lo, n_sh) - n_sh, hi - n_sh,
+  gu_mfma<C, C::FMT, HALF>(
+      sm, C::I, max(lo, HU * n_sh) - HU * n_sh, hi - HU * n_sh,
       [&](int tg, const uint8_t*& w, const void*& s, int& np) {
         const int slot = un.tg_slot[tg];
         const int e = un.slot_e[slot];
