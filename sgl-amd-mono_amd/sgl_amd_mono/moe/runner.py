@@ -225,7 +225,12 @@ class MoeRunner:
             )
 
     def clear_errors(self) -> None:
-        _lib.check(self.lib.mkmoe_clear_errors(self.ws.data_ptr(), self._stream()), "clear errors")
+        """Reset the workspace after a device error: the error words, and the hand-off state
+        (flags, polled router part sums) that a launch cut short by a deadline may leave."""
+        _lib.check(
+            self.lib.mkmoe_init_workspace(ctypes.byref(self.shape), self.ws.data_ptr(), self.ws.numel(), self._stream()),
+            "workspace init",
+        )
 
 
 def set_deadline(seconds: float) -> None:
