@@ -843,14 +843,15 @@ __device__ __forceinline__ void route_row(const Params& p, RouteSmem<C>& sm, int
   }
 }
 
-// every row's routing in this workgroup, into LDS (ids, wts: [rows][topk]); wave w selects
-// rows w, w + 8, ... of each kRouteRows chunk. Workgroup 0 also writes the workspace copies
-// and the outputs.
+// every row's routing in this workgroup, into LDS (ids, wts: [rows][topk]; rows_of: the rows
+// that picked each expert, as bitmaps); wave w selects rows w, w + 8, ... of each kRouteRows
+// chunk. Workgroup 0 also writes the workspace copies and the outputs.
 template <class C>
 __device__ __forceinline__ void route_all(const Params& p, RouteSmem<C>& sm, int* ids, float* wts,
-                                          int b) {
+                                          uint32_t (*rows_of)[2], int b) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const auto rs = ws_rsrc(p);
+  for (int e = threadIdx.x; e < C::E; e += kThreads) rows_of[e][0] = rows_of[e][1] = 0u;
   for (int r0 = 0; r0 < p.rows; r0 += kRouteRows) {
     const int n = min(kRouteRows, p.rows - r0);
     __syncthreads();  // the previous chunk's selections are done with the LDS
@@ -864,6 +865,7 @@ __device__ __forceinline__ void route_all(const Params& p, RouteSmem<C>& sm, int
       if (lane < C::K) {
         ids[r * C::K + lane] = id;
         wts[r * C::K + lane] = w;
+        atomicOr(&rows_of[id][r >> 5], 1u << (r & 31));
         if (b == 0) {
           dst32(rs, p.off[6] + (r * C::K + lane) * 4, (uint32_t)id);
           dst32(rs, p.off[7] + (r * C::K + lane) * 4, f2u(w));
@@ -1804,23 +1806,24 @@ __device__ __forceinline__ void build_union(const Params& p, Union<C>& un, bool 
   const int tgs = p.rows >= p.mfma_gate ? kMfmaPicks : kTokGroup;  // picks a token group
   const auto rs = ws_rsrc(p);
   __syncthreads();
-  for (int e = tid; e < C::E; e += kThreads) un.rows_of[e][0] = un.rows_of[e][1] = 0u;
-  __syncthreads();
-  // one pick a thread; its expert is kept for the placement below
+  // one pick a thread; its expert is kept for the placement below. local: the routing left
+  // the picks and the row bitmaps in LDS
   static_assert(kRowsMax * C::K <= kThreads, "a pick a thread");
   const int t = tid;
   int my_e = 0;
-  if (t < npk) {
-    if (local) {
-      my_e = un.ids[t];
-    } else {
+  if (local) {
+    if (t < npk) my_e = un.ids[t];
+  } else {
+    for (int e = tid; e < C::E; e += kThreads) un.rows_of[e][0] = un.rows_of[e][1] = 0u;
+    __syncthreads();
+    if (t < npk) {
       my_e = min(max((int)dld32(rs, p.off[6] + t * 4), 0), C::E - 1);
       un.wts[t] = u2f(dld32(rs, p.off[7] + t * 4));
+      const int r = t / C::K;
+      atomicOr(&un.rows_of[my_e][r >> 5], 1u << (r & 31));
     }
-    const int r = t / C::K;
-    atomicOr(&un.rows_of[my_e][r >> 5], 1u << (r & 31));
+    __syncthreads();
   }
-  __syncthreads();
   // wave 0: lane l takes experts l * EPL .. l * EPL + EPL - 1: slots, picks, token groups and
   // their gate_up costs (a group of c picks costs kColCost + c a column), prefix-summed
   if (tid < 64) {
@@ -2603,7 +2606,7 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   if (p.rows <= kLocalRouteMax) {
     // every workgroup routes the step itself, reading the router's part sums as they land:
     // no routing hand-off; the A hand-off (the x codes) is awaited before the gate_up
-    route_all<C>(p, sm.r, un.ids, un.wts, b);
+    route_all<C>(p, sm.r, un.ids, un.wts, un.rows_of, b);
     build_union<C>(p, un, true);
     await_all(p, kCtlA, nwg, kStageA);
   } else {
