@@ -352,16 +352,18 @@ __device__ __forceinline__ void record_error(const Params& p, int stage) {
 }
 
 // this workgroup is done with a stage: its sc1 stores acknowledged, then its flag set (an
-// sc1 store: cheaper to see than a device-scope atomic count, by about 1 µs)
+// sc1 store: cheaper to see than a device-scope atomic count, by about 1 µs). Wave 1 stores
+// it, so that wave 0's flag reads (await_all) do not complete behind the store (a wave's
+// memory operations complete in order); await_all counts the own flag as set.
 __device__ __forceinline__ void arrive(const Params& p, int which) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) dst32(ws_rsrc(p), kCtlFlags + (which * kFlagWgs + blockIdx.x) * 4, 1u);
+  if (threadIdx.x == 64) dst32(ws_rsrc(p), kCtlFlags + (which * kFlagWgs + blockIdx.x) * 4, 1u);
 }
 
 // wait until the first ``nwg`` workgroups' flags at ``which`` are set (or the deadline
-// passed): wave 0 reads all of them at once (a lane four); the data behind them is read with
-// sc1 loads afterwards
+// passed; this workgroup's own flag counts as set, it has arrived): wave 0 reads all of them
+// at once (a lane four); the data behind them is read with sc1 loads afterwards
 __device__ __forceinline__ void await_all(const Params& p, int which, int nwg, int stage) {
   static_assert(kFlagWgs == 64 * 4, "a lane reads four flags");
   if (threadIdx.x < 64) {
@@ -371,8 +373,9 @@ __device__ __forceinline__ void await_all(const Params& p, int which, int nwg, i
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
     while (true) {
       const u32x4 f = dld128(rs, off);
-      const bool ok = (f.x != 0u || 4 * lane >= nwg) && (f.y != 0u || 4 * lane + 1 >= nwg) &&
-                      (f.z != 0u || 4 * lane + 2 >= nwg) && (f.w != 0u || 4 * lane + 3 >= nwg);
+      const int i = 4 * lane, own = blockIdx.x;
+      const bool ok = (f.x != 0u || i == own || i >= nwg) && (f.y != 0u || i + 1 == own || i + 1 >= nwg) &&
+                      (f.z != 0u || i + 2 == own || i + 2 >= nwg) && (f.w != 0u || i + 3 == own || i + 3 >= nwg);
       if (__ballot(!ok) == 0ull) break;
       if (__builtin_amdgcn_s_memrealtime() - t0 > p.deadline) {
         if (lane == 0) record_error(p, stage);
