@@ -236,6 +236,19 @@ def test_staged_equals_fused_and_repeats(workload, rows):
     assert torch.equal(a.view(torch.int16), d.view(torch.int16)), "repeat differs"
 
 
+def test_row_counts_in_turn_on_one_workspace():
+    """Launches of changing row counts (local routing and the routing hand-off in turn) on one
+    runner: each launch must find the hand-off flags and the polled part sums as the previous
+    one left them, and be checked against its own oracle case."""
+    run = None
+    for rows in (4, 20, 1, 16, 3):
+        c = _case("cfg1_plumbing_fp8", rows)
+        if run is None:
+            run = _runner(c)
+        print(f"\ncfg1_plumbing_fp8 R={rows} on the shared workspace", flush=True)
+        _check(c, rows, run, exact=False)
+
+
 def test_graph_replay_bitwise():
     """Every row count of one preset in one graph, replayed with eager work between replays."""
     c = _case("cfg2_tp4_fp8", 8)
