@@ -180,3 +180,23 @@ def test_rmsnorm_close_to_fp64():
     ref = xd * torch.rsqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-6) * w.double()
     ulp = torch.ldexp(torch.ones_like(ref), torch.frexp(ref.abs())[1] - 8)
     assert float(((got.double() - ref).abs() / ulp).max()) <= 1.0
+
+
+def test_part_sums_never_take_the_unset_marker():
+    """The polled copy of the router's part sums marks an unwritten word with 0xFFFFFFFF.
+    No part sum takes that bit pattern: inputs with bf16 NaNs of every payload, infinities
+    of both signs (inf - inf and 0 * inf generate NaNs) and ordinary values."""
+    rng = np.random.default_rng(11)
+    h, e, r, parts = 1024, 16, 6, 2
+    x = torch.from_numpy(rng.standard_normal((r, h)).astype(np.float32)).to(torch.bfloat16)
+    w = torch.from_numpy(rng.standard_normal((e, h)).astype(np.float32)).to(torch.bfloat16)
+    xb, wb = x.view(torch.int16), w.view(torch.int16)
+    specials = [0x7FFF, -1, 0x7FC1, -64, 0x7F80, -128, 0]  # NaNs (payloads), +inf, -inf, 0
+    for i, v in enumerate(specials):
+        xb[i % r, (37 * i) % h] = v
+        wb[i % e, (37 * i + 5) % h] = v
+    xb[r - 1, 0], wb[0, 0] = 0x7F80, 0  # 0 * inf
+    xb[r - 1, 1], wb[1, 1] = 0x7F80, 0x3F80  # +inf ...
+    xb[r - 1, 9], wb[1, 9] = -128, 0x3F80  # ... and -inf in one sum
+    ps = rt.router_part_sums(x, w, parts)
+    assert np.isnan(ps).any() and not (ps.view(np.uint32) == 0xFFFFFFFF).any()
