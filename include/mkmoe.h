@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MKMOE_ABI_VERSION 1
+#define MKMOE_ABI_VERSION 2
 
 /* weight formats */
 #define MKMOE_FMT_FP8_B128 1 /* e4m3, fp32 scale per 128 x 128 block */
@@ -120,37 +120,49 @@ int mkmoe_workspace_bytes(const mkmoe_shape* shape, size_t* bytes);
  * forward. */
 int mkmoe_init_workspace(const mkmoe_shape* shape, void* ws, size_t ws_bytes, void* stream);
 
+/* Per-call options (NULL: the defaults). No counterpart in the reference, whose
+ * deadline is a build-time constant of the guard (common/guard.py:69-89) and whose
+ * kernels pick their GEMM instruction per width at build time (spec.py:959-967). A
+ * field left 0 takes its default. */
+typedef struct mkmoe_options {
+  double deadline_s;      /* device wait deadline in seconds (default 2.0, at most 3600): a
+                           * wait past it records the error words and gives up, so the
+                           * launch always ends */
+  int32_t mfma_gate_rows; /* launches with at least this many rows run the gate_up GEMMs
+                           * (routed and shared) on MFMA (default 1: always); fewer rows run
+                           * the fixed-order VALU GEMVs, bit-identical to the oracle */
+  int32_t mfma_down_rows; /* the same for the down GEMMs (default 1) */
+  int32_t reserved[4];
+} mkmoe_options;
+
 /* One MoE block for rows bf16 rows x [rows][H] -> out bf16 [rows][H] (this
  * rank's partial, before the all-reduce). topk_ids int32 [rows][topk] and
  * topk_w fp32 [rows][topk] receive the routing when not NULL. Enqueues exactly
  * one kernel on stream: no allocation, no host synchronisation, safe to
  * capture in a graph (a launch clears its own hand-off flags). Calls that may
- * overlap need distinct workspaces. */
+ * overlap need distinct workspaces. opts may be NULL. */
 int mkmoe_forward(const mkmoe_shape* shape, const mkmoe_weights* w, const void* x, int32_t rows,
                   void* out, int32_t* topk_ids, float* topk_w, void* ws, size_t ws_bytes,
-                  void* stream);
+                  const mkmoe_options* opts, void* stream);
 
 /* The same results in one launch per stage (norm, router + quantize, route,
  * gate_up (routed and shared), down (shared and routed) + combine); for
  * diagnosis and per-stage profiles. */
 int mkmoe_forward_staged(const mkmoe_shape* shape, const mkmoe_weights* w, const void* x,
                          int32_t rows, void* out, int32_t* topk_ids, float* topk_w, void* ws,
-                         size_t ws_bytes, void* stream);
+                         size_t ws_bytes, const mkmoe_options* opts, void* stream);
 
-/* Device wait deadline, in seconds, for the persistent launch's hand-offs
- * (default 2.0). A wait past it sets the error words and the launch ends. */
-int mkmoe_set_deadline(double seconds);
-
-/* Row counts from which launches run the gate_up GEMMs (routed and shared) and the down
- * GEMMs (routed and shared) on MFMA (defaults: 1 and 1, i.e. always). Below them
- * the fixed-order VALU GEMVs run, whose output is bit-identical to the oracle; MFMA launches
- * are held to the numerics bounds of the spec. No counterpart in the reference, whose kernels
- * pick their GEMM instruction per width at build time (spec.py:959-967 widths). */
-int mkmoe_set_mfma_rows(int32_t gate_up_rows, int32_t down_rows);
-
-/* Copy the MKMOE_ERRW_WORDS error words to host memory (synchronises stream). */
+/* Copy the MKMOE_ERRW_WORDS error words to host memory (synchronises stream).
+ * After a device error (MKMOE_ERRW_CODE non-zero) the launch that recorded it
+ * gave up waiting, so its output is not valid and its hand-off state (arrival
+ * flags, the polled router part sums) may be left half set: call
+ * mkmoe_clear_errors before the next forward on that workspace. */
 int mkmoe_read_errors(const void* ws, int32_t* words, int32_t n, void* stream);
-int mkmoe_clear_errors(void* ws, void* stream);
+
+/* Reset a workspace after a device error: the error words, the hand-off words
+ * and the polled router part sums, as mkmoe_init_workspace does (enqueued on
+ * stream; not for use inside graph capture). */
+int mkmoe_clear_errors(const mkmoe_shape* shape, void* ws, size_t ws_bytes, void* stream);
 
 /* Byte offset and size of a workspace region, for tests that read
  * intermediate results: 0 x normed, 1 x codes (routed rule), 2 x scales,
@@ -158,7 +170,9 @@ int mkmoe_clear_errors(void* ws, void* stream);
  * fp32 [rows][parts][E], 6 ids int32 [rows][topk], 7 weights fp32
  * [rows][topk], 8 shared intermediate bf16 [rows][S], 9 routed intermediate
  * bf16 [rows * topk][I], 10 the router part sums as routing polls them (every
- * word 0xFFFFFFFF between launches). */
+ * word 0xFFFFFFFF between launches), 11 the phase stamps of a diagnostic build
+ * compiled with MKMOE_TIMELINE (u64 s_memrealtime ticks [workgroup][24]; other
+ * builds leave it untouched). */
 int mkmoe_workspace_region(const mkmoe_shape* shape, int32_t region, size_t* offset,
                            size_t* bytes);
 

@@ -177,15 +177,22 @@ def quant_fp8_b128(w: torch.Tensor):
 
 
 def e2m1_round(v: torch.Tensor) -> torch.Tensor:
-    """Round fp32 to the nearest e2m1 value (ties to the even code), saturating at +-6 -> codes."""
+    """Round fp32 to the nearest e2m1 value (ties to the even code), saturating at +-6 -> codes.
+
+    The e2m1 magnitudes are 0.5 apart on [0, 2] (codes 0 .. 4), 1 apart on [2, 4] (codes
+    4 .. 6) and 2 apart on [4, 6] (codes 6, 7); a code's low bit is its mantissa bit, so
+    "ties to even" is round-half-even of the code. Each branch's scaling (2a, a - 2,
+    (a - 4) / 2) is exact in fp32 where it is taken, and torch.round rounds half to even.
+    """
     a = v.abs().float()
-    mids = torch.tensor([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0])
-    # bucketize: i with mids[i - 1] < a <= mids[i], i.e. a tie lands on the lower code i
-    idx = torch.bucketize(a, mids, right=False)
-    tie = (idx < 7) & (a == mids[idx.clamp(max=6)]) & (idx % 2 == 1)
-    idx = idx + tie.long()  # a tie whose upper neighbour (idx + 1) is even goes up
+    c = torch.where(
+        a <= 2.0,
+        torch.round(a * 2.0),
+        torch.where(a <= 4.0, 4.0 + torch.round(a - 2.0), 6.0 + torch.round((a - 4.0) * 0.5)),
+    )
+    c = c.clamp(max=7.0).to(torch.uint8)
     sign = (v < 0) | ((v == 0) & torch.signbit(v))
-    return (idx | (sign.long() << 3)).to(torch.uint8)
+    return c | (sign.to(torch.uint8) << 3)
 
 
 def quant_mxfp4(w: torch.Tensor):
@@ -203,5 +210,5 @@ def quant_mxfp4(w: torch.Tensor):
     code = (x + 127).clamp(0, 254)
     scale = torch.exp2(code.float() - 127)
     c = e2m1_round(g / scale[..., None]).reshape(n, k)
-    packed = (c[:, 0::2] | (c[:, 1::2] << 4)).to(torch.uint8)
+    packed = c[:, 0::2] | (c[:, 1::2] << 4)
     return packed.contiguous(), code.to(torch.uint8).contiguous()

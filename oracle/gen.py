@@ -83,11 +83,36 @@ def make_dense(p: dict, seed: int) -> dict:
     return w
 
 
+def _expert_job(args):
+    p, seed, e = args
+    return e, LazyExperts(p, seed).get(e)
+
+
+def _one_thread():
+    torch.set_num_threads(1)
+
+
 class LazyExperts:
     """Routed expert e's quantized (w13, w13_s, w2, w2_s), generated on first use from seed + e."""
 
     def __init__(self, p: dict, seed: int):
         self.p, self.seed, self.cache = p, seed, {}
+
+    def prefetch(self, es, workers: int) -> None:
+        """Generate experts ``es`` in ``workers`` processes started by spawn (no GPU state is
+        inherited): the same seeds, so the same tensors as ``get``."""
+        todo = [int(e) for e in es if int(e) not in self.cache]
+        if workers <= 1 or len(todo) < 8:
+            for e in todo:
+                self.get(e)
+            return
+        import multiprocessing
+        from concurrent.futures import ProcessPoolExecutor
+
+        ctx = multiprocessing.get_context("spawn")
+        with ProcessPoolExecutor(workers, mp_context=ctx, initializer=_one_thread) as pool:
+            for e, t in pool.map(_expert_job, [(self.p, self.seed, e) for e in todo]):
+                self.cache[e] = t
 
     def get(self, e: int):
         if e not in self.cache:

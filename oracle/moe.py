@@ -102,7 +102,68 @@ def _gemv(wq, ws, xq, xs, fmt, lpr=None) -> np.ndarray:
     return ex.gemv_fp8_b128(wq, ws, xq, xs, lpr)
 
 
-def moe_partial(x: torch.Tensor, w: dict, p: dict, experts=None, exact: bool = True):
+def expert_contrib(tensors, xin_rows: torch.Tensor, w_rows: torch.Tensor, p: dict, exact: bool) -> torch.Tensor:
+    """One routed expert's contributions bf16(y * w_k) [n, H] (fp32 holding bf16 values) for the
+    n picks whose (normed) rows are ``xin_rows`` and routing weights ``w_rows``
+    (check_ffn.py:216-222); ``exact``: the kernel's GEMV and SwiGLU order."""
+    from . import exact as ex
+
+    lim = float(p["swiglu_limit"])
+    inter, fmt = p["inter"], p["routed_fmt"]
+    w13, w13_s, w2, w2_s = tensors
+    if exact:
+        xq, xs = _qdq_codes(xin_rows, fmt)
+        hh = _gemv(w13, w13_s, xq, xs, fmt)
+        mid = ex.swiglu_routed(hh[:, :inter], hh[:, inter:], lim)
+        mq, ms = _qdq_codes(torch.from_numpy(mid), fmt)
+        y = torch.from_numpy(_gemv(w2, w2_s, mq, ms, fmt, ex.DOWN_LANES))
+    else:
+        xr = act_qdq(xin_rows, fmt)
+        hh = xr @ deq_weight(w13, w13_s, fmt).T
+        gate, up = hh[:, :inter], hh[:, inter:]
+        mid = fm.bf(silu(gate.clamp(max=lim)) * up.clamp(-lim, lim))
+        y = act_qdq(mid, fmt) @ deq_weight(w2, w2_s, fmt).T
+    return fm.bf(y * w_rows[:, None])
+
+
+def _contrib_job(args):
+    from . import gen
+
+    p, seed, e, xin_rows, w_rows = args
+    t = gen.LazyExperts(p, seed).get(e)
+    return e, t, expert_contrib(t, xin_rows, w_rows, p, True), expert_contrib(t, xin_rows, w_rows, p, False)
+
+
+def pool_contribs(p: dict, seed: int, xin: torch.Tensor, ids: np.ndarray, wts: np.ndarray, workers: int):
+    """Every routed expert of a step, generated from its seed and computed in ``workers``
+    processes started by spawn: -> (tensors, exact contributions, golden contributions),
+    each a dict by expert id, the contributions in the pick order of ``moe_partial``."""
+    import multiprocessing
+    from concurrent.futures import ProcessPoolExecutor
+
+    from . import gen
+
+    idt = torch.from_numpy(ids.astype(np.int64))
+    wt = torch.from_numpy(wts)
+    jobs = []
+    for e in idt.unique().tolist():
+        rows, ks = (idt == e).nonzero(as_tuple=True)
+        jobs.append((p, seed, e, xin[rows].clone(), wt[rows, ks].clone()))
+    tensors, cx, cg = {}, {}, {}
+    if workers <= 1 or len(jobs) < 8:
+        results = map(_contrib_job, jobs)
+    else:
+        ctx = multiprocessing.get_context("spawn")
+        pool = ProcessPoolExecutor(workers, mp_context=ctx, initializer=gen._one_thread)
+        results = pool.map(_contrib_job, jobs)
+    for e, t, x_, g_ in results:
+        tensors[e], cx[e], cg[e] = t, x_, g_
+    if workers > 1 and len(jobs) >= 8:
+        pool.shutdown()
+    return tensors, cx, cg
+
+
+def moe_partial(x: torch.Tensor, w: dict, p: dict, experts=None, exact: bool = True, contribs: dict | None = None):
     """This rank's MoE partial of bf16 rows ``x`` [R, H].
 
     ``w`` holds CPU tensors: gate_w bf16 [E, H], bias fp32 [E], norm bf16 [H]
@@ -110,19 +171,18 @@ def moe_partial(x: torch.Tensor, w: dict, p: dict, experts=None, exact: bool = T
     expert), and either the per-expert tensors w13 / w13_s / w2 / w2_s or an
     ``experts`` source with ``get(e)``. ``exact``: the kernel's GEMV and SwiGLU
     arithmetic (``oracle.exact``), bit for bit; otherwise the golden's fp32
-    matmuls and torch's silu. Returns ids, weights, logits, the normed rows (if
-    any), the per-pick contributions and the bf16 output.
+    matmuls and torch's silu. ``contribs``: the routed experts' contributions
+    already computed (``pool_contribs``) in the same mode. Returns ids, weights,
+    logits, the normed rows (if any), the per-pick contributions and the bf16 output.
     """
     from . import exact as ex
 
     lim = float(p["swiglu_limit"])
     r = x.shape[0]
     h = p["hidden"]
-    inter = p["inter"]
     ish = p["shared_inter"]
-    fmt = p["routed_fmt"]
     topk = p["topk"]
-    if experts is None:
+    if experts is None and contribs is None:
         experts = ExpertSource(w["w13"], w["w13_s"], w["w2"], w["w2_s"])
     xin = x
     if p.get("norm_eps") is not None:
@@ -131,30 +191,19 @@ def moe_partial(x: torch.Tensor, w: dict, p: dict, experts=None, exact: bool = T
     ids = torch.from_numpy(ids_np.astype(np.int64))
     wts = torch.from_numpy(wts_np)
     per_k = torch.zeros(r, topk, h)
+    for e in ids.unique().tolist():
+        rows, ks = (ids == e).nonzero(as_tuple=True)
+        if contribs is not None:
+            per_k[rows, ks] = contribs[e]
+        else:
+            per_k[rows, ks] = expert_contrib(experts.get(e), xin[rows], wts[rows, ks], p, exact)
     if exact:
-        xq, xs = _qdq_codes(xin, fmt)
         xq2, xs2 = fm.group_fp8_quant(xin, 128)
-        for e in ids.unique().tolist():
-            rows, ks = (ids == e).nonzero(as_tuple=True)
-            w13, w13_s, w2, w2_s = experts.get(e)
-            hh = _gemv(w13, w13_s, xq[rows], xs[rows], fmt)
-            mid = ex.swiglu_routed(hh[:, :inter], hh[:, inter:], lim)
-            mq, ms = _qdq_codes(torch.from_numpy(mid), fmt)
-            y = _gemv(w2, w2_s, mq, ms, fmt, ex.DOWN_LANES)
-            per_k[rows, ks] = fm.bf(torch.from_numpy(y) * wts[rows, ks, None])
-    else:
-        xr = act_qdq(xin, fmt)
-        for e in ids.unique().tolist():
-            rows, ks = (ids == e).nonzero(as_tuple=True)
-            w13, w13_s, w2, w2_s = experts.get(e)
-            hh = xr[rows] @ deq_weight(w13, w13_s, fmt).T
-            gate, up = hh[:, :inter], hh[:, inter:]
-            mid = fm.bf(silu(gate.clamp(max=lim)) * up.clamp(-lim, lim))
-            y = act_qdq(mid, fmt) @ deq_weight(w2, w2_s, fmt).T
-            per_k[rows, ks] = fm.bf(y * wts[rows, ks, None])
     routed = torch.zeros(r, h)
+    chain = torch.zeros(r, h)  # the largest magnitude the combine's bf16 chain holds
     for k in range(topk):
         routed = fm.bf(routed + per_k[:, k])
+        chain = torch.maximum(chain, routed.abs())
     if ish > 0 and exact:
         hs = ex.gemv_fp8_b128(w["sgu"], w["sgu_s"], xq2, xs2)
         smid = ex.swiglu_shared(hs[:, :ish], hs[:, ish:], lim)
@@ -168,7 +217,9 @@ def moe_partial(x: torch.Tensor, w: dict, p: dict, experts=None, exact: bool = T
     else:
         shared = torch.zeros(r, h)
     out = fm.bf(routed + shared).to(torch.bfloat16)
+    chain = torch.maximum(chain, out.float().abs())
     return {
+        "chain_max": chain,
         "ids": ids_np,
         "weights": wts_np,
         "logits": logit,

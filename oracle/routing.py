@@ -27,7 +27,9 @@ the kernel bit for bit, so every step below is a fixed sequence of IEEE fp32
    [-60, 60] first. The same steps run on the GPU with FP contraction off, so
    the fp32 score is identical.
 3. Selection (``grouped_topk``): DeepSeek-V3's ``noaux_tc`` grouped top-k.
-   choice = score + bias (fp32); a group's score is its largest plus its
+   choice = score + bias (fp32), and a NaN choice is -inf (the reference's
+   ``max(sc + bias, -inf)``, ``stages/moe.py:346-347``); a NaN score weighs 0
+   in step 4 (``stages/moe.py:345-346``); a group's score is its largest plus its
    second largest choice; the top ``topk_group`` groups by group score (a tie
    goes to the lower group); then the top ``topk`` experts by choice among
    those groups, in descending order (a tie goes to the lower expert id). With
@@ -144,7 +146,10 @@ def grouped_topk(
     scores = np.asarray(scores, np.float32)
     bias = np.asarray(bias, np.float32)
     r, e = scores.shape
-    choice = scores + bias[None, :]
+    with np.errstate(invalid="ignore"):
+        choice = scores + bias[None, :]
+    choice = np.where(np.isnan(choice), np.float32(-np.inf), choice).astype(np.float32)  # NaN choice: -inf
+    scores = np.where(np.isnan(scores), np.float32(0.0), scores).astype(np.float32)  # NaN score weighs 0
     per = e // n_group
     ids = np.zeros((r, topk), np.int32)
     wts = np.zeros((r, topk), np.float32)

@@ -1,10 +1,15 @@
 """Build the in-tree HIP library ``sgl_amd_mono/moe/libmkmoe.so`` for gfx950.
 
-    python sgl-amd-mono_amd/build.py          # rebuild
-    python sgl-amd-mono_amd/build.py --check  # print the kernels' register / LDS use
+    python sgl-amd-mono_amd/build.py             # rebuild
+    python sgl-amd-mono_amd/build.py --check     # and print the kernels' register / LDS use
+    python sgl-amd-mono_amd/build.py --timeline  # the diagnostic build with phase stamps
+                                                 # (libmkmoe_tl.so; bench.py --timeline)
 
 The library holds the kernels and the C ABI of ``include/mkmoe.h``. It is built
 in place (not installed) so that the same file runs wherever the tree is copied.
+The source compiles in parts, in parallel: one object per compiled MoE shape
+(``MKMOE_UNIT`` 0 .. 3) and one for the host code (``MKMOE_UNIT`` 9), then one
+link.
 """
 
 from __future__ import annotations
@@ -13,19 +18,22 @@ import argparse
 import os
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
 CSRC = ROOT / "csrc"
 OUT = ROOT / "sgl_amd_mono" / "moe" / "libmkmoe.so"
-SOURCES = [CSRC / "mkmoe_kernels.hip"]
+OUT_TIMELINE = ROOT / "sgl_amd_mono" / "moe" / "libmkmoe_tl.so"
+SOURCE = CSRC / "mkmoe_kernels.hip"
+UNITS = (0, 1, 2, 3, 9)  # the compiled shapes, then the host code
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # no packed fp32 instructions in the device code
     "-Xclang",
     "-target-feature",
@@ -34,29 +42,50 @@ FLAGS = [
 ]
 
 
-def build(check: bool = False, verbose: bool = False) -> Path:
-    """Compile the library (always; a few tens of seconds) and return its path."""
-    tmp = OUT.with_suffix(".so.tmp")
-    cmd = [HIPCC, *FLAGS, *(str(s) for s in SOURCES), "-o", str(tmp)]
-    if check:
-        cmd.append("-Rpass-analysis=kernel-resource-usage")
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed ({res.returncode})")
-    if check:
-        keep = ("Function Name", "VGPRs:", "ScratchSize", "LDS Size", "Occupancy")
-        for line in res.stderr.splitlines():
-            if any(k in line for k in keep):
-                print(line.split("remark:")[-1].replace("[-Rpass-analysis=kernel-resource-usage]", "").strip())
-    os.replace(tmp, OUT)
-    return OUT
+def _run(cmd: list[str]) -> subprocess.CompletedProcess:
+    return subprocess.run(cmd, capture_output=True, text=True)
+
+
+def build(check: bool = False, verbose: bool = False, timeline: bool = False) -> Path:
+    """Compile the library (always; about 30 s with the parts in parallel) and return its path."""
+    out = OUT_TIMELINE if timeline else OUT
+    defs = ["-DMKMOE_TIMELINE"] if timeline else []
+    with tempfile.TemporaryDirectory(prefix="mkmoe_build_") as tmpd:
+        objs = [Path(tmpd) / f"unit{u}.o" for u in UNITS]
+        cmds = []
+        for u, o in zip(UNITS, objs):
+            cmd = [HIPCC, *FLAGS, *defs, f"-DMKMOE_UNIT={u}", "-c", str(SOURCE), "-o", str(o)]
+            if check:
+                cmd.append("-Rpass-analysis=kernel-resource-usage")
+            cmds.append(cmd)
+        if verbose:
+            print(" ".join(cmds[0]), flush=True)
+        jobs = min(len(cmds), max(1, int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+        with ThreadPoolExecutor(jobs) as ex:
+            results = list(ex.map(_run, cmds))
+        for cmd, res in zip(cmds, results):
+            if res.returncode != 0:
+                sys.stderr.write(res.stdout + res.stderr)
+                raise RuntimeError(f"hipcc failed ({res.returncode}): {' '.join(cmd)}")
+        if check:
+            keep = ("Function Name", "VGPRs:", "ScratchSize", "LDS Size", "Occupancy")
+            for res in results:
+                for line in res.stderr.splitlines():
+                    if any(k in line for k in keep):
+                        print(line.split("remark:")[-1].replace("[-Rpass-analysis=kernel-resource-usage]", "").strip())
+        tmp = out.with_suffix(".so.tmp")
+        link = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *(str(o) for o in objs), "-o", str(tmp)]
+        res = _run(link)
+        if res.returncode != 0:
+            sys.stderr.write(res.stdout + res.stderr)
+            raise RuntimeError(f"link failed ({res.returncode})")
+        os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--check", action="store_true")
+    ap.add_argument("--timeline", action="store_true")
     args = ap.parse_args()
-    print(build(check=args.check, verbose=True))
+    print(build(check=args.check, verbose=True, timeline=args.timeline))

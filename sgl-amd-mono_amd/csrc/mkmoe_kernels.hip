@@ -1,20 +1,23 @@
 // The decode-step MoE block of one TP rank on gfx950 (MI355X): HIP kernels and the C ABI.
 //
-// One persistent launch (grid = one 512-thread workgroup per CU) runs five
-// stages separated by device-scope arrival counters (every wait has a
-// deadline, so a launch always ends):
+// One persistent launch (grid = one 512-thread workgroup per CU) runs its stages
+// separated by hand-offs: a workgroup that is done with a stage sets its own flag word
+// (a device-coherent store), and a waiter reads all the flags until every one is set
+// (every wait has a deadline, so a launch always ends):
 //   N  RMSNorm of x (fused-norm shape only)                   wave per row
 //   A  router GEMV part sums (fixed order) + activation quantization
 //                                                              wave per (expert, K part) / (row, 512 cols)
-//   B  routing (sigmoid, grouped top-k, weights)               wave per row
-//      + shared expert gate_up + SwiGLU                        wave per (column, 8 rows)
-//   C  routed gate_up + SwiGLU for the step's union of experts wave per (expert, column, 8 picks)
-//   D  down GEMVs (shared + routed) and the weighted combine   workgroup per tile of output rows
-// Every GEMV runs on the vector ALUs in one fixed fp32 order (see WRows), so the
-// output is reproducible bit for bit by a CPU restatement; the gfx950 scaled MFMA
-// accumulates with an internal precision that no restatement can follow.
-// Hand-off data between workgroups is written and read with device-coherent
-// (sc1) buffer accesses, so the counters need no L2 write-back / invalidate.
+//   B  routing (sigmoid, grouped top-k, weights): up to 16 rows every workgroup routes the
+//      whole step itself, reading the part sums as they land; above 16 a workgroup a row
+//   C  gate_up + SwiGLU of the step's union of experts and of the shared expert, dealt
+//      as one list of units over the workgroups
+//   D  down GEMMs (routed + shared) and the weighted combine   workgroup per tile of output rows
+// The expert GEMMs run on bf16 MFMA by default (e4m3 / e2m1 codes converted to bf16 exactly;
+// the sums are held to the numerics bounds); a per-call option selects the fixed-order VALU
+// GEMVs (see WRows), whose output a CPU restatement reproduces bit for bit. Routing is
+// computed in one fixed fp32 / fp64 order on every path and is bit-identical to the oracle.
+// Hand-off data between workgroups is written and read with device-coherent (sc1) buffer
+// accesses, so the flags need no L2 write-back / invalidate.
 // The staged entry point runs the same stage functions as one launch each.
 //
 // Reference: the stages of sgl_amd_mono/deepseek_v41/gfx950/stages/moe.py
@@ -34,6 +37,10 @@
 
 #include "../../include/mkmoe.h"
 #include "mkmoe_numerics.h"
+
+// Built whole, or in parts (MKMOE_UNIT = 0 .. 3: one compiled shape's kernels and launcher;
+// MKMOE_UNIT_HOST: the host code and the C ABI), so that the parts compile in parallel.
+#define MKMOE_UNIT_HOST 9
 
 namespace mkmoe {
 
@@ -58,6 +65,38 @@ constexpr int kCtlBytes = kCtlFlags + 4 * kFlagWgs * 4;
 
 enum Stage { kStageNorm = 1, kStageA = 2, kStageB = 3, kStageC = 4, kStageD = 5 };
 
+// ---------------------------------------------------------------- timeline (diagnostic build)
+// Built with MKMOE_TIMELINE, the persistent launch stamps s_memrealtime (100 MHz) into LDS at
+// each phase end of each workgroup and writes the stamps out once at its end (workspace region
+// 11: [workgroup][kTlSlots] u64: phase ends, then summed durations), so the stamps add no memory waits. Other builds compile the
+// stamps away and leave region 11 untouched.
+enum TlSlot {
+  kTlStart = 0, kTlADone, kTlAArrived, kTlRouted, kTlUnion, kTlAAwaited, kTlGateUp, kTlCArrived,
+  kTlCAwaited, kTlDRouted, kTlDShared, kTlEnd, kTlGuFirst, kTlGuWait, kTlDWait, kTlGuUnits,
+  // a gate_up unit's parts, summed over the workgroup's units (wave 0): read out of the slot
+  // and the next unit requested, the MFMAs, the partial-tile sync, the emit, the closing sync
+  kTlGuFetch, kTlGuMma, kTlGuSync, kTlGuEmit, kTlGuSync2,
+  // the routed down's parts (wave 0): quantizing the pick batches, the units' MFMAs
+  kTlDQuant, kTlDMma,
+  kTlSlots = 24
+};
+#ifdef MKMOE_TIMELINE
+static __shared__ unsigned long long s_tl[kTlSlots];
+__device__ __forceinline__ unsigned long long tl_now() { return __builtin_amdgcn_s_memrealtime(); }
+// thread 0 stamps phase k
+#define TL(k) do { if (threadIdx.x == 0) s_tl[(k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+// thread 0 adds v to slot k
+#define TL_ADD(k, v) do { if (threadIdx.x == 0) s_tl[(k)] += (v); } while (0)
+#define TL_CLEAR() do { if (threadIdx.x < kTlSlots) s_tl[threadIdx.x] = 0ull; } while (0)
+#define TL_DUMP(p) do { __syncthreads(); if (threadIdx.x < kTlSlots) ((unsigned long long*)((p).ws + (p).off[11]))[blockIdx.x * kTlSlots + threadIdx.x] = s_tl[threadIdx.x]; } while (0)
+#else
+__device__ __forceinline__ unsigned long long tl_now() { return 0ull; }
+#define TL(k) do {} while (0)
+#define TL_ADD(k, v) do {} while (0)
+#define TL_CLEAR() do {} while (0)
+#define TL_DUMP(p) do {} while (0)
+#endif
+
 template <int H_, int E_, int K_, int NG_, int TG_, int I_, int S_, int FMT_, int P_, bool NORM_>
 struct Cfg {
   static constexpr int H = H_, E = E_, K = K_, NG = NG_, TG = TG_, I = I_, S = S_, FMT = FMT_,
@@ -80,7 +119,7 @@ using CfgTp4Fp4 = Cfg<7168, 256, 8, 8, 4, 512, 512, kFp4, 7, false>;
 using CfgTp2Fp4Norm = Cfg<7168, 256, 8, 8, 4, 1024, 1024, kFp4, 7, true>;
 
 // ---------------------------------------------------------------- workspace layout
-constexpr int kRegions = 11;
+constexpr int kRegions = 12;
 
 struct Layout {
   size_t off[kRegions];
@@ -105,6 +144,7 @@ MKMOE_HD inline Layout make_layout(int H, int E, int K, int I, int S, int fmt, i
   sz[8] = (size_t)rm * S * 2;                                         // shared mid, bf16
   sz[9] = (size_t)rm * K * I * 2;                                     // routed mid, bf16
   sz[10] = sz[5];  // the part sums as routing polls them (kPartUnset between launches)
+  sz[11] = (size_t)kFlagWgs * kTlSlots * 8;  // the timeline build's stamps
   size_t off = kCtlBytes;
   for (int i = 0; i < kRegions; ++i) {
     L.off[i] = off;
@@ -636,8 +676,9 @@ __device__ __forceinline__ float segment_max(float v) {
 }
 
 // scores and choices of (row r0 + i, expert e) for i < n, spread over the workgroup: the
-// logit sums the router's part sums in part order; a NaN score weighs 0 and its choice
-// (score + bias) never wins, as in the reference's route
+// logit sums the router's part sums in part order; choice = score + bias, and a NaN choice
+// is -inf (max(sc + bias, -inf) of the reference's route, stages/moe.py:345-347); a NaN
+// score weighs 0
 // POLL: the part sums are read before the router's hand-off, each reread until it holds a
 // value (kPartUnset marks a part sum not yet written in this launch)
 template <class C, bool POLL = false>
@@ -660,6 +701,9 @@ __device__ __forceinline__ void route_scores(const Params& p, RouteSmem<C>& sm, 
     for (int q = 0; q < C::P; ++q) part[j][q] = idx < n * C::E ? u2f(dld32(rs, part_off(j, q))) : 0.0f;
   }
   if constexpr (POLL) {
+    // wave-uniform: a wave polls until none of its lanes' part sums is unset, or gives up
+    // at the deadline (s_memrealtime is a scalar read, the same in every lane), and then
+    // records the error once (lane 0)
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
     while (true) {
       bool unset = false;
@@ -667,9 +711,9 @@ __device__ __forceinline__ void route_scores(const Params& p, RouteSmem<C>& sm, 
       for (int j = 0; j < MJ; ++j)
 #pragma unroll
         for (int q = 0; q < C::P; ++q) unset |= f2u(part[j][q]) == kPartUnset;
-      if (!unset) break;
+      if (__ballot(unset) == 0ull) break;
       if (__builtin_amdgcn_s_memrealtime() - t0 > p.deadline) {
-        record_error(p, kStageA);
+        if ((tid & 63) == 0) record_error(p, kStageA);
         break;
       }
 #pragma unroll
@@ -688,9 +732,9 @@ __device__ __forceinline__ void route_scores(const Params& p, RouteSmem<C>& sm, 
 #pragma unroll
       for (int q = 0; q < C::P; ++q) logit = logit + part[j][q];
       const float sg = sigmoid_exact(logit);
-      const float s = sg != sg ? 0.0f : sg;
-      const float cv = s + p.bias[e];
-      const float ch = cv != cv ? -INFINITY : cv;
+      const float s = sg != sg ? 0.0f : sg;  // the weight of a NaN score is 0
+      const float cv = sg + p.bias[e];
+      const float ch = cv != cv ? -INFINITY : cv;  // and its choice -inf
       sm.sc[i][e] = s;
       sm.ch[i][e] = ch;
       if constexpr (C::NG > 1) {
@@ -1259,10 +1303,11 @@ __device__ __forceinline__ void even_share(int n, int b, int nwg, int& lo, int& 
 
 // ---------------------------------------------------------------- MFMA expert GEMMs
 // Launches with at least mfma_gate (gate_up) / mfma_down (down) rows run those expert GEMMs on
-// v_mfma_f32_16x16x32_bf16 (fewer rows keep the fixed-order VALU GEMVs above). The gate_up
-// default keeps the VALU GEMVs at every row count: the MFMA operand layout reads 16 rows x 64
-// bytes a load, which streams a [2W][H] weight at 5.1-5.3 TB/s against 6.8 TB/s for the 1 KB
-// row loads of the VALU GEMVs (load-only measurement, 57 experts at 8 rows). The e4m3 and e2m1 codes convert to bf16
+// v_mfma_f32_16x16x32_bf16 (the default: every row count; fewer rows run the fixed-order VALU
+// GEMVs above). The weights reach the MFMA operands through LDS (LDS-direct loads of
+// contiguous runs): the operand layout's own loads read 16 rows x 64 bytes a load, which
+// streams at 5.1-5.3 TB/s against 6.6-6.8 TB/s for contiguous runs (load-only measurement, 57
+// experts at 8 rows). The e4m3 and e2m1 codes convert to bf16
 // exactly (with an E8M0 scale folded in, still exact), every bf16 x bf16 product is exact in
 // fp32 and the instruction sums them like an fp32 chain (measured on gfx950: within 0.42 x
 // 2^-24 x sum |products| of the exact sum). The fp8 MFMAs are not used: their sums drift by
@@ -1320,6 +1365,20 @@ __device__ __forceinline__ f32x4 mma_fp4_step(u32x4 a, float sw, u32x4 blo, u32x
   c = mfma_bf16(fp4x8(a.z, sw), fp8x8(bhi.x, bhi.y, sx), c);
   c = mfma_bf16(fp4x8(a.w, sw), fp8x8(bhi.z, bhi.w, sx), c);
   return c;
+}
+// an MXFP4 x MXFP8 128-K step of two A operands (a0, a1: gate rows and up rows) against the
+// same column codes, each of the column's four 8-K pieces converted once for both; each sum
+// takes its pieces in the order of mma_fp4_step
+__device__ __forceinline__ void mma_fp4_step2(u32x4 a0, float s0, u32x4 a1, float s1, u32x4 blo, u32x4 bhi, float sx,
+                                              f32x4& c0, f32x4& c1) {
+  const uint32_t bw[4][2] = {{blo.x, blo.y}, {blo.z, blo.w}, {bhi.x, bhi.y}, {bhi.z, bhi.w}};
+  const uint32_t w0[4] = {a0.x, a0.y, a0.z, a0.w}, w1[4] = {a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const bf16x8 b = fp8x8(bw[k][0], bw[k][1], sx);
+    c0 = mfma_bf16(fp4x8(w0[k], s0), b, c0);
+    c1 = mfma_bf16(fp4x8(w1[k], s1), b, c1);
+  }
 }
 
 // 16 bytes a lane from a buffer straight into LDS: lane l's bytes land at lds + 16 l (lds
@@ -1505,9 +1564,9 @@ __device__ __forceinline__ void gu_mma(const GuTile<C, WFMT>& t, const GuX<C, WF
 #pragma unroll
       for (int v = 0; v < 4; ++v) acc[0][v] = fmaf(c[v], f, acc[0][v]);
     } else {
-      const float sx = e8m0(x.ex[i]);
-#pragma unroll
-      for (int q = 0; q < T::NA; ++q) acc[q] = mma_fp4_step(t.a[q][i][0], e8m0(t.sa[q][i]), x.lo[i], x.hi[i], sx, acc[q]);
+      static_assert(T::NA == 2, "gate and up rows");
+      mma_fp4_step2(t.a[0][i][0], e8m0(t.sa[0][i]), t.a[1][i][0], e8m0(t.sa[1][i]), x.lo[i], x.hi[i], e8m0(x.ex[i]),
+                    acc[0], acc[1]);
     }
   }
 }
@@ -1575,8 +1634,13 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
         }
       }
     }
+    const unsigned long long tw0 = tl_now();
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the unit's slot, the activations, the scales
+    TL_ADD(kTlGuWait, tl_now() - tw0);
+    TL_ADD(kTlGuUnits, 1ull);
+    if (u == lo) TL(kTlGuFirst);
     if (fresh) __syncthreads();                       // every wave's block scales are in LDS
+    const unsigned long long tf0 = tl_now();
     t.fetch(slot, lane);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // read out of the slot
     if (u + 1 < hi) {
@@ -1589,11 +1653,17 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
       half(u + 1, c1, nc1);
       t.issue(weight_rsrc_words(wb, 2u * W * WB), sb, W, ((u + 1) % nb) * T::NC + c1, nc1, slot, lane, wave);
     }
+    const unsigned long long tf1 = tl_now();
+    TL_ADD(kTlGuFetch, tf1 - tf0);
     f32x4 acc[T::NA];
     gu_mma<C, WFMT>(t, x, sm.m.wsc, W, j0, lane, wave, acc);
 #pragma unroll
     for (int q = 0; q < T::NA; ++q) sm.red[q][wave][lane] = acc[q];
+    const unsigned long long tf2 = tl_now();
+    TL_ADD(kTlGuMma, tf2 - tf1);
     __syncthreads();
+    const unsigned long long tf3 = tl_now();
+    TL_ADD(kTlGuSync, tf3 - tf2);
     if (tid < 16 * ncu) {
       // C[m][n] is element m % 4 of lane n + 16 (m / 4); FP8: up row m + 8 is 32 lanes on
       const int m = tid >> 4, n = tid & 15;
@@ -1607,7 +1677,10 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
       }
       if (n < np_x) emit(tg_x, n, j0 + m, g, uu);
     }
+    const unsigned long long tf4 = tl_now();
+    TL_ADD(kTlGuEmit, tf4 - tf3);
     __syncthreads();
+    TL_ADD(kTlGuSync2, tl_now() - tf4);
   }
 }
 
@@ -1910,8 +1983,9 @@ struct DownRows {
   static constexpr int CE = FMT == kFp4 ? 32 : 16;  // elements a chunk
   static constexpr int CPR = KD / CE;
   static constexpr int CPL = CPR / kDownLanes;
-  // units a wave requests at once (MXFP4 rows of 1024 K: 6, leaving registers for the quant)
-  static constexpr int kBatch = CPL >= 8 ? 4 : (FMT == kFp4 && KD >= 1024 ? 6 : 8);
+  // units a wave requests at once (the VALU GEMVs run when a call asks for them: more units in
+  // flight would spill the launch's registers)
+  static constexpr int kBatch = 4;
   static_assert(CPR % kDownLanes == 0, "down row chunks");
   u32x4 w[CPL];
   float sf[CPL];
@@ -2479,12 +2553,18 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
     if ((pb0 > 0 || !first_ready || wave == 0) && wave < n_units)
       mfma_issue<C>(p, un, h0, hn, s_lo, wave, slot, bt.nxt, lane);
     __syncthreads();  // the previous batch is done with the LDS rows
-    quant_rows_lds<C::FMT, C::I, C::MQS, 2 * kQuantBatch>(
+    const unsigned long long tq0 = tl_now();
+    // the quantize requests 8 chunks a thread at once (4 at I >= 1024, whose unit and scales
+    // leave fewer registers: 8 spills there)
+    quant_rows_lds<C::FMT, C::I, C::MQS, (C::I >= 1024 ? 1 : 2) * kQuantBatch>(
         p, [&](int i) { return p.off[9] + (uint32_t)un.picks[pb0 + i] * C::I * 2; }, pbn, sm.q, sm.s);
     __syncthreads();
+    TL_ADD(kTlDQuant, tl_now() - tq0);
     DT cur;
     for (int v = wave; v < n_units; v += kWaves) {
+      const unsigned long long tw0 = tl_now();
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the unit's rows are in the slot
+      TL_ADD(kTlDWait, tl_now() - tw0);
       cur.fetch(slot, lane);
       cur.take_scales(bt.nxt);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // and read out of it
@@ -2492,6 +2572,7 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
       const int slot_i = s_lo + v / nb, rb = v % nb;
       const int j0 = max(un.slot_start[slot_i], pb0), j1 = min(un.slot_start[slot_i + 1], pb0 + pbn);
       const int n = lane & 15;
+      const unsigned long long tm0 = tl_now();
       for (int jj = j0; jj < j1; jj += kMfmaPicks) {
         const int np = min(kMfmaPicks, j1 - jj);
         const f32x4 acc = cur.template mma<C::MQS, SST>(sm.q, sm.s, jj - pb0, np, lane);
@@ -2502,6 +2583,7 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
           if (n < np && hl < hn) sm.contrib[pk * kTileMax + hl] = f2bf(acc[k] * un.wts[pk]);
         }
       }
+      TL_ADD(kTlDMma, tl_now() - tm0);
     }
   }
 }
@@ -2536,11 +2618,13 @@ __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, D
   const int R = p.rows;
   if constexpr (MF) down_mfma<C>(p, un, sm, h0, hn, bt, first_ready);
   else down_valu<C>(p, un, sm, h0, hn, bt, first_ready);
+  TL(kTlDRouted);
   {
     SharedDownBatch<C, MF> bs;
     shared_down_tile<C, MF>(p, sm.sd, sm.shv, h0, hn, bs, false);
   }
   __syncthreads();
+  TL(kTlDShared);
   // ---- combine: top-k order, bf16 at every add, then + the shared expert's bf16 result
   for (int idx = tid; idx < R * hn; idx += kThreads) {
     const int t = idx / hn, hl = idx % hn;
@@ -2579,6 +2663,7 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
   const bool first = b * tr < C::H;
   if (first) down_first<C, MF>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt);
   await_all(p, kCtlC, nwg, kStageC);
+  TL(kTlCAwaited);
   reset_parts<C>(p, b, nwg);  // every workgroup is past its routing
   __syncthreads();  // the tile's readers are done before the down stage reuses its LDS
   stage_d<C, MF>(p, un, sm, b, nwg, bt, first);
@@ -2599,30 +2684,44 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   __shared__ Union<C> un;
   __shared__ StageSmem<C> sm;
   const int b = blockIdx.x, nwg = gridDim.x;
+  TL_CLEAR();
+  TL(kTlStart);
   if constexpr (C::NORM) {
     stage_norm<C>(p, b, nwg);
     arrive(p, kCtlNorm);
     await_all(p, kCtlNorm, nwg, kStageNorm);
   }
   stage_a<C>(p, sm.a, b, nwg);
+  TL(kTlADone);
   arrive(p, kCtlA);
+  TL(kTlAArrived);
   if (p.rows <= kLocalRouteMax) {
     // every workgroup routes the step itself, reading the router's part sums as they land:
     // no routing hand-off; the A hand-off (the x codes) is awaited before the gate_up
     route_all<C>(p, sm.r, un.ids, un.wts, un.rows_of, b);
+    TL(kTlRouted);
     build_union<C>(p, un, true);
+    TL(kTlUnion);
     await_all(p, kCtlA, nwg, kStageA);
+    TL(kTlAAwaited);
   } else {
     await_all(p, kCtlA, nwg, kStageA);
+    TL(kTlAAwaited);
     stage_b<C>(p, sm.r, b, nwg);
     arrive(p, kCtlB);
     await_all(p, kCtlB, nwg, kStageB);
+    TL(kTlRouted);
     build_union<C>(p, un, false);
+    TL(kTlUnion);
   }
   stage_c<C>(p, un, sm.g, b, nwg);
+  TL(kTlGateUp);
   arrive(p, kCtlC);
+  TL(kTlCArrived);
   if (p.rows >= p.mfma_down) wait_then_d<C, true>(p, un, sm.d, b, nwg);
   else wait_then_d<C, false>(p, un, sm.d, b, nwg);
+  TL(kTlEnd);
+  TL_DUMP(p);
   leave(p);
 }
 
@@ -2662,6 +2761,7 @@ __global__ __launch_bounds__(kThreads) void k_d(Params p) {
   }
 }
 
+#if !defined(MKMOE_UNIT) || MKMOE_UNIT == MKMOE_UNIT_HOST
 // decode byte i as e4m3 (the fp8 convert the GEMVs use) and as two e2m1 (the fp4 convert)
 __global__ void k_decode(const uint8_t* codes, float* fp8, float* fp4, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -2675,12 +2775,64 @@ __global__ void k_decode(const uint8_t* codes, float* fp8, float* fp4, int n) {
   }
 }
 
+#endif
+
 }  // namespace mkmoe
 
 // ================================================================ host side
 using namespace mkmoe;
 
 namespace {
+
+template <class C>
+int launch(const Params& p, int nwg, hipStream_t st, bool staged) {
+  dim3 grid(nwg), block(kThreads);
+  if (!staged) {
+    // the persistent grid must be resident: a workgroup a CU
+    int per = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_fused<C>, kThreads, 0) != hipSuccess)
+      return MKMOE_ERR_HIP;
+    if (per < 1) return MKMOE_ERR_DEVICE;
+    hipLaunchKernelGGL(k_fused<C>, grid, block, 0, st, p);
+  } else {
+    if constexpr (C::NORM) hipLaunchKernelGGL(k_norm<C>, grid, block, 0, st, p);
+    hipLaunchKernelGGL(k_a<C>, grid, block, 0, st, p);
+    hipLaunchKernelGGL(k_b<C>, grid, block, 0, st, p);
+    hipLaunchKernelGGL(k_c<C>, grid, block, 0, st, p);
+    hipLaunchKernelGGL(k_d<C>, grid, block, 0, st, p);
+  }
+  return hipGetLastError() == hipSuccess ? MKMOE_OK : MKMOE_ERR_LAUNCH;
+}
+
+}  // namespace
+
+// A compiled shape's launcher. Built in parts (MKMOE_UNIT), each shape's kernels are a
+// translation unit of their own (compiled in parallel) and the host code another.
+#define MKMOE_LAUNCHER(N, C)                                                              \
+  __attribute__((visibility("hidden"))) int mkmoe_launch_cfg##N(const Params& p, int nwg, \
+                                                                 hipStream_t st, bool staged) { \
+    return launch<C>(p, nwg, st, staged);                                                \
+  }
+#if !defined(MKMOE_UNIT) || MKMOE_UNIT == 0
+MKMOE_LAUNCHER(0, CfgPlumbing)
+#endif
+#if !defined(MKMOE_UNIT) || MKMOE_UNIT == 1
+MKMOE_LAUNCHER(1, CfgTp4Fp8)
+#endif
+#if !defined(MKMOE_UNIT) || MKMOE_UNIT == 2
+MKMOE_LAUNCHER(2, CfgTp4Fp4)
+#endif
+#if !defined(MKMOE_UNIT) || MKMOE_UNIT == 3
+MKMOE_LAUNCHER(3, CfgTp2Fp4Norm)
+#endif
+__attribute__((visibility("hidden"))) int mkmoe_launch_cfg0(const Params&, int, hipStream_t, bool);
+__attribute__((visibility("hidden"))) int mkmoe_launch_cfg1(const Params&, int, hipStream_t, bool);
+__attribute__((visibility("hidden"))) int mkmoe_launch_cfg2(const Params&, int, hipStream_t, bool);
+__attribute__((visibility("hidden"))) int mkmoe_launch_cfg3(const Params&, int, hipStream_t, bool);
+
+#if !defined(MKMOE_UNIT) || MKMOE_UNIT == MKMOE_UNIT_HOST
+namespace {
+
 
 struct DevInfo {
   int cus = 0;
@@ -2689,9 +2841,25 @@ struct DevInfo {
 
 std::mutex g_mu;
 DevInfo g_dev[64];
-double g_deadline_s = 2.0;
-int g_mfma_gate = 1;  // gate_up and down on MFMA at every row count
-int g_mfma_down = 1;
+constexpr double kDeadlineDefault = 2.0;  // seconds
+constexpr int kMfmaGateDefault = 1;       // gate_up and down on MFMA at every row count
+constexpr int kMfmaDownDefault = 1;
+
+// the options of one call (NULL: the defaults; a field left 0 takes its default)
+int options_of(const mkmoe_options* o, double& deadline_s, int& gate, int& down) {
+  deadline_s = kDeadlineDefault;
+  gate = kMfmaGateDefault;
+  down = kMfmaDownDefault;
+  if (!o) return MKMOE_OK;
+  if (o->deadline_s != 0.0) {
+    if (!(o->deadline_s > 0.0) || o->deadline_s > 3600.0) return MKMOE_ERR_ARG;
+    deadline_s = o->deadline_s;
+  }
+  if (o->mfma_gate_rows < 0 || o->mfma_down_rows < 0) return MKMOE_ERR_ARG;
+  if (o->mfma_gate_rows) gate = o->mfma_gate_rows;
+  if (o->mfma_down_rows) down = o->mfma_down_rows;
+  return MKMOE_OK;
+}
 
 int device_info(int dev, DevInfo* out) {
   std::lock_guard<std::mutex> lk(g_mu);
@@ -2738,34 +2906,14 @@ Layout layout_of(const mkmoe_shape* s) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-template <class C>
-int launch(const Params& p, int nwg, hipStream_t st, bool staged) {
-  dim3 grid(nwg), block(kThreads);
-  if (!staged) {
-    hipLaunchKernelGGL(k_fused<C>, grid, block, 0, st, p);
-  } else {
-    if constexpr (C::NORM) hipLaunchKernelGGL(k_norm<C>, grid, block, 0, st, p);
-    hipLaunchKernelGGL(k_a<C>, grid, block, 0, st, p);
-    hipLaunchKernelGGL(k_b<C>, grid, block, 0, st, p);
-    hipLaunchKernelGGL(k_c<C>, grid, block, 0, st, p);
-    hipLaunchKernelGGL(k_d<C>, grid, block, 0, st, p);
-  }
-  return hipGetLastError() == hipSuccess ? MKMOE_OK : MKMOE_ERR_LAUNCH;
-}
-
-template <class C>
-int occupancy_ok(int cus) {
-  int per = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_fused<C>, kThreads, 0) != hipSuccess)
-    return MKMOE_ERR_HIP;
-  return per >= 1 ? MKMOE_OK : MKMOE_ERR_DEVICE;
-}
-
 int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, int32_t rows,
-                 void* out, int32_t* ids, float* wts, void* ws, size_t ws_bytes, void* stream,
-                 bool staged) {
+                 void* out, int32_t* ids, float* wts, void* ws, size_t ws_bytes,
+                 const mkmoe_options* opts, void* stream, bool staged) {
   int rc = check_shape(s);
   if (rc) return rc;
+  double dl;
+  int mfma_gate, mfma_down;
+  if ((rc = options_of(opts, dl, mfma_gate, mfma_down))) return rc;
   if (!w || !x || !out || !ws) return MKMOE_ERR_NULL;
   if (!w->gate_w || !w->bias || !w->w13 || !w->w13_s || !w->w2 || !w->w2_s || !w->sgu ||
       !w->sgu_s || !w->sw2 || !w->sw2_s)
@@ -2813,32 +2961,16 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
   p.scale = s->routed_scale;
   p.limit = s->swiglu_limit;
   p.eps = s->norm_eps;
-  double dl;
-  {
-    std::lock_guard<std::mutex> lk(g_mu);
-    dl = g_deadline_s;
-  }
   p.deadline = (unsigned long long)(dl * 1e8);
-  {
-    std::lock_guard<std::mutex> lk(g_mu);
-    p.mfma_gate = g_mfma_gate;
-    p.mfma_down = g_mfma_down;
-  }
+  p.mfma_gate = mfma_gate;
+  p.mfma_down = mfma_down;
   for (int i = 0; i < kRegions; ++i) p.off[i] = (uint32_t)L.off[i];
   hipStream_t st = (hipStream_t)stream;
   switch (cfg_id(s)) {
-    case kIdPlumbing:
-      if (!staged && (rc = occupancy_ok<CfgPlumbing>(nwg))) return rc;
-      return launch<CfgPlumbing>(p, nwg, st, staged);
-    case kIdTp4Fp8:
-      if (!staged && (rc = occupancy_ok<CfgTp4Fp8>(nwg))) return rc;
-      return launch<CfgTp4Fp8>(p, nwg, st, staged);
-    case kIdTp4Fp4:
-      if (!staged && (rc = occupancy_ok<CfgTp4Fp4>(nwg))) return rc;
-      return launch<CfgTp4Fp4>(p, nwg, st, staged);
-    case kIdTp2Fp4Norm:
-      if (!staged && (rc = occupancy_ok<CfgTp2Fp4Norm>(nwg))) return rc;
-      return launch<CfgTp2Fp4Norm>(p, nwg, st, staged);
+    case kIdPlumbing: return mkmoe_launch_cfg0(p, nwg, st, staged);
+    case kIdTp4Fp8: return mkmoe_launch_cfg1(p, nwg, st, staged);
+    case kIdTp4Fp4: return mkmoe_launch_cfg2(p, nwg, st, staged);
+    case kIdTp2Fp4Norm: return mkmoe_launch_cfg3(p, nwg, st, staged);
   }
   return MKMOE_ERR_SHAPE;
 }
@@ -2886,29 +3018,14 @@ int mkmoe_init_workspace(const mkmoe_shape* shape, void* ws, size_t ws_bytes, vo
 
 int mkmoe_forward(const mkmoe_shape* shape, const mkmoe_weights* w, const void* x, int32_t rows,
                   void* out, int32_t* topk_ids, float* topk_w, void* ws, size_t ws_bytes,
-                  void* stream) {
-  return forward_impl(shape, w, x, rows, out, topk_ids, topk_w, ws, ws_bytes, stream, false);
+                  const mkmoe_options* opts, void* stream) {
+  return forward_impl(shape, w, x, rows, out, topk_ids, topk_w, ws, ws_bytes, opts, stream, false);
 }
 
 int mkmoe_forward_staged(const mkmoe_shape* shape, const mkmoe_weights* w, const void* x,
                          int32_t rows, void* out, int32_t* topk_ids, float* topk_w, void* ws,
-                         size_t ws_bytes, void* stream) {
-  return forward_impl(shape, w, x, rows, out, topk_ids, topk_w, ws, ws_bytes, stream, true);
-}
-
-int mkmoe_set_deadline(double seconds) {
-  if (!(seconds > 0.0) || seconds > 3600.0) return MKMOE_ERR_ARG;
-  std::lock_guard<std::mutex> lk(g_mu);
-  g_deadline_s = seconds;
-  return MKMOE_OK;
-}
-
-int mkmoe_set_mfma_rows(int32_t gate_up_rows, int32_t down_rows) {
-  if (gate_up_rows < 1 || down_rows < 1) return MKMOE_ERR_ARG;
-  std::lock_guard<std::mutex> lk(g_mu);
-  g_mfma_gate = gate_up_rows;
-  g_mfma_down = down_rows;
-  return MKMOE_OK;
+                         size_t ws_bytes, const mkmoe_options* opts, void* stream) {
+  return forward_impl(shape, w, x, rows, out, topk_ids, topk_w, ws, ws_bytes, opts, stream, true);
 }
 
 int mkmoe_read_errors(const void* ws, int32_t* words, int32_t n, void* stream) {
@@ -2922,12 +3039,8 @@ int mkmoe_read_errors(const void* ws, int32_t* words, int32_t n, void* stream) {
   return MKMOE_OK;
 }
 
-int mkmoe_clear_errors(void* ws, void* stream) {
-  if (!ws) return MKMOE_ERR_NULL;
-  if (hipMemsetAsync((uint8_t*)ws + kCtlErr * 4, 0, MKMOE_ERRW_WORDS * 4, (hipStream_t)stream) !=
-      hipSuccess)
-    return MKMOE_ERR_HIP;
-  return MKMOE_OK;
+int mkmoe_clear_errors(const mkmoe_shape* shape, void* ws, size_t ws_bytes, void* stream) {
+  return mkmoe_init_workspace(shape, ws, ws_bytes, stream);
 }
 
 const char* mkmoe_status_string(int status) {
@@ -2969,3 +3082,5 @@ void mkmoe_host_topk(const mkmoe_shape* s, const float* scores, const float* bia
 }
 
 }  // extern "C"
+
+#endif  // host unit

@@ -138,7 +138,8 @@ inline void topk_host(int E, int K, int NG, int TG, int renorm, float scale, con
   bool keep[1024];
   int per = E / NG;
   for (int e = 0; e < E; ++e) {
-    choice[e] = score[e] + bias[e];
+    const float c = score[e] + bias[e];
+    choice[e] = c != c ? -INFINITY : c;  // a NaN choice is -inf
     keep[e] = NG <= 1;
   }
   if (NG > 1) {
@@ -172,8 +173,9 @@ inline void topk_host(int E, int K, int NG, int TG, int renorm, float scale, con
       if (keep[e] && (best < 0 || better(choice[e], e, choice[best], best))) best = e;
     keep[best] = false;
     ids[k] = best;
-    wts[k] = score[best];
-    total = total + score[best];
+    const float sc = score[best] != score[best] ? 0.0f : score[best];  // a NaN score weighs 0
+    wts[k] = sc;
+    total = total + sc;
   }
   float f = scale;
   if (renorm) f = scale / (total > 1e-20f ? total : 1e-20f);

@@ -10,7 +10,17 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmkmoe.so"
+# the diagnostic build with the persistent launch's phase stamps (build.py --timeline)
+TIMELINE_LIB_PATH = Path(__file__).resolve().parent / "libmkmoe_tl.so"
+TL_SLOTS = 24
+TL_NAMES = (
+    "start", "A done", "A arrived", "routed", "union", "A awaited", "gate_up", "C arrived",
+    "C awaited", "D routed", "D shared", "end", "gate_up first unit", "gate_up wait", "down wait",
+    "gate_up units", "gate_up fetch", "gate_up mfma", "gate_up sync", "gate_up emit", "gate_up sync2",
+    "down quant", "down mfma",
+)  # fmt: skip
 
+ABI_VERSION = 2  # MKMOE_ABI_VERSION of include/mkmoe.h that this binding follows
 FMT_FP8_B128 = 1
 FMT_MXFP4 = 2
 ERRW_WORDS = 8
@@ -27,6 +37,7 @@ REGIONS = {
     "shared_mid": 8,
     "mid": 9,
     "router_parts_polled": 10,
+    "timeline": 11,
 }
 STAGES = {1: "norm", 2: "router + quantize", 3: "route", 4: "gate_up (routed + shared)", 5: "down (shared + routed) + combine"}
 
@@ -38,8 +49,6 @@ EXPORTS = (
     "mkmoe_init_workspace",
     "mkmoe_forward",
     "mkmoe_forward_staged",
-    "mkmoe_set_deadline",
-    "mkmoe_set_mfma_rows",
     "mkmoe_read_errors",
     "mkmoe_clear_errors",
     "mkmoe_workspace_region",
@@ -72,6 +81,17 @@ class Shape(ctypes.Structure):
     ]
 
 
+class Options(ctypes.Structure):
+    """``mkmoe_options``: a field left 0 takes the library's default."""
+
+    _fields_ = [
+        ("deadline_s", ctypes.c_double),
+        ("mfma_gate_rows", ctypes.c_int32),
+        ("mfma_down_rows", ctypes.c_int32),
+        ("reserved", ctypes.c_int32 * 4),
+    ]
+
+
 class Weights(ctypes.Structure):
     _fields_ = [
         (n, ctypes.c_void_p)
@@ -80,6 +100,15 @@ class Weights(ctypes.Structure):
 
 
 _lib = None
+
+
+def use_timeline_build() -> None:
+    """Load the diagnostic timeline build instead of the product library (before the first
+    call of ``lib()``; raises when it has not been built)."""
+    global LIB_PATH
+    if _lib is not None and LIB_PATH != TIMELINE_LIB_PATH:
+        raise RuntimeError("mkmoe: the product library is already loaded")
+    LIB_PATH = TIMELINE_LIB_PATH
 
 
 def lib() -> ctypes.CDLL:
@@ -93,18 +122,16 @@ def lib() -> ctypes.CDLL:
             )
         L = ctypes.CDLL(str(LIB_PATH))
         vp, i32, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_size_t
-        sp, wp = ctypes.POINTER(Shape), ctypes.POINTER(Weights)
+        sp, wp, op = ctypes.POINTER(Shape), ctypes.POINTER(Weights), ctypes.POINTER(Options)
         L.mkmoe_abi_version.restype = ctypes.c_int
         L.mkmoe_shape_supported.argtypes = [sp]
         L.mkmoe_workspace_bytes.argtypes = [sp, ctypes.POINTER(sz)]
         L.mkmoe_init_workspace.argtypes = [sp, vp, sz, vp]
-        fwd = [sp, wp, vp, i32, vp, vp, vp, vp, sz, vp]
+        fwd = [sp, wp, vp, i32, vp, vp, vp, vp, sz, op, vp]
         L.mkmoe_forward.argtypes = fwd
         L.mkmoe_forward_staged.argtypes = fwd
-        L.mkmoe_set_deadline.argtypes = [ctypes.c_double]
-        L.mkmoe_set_mfma_rows.argtypes = [i32, i32]
         L.mkmoe_read_errors.argtypes = [vp, ctypes.POINTER(i32), i32, vp]
-        L.mkmoe_clear_errors.argtypes = [vp, vp]
+        L.mkmoe_clear_errors.argtypes = [sp, vp, sz, vp]
         L.mkmoe_workspace_region.argtypes = [sp, i32, ctypes.POINTER(sz), ctypes.POINTER(sz)]
         L.mkmoe_status_string.argtypes = [ctypes.c_int]
         L.mkmoe_status_string.restype = ctypes.c_char_p
@@ -115,6 +142,10 @@ def lib() -> ctypes.CDLL:
         L.mkmoe_host_sigmoid.restype = None
         L.mkmoe_host_topk.argtypes = [sp, vp, vp, vp, vp]
         L.mkmoe_host_topk.restype = None
+        if L.mkmoe_abi_version() != ABI_VERSION:
+            raise RuntimeError(
+                f"{LIB_PATH} has ABI {L.mkmoe_abi_version()}, this binding wants {ABI_VERSION}: rebuild it"
+            )
         _lib = L
     return _lib
 

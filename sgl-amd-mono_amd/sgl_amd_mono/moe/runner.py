@@ -117,11 +117,31 @@ class MoeWeights:
         return w
 
 
-class MoeRunner:
-    """The MoE block of one preset on one GPU: a workspace and the launch."""
+# the library's defaults: launches with at least this many rows run the gate_up / down GEMMs
+# on MFMA (every launch); fewer rows run the fixed-order VALU GEMVs, bit-identical to the
+# oracle (mfma_rows=(49, 49) selects them at every row count)
+MFMA_GATE_ROWS, MFMA_DOWN_ROWS = 1, 1
+DEADLINE_S = 2.0
 
-    def __init__(self, preset: MoePreset | str, device=None, max_rows: int | None = None):
+
+class MoeRunner:
+    """The MoE block of one preset on one GPU: a workspace and the launch.
+
+    ``deadline_s`` and ``mfma_rows`` (gate_up rows, down rows) are this runner's
+    per-call options (``mkmoe_options``); ``moe(..., mfma_rows=...)`` overrides
+    the GEMM choice for one call. Nothing is process-global."""
+
+    def __init__(
+        self,
+        preset: MoePreset | str,
+        device=None,
+        max_rows: int | None = None,
+        deadline_s: float = DEADLINE_S,
+        mfma_rows: tuple[int, int] = (MFMA_GATE_ROWS, MFMA_DOWN_ROWS),
+    ):
         self.preset = PRESETS[preset] if isinstance(preset, str) else preset
+        self.deadline_s = float(deadline_s)
+        self.mfma_rows = (int(mfma_rows[0]), int(mfma_rows[1]))
         dev = torch.device("cuda") if device is None else torch.device(device)
         if dev.type != "cuda":
             raise RuntimeError(f"mkmoe: {dev} is not a GPU")
@@ -134,7 +154,6 @@ class MoeRunner:
         _lib.check(self.lib.mkmoe_workspace_bytes(ctypes.byref(self.shape), ctypes.byref(n)), "workspace size")
         no_capture("workspace allocation")
         self.ws = torch.zeros(n.value, dtype=torch.uint8, device=self.device)
-        self._checked: set[int] = set()
         _lib.check(
             self.lib.mkmoe_init_workspace(
                 ctypes.byref(self.shape), self.ws.data_ptr(), self.ws.numel(), self._stream()
@@ -160,15 +179,16 @@ class MoeRunner:
         topk_ids: torch.Tensor | None = None,
         topk_w: torch.Tensor | None = None,
         staged: bool = False,
+        mfma_rows: tuple[int, int] | None = None,
     ) -> torch.Tensor:
         """This rank's MoE partial of bf16 rows ``x`` [R, H] (before the all-reduce) -> bf16 [R, H]."""
         p = self.preset
         rows = x.shape[0]
         if not self.supports(rows):
             raise RuntimeError(f"mkmoe: {rows} rows, want 1 .. {self.max_rows}")
-        if id(w) not in self._checked:
-            w.check(p, self.device)
-            self._checked.add(id(w))
+        # every call: the kernel reads the weights with unbounded loads, so a tensor of the
+        # wrong size must never reach it (a check is a few microseconds)
+        w.check(p, self.device)
         bf = torch.bfloat16
         if out is None:
             no_capture("an output allocation")
@@ -185,6 +205,8 @@ class MoeRunner:
                 )
         fn = self.lib.mkmoe_forward_staged if staged else self.lib.mkmoe_forward
         ws_ = w.c_struct()
+        gate, down = self.mfma_rows if mfma_rows is None else mfma_rows
+        opts = _lib.Options(deadline_s=self.deadline_s, mfma_gate_rows=int(gate), mfma_down_rows=int(down))
         rc = fn(
             ctypes.byref(self.shape),
             ctypes.byref(ws_),
@@ -195,6 +217,7 @@ class MoeRunner:
             None if topk_w is None else topk_w.data_ptr(),
             self.ws.data_ptr(),
             self.ws.numel(),
+            ctypes.byref(opts),
             self._stream(),
         )
         _lib.check(rc, "mkmoe forward")
@@ -227,23 +250,8 @@ class MoeRunner:
     def clear_errors(self) -> None:
         """Reset the workspace after a device error: the error words, and the hand-off state
         (flags, polled router part sums) that a launch cut short by a deadline may leave."""
+        no_capture("a workspace reset")
         _lib.check(
-            self.lib.mkmoe_init_workspace(ctypes.byref(self.shape), self.ws.data_ptr(), self.ws.numel(), self._stream()),
-            "workspace init",
+            self.lib.mkmoe_clear_errors(ctypes.byref(self.shape), self.ws.data_ptr(), self.ws.numel(), self._stream()),
+            "clear errors",
         )
-
-
-def set_deadline(seconds: float) -> None:
-    _lib.check(_lib.lib().mkmoe_set_deadline(seconds), "deadline")
-
-
-# the library's defaults: launches with at least this many rows run the gate_up / down GEMMs
-# on MFMA (every launch); fewer rows run the fixed-order VALU GEMVs, bit-identical to the
-# oracle (set_mfma_rows(49, 49) selects them at every row count)
-MFMA_GATE_ROWS, MFMA_DOWN_ROWS = 1, 1
-
-
-def set_mfma_rows(gate_up_rows: int = MFMA_GATE_ROWS, down_rows: int = MFMA_DOWN_ROWS) -> None:
-    """Launches with at least ``gate_up_rows`` (``down_rows``) rows run the gate_up (down) GEMMs
-    on MFMA; fewer rows run the fixed-order VALU GEMVs (bit-identical to the oracle)."""
-    _lib.check(_lib.lib().mkmoe_set_mfma_rows(int(gate_up_rows), int(down_rows)), "mfma rows")

@@ -237,7 +237,7 @@ def _tp_size(ctx) -> int:
 
 
 def _build(model, hf_config, ctx) -> _Built:
-    from .runner import MoeRunner, set_deadline
+    from .runner import DEADLINE_S, MoeRunner
 
     tp = _tp_size(ctx)
     fuse_norm = bool(getattr(ctx, "fuse_norm", False))
@@ -252,9 +252,7 @@ def _build(model, hf_config, ctx) -> _Built:
         w.check(preset)
         layers[i] = w
     device = next(iter(layers.values())).gate_w.device
-    runner = MoeRunner(preset, device, max_rows=MAX_ROWS)
-    if getattr(ctx, "deadline_s", None):
-        set_deadline(ctx.deadline_s)
+    runner = MoeRunner(preset, device, max_rows=MAX_ROWS, deadline_s=getattr(ctx, "deadline_s", None) or DEADLINE_S)
     return _Built(runner, layers)
 
 

@@ -1,14 +1,16 @@
-"""Build one MoE layer on the GPU from the oracle's seeded CPU inputs, plus its oracle result.
+"""Build one MoE layer on the GPU from the oracle's seeded CPU inputs, plus its oracle results.
 
-Every expert that a checked row routes to holds its seeded weights (generated
-on the CPU, expert by expert); every other expert holds random but finite bytes
-drawn on the GPU, so a kernel that reads a wrong expert for a checked row
-fails the comparison. Routing (cheap) is checked for every row; the output for
-``check`` rows (all rows up to 8, else 8 rows spread over the step).
+Every expert the step routes to holds its seeded weights (generated on the CPU,
+expert by expert, in a process pool); every other expert holds random but finite
+bytes drawn on the GPU, which the kernel must never read. Routing is checked for
+every row, and the output of every row against both of the oracle's forms: its
+exact restatement of the kernel's arithmetic order and the golden's fp32-matmul
+form (the reference's own check compares every token, ``check_ffn.py:327-343``).
 """
 
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass
 
 import numpy as np
@@ -19,6 +21,10 @@ from oracle import moe as om
 from oracle import routing as rt
 from sgl_amd_mono.moe.presets import PRESETS, WORKLOADS, workload_dict
 from sgl_amd_mono.moe.runner import MoeWeights
+
+
+def _workers() -> int:
+    return max(1, min(16, len(os.sched_getaffinity(0))))
 
 
 @dataclass
@@ -33,9 +39,10 @@ class Case:
     wts: np.ndarray  # oracle weights [R, k]
     parts: np.ndarray  # oracle router part sums [R, E, P]
     xin: torch.Tensor  # oracle normed (or raw) x, CPU bf16
-    check: np.ndarray  # rows whose output the oracle computed
-    ref: torch.Tensor  # oracle output bf16 [len(check), H] (the kernel's arithmetic order)
-    golden: torch.Tensor  # the golden's fp32-matmul output bf16 [len(check), H]
+    check: np.ndarray  # rows compared (every row)
+    ref: torch.Tensor  # the oracle's exact output bf16 [R, H] (the kernel's arithmetic order)
+    golden: torch.Tensor  # the golden's fp32-matmul output bf16 [R, H]
+    chain: torch.Tensor  # fp32 [R, H]: the largest magnitude either form's bf16 combine chain held
 
 
 def _random_fill(shape, dtype, fmt, kind, device, g):
@@ -50,31 +57,43 @@ def _random_fill(shape, dtype, fmt, kind, device, g):
 
 
 def check_rows(rows: int) -> np.ndarray:
-    if rows <= 8:
-        return np.arange(rows)
-    return np.unique(np.linspace(0, rows - 1, 8).round().astype(int))
+    return np.arange(rows)
+
+
+# the CPU side of a case (inputs, oracle results, the seeded experts) per (workload, rows, seed)
+_CPU: dict = {}
+
+
+def _cpu_side(workload: str, rows: int, seed: int):
+    key = (workload, rows, seed)
+    if key not in _CPU:  # kept for the session: a 48-row case holds about 2 GB of experts
+        p = workload_dict(workload)
+        preset = PRESETS[WORKLOADS[workload]["preset"]]
+        x = gen.make_x(p, rows, seed)
+        dense = gen.make_dense(p, seed)
+        xin = rt.rmsnorm_exact(x, dense["norm"], p["norm_eps"]) if p["norm_eps"] is not None else x
+        parts = rt.router_part_sums(xin, dense["gate_w"], p["router_parts"])
+        scores = rt.sigmoid_exact(rt.logits_from_parts(parts))
+        ids, wts = rt.grouped_topk(
+            scores, dense["bias"].numpy(), p["topk"], p["n_group"], p["topk_group"], p["routed_scale"]
+        )
+        tensors, cx, cg = om.pool_contribs(p, seed, xin, ids, wts, _workers())
+        res = om.moe_partial(x, dense, p, exact=True, contribs=cx)
+        golden = om.moe_partial(x, dense, p, exact=False, contribs=cg)
+        assert np.array_equal(res["ids"], ids) and np.array_equal(golden["ids"], ids)
+        chain = torch.maximum(res["chain_max"], golden["chain_max"])
+        _CPU[key] = (p, preset, x, dense, xin, parts, ids, wts, check_rows(rows), res["out"], golden["out"], tensors, chain)
+    return _CPU[key]
 
 
 def build(workload: str, rows: int, seed: int = 0, device="cuda") -> Case:
-    p = workload_dict(workload)
-    preset = PRESETS[WORKLOADS[workload]["preset"]]
-    x = gen.make_x(p, rows, seed)
-    dense = gen.make_dense(p, seed)
-    xin = rt.rmsnorm_exact(x, dense["norm"], p["norm_eps"]) if p["norm_eps"] is not None else x
-    parts = rt.router_part_sums(xin, dense["gate_w"], p["router_parts"])
-    scores = rt.sigmoid_exact(rt.logits_from_parts(parts))
-    ids, wts = rt.grouped_topk(scores, dense["bias"].numpy(), p["topk"], p["n_group"], p["topk_group"], p["routed_scale"])
-    check = check_rows(rows)
-    ex = gen.LazyExperts(p, seed)
-    res = om.moe_partial(x[torch.from_numpy(check)], dense, p, experts=ex)
-    assert np.array_equal(res["ids"], ids[check])
-    golden = om.moe_partial(x[torch.from_numpy(check)], dense, p, experts=ex, exact=False)["out"]
+    p, preset, x, dense, xin, parts, ids, wts, check, ref, golden, tensors, chain = _cpu_side(workload, rows, seed)
     g = torch.Generator(device=device).manual_seed(1234 + seed)
     dev = {}
     for name, (shape, dtype) in gen.expert_shapes(p).items():
         kind = "scale" if name.endswith("_s") else "w"
         dev[name] = _random_fill(shape, dtype, p["routed_fmt"], kind, device, g)
-    for e, (w13, w13_s, w2, w2_s) in ex.cache.items():
+    for e, (w13, w13_s, w2, w2_s) in tensors.items():
         dev["w13"][e].copy_(w13.to(device))
         dev["w13_s"][e].copy_(w13_s.to(device))
         dev["w2"][e].copy_(w2.to(device))
@@ -89,15 +108,40 @@ def build(workload: str, rows: int, seed: int = 0, device="cuda") -> Case:
         norm=dense["norm"].to(device) if "norm" in dense else None,
         **dev,
     )
-    return Case(workload, preset, p, rows, x.to(device), w, ids, wts, parts, xin, check, res["out"], golden)
+    return Case(workload, preset, p, rows, x.to(device), w, ids, wts, parts, xin, check, ref, golden, chain)
 
 
-def errors(out: torch.Tensor, ref: torch.Tensor) -> dict:
-    """max-abs, relative L2, cosine, and the largest difference in bf16 ulps of the reference."""
+def within_bar(e: dict, numel: int) -> bool:
+    """The output bar of a launch whose sums are not bit-identical to the reference's: relative
+    L2 <= 1e-2; every element within max(2e-2, two bf16 ulps of the largest magnitude its
+    combine chain held); at most max(1, 1e-4 of the elements) beyond 2e-2. Each pick's
+    contribution and every add of the combine round to bf16 (check_ffn.py:216-225), so an
+    fp32-level difference in one pick's sum can flip that contribution by one ulp, which the
+    later bf16 adds can carry to two ulps of the running sum: 0.03125 at |sum| in [2, 4),
+    beyond 2e-2 (and a sum that later cancels keeps that error). The oracle's restatement of the
+    kernel's order itself lands that far from the golden's fp32 matmuls on 1 of 344064
+    elements (cfg2, 48 rows), and the MFMA launches land that far from the restatement on 1
+    (cfg2) to 6 (cfg5) of 344064 elements at 48 rows; a launch bit-identical to the
+    restatement is held to the bits."""
+    return (
+        not e["nan"]
+        and e["rel_l2"] <= 1e-2
+        and e["n_over_bar"] == 0
+        and e["n_over_2e-2"] <= max(1, int(1e-4 * numel))
+    )
+
+
+def errors(out: torch.Tensor, ref: torch.Tensor, chain: torch.Tensor | None = None) -> dict:
+    """max-abs, relative L2, cosine, and the largest difference in bf16 ulps of the reference
+    (of the largest magnitude the combine chain held, when ``chain`` is given)."""
     a, b = out.float().cpu(), ref.float().cpu()
     d = (a - b).abs()
-    ulp = torch.ldexp(torch.ones_like(b), torch.frexp(b.abs().clamp_min(2.0**-20))[1] - 8)
+    m = b.abs() if chain is None else torch.maximum(b.abs(), chain.float().cpu())
+    ulp = torch.ldexp(torch.ones_like(b), torch.frexp(m.clamp_min(2.0**-20))[1] - 8)
+    bar = torch.maximum(torch.full_like(ulp, 2e-2), 2 * ulp)
     return {
+        # elements off by more than max(2e-2, two bf16 ulps of the reference value)
+        "n_over_bar": int((d > bar).sum()),
         "max_abs": float(d.max()),
         "rel_l2": float((a - b).norm() / b.norm()),
         "cos": float(torch.nn.functional.cosine_similarity(a.reshape(-1), b.reshape(-1), dim=0)),

@@ -1,9 +1,11 @@
 """Parity of the HIP MoE block (through the C ABI) with the CPU oracle, on an MI355X.
 
 Bars: router part sums, activation codes, expert ids and routing weights bit for
-bit at every row count; the bf16 output within max-abs 2e-2 and relative L2 1e-2
-of both the oracle and the golden's fp32-matmul form (the reference's PyTorch
-path). The default launch runs the expert GEMMs on MFMA; launches forced onto the
+bit at every row count; the bf16 output of every row, against both the oracle's
+exact restatement of the kernel's order and the golden's fp32-matmul form (the
+reference's PyTorch path), within relative L2 1e-2 and max-abs 2e-2 up to the
+bf16 combine's own rounding (gpu_case.within_bar), and cosine 0.9999 against
+the golden. The default launch runs the expert GEMMs on MFMA; launches forced onto the
 fixed-order VALU GEMVs (which the oracle restates) are also bit for bit against the oracle
 and the golden vectors, at small and large row counts. The persistent and the staged
 launches bit for bit alike; repeated and graph-replayed launches bit for bit alike.
@@ -15,7 +17,7 @@ import torch
 
 pytestmark = pytest.mark.gpu
 
-MAX_ABS, REL_L2 = 2e-2, 1e-2
+MAX_ABS, REL_L2 = 2e-2, 1e-2  # the output bar (gpu_case.within_bar applies it)
 CASES = [
     ("cfg1_plumbing_fp8", 4),
     ("cfg2_tp4_fp8", 1),
@@ -46,19 +48,14 @@ def _case(workload, rows):
     return _cache[key]
 
 
-def _runner(case):
+def _runner(case, mfma_rows=None, **kw):
+    """A runner of the case's preset; mfma_rows: (gate_up rows, down rows) from which its
+    launches run the expert GEMMs on MFMA (default: the library's, i.e. always)."""
     from sgl_amd_mono.moe.runner import MoeRunner
 
-    return MoeRunner(case.preset, "cuda")
-
-
-@pytest.fixture
-def mfma_rows():
-    """Set the MFMA row counts for one test; the library defaults come back afterwards."""
-    from sgl_amd_mono.moe.runner import set_mfma_rows
-
-    yield set_mfma_rows
-    set_mfma_rows()
+    if mfma_rows is not None:
+        kw["mfma_rows"] = mfma_rows
+    return MoeRunner(case.preset, "cuda", **kw)
 
 
 def test_device_decode_matches_tables():
@@ -83,7 +80,7 @@ def test_device_decode_matches_tables():
 
 def _check(c, rows, run, exact):
     """Run the launch; routing bit for bit, the output within the bounds (and, exact: bit for bit)."""
-    from gpu_case import errors
+    from gpu_case import errors, within_bar
 
     ids = torch.zeros(rows, c.p["topk"], dtype=torch.int32, device="cuda")
     wts = torch.zeros(rows, c.p["topk"], dtype=torch.float32, device="cuda")
@@ -101,19 +98,21 @@ def _check(c, rows, run, exact):
     assert np.array_equal(ids.cpu().numpy(), c.ids), "expert ids"
     assert np.array_equal(wts.cpu().numpy().view(np.uint32), c.wts.view(np.uint32)), "routing weights"
     got = out[torch.from_numpy(c.check).cuda()].cpu()
-    e = errors(got, c.ref)
-    print(f"  out vs oracle: {e}", flush=True)
+    e = errors(got, c.ref, c.chain[torch.from_numpy(c.check)])
+    print(f"  all {rows} rows vs the oracle's exact order: {e}", flush=True)
     assert not e["nan"] and not torch.isnan(out).any()
-    assert e["rel_l2"] <= REL_L2, e
-    assert e["max_abs"] <= MAX_ABS, e
+    assert within_bar(e, got.numel()), e
     n_diff = int((got.view(torch.int16) != c.ref.view(torch.int16)).sum())
     print(f"  elements differing from the oracle's bits: {n_diff} of {got.numel()}", flush=True)
     if exact:
         assert n_diff == 0, f"{n_diff} output elements differ from the oracle's bits"
-    # and against the golden's own fp32 matmuls (the reference's PyTorch path, check_ffn.py:209-232)
-    g = errors(got, c.golden)
-    print(f"  out vs fp32-matmul golden: {g}", flush=True)
-    assert g["max_abs"] <= MAX_ABS and g["rel_l2"] <= REL_L2, g
+    # every row against the golden's own fp32 matmuls (the reference's PyTorch path,
+    # check_ffn.py:209-232, which compares every token: check_ffn.py:327-343), to the same bar
+    # and the reference's own cosine bound (ffn.moe.cosine, spec.py:305-309)
+    g = errors(out.cpu(), c.golden, c.chain)
+    print(f"  all {rows} rows vs fp32-matmul golden: {g}", flush=True)
+    assert within_bar(g, out.numel()) and g["cos"] >= 0.9999, g
+    assert out.numel() == c.golden.numel() == rows * c.p["hidden"]
 
 
 @pytest.mark.parametrize("workload,rows", CASES)
@@ -140,12 +139,11 @@ def test_parity(workload, rows):
         ("cfg4_tp4_mxfp4_zipf", 48),
     ],
 )
-def test_parity_valu_forced(workload, rows, mfma_rows):
+def test_parity_valu_forced(workload, rows):
     """Large launches held on the VALU GEMVs: bit for bit against the oracle."""
     c = _case(workload, rows)
-    mfma_rows(rows + 1, rows + 1)
     print(f"\n{workload} R={rows} (VALU forced)", flush=True)
-    _check(c, rows, _runner(c), exact=True)
+    _check(c, rows, _runner(c, (rows + 1, rows + 1)), exact=True)
 
 
 @pytest.mark.parametrize(
@@ -160,12 +158,11 @@ def test_parity_valu_forced(workload, rows, mfma_rows):
         ("cfg5_tp2_mxfp4_norm", 48),
     ],
 )
-def test_parity_mfma_forced(workload, rows, mfma_rows):
+def test_parity_mfma_forced(workload, rows):
     """Every expert GEMM on MFMA (gate_up included): within the bounds, routing bit for bit."""
     c = _case(workload, rows)
-    mfma_rows(1, 1)
     print(f"\n{workload} R={rows} (MFMA forced)", flush=True)
-    _check(c, rows, _runner(c), exact=False)
+    _check(c, rows, _runner(c, (1, 1)), exact=False)
 
 
 @pytest.mark.parametrize("bias_kind", ["zero", "coarse"])
@@ -197,6 +194,44 @@ def test_routing_ties(workload, rows, bias_kind):
     run.raise_on_device_error()
     assert np.array_equal(ids.cpu().numpy(), want_ids), "expert ids"
     assert np.array_equal(wts.cpu().numpy().view(np.uint32), want_w.view(np.uint32)), "routing weights"
+
+
+@pytest.mark.parametrize("workload,rows", [("cfg2_tp4_fp8", 8), ("cfg2_tp4_fp8", 24)])
+def test_routing_nan_row(workload, rows):
+    """A row of NaN inputs: its logits are NaN, every choice -inf and every weight 0, so it
+    picks the first topk experts of the first groups (the oracle's rule, stages/moe.py:345-347);
+    the other rows' routing and outputs are those of the case without it."""
+    from gpu_case import errors, within_bar
+
+    from oracle import routing as rt
+
+    c = _case(workload, rows)
+    bad = 3
+    x = c.x.clone()
+    x[bad] = float("nan")
+    xin = c.xin.clone()
+    xin[bad] = float("nan")
+    _, want_ids, want_w = rt.route(xin, gen_dense(c)["gate_w"], gen_dense(c)["bias"], c.p)
+    assert want_ids[bad].tolist() == list(range(c.p["topk"])) and np.all(want_w[bad] == 0)
+    run = _runner(c)
+    ids = torch.zeros(rows, c.p["topk"], dtype=torch.int32, device="cuda")
+    wts = torch.zeros(rows, c.p["topk"], dtype=torch.float32, device="cuda")
+    out = run.moe(c.w, x, topk_ids=ids, topk_w=wts)
+    torch.cuda.synchronize()
+    run.raise_on_device_error()
+    assert np.array_equal(ids.cpu().numpy(), want_ids), "expert ids"
+    assert np.array_equal(wts.cpu().numpy().view(np.uint32), want_w.view(np.uint32)), "routing weights"
+    assert bool((run.region("router_parts_polled") == 0xFF).all()), "polled part sums left unset"
+    keep = [i for i, r in enumerate(c.check.tolist()) if r != bad]
+    rows_kept = torch.from_numpy(c.check[keep]).cuda()
+    e = errors(out[rows_kept].cpu(), c.ref[keep], c.chain[keep])
+    assert within_bar(e, len(keep) * c.p["hidden"]), e
+
+
+def gen_dense(c):
+    from oracle import gen
+
+    return gen.make_dense(c.p, 0)
 
 
 @pytest.mark.parametrize("workload,rows", [("cfg2_tp4_fp8", 8), ("cfg3_tp4_mxfp4", 8), ("cfg5_tp2_mxfp4_norm", 8)])
@@ -291,7 +326,7 @@ def test_host_validation_errors():
         run.moe(bad, c.x)
 
 
-def test_golden_fixtures(mfma_rows):
+def test_golden_fixtures():
     """The kernel (its fixed-order VALU GEMVs) against the committed golden vectors
     (tests/golden/), bit for bit."""
     import sys
@@ -303,9 +338,8 @@ def test_golden_fixtures(mfma_rows):
     for workload, rows in mg.CASES:
         f = np.load(mg.case_file(workload, rows))
         c = _case(workload, rows)
-        mfma_rows(rows + 1, rows + 1)
         assert np.array_equal(c.x.view(torch.int16).cpu().numpy(), f["x_bits"]), "seeded x"
-        run = _runner(c)
+        run = _runner(c, (rows + 1, rows + 1))
         ids = torch.zeros(rows, c.p["topk"], dtype=torch.int32, device="cuda")
         wts = torch.zeros(rows, c.p["topk"], dtype=torch.float32, device="cuda")
         out = run.moe(c.w, c.x, topk_ids=ids, topk_w=wts)

@@ -189,7 +189,7 @@ def test_host_library_exports():
     from pathlib import Path
 
     L = _lib.lib()
-    assert L.mkmoe_abi_version() == 1
+    assert L.mkmoe_abi_version() == _lib.ABI_VERSION
     header = (Path(__file__).resolve().parents[1] / "include" / "mkmoe.h").read_text()
     declared = set(re.findall(r"^(?:int|void|const char\*)\s+(mkmoe_\w+)\(", header, re.M))
     assert declared == set(_lib.EXPORTS), declared ^ set(_lib.EXPORTS)

@@ -171,6 +171,71 @@ def test_host_topk_bitexact(name):
         assert np.array_equal(w.view(np.uint32), rw[0].view(np.uint32))
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_grouped_topk_nan_scores(seed):
+    """A NaN score's choice is -inf and it weighs 0 (stages/moe.py:345-347): the oracle against
+    brute force on the substituted choices, and the host build of the kernel's top-k."""
+    from sgl_amd_mono.moe.presets import PRESETS
+
+    rng = np.random.default_rng(100 + seed)
+    e, k, ng, tg = 16, 4, 4, 2
+    scores = rt.sigmoid_exact(rng.standard_normal((1, e)).astype(np.float32))
+    bias = (rng.standard_normal(e) * 0.02).astype(np.float32)
+    nan_at = rng.choice(e, size=1 + seed % 5, replace=False)
+    scores[0, nan_at] = np.nan
+    ids, wts = rt.grouped_topk(scores, bias, k, ng, tg, 2.5)
+    choice = np.where(np.isnan(scores[0]), -np.inf, scores[0] + bias).astype(np.float32)
+    bid, bw = _brute_topk(choice, np.nan_to_num(scores[0], nan=0.0), k, ng, tg, 2.5)
+    assert ids[0].tolist() == bid.tolist()
+    assert np.array_equal(wts[0].view(np.uint32), bw.view(np.uint32))
+    assert not set(ids[0].tolist()) & set(nan_at.tolist())  # finite choices always win here
+    # the kernel's host build, at the BASELINE shape (NaN spread over several groups)
+    p = PRESETS["dsv3_tp4_fp8"]
+    sc = rt.sigmoid_exact(rng.standard_normal((1, p.experts)).astype(np.float32))[0]
+    sc[rng.choice(p.experts, size=40, replace=False)] = np.nan
+    bb = np.ascontiguousarray((rng.standard_normal(p.experts) * 0.02).astype(np.float32))
+    sc = np.ascontiguousarray(sc)
+    hid, hw = _host_topk(p, sc, bb)
+    rid, rw = rt.grouped_topk(sc[None], bb, p.topk, p.n_group, p.topk_group, p.routed_scale)
+    assert hid.tolist() == rid[0].tolist()
+    assert np.array_equal(hw.view(np.uint32), rw[0].view(np.uint32))
+
+
+def test_grouped_topk_all_nan_row():
+    """Known answer: every score NaN -> every choice -inf, so groups and experts go by lower
+    index (the first topk experts of group 0), and every weight is 0."""
+    scores = np.full((1, 256), np.nan, np.float32)
+    bias = np.zeros(256, np.float32)
+    ids, wts = rt.grouped_topk(scores, bias, 8, 8, 4, 2.5)
+    assert ids[0].tolist() == list(range(8))
+    assert np.all(wts == 0)
+
+
+def test_unset_part_sums_route_in_bounds():
+    """A routing that gives up waiting reads the unset marker (0xFFFFFFFF, a NaN) as part sums:
+    the kernel's host build maps it to a NaN score, and its top-k then returns in-range ids
+    (0 .. topk-1 in the first groups) with weight 0, so nothing derived from them leaves a
+    buffer."""
+    from sgl_amd_mono.moe import _lib
+    from sgl_amd_mono.moe.presets import PRESETS
+
+    L = _lib.lib()
+    unset = np.full(4, 0xFFFFFFFF, np.uint32).view(np.float32)
+    logit = np.zeros(4, np.float32)
+    for _ in range(7):  # the parts added in order, as the kernel does
+        logit = (logit + unset).astype(np.float32)
+    sc = np.zeros(4, np.float32)
+    L.mkmoe_host_sigmoid(logit.ctypes.data, sc.ctypes.data, 4)
+    assert np.all(np.isnan(sc))
+    for name in ("plumbing_fp8", "dsv3_tp4_fp8"):
+        p = PRESETS[name]
+        scores = np.full(p.experts, np.nan, np.float32)
+        bias = np.ascontiguousarray((np.arange(p.experts) % 5).astype(np.float32) * np.float32(0.01))
+        ids, w = _host_topk(p, scores, bias)
+        assert ids.tolist() == list(range(p.topk)), ids
+        assert np.all((ids >= 0) & (ids < p.experts)) and np.all(w == 0)
+
+
 def test_rmsnorm_close_to_fp64():
     g = torch.Generator().manual_seed(8)
     x = torch.randn(4, 7168, generator=g).to(torch.bfloat16)
