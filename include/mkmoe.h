@@ -152,6 +152,23 @@ int mkmoe_forward_staged(const mkmoe_shape* shape, const mkmoe_weights* w, const
                          int32_t rows, void* out, int32_t* topk_ids, float* topk_w, void* ws,
                          size_t ws_bytes, const mkmoe_options* opts, void* stream);
 
+/* The same launch with the workspace in a static device array, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). No counterpart in the reference. It
+ * allocates nothing: the array (MKMOE_STATIC_WS_BYTES, 4 MiB, enough for every
+ * compiled shape at 48 rows; a larger layout returns MKMOE_ERR_WORKSPACE) lives
+ * in each GPU the library runs on until the process ends. Each call enqueues a
+ * small fill kernel that clears the array's hand-off and error words and marks
+ * the call's polled router part sums unset, then the forward kernel: two
+ * launches, both safe to capture. Every call on one GPU shares that GPU's
+ * array, so calls that may overlap on one GPU (other streams, other threads)
+ * race and must not be issued. Its device error words are not readable
+ * through the C ABI; a caller that needs them uses mkmoe_forward. */
+#define MKMOE_STATIC_WS_BYTES (4u << 20)
+int mkmoe_forward_static(const mkmoe_shape* shape, const mkmoe_weights* w, const void* x,
+                         int32_t rows, void* out, int32_t* topk_ids, float* topk_w,
+                         const mkmoe_options* opts, void* stream);
+
 /* Copy the MKMOE_ERRW_WORDS error words to host memory (synchronises stream).
  * After a device error (MKMOE_ERRW_CODE non-zero) the launch that recorded it
  * gave up waiting, so its output is not valid and its hand-off state (arrival

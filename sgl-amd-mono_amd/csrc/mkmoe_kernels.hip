@@ -2833,6 +2833,24 @@ __attribute__((visibility("hidden"))) int mkmoe_launch_cfg3(const Params&, int, 
 #if !defined(MKMOE_UNIT) || MKMOE_UNIT == MKMOE_UNIT_HOST
 namespace {
 
+// The workspace of mkmoe_forward_static (for callers that cannot allocate): one array per GPU,
+// held until the process ends. In host code ``scratch`` names a host-side stand-in, not device
+// memory: its device address comes from hipGetSymbolAddress (once per device, that device
+// current) and only that address is used.
+constexpr size_t kStaticWsBytes = MKMOE_STATIC_WS_BYTES;
+static __device__ __align__(256) uint8_t scratch[kStaticWsBytes];
+
+// before each mkmoe_forward_static launch: the hand-off and error words cleared, the polled
+// router part sums of the call's rows unset (a fill kernel: no memset, so a capture may hold it)
+__global__ void k_static_reset(uint8_t* ws, uint32_t ctl_bytes, uint32_t off10, uint32_t bytes10) {
+  const uint32_t nctl = ctl_bytes / 16, n = nctl + bytes10 / 16;
+  for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < n; k += gridDim.x * blockDim.x) {
+    if (k < nctl)
+      *(u32x4*)(ws + (size_t)k * 16) = u32x4{0u, 0u, 0u, 0u};
+    else
+      *(u32x4*)(ws + off10 + (size_t)(k - nctl) * 16) = u32x4{kPartUnset, kPartUnset, kPartUnset, kPartUnset};
+  }
+}
 
 struct DevInfo {
   int cus = 0;
@@ -2841,6 +2859,20 @@ struct DevInfo {
 
 std::mutex g_mu;
 DevInfo g_dev[64];
+void* g_scratch[64];  // scratch's device address per device
+
+// scratch's device address on device dev (the current device)
+int static_workspace(int dev, void** ws) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (dev < 0 || dev >= 64) return MKMOE_ERR_DEVICE;
+  if (!g_scratch[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return MKMOE_ERR_HIP;
+    g_scratch[dev] = ptr;
+  }
+  *ws = g_scratch[dev];
+  return MKMOE_OK;
+}
 constexpr double kDeadlineDefault = 2.0;  // seconds
 constexpr int kMfmaGateDefault = 1;       // gate_up and down on MFMA at every row count
 constexpr int kMfmaDownDefault = 1;
@@ -2906,14 +2938,21 @@ Layout layout_of(const mkmoe_shape* s) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// static_ws: the workspace is this device's scratch (ws and ws_bytes are ignored)
 int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, int32_t rows,
                  void* out, int32_t* ids, float* wts, void* ws, size_t ws_bytes,
-                 const mkmoe_options* opts, void* stream, bool staged) {
+                 const mkmoe_options* opts, void* stream, bool staged, bool static_ws = false) {
   int rc = check_shape(s);
   if (rc) return rc;
   double dl;
   int mfma_gate, mfma_down;
   if ((rc = options_of(opts, dl, mfma_gate, mfma_down))) return rc;
+  if (static_ws) {
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) return MKMOE_ERR_HIP;
+    if ((rc = static_workspace(cur, &ws))) return rc;
+    ws_bytes = kStaticWsBytes;
+  }
   if (!w || !x || !out || !ws) return MKMOE_ERR_NULL;
   if (!w->gate_w || !w->bias || !w->w13 || !w->w13_s || !w->w2 || !w->w2_s || !w->sgu ||
       !w->sgu_s || !w->sw2 || !w->sw2_s)
@@ -2966,6 +3005,12 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
   p.mfma_down = mfma_down;
   for (int i = 0; i < kRegions; ++i) p.off[i] = (uint32_t)L.off[i];
   hipStream_t st = (hipStream_t)stream;
+  if (static_ws) {
+    const uint32_t bytes10 = (uint32_t)rows * s->router_parts * s->experts * 4;
+    hipLaunchKernelGGL(k_static_reset, dim3(8), dim3(256), 0, st, (uint8_t*)ws, (uint32_t)kCtlBytes,
+                       (uint32_t)L.off[10], bytes10);
+    if (hipGetLastError() != hipSuccess) return MKMOE_ERR_LAUNCH;
+  }
   switch (cfg_id(s)) {
     case kIdPlumbing: return mkmoe_launch_cfg0(p, nwg, st, staged);
     case kIdTp4Fp8: return mkmoe_launch_cfg1(p, nwg, st, staged);
@@ -3026,6 +3071,12 @@ int mkmoe_forward_staged(const mkmoe_shape* shape, const mkmoe_weights* w, const
                          int32_t rows, void* out, int32_t* topk_ids, float* topk_w, void* ws,
                          size_t ws_bytes, const mkmoe_options* opts, void* stream) {
   return forward_impl(shape, w, x, rows, out, topk_ids, topk_w, ws, ws_bytes, opts, stream, true);
+}
+
+int mkmoe_forward_static(const mkmoe_shape* shape, const mkmoe_weights* w, const void* x,
+                         int32_t rows, void* out, int32_t* topk_ids, float* topk_w,
+                         const mkmoe_options* opts, void* stream) {
+  return forward_impl(shape, w, x, rows, out, topk_ids, topk_w, nullptr, 0, opts, stream, false, true);
 }
 
 int mkmoe_read_errors(const void* ws, int32_t* words, int32_t n, void* stream) {

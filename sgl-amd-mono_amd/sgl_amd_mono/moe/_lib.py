@@ -49,6 +49,7 @@ EXPORTS = (
     "mkmoe_init_workspace",
     "mkmoe_forward",
     "mkmoe_forward_staged",
+    "mkmoe_forward_static",
     "mkmoe_read_errors",
     "mkmoe_clear_errors",
     "mkmoe_workspace_region",
@@ -130,6 +131,7 @@ def lib() -> ctypes.CDLL:
         fwd = [sp, wp, vp, i32, vp, vp, vp, vp, sz, op, vp]
         L.mkmoe_forward.argtypes = fwd
         L.mkmoe_forward_staged.argtypes = fwd
+        L.mkmoe_forward_static.argtypes = [sp, wp, vp, i32, vp, vp, vp, op, vp]
         L.mkmoe_read_errors.argtypes = [vp, ctypes.POINTER(i32), i32, vp]
         L.mkmoe_clear_errors.argtypes = [sp, vp, sz, vp]
         L.mkmoe_workspace_region.argtypes = [sp, i32, ctypes.POINTER(sz), ctypes.POINTER(sz)]

@@ -196,3 +196,20 @@ def test_host_library_exports():
     for name in _lib.EXPORTS:
         assert hasattr(L, name), name
     assert ctypes.c_char_p(L.mkmoe_status_string(-2)).value
+
+
+def test_static_workspace_holds_every_compiled_shape():
+    """mkmoe_forward_static's array (MKMOE_STATIC_WS_BYTES) holds the workspace of every
+    compiled shape at the largest row count."""
+    import re
+    from pathlib import Path
+
+    from sgl_amd_mono.moe import _lib
+    from sgl_amd_mono.moe.presets import PRESETS
+
+    header = (Path(__file__).resolve().parents[1] / "include" / "mkmoe.h").read_text()
+    limit = eval(re.search(r"#define MKMOE_STATIC_WS_BYTES \((.+)\)", header).group(1).replace("u", ""))
+    for p in PRESETS.values():
+        n = ctypes.c_size_t()
+        assert _lib.lib().mkmoe_workspace_bytes(ctypes.byref(_lib.shape_of(p, 48)), ctypes.byref(n)) == 0
+        assert n.value <= limit, (p.name, n.value, limit)
