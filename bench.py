@@ -328,6 +328,8 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--staged", action="store_true", help="time the one-launch-per-stage variant")
+    ap.add_argument("--mxfp4-scaled-rows", type=int, default=None,
+                    help="MXFP4 launches with at least this many rows on the scaled fp4 x fp8 MFMA")
     ap.add_argument("--timeline", action="store_true",
                     help="phase timeline of the diagnostic build (build.py --timeline); no JSON line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -368,7 +370,8 @@ def main() -> int:
         log(f"{name}: generating {args.layers} layers of {preset.name} weights on the GPU")
         layers = [make_layer(preset, g, device, zipf) for _ in range(args.layers)]
         torch.cuda.synchronize()
-        runner = MoeRunner(preset, device, max_rows=max(48, max(rows_list)))
+        kw = {} if args.mxfp4_scaled_rows is None else {"mxfp4_scaled_rows": args.mxfp4_scaled_rows}
+        runner = MoeRunner(preset, device, max_rows=max(48, max(rows_list)), **kw)
         if args.staged:
             orig = runner.moe
             runner.moe = lambda *a, **k: orig(*a, staged=True, **k)

@@ -132,7 +132,11 @@ typedef struct mkmoe_options {
                            * (routed and shared) on MFMA (default 1: always); fewer rows run
                            * the fixed-order VALU GEMVs, bit-identical to the oracle */
   int32_t mfma_down_rows; /* the same for the down GEMMs (default 1) */
-  int32_t reserved[4];
+  int32_t mxfp4_scaled_rows; /* MXFP4 shapes: launches with at least this many rows (and on
+                              * MFMA) run both expert GEMMs on the scaled fp4 x fp8 MFMA
+                              * (v_mfma_scale_f32_16x16x128_f8f6f4), with no conversion of
+                              * the codes; 0: the default (never) */
+  int32_t reserved[3];
 } mkmoe_options;
 
 /* One MoE block for rows bf16 rows x [rows][H] -> out bf16 [rows][H] (this
@@ -199,6 +203,15 @@ const char* mkmoe_status_string(int status);
  * fp4[2i], fp4[2i + 1] = the e2m1 values of its low and high nibble, through
  * the same hardware converts the kernels use (for tests of those converts). */
 int mkmoe_device_decode(const uint8_t* codes, float* fp8, float* fp4, int32_t n, void* stream);
+
+/* Device run of the scaled MFMA the MXFP4 option uses (v_mfma_scale_f32_16x16x128_f8f6f4,
+ * C = 0), for its known-answer tests; no counterpart in the reference, which calls the
+ * instruction through FlyDSL (common/mx.py:60-66). tiles waves, one 16x16x128 tile each: a
+ * and b hold eight 32-bit words a lane ([tiles][64][8]; an e2m1 A (fmt_a 4) uses the first
+ * four, an e4m3 A is fmt_a 0; B is e4m3), sa and sb one E8M0 code a lane ([tiles][64]), d
+ * four floats a lane ([tiles][64][4]: C[m][n] in lane n + 16 (m / 4), element m % 4). */
+int mkmoe_device_mfma_scaled(const void* a, const void* b, const void* sa, const void* sb, float* d,
+                             int32_t fmt_a, int32_t tiles, void* stream);
 
 /* Host builds of the kernels' exact arithmetic (no device needed): */
 void mkmoe_host_e4m3_encode(const float* x, uint8_t* out, int64_t n);

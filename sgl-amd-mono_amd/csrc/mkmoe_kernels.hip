@@ -111,6 +111,9 @@ struct Cfg {
   static constexpr int MQS = I + 16;  // LDS row stride of quantized mid (bank spread)
   static constexpr int SQS = S + 16;
   static constexpr int MSC = FMT == kFp4 ? I / 32 : I / 128;  // mid scales a pick
+  // 16-row blocks of a routed down unit: MXFP4 rows of 512 K are 256 bytes, so a unit of 32 rows
+  // keeps 8 KB a wave in flight (as 16 rows do at FP8, or at MXFP4 with 1024 K)
+  static constexpr int DNA = FMT == kFp4 && I <= 512 ? 2 : 1;
 };
 
 using CfgPlumbing = Cfg<1024, 16, 4, 1, 1, 512, 512, kFp8, 2, false>;
@@ -179,6 +182,7 @@ struct Params {
   int tile_rows;
   int mfma_gate;  // launches with at least this many rows run the gate_up GEMMs on MFMA
   int mfma_down;  // ... and the down GEMMs
+  int mx_scaled;  // MXFP4 expert GEMMs on the scaled fp4 x fp8 MFMA (no converts)
   float scale;
   float limit;
   float eps;
@@ -1381,6 +1385,19 @@ __device__ __forceinline__ void mma_fp4_step2(u32x4 a0, float s0, u32x4 a1, floa
   }
 }
 
+// an MXFP4 x MXFP8 128-K step on the scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4), no
+// converts: A lane (m, j) holds row m's 32 e2m1 of K [32 j, 32 j + 32) (16 bytes), B lane
+// (n, j) column n's e4m3 of K [16 j, 16 j + 16) then [64 + 16 j, 64 + 16 j + 16) (blo, bhi);
+// each lane gives the E8M0 codes of the 32-K block j of its row (sa) and its column (sb), and
+// the instruction scales every product by its block's codes (measured on gfx950 with exactly
+// summable operands: this layout reproduces the exact dot). Its internal sum keeps fewer bits
+// than fp32 (the known-answer test bounds it), so its launches are held to the numerics bar.
+__device__ __forceinline__ f32x4 mma_fp4_scaled(u32x4 a, uint32_t sa, u32x4 blo, u32x4 bhi, uint32_t sb, f32x4 c) {
+  const i32x8 av = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
+  const i32x8 bv = {(int)blo.x, (int)blo.y, (int)blo.z, (int)blo.w, (int)bhi.x, (int)bhi.y, (int)bhi.z, (int)bhi.w};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 4, 0, 0, (int)sa, 0, (int)sb);
+}
+
 // 16 bytes a lane from a buffer straight into LDS: lane l's bytes land at lds + 16 l (lds
 // the same in every lane of the wave)
 __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, void* lds, uint32_t voff, int aux) {
@@ -1430,11 +1447,14 @@ __device__ __forceinline__ void stage_x_lds(const Params& p, XTile<C>& xt, int n
 // partial C tiles (gate, up)
 template <class C>
 struct GuSmem {
+  // MXFP4: a wave's slot of its K slice's E8M0 scales of a unit (32 rows x 32 bytes)
+  static constexpr int SSLOT = C::FMT == kFp4 ? 1024 : 16;
   union {
     XTile<C> x;
     struct {
       uint8_t wslot[kWaves][2 * C::H];
       float wsc[XTile<C>::WSC];
+      uint8_t sslot[kWaves][SSLOT];
     } m;
   };
   f32x4 red[2][kWaves][64];
@@ -1453,8 +1473,7 @@ struct GuTile {
   static constexpr int NC = WFMT == kFp8 ? 8 : 16;  // columns a unit
   static constexpr int NW = WFMT == kFp8 ? 2 : 1;   // 16-byte words of a lane's step
   u32x4 a[NA][SPW][NW];
-  uint32_t sa[NA][SPW];   // MXFP4: the E8M0 byte of the lane's row and block
-  uint32_t nsa[NA][SPW];  // and the next unit's, requested with its rows
+  uint32_t sa[NA][SPW];  // MXFP4: the E8M0 byte of the lane's row and block
 
   // A unit's weight rows (FP8: gate rows j0 .. j0 + 7 then up rows W + j0 ..; MXFP4: 16 gate
   // rows then 16 up rows), this wave's K steps, go through the wave's LDS slot: LDS-direct
@@ -1471,11 +1490,12 @@ struct GuTile {
   __device__ __forceinline__ static int wrow(int W, int j0, int r) {
     return WFMT == kFp8 ? (r < 8 ? j0 + r : W + j0 + r - 8) : (r >> 4) * W + j0 + (r & 15);
   }
-  // w: the [2W][H] weight (wr: its resource words), s: its scales; the unit's columns
-  // j0 .. j0 + nc - 1 (nc = NC, or NC / 2 at a share's ends: the other rows are requested
-  // past the resource, so the slot holds zeros there and no memory is read)
-  __device__ __forceinline__ void issue(i32x4 wr, const void* s, int W, int j0, int nc, uint8_t* slot, int lane,
-                                        int wave) {
+  // w: the [2W][H] weight (wr: its resource words), sr: its MXFP4 scales' resource words
+  // ([2W][H / 32] bytes); the unit's columns j0 .. j0 + nc - 1 (nc = NC, or NC / 2 at a
+  // share's ends: the other rows are requested past the resource, so the slot holds zeros
+  // there and no memory is read)
+  __device__ __forceinline__ void issue(i32x4 wr, i32x4 sr, int W, int j0, int nc, uint8_t* slot, uint8_t* sslot,
+                                        int lane, int wave) {
     const int s0 = wave * SPW;
     constexpr int ROWB = WFMT == kFp8 ? C::H : C::H / 2;  // bytes a weight row
 #pragma unroll
@@ -1485,15 +1505,17 @@ struct GuTile {
       lds_dma16(wr, slot + i * 1024, live ? (uint32_t)wrow(W, j0, r) * ROWB + s0 * (RB / SPW) + c * 16 : kNoLoad);
     }
     if constexpr (WFMT == kFp4) {
-      const int m = lane & 15, j = lane >> 4;
-      const uint8_t* ss = (const uint8_t*)s;
-#pragma unroll
-      for (int q = 0; q < 2; ++q)
-#pragma unroll
-        for (int i = 0; i < SPW; ++i) nsa[q][i] = ss[(size_t)(q * W + j0 + m) * (C::H / 32) + (s0 + i) * 4 + j];
+      // the scales of the wave's K steps (4 SPW bytes a row, from byte 4 s0) in one LDS-direct
+      // load: lane 2 r + h takes 16 bytes of row r from byte 16 h of its slice, to sslot + 32 r +
+      // 16 h (the 32 - 4 SPW bytes past the slice are never read; past the resource the load
+      // returns zeros)
+      static_assert(4 * SPW <= 32, "a row's slice in two 16-byte pieces");
+      const int r = lane >> 1, h = lane & 1;
+      const bool live = (r & 15) < nc;
+      lds_dma16(sr, sslot, live ? (uint32_t)wrow(W, j0, r) * (C::H / 32) + s0 * 4 + h * 16 : kNoLoad);
     }
   }
-  __device__ __forceinline__ void fetch(const uint8_t* slot, int lane) {
+  __device__ __forceinline__ void fetch(const uint8_t* slot, const uint8_t* sslot, int lane) {
     const int m = lane & 15, j = lane >> 4;
 #pragma unroll
     for (int q = 0; q < NA; ++q)
@@ -1504,8 +1526,18 @@ struct GuTile {
           const int r = q * 16 + m;
           const int c = WFMT == kFp8 ? i * 8 + j + 4 * w : i * 4 + j;
           a[q][i][w] = *(const u32x4*)(slot + (r * CPW + (c ^ key(r))) * 16);
-          if (WFMT == kFp4 && w == 0) sa[q][i] = nsa[q][i];
         }
+    if constexpr (WFMT == kFp4) {
+      // byte j of dword i of row q 16 + m's slice: the E8M0 of the lane's row and block
+#pragma unroll
+      for (int q = 0; q < NA; ++q) {
+        const u32x4 d0 = *(const u32x4*)(sslot + (q * 16 + m) * 32);
+        const u32x4 d1 = *(const u32x4*)(sslot + (q * 16 + m) * 32 + 16);
+        const uint32_t dw[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+#pragma unroll
+        for (int i = 0; i < SPW; ++i) sa[q][i] = (dw[i] >> (8 * j)) & 0xffu;
+      }
+    }
   }
 };
 
@@ -1533,8 +1565,11 @@ struct GuX {
         hi[i] = dld128(rs, qoff + t * C::H + k0 + 64 + 16 * j);
         sx[i] = u2f(dld32(rs, soff + (t * (C::H / 128) + s0 + i) * 4));
       } else {
-        lo[i] = dld128(rs, qoff + t * C::H + k0 + 32 * j);
-        hi[i] = dld128(rs, qoff + t * C::H + k0 + 32 * j + 16);
+        // the scaled MFMA takes K [16 j, 16 j + 16) and [64 + 16 j, ..); the converting path
+        // the 32-K block j itself
+        const uint32_t klo = p.mx_scaled ? 16 * j : 32 * j, khi = p.mx_scaled ? 64 + 16 * j : 32 * j + 16;
+        lo[i] = dld128(rs, qoff + t * C::H + k0 + klo);
+        hi[i] = dld128(rs, qoff + t * C::H + k0 + khi);
         ex[i] = dld8(rs, soff + t * (C::H / 32) + k0 / 32 + j);
       }
     }
@@ -1548,7 +1583,7 @@ struct GuX {
 // wsc the FP8 weight's block scales in LDS
 template <class C, int WFMT>
 __device__ __forceinline__ void gu_mma(const GuTile<C, WFMT>& t, const GuX<C, WFMT>& x, const float* wsc, int W, int j0,
-                                       int lane, int wave, f32x4 (&acc)[GuTile<C, WFMT>::NA]) {
+                                       int lane, int wave, bool scaled, f32x4 (&acc)[GuTile<C, WFMT>::NA]) {
   using T = GuTile<C, WFMT>;
   const int s0 = wave * T::SPW;
 #pragma unroll
@@ -1565,8 +1600,13 @@ __device__ __forceinline__ void gu_mma(const GuTile<C, WFMT>& t, const GuX<C, WF
       for (int v = 0; v < 4; ++v) acc[0][v] = fmaf(c[v], f, acc[0][v]);
     } else {
       static_assert(T::NA == 2, "gate and up rows");
-      mma_fp4_step2(t.a[0][i][0], e8m0(t.sa[0][i]), t.a[1][i][0], e8m0(t.sa[1][i]), x.lo[i], x.hi[i], e8m0(x.ex[i]),
-                    acc[0], acc[1]);
+      if (scaled) {
+        acc[0] = mma_fp4_scaled(t.a[0][i][0], t.sa[0][i], x.lo[i], x.hi[i], x.ex[i], acc[0]);
+        acc[1] = mma_fp4_scaled(t.a[1][i][0], t.sa[1][i], x.lo[i], x.hi[i], x.ex[i], acc[1]);
+      } else {
+        mma_fp4_step2(t.a[0][i][0], e8m0(t.sa[0][i]), t.a[1][i][0], e8m0(t.sa[1][i]), x.lo[i], x.hi[i],
+                      e8m0(x.ex[i]), acc[0], acc[1]);
+      }
     }
   }
 }
@@ -1579,7 +1619,7 @@ __device__ __forceinline__ void gu_mma(const GuTile<C, WFMT>& t, const GuX<C, WF
 // unit's MFMAs run and its partial tiles add in LDS (in wave order). An FP8 weight's block
 // scales go to LDS when the group changes.
 template <class C, int WFMT, bool HALF, class GroupFn, class XFn, class EmitFn>
-__device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h, GroupFn group, XFn xload,
+__device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h, bool scaled, GroupFn group, XFn xload,
                                         EmitFn emit) {
   using T = GuTile<C, WFMT>;
   if (lo_h >= hi_h) return;
@@ -1599,6 +1639,9 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
   const int nb = W / T::NC;
   constexpr uint32_t WB = WFMT == kFp8 ? C::H : C::H / 2;  // bytes a weight row
   uint8_t* slot = sm.m.wslot[wave];
+  uint8_t* sslot = sm.m.sslot[wave];
+  // an MXFP4 weight's scales ([2W][H / 32] E8M0) as a resource (unused for FP8)
+  auto srsc = [&](const void* sp) { return weight_rsrc_words(sp, WFMT == kFp4 ? 2u * W * (C::H / 32) : 0u); };
   T t;
   GuX<C, WFMT> x;
   const uint8_t* wb;
@@ -1609,7 +1652,7 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
   {
     int c0, nc;
     half(lo, c0, nc);
-    t.issue(weight_rsrc_words(wb, 2u * W * WB), sb, W, (lo % nb) * T::NC + c0, nc, slot, lane, wave);
+    t.issue(weight_rsrc_words(wb, 2u * W * WB), srsc(sb), W, (lo % nb) * T::NC + c0, nc, slot, sslot, lane, wave);
   }
   int tg_x = -1, np_x = 0;  // the group in x
   const void* sb_x = sb;
@@ -1641,7 +1684,7 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
     if (u == lo) TL(kTlGuFirst);
     if (fresh) __syncthreads();                       // every wave's block scales are in LDS
     const unsigned long long tf0 = tl_now();
-    t.fetch(slot, lane);
+    t.fetch(slot, sslot, lane);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // read out of the slot
     if (u + 1 < hi) {
       const int tn = (u + 1) / nb;
@@ -1651,12 +1694,13 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
       }
       int c1, nc1;
       half(u + 1, c1, nc1);
-      t.issue(weight_rsrc_words(wb, 2u * W * WB), sb, W, ((u + 1) % nb) * T::NC + c1, nc1, slot, lane, wave);
+      t.issue(weight_rsrc_words(wb, 2u * W * WB), srsc(sb), W, ((u + 1) % nb) * T::NC + c1, nc1, slot, sslot, lane,
+              wave);
     }
     const unsigned long long tf1 = tl_now();
     TL_ADD(kTlGuFetch, tf1 - tf0);
     f32x4 acc[T::NA];
-    gu_mma<C, WFMT>(t, x, sm.m.wsc, W, j0, lane, wave, acc);
+    gu_mma<C, WFMT>(t, x, sm.m.wsc, W, j0, lane, wave, scaled, acc);
 #pragma unroll
     for (int q = 0; q < T::NA; ++q) sm.red[q][wave][lane] = acc[q];
     const unsigned long long tf2 = tl_now();
@@ -1684,32 +1728,37 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
   }
 }
 
-// MFMA down: rows [hb, hb + 16) of a [H][KD] weight (nv of them real), all K steps, in
-// registers; mma() gives C[m][n] = row hb + m against pick column n of an LDS mid tile
-template <int WFMT, int KD>
+// MFMA down: rows [hb, hb + 16 NA) of a [H][KD] weight (nv of them real), all K steps, in
+// registers; mma() gives C[m][n] = row hb + 16 q + m against pick column n of an LDS mid tile,
+// for each of the NA 16-row blocks q
+template <int WFMT, int KD, int NA_ = 1>
 struct DownTile {
+  static constexpr int NA = NA_;  // 16-row A operands a unit
   static constexpr int KS = KD / 128;
   static constexpr int NW = WFMT == kFp8 ? 2 : 1;  // 16-byte words of a lane's step
-  static constexpr int BYTES = NW * 16 * 64 * KS;  // registers' bytes a unit
+  static constexpr int BYTES = NA * NW * 16 * 64 * KS;  // registers' bytes a unit
   // units a wave requests at once: 16 KB of codes (MXFP4 rows of 1024 K: one unit, leaving
   // registers for the conversions)
   static constexpr int kBatch =
       (WFMT == kFp4 && KS >= 8) || BYTES >= 16384 ? 1 : (16384 / BYTES > 4 ? 4 : 16384 / BYTES);
-  u32x4 a[KS][NW];
-  uint32_t sa[KS];        // MXFP4: the E8M0 byte of the lane's row and block
-  float s0[KS], s1[KS];   // FP8: block scales of the lane's first and last C row
-  int split;              // FP8: C elements v < split take s0, the rest s1
+  static_assert(NA == 1 || WFMT == kFp4, "FP8 units are one 16-row block");
+  u32x4 a[NA][KS][NW];
+  uint32_t sa[NA][KS];   // MXFP4: the E8M0 byte of the lane's row and block
+  float s0[KS], s1[KS];  // FP8: block scales of the lane's first and last C row
+  int split;             // FP8: C elements v < split take s0, the rest s1
 
-  // The unit through LDS. issue() requests its 16 rows into a wave's slot by LDS-direct
+  // The unit through LDS. issue() requests its 16 NA rows into a wave's slot by LDS-direct
   // 16-byte loads, each load a contiguous KB of the weight (the operand layout's own loads read
   // 64-byte runs, which stream at about 5.1 against 6.6 TB/s: measured, loads alone). Chunk c
-  // (16 bytes) of row r sits at slot position r * CPR + (c ^ r), so that the 16 rows' reads of
-  // one chunk fall in distinct banks. Rows past nv are requested past the resource (zeros, no
-  // memory access). fetch() reads the slot into a[][] in the operand layout.
+  // (16 bytes) of row r sits at slot position r * CPR + (c ^ (r % 16)), so that the 16 rows'
+  // reads of one chunk fall in distinct banks. Rows past nv are requested past the resource
+  // (zeros, no memory access). fetch() reads the slot into a[][] in the operand layout; the
+  // scales travel in registers (load_scales, take_scales).
   static constexpr int RB = WFMT == kFp8 ? KD : KD / 2;  // bytes a row
   static constexpr int CPR = RB / 16;                   // chunks a row
-  static constexpr int SLOT = 16 * RB;                  // bytes a unit
+  static constexpr int SLOT = 16 * NA * RB;             // bytes a unit
   static_assert(CPR >= 16 && (CPR & (CPR - 1)) == 0 && SLOT % 1024 == 0, "slot layout");
+  static_assert(WFMT == kFp8 || KS % 4 == 0, "MXFP4 scales in 16-byte loads");
   // wr: a resource over the weight from row 0 (H x RB bytes a matrix); wrow: the unit's first
   // row's byte offset in it
   __device__ __forceinline__ static void issue(__amdgpu_buffer_rsrc_t wr, uint32_t wrow, int nv, uint8_t* slot,
@@ -1717,7 +1766,7 @@ struct DownTile {
 #pragma unroll
     for (int i = 0; i < SLOT / 1024; ++i) {
       const int pos = i * 64 + lane;
-      const int r = pos / CPR, c = (pos % CPR) ^ r;
+      const int r = pos / CPR, c = (pos % CPR) ^ (r & 15);
       const uint32_t off = r < nv ? wrow + (uint32_t)r * RB + c * 16 : kNoLoad;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(slot + i * 1024), 16,
                                                off, 0, 0, kAuxNt);
@@ -1726,14 +1775,18 @@ struct DownTile {
   __device__ __forceinline__ void fetch(const uint8_t* slot, int lane) {
     const int m = lane & 15, j = lane >> 4;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
+    for (int q = 0; q < NA; ++q)
 #pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        const int c = WFMT == kFp8 ? ks * 8 + j + 4 * w : ks * 4 + j;
-        a[ks][w] = *(const u32x4*)(slot + (m * CPR + (c ^ m)) * 16);
-      }
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const int c = WFMT == kFp8 ? ks * 8 + j + 4 * w : ks * 4 + j;
+          a[q][ks][w] = *(const u32x4*)(slot + ((q * 16 + m) * CPR + (c ^ m)) * 16);
+        }
   }
-  // the unit's scales alone (as load() sets them)
+  // the unit's scales alone (as load() sets them). FP8: the 128 x 128 block scales of the
+  // lane's C rows; MXFP4: the lane's row's KD / 32 E8M0 bytes in 16-byte loads (byte j of
+  // dword ks is its block's), rows past nv unit scales
   __device__ __forceinline__ void load_scales(const void* s, int hb, int nv, int lane) {
     const int m = lane & 15, j = lane >> 4;
     if constexpr (WFMT == kFp8) {
@@ -1746,25 +1799,35 @@ struct DownTile {
       }
       split = r0 / 128 == r3 / 128 ? 4 : 128 - (hb + 4 * j) % 128;
     } else {
-      const bool ok = m < nv;
-      const size_t h = (size_t)hb + (ok ? m : 0);
       const uint8_t* ss = (const uint8_t*)s;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) sa[ks] = ok ? ss[h * (KD / 32) + ks * 4 + j] : 127u;
+      for (int q = 0; q < NA; ++q) {
+        const bool ok = q * 16 + m < nv;
+        const size_t h = (size_t)hb + (ok ? q * 16 + m : 0);
+#pragma unroll
+        for (int k4 = 0; k4 < KS; k4 += 4) {
+          const u32x4 d = ok ? ld16(ss + h * (KD / 32) + k4 * 4) : u32x4{0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu};
+          const uint32_t dw[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) sa[q][k4 + t] = (dw[t] >> (8 * j)) & 0xffu;
+        }
+      }
     }
   }
   __device__ __forceinline__ void take_scales(const DownTile& o) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      sa[ks] = o.sa[ks];
       s0[ks] = o.s0[ks];
       s1[ks] = o.s1[ks];
+#pragma unroll
+      for (int q = 0; q < NA; ++q) sa[q][ks] = o.sa[q][ks];
     }
     split = o.split;
   }
 
   // w: row 0 of the weight; s: its scales (FP8 [H / 128][KD / 128] fp32, MXFP4 [H][KD / 32])
   __device__ __forceinline__ void load(const uint8_t* w, const void* s, int hb, int nv, int lane) {
+    static_assert(NA == 1, "register units are one 16-row block");
     const int m = lane & 15, j = lane >> 4;
     const bool ok = m < nv;
     const size_t h = (size_t)hb + (ok ? m : 0);
@@ -1773,62 +1836,60 @@ struct DownTile {
       for (int ks = 0; ks < KS; ++ks) {
         const uint8_t* p = w + h * KD + ks * 128 + 16 * j;
         if (ok) {
-          a[ks][0] = ld16_nt(p);
-          a[ks][1] = ld16_nt(p + 64);
+          a[0][ks][0] = ld16_nt(p);
+          a[0][ks][1] = ld16_nt(p + 64);
         } else {
-          a[ks][0] = a[ks][1] = u32x4{0u, 0u, 0u, 0u};
+          a[0][ks][0] = a[0][ks][1] = u32x4{0u, 0u, 0u, 0u};
         }
       }
-      // this lane's C rows hb + 4j .. hb + 4j + 3 (the real ones) and where a 128-row block ends
-      const int r0 = hb + min(4 * j, nv - 1), r3 = hb + min(4 * j + 3, nv - 1);
-      const float* sp = (const float*)s;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        s0[ks] = sp[(r0 / 128) * (KD / 128) + ks];
-        s1[ks] = sp[(r3 / 128) * (KD / 128) + ks];
-      }
-      split = r0 / 128 == r3 / 128 ? 4 : 128 - (hb + 4 * j) % 128;
+      load_scales(s, hb, nv, lane);
     } else {
-      const uint8_t* ss = (const uint8_t*)s;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        if (ok) {
-          a[ks][0] = ld16_nt(w + h * (KD / 2) + ks * 64 + 16 * j);
-          sa[ks] = ss[h * (KD / 32) + ks * 4 + j];
-        } else {
-          a[ks][0] = u32x4{0u, 0u, 0u, 0u};
-          sa[ks] = 127u;
-        }
-      }
+      for (int ks = 0; ks < KS; ++ks)
+        a[0][ks][0] = ok ? ld16_nt(w + h * (KD / 2) + ks * 64 + 16 * j) : u32x4{0u, 0u, 0u, 0u};
+      load_scales(s, hb, nv, lane);
     }
   }
 
-  // C tile against picks [lp, lp + np) of the LDS mid rows (codes xq, row stride QS; scales
-  // xs, SST bytes a row: fp32 per 128, or E8M0 per 32)
+  // C tiles (one a 16-row block) against picks [lp, lp + np) of the LDS mid rows (codes xq, row
+  // stride QS; scales xs, SST bytes a row: fp32 per 128, or E8M0 per 32)
   template <int QS, int SST>
-  __device__ __forceinline__ f32x4 mma(const uint8_t* xq, const uint8_t* xs, int lp, int np, int lane) const {
+  __device__ __forceinline__ void mma(const uint8_t* xq, const uint8_t* xs, int lp, int np, int lane, bool scaled,
+                                      f32x4 (&acc)[NA]) const {
     const int n = lane & 15, j = lane >> 4;
     const bool live = n < np;
     const int row = lp + (live ? n : 0);
     const uint8_t* xr = xq + (size_t)row * QS;
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int q = 0; q < NA; ++q) acc[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       if constexpr (WFMT == kFp8) {
         u32x4 blo = *(const u32x4*)(xr + ks * 128 + 16 * j), bhi = *(const u32x4*)(xr + ks * 128 + 64 + 16 * j);
         if (!live) blo = bhi = u32x4{0u, 0u, 0u, 0u};
         const float sx = ((const float*)(xs + row * SST))[ks];
-        const f32x4 c = mma_fp8_step(a[ks][0], a[ks][1], blo, bhi);
+        const f32x4 c = mma_fp8_step(a[0][ks][0], a[0][ks][1], blo, bhi);
         const float f0 = s0[ks] * sx, f1 = s1[ks] * sx;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[v] = fmaf(c[v], v < split ? f0 : f1, acc[v]);
+        for (int v = 0; v < 4; ++v) acc[0][v] = fmaf(c[v], v < split ? f0 : f1, acc[0][v]);
+      } else if (scaled) {
+        // the scaled MFMA's K layout for the column (see mma_fp4_scaled)
+        u32x4 blo = *(const u32x4*)(xr + ks * 128 + 16 * j), bhi = *(const u32x4*)(xr + ks * 128 + 64 + 16 * j);
+        if (!live) blo = bhi = u32x4{0u, 0u, 0u, 0u};
+        const uint32_t sx = xs[row * SST + ks * 4 + j];
+#pragma unroll
+        for (int q = 0; q < NA; ++q) acc[q] = mma_fp4_scaled(a[q][ks][0], sa[q][ks], blo, bhi, sx, acc[q]);
       } else {
         u32x4 blo = *(const u32x4*)(xr + ks * 128 + 32 * j), bhi = *(const u32x4*)(xr + ks * 128 + 32 * j + 16);
         if (!live) blo = bhi = u32x4{0u, 0u, 0u, 0u};
-        acc = mma_fp4_step(a[ks][0], e8m0(sa[ks]), blo, bhi, e8m0(xs[row * SST + ks * 4 + j]), acc);
+        const float sx = e8m0(xs[row * SST + ks * 4 + j]);
+        if constexpr (NA == 2) {
+          mma_fp4_step2(a[0][ks][0], e8m0(sa[0][ks]), a[1][ks][0], e8m0(sa[1][ks]), blo, bhi, sx, acc[0], acc[1]);
+        } else {
+          acc[0] = mma_fp4_step(a[0][ks][0], e8m0(sa[0][ks]), blo, bhi, sx, acc[0]);
+        }
       }
     }
-    return acc;
   }
 };
 
@@ -2246,7 +2307,8 @@ __device__ __forceinline__ void shared_down_tile(const Params& p, SharedDownSmem
   auto load = shared_down_loader<C, MF>(p, h0, hn);
   if (!first_ready) bt.load(threadIdx.x >> 6, n_units, load);
   __syncthreads();  // the previous user of the LDS is done
-  quant_rows_lds<kFp8, C::S, C::SQS>(
+  // (2 chunks a thread at once with MXFP4 routed experts: 4 spill the persistent launch there)
+  quant_rows_lds<kFp8, C::S, C::SQS, C::FMT == kFp4 ? 2 : kQuantBatch>(
       p, [&](int i) { return p.off[8] + (uint32_t)i * C::S * 2; }, R, sm.q, sm.s);
   __syncthreads();
   if constexpr (MF) {
@@ -2255,12 +2317,13 @@ __device__ __forceinline__ void shared_down_tile(const Params& p, SharedDownSmem
     down_pipeline<DT>(bt, n_units, load, [&](int v, const DT& dt) {
       const int rb = v % nb, pt = v / nb;
       const int t0 = pt * kMfmaPicks, np = min(kMfmaPicks, R - t0);
-      const f32x4 acc = dt.template mma<C::SQS, (C::S / 128) * 4>(sm.q, (const uint8_t*)sm.s, t0, np, lane);
+      f32x4 acc[1];
+      dt.template mma<C::SQS, (C::S / 128) * 4>(sm.q, (const uint8_t*)sm.s, t0, np, lane, false, acc);
       const int n = lane & 15;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int hl = rb * 16 + 4 * (lane >> 4) + k;
-        if (n < np && hl < hn) out[(t0 + n) * hn + hl] = f2bf(acc[k]);
+        if (n < np && hl < hn) out[(t0 + n) * hn + hl] = f2bf(acc[0][k]);
       }
     });
   } else {
@@ -2362,7 +2425,7 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
     const uint32_t qoff = C::FMT == kFp4 ? p.off[3] : p.off[1];
     const uint32_t soff = C::FMT == kFp4 ? p.off[4] : p.off[2];
     gu_mfma<C, kFp8, HALF>(
-        sm, C::S, lo, min(hi, HU * n_sh),
+        sm, C::S, lo, min(hi, HU * n_sh), false,
         [&](int tg, const uint8_t*& w, const void*& s, int& np) {
           w = p.sgu;
           s = p.sgu_s;
@@ -2380,7 +2443,7 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
     return un.slot_start[slot] + (tg - un.tg_start[slot]) * kMfmaPicks;
   };
   gu_mfma<C, C::FMT, HALF>(
-      sm, C::I, max(lo, HU * n_sh) - HU * n_sh, hi - HU * n_sh,
+      sm, C::I, max(lo, HU * n_sh) - HU * n_sh, hi - HU * n_sh, C::FMT == kFp4 && p.mx_scaled,
       [&](int tg, const uint8_t*& w, const void*& s, int& np) {
         const int slot = un.tg_slot[tg];
         const int e = un.slot_e[slot];
@@ -2423,7 +2486,7 @@ struct DownSmem {
   };
   uint16_t shv[kRowsMax * kTileMax];  // the shared expert's bf16 results of the tile
   // MFMA down: a wave's slot of weight rows (one unit)
-  uint8_t wslot[kWaves][DownTile<C::FMT, C::I>::SLOT] __attribute__((aligned(16)));
+  uint8_t wslot[kWaves][DownTile<C::FMT, C::I, C::DNA>::SLOT] __attribute__((aligned(16)));
 };
 
 // the slots holding picks [pb0, pb0 + pbn) of the step (picks are stored slot by slot)
@@ -2444,7 +2507,7 @@ __device__ __forceinline__ void batch_slots(const Union<C>& un, int pb0, int pbn
 template <class C>
 using DownRowsOf = DownRows<C::FMT, C::I>;
 template <class C>
-using DownTileOf = DownTile<C::FMT, C::I>;
+using DownTileOf = DownTile<C::FMT, C::I, C::DNA>;
 // the down stage's batch of units: MFMA (MF) or VALU
 // the MFMA down's unit in flight: its rows in the wave's LDS slot, its scales in nxt
 template <class C>
@@ -2479,9 +2542,10 @@ template <class C>
 __device__ __forceinline__ void mfma_issue(const Params& p, const Union<C>& un, int h0, int hn, int s_lo, int v,
                                            uint8_t* slot, DownTileOf<C>& nx, int lane) {
   using DT = DownTileOf<C>;
-  const int nb = (hn + 15) / 16;
+  constexpr int UR = 16 * DT::NA;  // rows a unit
+  const int nb = (hn + UR - 1) / UR;
   const int e = un.slot_e[s_lo + v / nb], rb = v % nb;
-  const int hb = h0 + rb * 16, nv = min(16, hn - rb * 16);
+  const int hb = h0 + rb * UR, nv = min(UR, hn - rb * UR);
   static_assert((long long)C::E * C::H * DT::RB < (1ll << 31), "offsets within a 32-bit resource");
   const auto wr = weight_rsrc(p.w2, (uint32_t)(C::E * C::H * DT::RB));
   DT::issue(wr, (uint32_t)(e * C::H + hb) * DT::RB, nv, slot, lane);
@@ -2543,7 +2607,8 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
   const int npk = p.rows * C::K;
   using DT = DownTileOf<C>;
   constexpr int SST = C::FMT == kFp4 ? C::I / 32 : (C::I / 128) * 4;  // scale bytes of a pick
-  const int nb = (hn + 15) / 16;
+  constexpr int UR = 16 * DT::NA;  // rows a unit
+  const int nb = (hn + UR - 1) / UR;
   uint8_t* slot = sm.wslot[wave];
   for (int pb0 = 0; pb0 < npk; pb0 += C::PB) {
     const int pbn = min(C::PB, npk - pb0);
@@ -2554,9 +2619,9 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
       mfma_issue<C>(p, un, h0, hn, s_lo, wave, slot, bt.nxt, lane);
     __syncthreads();  // the previous batch is done with the LDS rows
     const unsigned long long tq0 = tl_now();
-    // the quantize requests 8 chunks a thread at once (4 at I >= 1024, whose unit and scales
-    // leave fewer registers: 8 spills there)
-    quant_rows_lds<C::FMT, C::I, C::MQS, (C::I >= 1024 ? 1 : 2) * kQuantBatch>(
+    // the quantize requests 8 chunks a thread at once (4 where a unit's scales take more
+    // registers: MXFP4, whose 8 spill there)
+    quant_rows_lds<C::FMT, C::I, C::MQS, (C::FMT == kFp4 ? 1 : 2) * kQuantBatch>(
         p, [&](int i) { return p.off[9] + (uint32_t)un.picks[pb0 + i] * C::I * 2; }, pbn, sm.q, sm.s);
     __syncthreads();
     TL_ADD(kTlDQuant, tl_now() - tq0);
@@ -2575,13 +2640,16 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
       const unsigned long long tm0 = tl_now();
       for (int jj = j0; jj < j1; jj += kMfmaPicks) {
         const int np = min(kMfmaPicks, j1 - jj);
-        const f32x4 acc = cur.template mma<C::MQS, SST>(sm.q, sm.s, jj - pb0, np, lane);
+        f32x4 acc[DT::NA];
+        cur.template mma<C::MQS, SST>(sm.q, sm.s, jj - pb0, np, lane, C::FMT == kFp4 && p.mx_scaled, acc);
         const int pk = n < np ? un.picks[jj + n] : 0;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int hl = rb * 16 + 4 * (lane >> 4) + k;
-          if (n < np && hl < hn) sm.contrib[pk * kTileMax + hl] = f2bf(acc[k] * un.wts[pk]);
-        }
+        for (int q = 0; q < DT::NA; ++q)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int hl = rb * UR + q * 16 + 4 * (lane >> 4) + k;
+            if (n < np && hl < hn) sm.contrib[pk * kTileMax + hl] = f2bf(acc[q][k] * un.wts[pk]);
+          }
       }
       TL_ADD(kTlDMma, tl_now() - tm0);
     }
@@ -2601,7 +2669,8 @@ __device__ __forceinline__ void down_first(const Params& p, const Union<C>& un, 
   // these weights (a wave's loads return in order)
   if (wave == 0) return;
   if constexpr (MF) {
-    if (wave < (s_hi - s_lo + 1) * ((hn + 15) / 16))
+    constexpr int UR = 16 * DownTileOf<C>::NA;
+    if (wave < (s_hi - s_lo + 1) * ((hn + UR - 1) / UR))
       mfma_issue<C>(p, un, h0, hn, s_lo, wave, sm.wslot[wave], bt.nxt, threadIdx.x & 63);
   } else {
     bt.load(wave, (s_hi - s_lo + 1) * kRowBlocks, valu_down_loader<C>(p, un, h0, hn, s_lo));
@@ -2762,6 +2831,27 @@ __global__ __launch_bounds__(kThreads) void k_d(Params p) {
 }
 
 #if !defined(MKMOE_UNIT) || MKMOE_UNIT == MKMOE_UNIT_HOST
+// one v_mfma_scale_f32_16x16x128_f8f6f4 a tile (a wave a workgroup, C = 0): A and B eight
+// words a lane (an e2m1 A uses the first four), the E8M0 codes one word a lane; D four
+// floats a lane (C[m][n] in lane n + 16 (m / 4), element m % 4)
+template <int FA>
+__global__ void k_mfma_scaled(const uint32_t* a, const uint32_t* b, const uint32_t* sa, const uint32_t* sb, float* d,
+                              int tiles) {
+  const int t = blockIdx.x, l = threadIdx.x;
+  if (t >= tiles || l >= 64) return;
+  const size_t base = (size_t)t * 64 + l;
+  i32x8 av, bv;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    av[i] = (int)a[base * 8 + i];
+    bv[i] = (int)b[base * 8 + i];
+  }
+  f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+  c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, FA, 0, 0, (int)sa[base], 0, (int)sb[base]);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) d[base * 4 + v] = c[v];
+}
+
 // decode byte i as e4m3 (the fp8 convert the GEMVs use) and as two e2m1 (the fp4 convert)
 __global__ void k_decode(const uint8_t* codes, float* fp8, float* fp4, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -2876,13 +2966,17 @@ int static_workspace(int dev, void** ws) {
 constexpr double kDeadlineDefault = 2.0;  // seconds
 constexpr int kMfmaGateDefault = 1;       // gate_up and down on MFMA at every row count
 constexpr int kMfmaDownDefault = 1;
+constexpr int kMxScaledDefault = 1 << 30;  // the MXFP4 GEMMs convert to bf16 at every row count
 
 // the options of one call (NULL: the defaults; a field left 0 takes its default)
-int options_of(const mkmoe_options* o, double& deadline_s, int& gate, int& down) {
+int options_of(const mkmoe_options* o, double& deadline_s, int& gate, int& down, int& scaled) {
   deadline_s = kDeadlineDefault;
   gate = kMfmaGateDefault;
   down = kMfmaDownDefault;
+  scaled = kMxScaledDefault;
   if (!o) return MKMOE_OK;
+  if (o->mxfp4_scaled_rows < 0) return MKMOE_ERR_ARG;
+  if (o->mxfp4_scaled_rows) scaled = o->mxfp4_scaled_rows;
   if (o->deadline_s != 0.0) {
     if (!(o->deadline_s > 0.0) || o->deadline_s > 3600.0) return MKMOE_ERR_ARG;
     deadline_s = o->deadline_s;
@@ -2945,8 +3039,8 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
   int rc = check_shape(s);
   if (rc) return rc;
   double dl;
-  int mfma_gate, mfma_down;
-  if ((rc = options_of(opts, dl, mfma_gate, mfma_down))) return rc;
+  int mfma_gate, mfma_down, mx_scaled;
+  if ((rc = options_of(opts, dl, mfma_gate, mfma_down, mx_scaled))) return rc;
   if (static_ws) {
     int cur = 0;
     if (hipGetDevice(&cur) != hipSuccess) return MKMOE_ERR_HIP;
@@ -3003,6 +3097,7 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
   p.deadline = (unsigned long long)(dl * 1e8);
   p.mfma_gate = mfma_gate;
   p.mfma_down = mfma_down;
+  p.mx_scaled = rows >= mx_scaled && rows >= mfma_gate && rows >= mfma_down ? 1 : 0;
   for (int i = 0; i < kRegions; ++i) p.off[i] = (uint32_t)L.off[i];
   hipStream_t st = (hipStream_t)stream;
   if (static_ws) {
@@ -3108,6 +3203,20 @@ const char* mkmoe_status_string(int status) {
     case MKMOE_ERR_HIP: return "a HIP runtime call failed";
   }
   return "unknown status";
+}
+
+int mkmoe_device_mfma_scaled(const void* a, const void* b, const void* sa, const void* sb, float* d,
+                             int32_t fmt_a, int32_t tiles, void* stream) {
+  if (!a || !b || !sa || !sb || !d) return MKMOE_ERR_NULL;
+  if (tiles < 1 || (fmt_a != 0 && fmt_a != 4)) return MKMOE_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  const uint32_t *pa = (const uint32_t*)a, *pb = (const uint32_t*)b, *psa = (const uint32_t*)sa,
+                 *psb = (const uint32_t*)sb;
+  if (fmt_a == 4)
+    hipLaunchKernelGGL(k_mfma_scaled<4>, dim3(tiles), dim3(64), 0, st, pa, pb, psa, psb, d, tiles);
+  else
+    hipLaunchKernelGGL(k_mfma_scaled<0>, dim3(tiles), dim3(64), 0, st, pa, pb, psa, psb, d, tiles);
+  return hipGetLastError() == hipSuccess ? MKMOE_OK : MKMOE_ERR_LAUNCH;
 }
 
 int mkmoe_device_decode(const uint8_t* codes, float* fp8, float* fp4, int32_t n, void* stream) {

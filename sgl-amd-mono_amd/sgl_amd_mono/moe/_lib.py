@@ -55,6 +55,7 @@ EXPORTS = (
     "mkmoe_workspace_region",
     "mkmoe_status_string",
     "mkmoe_device_decode",
+    "mkmoe_device_mfma_scaled",
     "mkmoe_host_e4m3_encode",
     "mkmoe_host_sigmoid",
     "mkmoe_host_topk",
@@ -89,7 +90,8 @@ class Options(ctypes.Structure):
         ("deadline_s", ctypes.c_double),
         ("mfma_gate_rows", ctypes.c_int32),
         ("mfma_down_rows", ctypes.c_int32),
-        ("reserved", ctypes.c_int32 * 4),
+        ("mxfp4_scaled_rows", ctypes.c_int32),
+        ("reserved", ctypes.c_int32 * 3),
     ]
 
 
@@ -138,6 +140,7 @@ def lib() -> ctypes.CDLL:
         L.mkmoe_status_string.argtypes = [ctypes.c_int]
         L.mkmoe_status_string.restype = ctypes.c_char_p
         L.mkmoe_device_decode.argtypes = [vp, vp, vp, i32, vp]
+        L.mkmoe_device_mfma_scaled.argtypes = [vp, vp, vp, vp, vp, i32, i32, vp]
         L.mkmoe_host_e4m3_encode.argtypes = [vp, vp, ctypes.c_int64]
         L.mkmoe_host_e4m3_encode.restype = None
         L.mkmoe_host_sigmoid.argtypes = [vp, vp, ctypes.c_int64]

@@ -122,14 +122,17 @@ class MoeWeights:
 # oracle (mfma_rows=(49, 49) selects them at every row count)
 MFMA_GATE_ROWS, MFMA_DOWN_ROWS = 1, 1
 DEADLINE_S = 2.0
+# MXFP4 shapes: launches with at least this many rows run the expert GEMMs on the scaled fp4 x
+# fp8 MFMA (0: the library's default, never)
+MXFP4_SCALED_ROWS = 0
 
 
 class MoeRunner:
     """The MoE block of one preset on one GPU: a workspace and the launch.
 
-    ``deadline_s`` and ``mfma_rows`` (gate_up rows, down rows) are this runner's
-    per-call options (``mkmoe_options``); ``moe(..., mfma_rows=...)`` overrides
-    the GEMM choice for one call. Nothing is process-global."""
+    ``deadline_s``, ``mfma_rows`` (gate_up rows, down rows) and ``mxfp4_scaled_rows``
+    are this runner's per-call options (``mkmoe_options``); ``moe(...)`` overrides
+    the GEMM choices for one call. Nothing is process-global."""
 
     def __init__(
         self,
@@ -138,10 +141,12 @@ class MoeRunner:
         max_rows: int | None = None,
         deadline_s: float = DEADLINE_S,
         mfma_rows: tuple[int, int] = (MFMA_GATE_ROWS, MFMA_DOWN_ROWS),
+        mxfp4_scaled_rows: int = MXFP4_SCALED_ROWS,
     ):
         self.preset = PRESETS[preset] if isinstance(preset, str) else preset
         self.deadline_s = float(deadline_s)
         self.mfma_rows = (int(mfma_rows[0]), int(mfma_rows[1]))
+        self.mxfp4_scaled_rows = int(mxfp4_scaled_rows)
         dev = torch.device("cuda") if device is None else torch.device(device)
         if dev.type != "cuda":
             raise RuntimeError(f"mkmoe: {dev} is not a GPU")
@@ -180,6 +185,7 @@ class MoeRunner:
         topk_w: torch.Tensor | None = None,
         staged: bool = False,
         mfma_rows: tuple[int, int] | None = None,
+        mxfp4_scaled_rows: int | None = None,
     ) -> torch.Tensor:
         """This rank's MoE partial of bf16 rows ``x`` [R, H] (before the all-reduce) -> bf16 [R, H]."""
         p = self.preset
@@ -206,7 +212,10 @@ class MoeRunner:
         fn = self.lib.mkmoe_forward_staged if staged else self.lib.mkmoe_forward
         ws_ = w.c_struct()
         gate, down = self.mfma_rows if mfma_rows is None else mfma_rows
-        opts = _lib.Options(deadline_s=self.deadline_s, mfma_gate_rows=int(gate), mfma_down_rows=int(down))
+        sc = self.mxfp4_scaled_rows if mxfp4_scaled_rows is None else int(mxfp4_scaled_rows)
+        opts = _lib.Options(
+            deadline_s=self.deadline_s, mfma_gate_rows=int(gate), mfma_down_rows=int(down), mxfp4_scaled_rows=sc
+        )
         rc = fn(
             ctypes.byref(self.shape),
             ctypes.byref(ws_),
