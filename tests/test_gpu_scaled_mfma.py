@@ -24,7 +24,7 @@ import torch
 pytestmark = pytest.mark.gpu
 
 TILES = 256
-# measured on gfx950 (max over the tiles below), with margin; see DESIGN.md
+# measured on gfx950 (max over the tiles below), with margin
 BOUND_FP4_MX = 400.0  # measured 147 (mean 3.6)
 BOUND_FP8 = 8000.0  # measured 2860 (mean 304) here, up to 4410 on other draws
 

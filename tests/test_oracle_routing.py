@@ -189,7 +189,7 @@ def test_grouped_topk_nan_scores(seed):
     assert ids[0].tolist() == bid.tolist()
     assert np.array_equal(wts[0].view(np.uint32), bw.view(np.uint32))
     assert not set(ids[0].tolist()) & set(nan_at.tolist())  # finite choices always win here
-    # the kernel's host build, at the BASELINE shape (NaN spread over several groups)
+    # the kernel's host build, at 256 experts in 8 groups (NaN spread over several groups)
     p = PRESETS["dsv3_tp4_fp8"]
     sc = rt.sigmoid_exact(rng.standard_normal((1, p.experts)).astype(np.float32))[0]
     sc[rng.choice(p.experts, size=40, replace=False)] = np.nan
