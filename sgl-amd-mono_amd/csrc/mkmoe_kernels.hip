@@ -224,6 +224,14 @@ __device__ __forceinline__ void lds_dma16(i32x4 rs, void* lds, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen nt lds" ::"v"(voff), "s"(m0), "s"(rs)
                : "memory", "m0");
 }
+// the same with the default cache policy, for data that neighbouring waves read again from the
+// same 128-byte lines (a streaming load lets the L2 drop the line before they come)
+__device__ __forceinline__ void lds_dma16_cached(i32x4 rs, void* lds, uint32_t voff) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(uint8_t*)lds);
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(voff), "s"(m0), "s"(rs)
+               : "memory", "m0");
+}
 
 // the workspace as a buffer resource: hand-off data goes through sc1 (device-coherent) accesses
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(const Params& p) {
@@ -1508,11 +1516,11 @@ struct GuTile {
       // the scales of the wave's K steps (4 SPW bytes a row, from byte 4 s0) in one LDS-direct
       // load: lane 2 r + h takes 16 bytes of row r from byte 16 h of its slice, to sslot + 32 r +
       // 16 h (the 32 - 4 SPW bytes past the slice are never read; past the resource the load
-      // returns zeros)
+      // returns zeros). The 8 waves' slices of a row share its lines: cached loads
       static_assert(4 * SPW <= 32, "a row's slice in two 16-byte pieces");
       const int r = lane >> 1, h = lane & 1;
       const bool live = (r & 15) < nc;
-      lds_dma16(sr, sslot, live ? (uint32_t)wrow(W, j0, r) * (C::H / 32) + s0 * 4 + h * 16 : kNoLoad);
+      lds_dma16_cached(sr, sslot, live ? (uint32_t)wrow(W, j0, r) * (C::H / 32) + s0 * 4 + h * 16 : kNoLoad);
     }
   }
   __device__ __forceinline__ void fetch(const uint8_t* slot, const uint8_t* sslot, int lane) {
