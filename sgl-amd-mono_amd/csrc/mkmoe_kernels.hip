@@ -1742,6 +1742,7 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
 template <int WFMT, int KD, int NA_ = 1>
 struct DownTile {
   static constexpr int NA = NA_;  // 16-row A operands a unit
+  static constexpr bool kIsTile = true;
   static constexpr int KS = KD / 128;
   static constexpr int NW = WFMT == kFp8 ? 2 : 1;  // 16-byte words of a lane's step
   static constexpr int BYTES = NA * NW * 16 * 64 * KS;  // registers' bytes a unit
@@ -1821,6 +1822,17 @@ struct DownTile {
         }
       }
     }
+  }
+  // the weight registers as values the compiler cannot see through: a loop over pick groups
+  // converts them again each time instead of keeping the converted operands (twice the
+  // registers) from the first
+  __device__ __forceinline__ void opaque() {
+#pragma unroll
+    for (int q = 0; q < NA; ++q)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int w = 0; w < NW; ++w) asm volatile("" : "+v"(a[q][ks][w]));
   }
   __device__ __forceinline__ void take_scales(const DownTile& o) {
 #pragma unroll
@@ -2049,6 +2061,7 @@ constexpr int kPickBlock = 4;  // picks a down unit computes per pass over its c
 
 template <int FMT, int KD>
 struct DownRows {
+  static constexpr bool kIsTile = false;
   static constexpr int CE = FMT == kFp4 ? 32 : 16;  // elements a chunk
   static constexpr int CPR = KD / CE;
   static constexpr int CPL = CPR / kDownLanes;
@@ -2271,24 +2284,24 @@ struct SharedDownSmem {
   float s[kRowsMax * (C::S / 128)];
 };
 
-// the shared down's units a wave requests at once: up to 8 KB of codes
+// the shared down's units a wave requests at once: one (MFMA: a 16-row block for every row of
+// the step; a 28-row tile has two), up to two 8-row blocks (VALU)
 template <class Rows>
 struct Batched : Rows {
-  static constexpr int kBatch = Rows::kBatch < 2 ? Rows::kBatch : 2;
+  static constexpr int kBatch = Rows::kBatch < 2 ? Rows::kBatch : (Rows::kIsTile ? 1 : 2);
 };
 template <class C, bool MF>
 using SharedDownBatch =
     DownBatch<Batched<typename std::conditional<MF, DownTile<kFp8, C::S>, DownRows<kFp8, C::S>>::type>>;
 
-// loader of the shared down's units of tile rows [h0, h0 + hn)
+// loader of the shared down's units of tile rows [h0, h0 + hn) (MFMA: unit v is the 16-row
+// block v, for every row of the step; VALU: an 8-row block and kPickBlock rows)
 template <class C, bool MF>
 __device__ __forceinline__ auto shared_down_loader(const Params& p, int h0, int hn) {
   const int lane = threadIdx.x & 63, g = lane / kDownLanes, l = lane % kDownLanes;
   if constexpr (MF) {
-    const int nb = (hn + 15) / 16;
-    return [&p, h0, hn, nb, lane](int v, DownTile<kFp8, C::S>& dt) {
-      const int rb = v % nb;
-      dt.load(p.sw2, p.sw2_s, h0 + rb * 16, min(16, hn - rb * 16), lane);
+    return [&p, h0, hn, lane](int v, DownTile<kFp8, C::S>& dt) {
+      dt.load(p.sw2, p.sw2_s, h0 + v * 16, min(16, hn - v * 16), lane);
     };
   } else {
     return [&p, h0, hn, g, l](int v, DownRows<kFp8, C::S>& wr) {
@@ -2300,12 +2313,16 @@ __device__ __forceinline__ auto shared_down_loader(const Params& p, int h0, int 
 }
 template <class C, bool MF>
 __device__ __forceinline__ int shared_down_units(int R, int hn) {
-  if constexpr (MF) return ((hn + 15) / 16) * ((R + kMfmaPicks - 1) / kMfmaPicks);
+  if constexpr (MF) return (hn + 15) / 16;
   else return kRowBlocks * ((R + kPickBlock - 1) / kPickBlock);
 }
+// the wave that takes the shared down's unit v first: wave 1 unit 0 and so on, wave 0 last (its
+// unit is requested after the hand-off it polls)
+__device__ __forceinline__ int shared_down_vwave() { return ((threadIdx.x >> 6) + kWaves - 1) % kWaves; }
+
 
 // the shared down of tile rows [h0, h0 + hn) into out[t * hn + hl] (bf16); first_ready: the
-// first units are already requested into bt
+// first units of waves 1-7 are already requested into bt (shared_down_first)
 template <class C, bool MF>
 __device__ __forceinline__ void shared_down_tile(const Params& p, SharedDownSmem<C>& sm, uint16_t* out, int h0, int hn,
                                                  SharedDownBatch<C, MF>& bt, bool first_ready) {
@@ -2313,7 +2330,7 @@ __device__ __forceinline__ void shared_down_tile(const Params& p, SharedDownSmem
   const int R = p.rows;
   const int n_units = shared_down_units<C, MF>(R, hn);
   auto load = shared_down_loader<C, MF>(p, h0, hn);
-  if (!first_ready) bt.load(threadIdx.x >> 6, n_units, load);
+  if (!first_ready || (threadIdx.x >> 6) == 0) bt.load(shared_down_vwave(), n_units, load);
   __syncthreads();  // the previous user of the LDS is done
   // (2 chunks a thread at once with MXFP4 routed experts: 4 spill the persistent launch there)
   quant_rows_lds<kFp8, C::S, C::SQS, C::FMT == kFp4 ? 2 : kQuantBatch>(
@@ -2321,17 +2338,19 @@ __device__ __forceinline__ void shared_down_tile(const Params& p, SharedDownSmem
   __syncthreads();
   if constexpr (MF) {
     using DT = Batched<DownTile<kFp8, C::S>>;
-    const int nb = (hn + 15) / 16;
-    down_pipeline<DT>(bt, n_units, load, [&](int v, const DT& dt) {
-      const int rb = v % nb, pt = v / nb;
-      const int t0 = pt * kMfmaPicks, np = min(kMfmaPicks, R - t0);
-      f32x4 acc[1];
-      dt.template mma<C::SQS, (C::S / 128) * 4>(sm.q, (const uint8_t*)sm.s, t0, np, lane, false, acc);
+    down_pipeline<DT>(bt, n_units, load, [&](int v, DT& dt) {
       const int n = lane & 15;
+#pragma unroll 1
+      for (int t0 = 0; t0 < R; t0 += kMfmaPicks) {  // the unit's rows stay in registers
+        const int np = min(kMfmaPicks, R - t0);
+        f32x4 acc[1];
+        dt.opaque();
+        dt.template mma<C::SQS, (C::S / 128) * 4>(sm.q, (const uint8_t*)sm.s, t0, np, lane, false, acc);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int hl = rb * 16 + 4 * (lane >> 4) + k;
-        if (n < np && hl < hn) out[(t0 + n) * hn + hl] = f2bf(acc[0][k]);
+        for (int k = 0; k < 4; ++k) {
+          const int hl = v * 16 + 4 * (lane >> 4) + k;
+          if (n < np && hl < hn) out[(t0 + n) * hn + hl] = f2bf(acc[0][k]);
+        }
       }
     });
   } else {
