@@ -330,6 +330,9 @@ def main() -> int:
     ap.add_argument("--staged", action="store_true", help="time the one-launch-per-stage variant")
     ap.add_argument("--mxfp4-scaled-rows", type=int, default=None,
                     help="MXFP4 launches with at least this many rows on the scaled fp4 x fp8 MFMA")
+    ap.add_argument("--layout", default="row_major", choices=("row_major", "aiter"),
+                    help="the MXFP4 workloads' expert layout: row-major, or SGLang's loaded gfx950 layout "
+                    "(aiter's shuffles; the random weight bytes are read as such)")
     ap.add_argument("--timeline", action="store_true",
                     help="phase timeline of the diagnostic build (build.py --timeline); no JSON line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -371,6 +374,8 @@ def main() -> int:
         layers = [make_layer(preset, g, device, zipf) for _ in range(args.layers)]
         torch.cuda.synchronize()
         kw = {} if args.mxfp4_scaled_rows is None else {"mxfp4_scaled_rows": args.mxfp4_scaled_rows}
+        if preset.routed_fmt == "mxfp4":
+            kw["layout"] = args.layout
         runner = MoeRunner(preset, device, max_rows=max(48, max(rows_list)), **kw)
         if args.staged:
             orig = runner.moe
@@ -445,6 +450,7 @@ def main() -> int:
             "rows": hrows,
             "layers_rotated": args.layers,
             "launch": "staged" if args.staged else "persistent",
+            "layout": args.layout if hpreset.routed_fmt == "mxfp4" else "row_major",
         },
         "roofline": {
             "bound": "hbm",

@@ -38,6 +38,10 @@ extern "C" {
 /* weight formats */
 #define MKMOE_FMT_FP8_B128 1 /* e4m3, fp32 scale per 128 x 128 block */
 #define MKMOE_FMT_MXFP4 2    /* e2m1 (2 a byte, even K low nibble), E8M0 per 32 K */
+/* MXFP4 in SGLang's loaded gfx950 layout, read in place: the tensors the reference's
+ * FFNWeights hold (deepseek_v41/gfx950/runner.py:139-142: aiter's (16, 16) shuffle with the
+ * gate/up interleave, scales in shuffle_scale order; made by check_ffn.py:169-173) */
+#define MKMOE_FMT_MXFP4_AITER 3
 
 /* status codes (negative: an error; the call enqueued nothing) */
 #define MKMOE_OK 0
@@ -89,6 +93,14 @@ typedef struct mkmoe_shape {
  *             w2 [E][H][I],   w2_s fp32 [E][H/128][I/128]
  *   MXFP4:    w13 [E][2I][H/2], w13_s E8M0 [E][2I][H/32],
  *             w2 [E][H][I/2],   w2_s E8M0 [E][H][I/32]
+ *   MXFP4_AITER: the same sizes, permuted. w13's rows in 16-row groups alternating gate
+ *             and up (group 2b: gate rows 16b.., group 2b+1: up rows 16b..); w13 and w2 in
+ *             the (16, 16) shuffle: a 16-row group's bytes per 128-K step (64 bytes a row)
+ *             as 1 KB in which byte 16 (m + 16 j) starts row m's K [32 j, 32 j + 32); the
+ *             scales (w13_s in the interleaved row order) as one [rows][cols] byte matrix
+ *             per tensor, byte (r, c) at ((((r/32 cols/8 + c/8) 4 + c%4) 16 + r%16) 2 +
+ *             (c/4)%2) 2 + (r/16)%2 (common/mx.py:40-44). The GEMMs run on MFMA at every
+ *             row count (mfma_*_rows above 1 are refused)
  *   sgu e4m3 [2S][H] (gate rows, then up rows), sgu_s fp32 [2S/128][H/128],
  *   sw2 e4m3 [H][S], sw2_s fp32 [H/128][S/128]
  * w13 holds each expert's gate rows [0, I) then its up rows [I, 2I). */

@@ -38,7 +38,7 @@
 #include "../../include/mkmoe.h"
 #include "mkmoe_numerics.h"
 
-// Built whole, or in parts (MKMOE_UNIT = 0 .. 3: one compiled shape's kernels and launcher;
+// Built whole, or in parts (MKMOE_UNIT = 0 .. 5: one compiled shape's kernels and launcher;
 // MKMOE_UNIT_HOST: the host code and the C ABI), so that the parts compile in parallel.
 #define MKMOE_UNIT_HOST 9
 
@@ -50,6 +50,7 @@ constexpr int kRowsMax = 48;   // rows a launch takes at most
 constexpr int kTileMax = 32;   // output rows of a down tile, at most
 constexpr int kFp8 = MKMOE_FMT_FP8_B128;
 constexpr int kFp4 = MKMOE_FMT_MXFP4;
+constexpr int kFp4Aiter = MKMOE_FMT_MXFP4_AITER;  // MXFP4 in SGLang's loaded (aiter-shuffled) layout
 constexpr int kAuxDev = 16;  // sc1: device-coherent access
 constexpr int kAuxNt = 2;    // nt: streamed once
 
@@ -97,11 +98,16 @@ __device__ __forceinline__ unsigned long long tl_now() { return 0ull; }
 #define TL_DUMP(p) do {} while (0)
 #endif
 
-template <int H_, int E_, int K_, int NG_, int TG_, int I_, int S_, int FMT_, int P_, bool NORM_>
+template <int H_, int E_, int K_, int NG_, int TG_, int I_, int S_, int FMT_, int P_, bool NORM_, bool SHUF_ = false>
 struct Cfg {
   static constexpr int H = H_, E = E_, K = K_, NG = NG_, TG = TG_, I = I_, S = S_, FMT = FMT_,
                        P = P_;
   static constexpr bool NORM = NORM_;
+  // MXFP4 routed experts in SGLang's loaded gfx950 layout (aiter's (16, 16) shuffle, w13's
+  // 16-row gate/up interleave, scales in shuffle_scale order), read in place; such shapes run
+  // every expert GEMM on MFMA (the VALU GEMVs read row-major rows)
+  static constexpr bool SHUF = SHUF_;
+  static_assert(!SHUF || FMT == kFp4, "the shuffled layout is MXFP4's");
   static constexpr int CH512 = H / 512;  // router / quantize chunks of a row
   static_assert(H % 1024 == 0 && CH512 % P == 0, "router chunks, K split over 8 waves");
   static_assert(I % 128 == 0 && S % 128 == 0, "widths");
@@ -120,6 +126,14 @@ using CfgPlumbing = Cfg<1024, 16, 4, 1, 1, 512, 512, kFp8, 2, false>;
 using CfgTp4Fp8 = Cfg<7168, 256, 8, 8, 4, 512, 512, kFp8, 7, false>;
 using CfgTp4Fp4 = Cfg<7168, 256, 8, 8, 4, 512, 512, kFp4, 7, false>;
 using CfgTp2Fp4Norm = Cfg<7168, 256, 8, 8, 4, 1024, 1024, kFp4, 7, true>;
+using CfgTp4Fp4Aiter = Cfg<7168, 256, 8, 8, 4, 512, 512, kFp4, 7, false, true>;
+using CfgTp2Fp4NormAiter = Cfg<7168, 256, 8, 8, 4, 1024, 1024, kFp4, 7, true, true>;
+
+// the expert GEMMs of a launch on MFMA (else the VALU GEMVs)
+template <class C>
+__device__ __forceinline__ bool gate_on_mfma(int rows, int mfma_gate) { return C::SHUF || rows >= mfma_gate; }
+template <class C>
+__device__ __forceinline__ bool down_on_mfma(int rows, int mfma_down) { return C::SHUF || rows >= mfma_down; }
 
 // ---------------------------------------------------------------- workspace layout
 constexpr int kRegions = 12;
@@ -1472,7 +1486,7 @@ struct GuSmem {
 // split the H / 128 steps evenly), in registers: FP8 units are 8 columns (one A operand: gate
 // rows j0 .. j0 + 7 in A rows 0..7, up rows W + j0 .. in A rows 8..15), MXFP4 units 16 columns
 // (A operands of gate rows j0 .. j0 + 15 and of up rows W + j0 ..): 56 registers a wave either way
-template <class C, int WFMT>
+template <class C, int WFMT, bool SH = false>
 struct GuTile {
   static constexpr int KS = C::H / 128;
   static constexpr int SPW = KS / kWaves;
@@ -1494,6 +1508,10 @@ struct GuTile {
   static constexpr int CPW = RB / 16;
   static constexpr int SLOT = RW * RB;
   static_assert(SLOT == 2 * C::H && SLOT % 1024 == 0 && CPW % (WFMT == kFp8 ? 8 : 4) == 0, "slot layout");
+  static_assert(!SH || (WFMT == kFp4 && SLOT == 2 * SPW * 1024), "shuffled: a 1 KB block a row group and K step");
+  // shuffled scales: the wave's K steps lie in four 256-byte chunks (two steps each) of the
+  // 32-row block, which end within it
+  static_assert(!SH || ((SPW + 2) / 2 <= 4 && ((kWaves - 1) * SPW / 2) * 256 + 1024 <= C::H), "scale chunks");
   __device__ __forceinline__ static int key(int r) { return WFMT == kFp8 ? (r >> 1) : ((r & 15) >> 2); }
   __device__ __forceinline__ static int wrow(int W, int j0, int r) {
     return WFMT == kFp8 ? (r < 8 ? j0 + r : W + j0 + r - 8) : (r >> 4) * W + j0 + (r & 15);
@@ -1506,6 +1524,21 @@ struct GuTile {
                                         int lane, int wave) {
     const int s0 = wave * SPW;
     constexpr int ROWB = WFMT == kFp8 ? C::H : C::H / 2;  // bytes a weight row
+    if constexpr (SH) {
+      // SGLang's layout: the column block's gate tile is row group 2 b and its up tile 2 b + 1
+      // (16 rows each), stored per K step as 1 KB in the MFMA operand's lane order; slot
+      // block q SPW + i takes K step s0 + i of tile q whole (lane l's 16 bytes at 16 l). The
+      // scales of the 32 rows (one shuffle_scale block of H bytes) come in 256-byte chunks of
+      // two K steps: the four from chunk s0 / 2 in one load
+      const int b = j0 / 16;
+#pragma unroll
+      for (int blk = 0; blk < 2 * SPW; ++blk) {
+        const int q = blk / SPW, i = blk % SPW;
+        lds_dma16(wr, slot + blk * 1024, (uint32_t)(2 * b + q) * 16 * ROWB + (s0 + i) * 1024 + lane * 16);
+      }
+      lds_dma16_cached(sr, sslot, (uint32_t)b * C::H + (s0 / 2) * 256 + lane * 16);
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < SLOT / 1024; ++i) {
       const int pos = i * 64 + lane, r = pos / CPW, c = (pos % CPW) ^ key(r);
@@ -1523,8 +1556,24 @@ struct GuTile {
       lds_dma16_cached(sr, sslot, live ? (uint32_t)wrow(W, j0, r) * (C::H / 32) + s0 * 4 + h * 16 : kNoLoad);
     }
   }
-  __device__ __forceinline__ void fetch(const uint8_t* slot, const uint8_t* sslot, int lane) {
+  __device__ __forceinline__ void fetch(const uint8_t* slot, const uint8_t* sslot, int lane, int wave) {
     const int m = lane & 15, j = lane >> 4;
+    if constexpr (SH) {
+      // lane (m, j)'s dword of a scale chunk holds its row's bytes of the chunk's two K steps,
+      // gate and up: byte 2 (step % 2) + q
+      const int s0 = wave * SPW;
+#pragma unroll
+      for (int i = 0; i < SPW; ++i) {
+        const int st = s0 + i;
+        const uint32_t dw = *(const uint32_t*)(sslot + ((st / 2 - s0 / 2) * 64 + lane) * 4);
+#pragma unroll
+        for (int q = 0; q < NA; ++q) {
+          a[q][i][0] = *(const u32x4*)(slot + (q * SPW + i) * 1024 + lane * 16);
+          sa[q][i] = (dw >> (8 * (2 * (st & 1) + q))) & 0xffu;
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int q = 0; q < NA; ++q)
 #pragma unroll
@@ -1589,10 +1638,10 @@ struct GuX {
 
 // this wave's partial C tiles of unit j0 over its K steps: t's weights against x's picks;
 // wsc the FP8 weight's block scales in LDS
-template <class C, int WFMT>
-__device__ __forceinline__ void gu_mma(const GuTile<C, WFMT>& t, const GuX<C, WFMT>& x, const float* wsc, int W, int j0,
-                                       int lane, int wave, bool scaled, f32x4 (&acc)[GuTile<C, WFMT>::NA]) {
-  using T = GuTile<C, WFMT>;
+template <class C, int WFMT, bool SH>
+__device__ __forceinline__ void gu_mma(const GuTile<C, WFMT, SH>& t, const GuX<C, WFMT>& x, const float* wsc, int W,
+                                       int j0, int lane, int wave, bool scaled, f32x4 (&acc)[GuTile<C, WFMT, SH>::NA]) {
+  using T = GuTile<C, WFMT, SH>;
   const int s0 = wave * T::SPW;
 #pragma unroll
   for (int q = 0; q < T::NA; ++q) acc[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1626,10 +1675,10 @@ __device__ __forceinline__ void gu_mma(const GuTile<C, WFMT>& t, const GuX<C, WF
 // LDS slot as soon as the current one is read out of it, so it streams while the current
 // unit's MFMAs run and its partial tiles add in LDS (in wave order). An FP8 weight's block
 // scales go to LDS when the group changes.
-template <class C, int WFMT, bool HALF, class GroupFn, class XFn, class EmitFn>
+template <class C, int WFMT, bool HALF, bool SH, class GroupFn, class XFn, class EmitFn>
 __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h, bool scaled, GroupFn group, XFn xload,
                                         EmitFn emit) {
-  using T = GuTile<C, WFMT>;
+  using T = GuTile<C, WFMT, SH>;
   if (lo_h >= hi_h) return;
   // HALF: the share is half-units [lo_h, hi_h): whole units, but at either end possibly one
   // half; else units [lo_h, hi_h)
@@ -1692,7 +1741,7 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
     if (u == lo) TL(kTlGuFirst);
     if (fresh) __syncthreads();                       // every wave's block scales are in LDS
     const unsigned long long tf0 = tl_now();
-    t.fetch(slot, sslot, lane);
+    t.fetch(slot, sslot, lane, wave);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // read out of the slot
     if (u + 1 < hi) {
       const int tn = (u + 1) / nb;
@@ -1708,7 +1757,7 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
     const unsigned long long tf1 = tl_now();
     TL_ADD(kTlGuFetch, tf1 - tf0);
     f32x4 acc[T::NA];
-    gu_mma<C, WFMT>(t, x, sm.m.wsc, W, j0, lane, wave, scaled, acc);
+    gu_mma<C, WFMT, SH>(t, x, sm.m.wsc, W, j0, lane, wave, scaled, acc);
 #pragma unroll
     for (int q = 0; q < T::NA; ++q) sm.red[q][wave][lane] = acc[q];
     const unsigned long long tf2 = tl_now();
@@ -1739,9 +1788,10 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
 // MFMA down: rows [hb, hb + 16 NA) of a [H][KD] weight (nv of them real), all K steps, in
 // registers; mma() gives C[m][n] = row hb + 16 q + m against pick column n of an LDS mid tile,
 // for each of the NA 16-row blocks q
-template <int WFMT, int KD, int NA_ = 1>
+template <int WFMT, int KD, int NA_ = 1, bool SH = false>
 struct DownTile {
   static constexpr int NA = NA_;  // 16-row A operands a unit
+  static_assert(!SH || WFMT == kFp4, "the shuffled layout is MXFP4's");
   static constexpr bool kIsTile = true;
   static constexpr int KS = KD / 128;
   static constexpr int NW = WFMT == kFp8 ? 2 : 1;  // 16-byte words of a lane's step
@@ -1772,6 +1822,25 @@ struct DownTile {
   // row's byte offset in it
   __device__ __forceinline__ static void issue(__amdgpu_buffer_rsrc_t wr, uint32_t wrow, int nv, uint8_t* slot,
                                                int lane) {
+    if constexpr (SH) {
+      // SGLang's layout: a row's 16-byte piece j of K step ks sits in its 16-row group's 1 KB
+      // block ks, at lane (row % 16) + 16 j (the unit's rows may straddle two groups). Slot
+      // block q KS + ks takes the unit's rows 16 q .. of K step ks in the operand's lane
+      // order, lane l's 16 bytes at 16 l
+      const int m = lane & 15, j = lane >> 4;
+      const uint32_t row0 = wrow / RB;
+#pragma unroll
+      for (int q = 0; q < NA; ++q) {
+        const uint32_t row = row0 + q * 16 + m;
+        const uint32_t base = (row / 16) * 16 * RB + ((row % 16) + 16 * j) * 16;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              wr, (__attribute__((address_space(3))) void*)(slot + (q * KS + ks) * 1024), 16,
+              q * 16 + m < nv ? base + ks * 1024 : kNoLoad, 0, 0, kAuxNt);
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < SLOT / 1024; ++i) {
       const int pos = i * 64 + lane;
@@ -1783,6 +1852,13 @@ struct DownTile {
   }
   __device__ __forceinline__ void fetch(const uint8_t* slot, int lane) {
     const int m = lane & 15, j = lane >> 4;
+    if constexpr (SH) {
+#pragma unroll
+      for (int q = 0; q < NA; ++q)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) a[q][ks][0] = *(const u32x4*)(slot + (q * KS + ks) * 1024 + lane * 16);
+      return;
+    }
 #pragma unroll
     for (int q = 0; q < NA; ++q)
 #pragma unroll
@@ -1807,6 +1883,25 @@ struct DownTile {
         s1[ks] = sp[(r3 / 128) * (KD / 128) + ks];
       }
       split = r0 / 128 == r3 / 128 ? 4 : 128 - (hb + 4 * j) % 128;
+    } else if constexpr (SH) {
+      // shuffle_scale order (a [H][KD / 32] matrix of the expert): row h's bytes of K steps
+      // 2 c and 2 c + 1, column j of each, are bytes 2 (step % 2) + (h / 16) % 2 of the dword
+      // at 32-row block h / 32, chunk c (256 bytes), position 16 j + h % 16
+      const uint8_t* ss = (const uint8_t*)s;
+#pragma unroll
+      for (int q = 0; q < NA; ++q) {
+        const bool ok = q * 16 + m < nv;
+        const int h = hb + (ok ? q * 16 + m : 0);
+        const int a = (h >> 4) & 1;
+#pragma unroll
+        for (int c = 0; c < KS / 2; ++c) {
+          const uint32_t dw = ok ? *(const uint32_t*)(ss + (size_t)(h / 32) * (KD / 32) * 32 + c * 256 +
+                                                      (16 * j + (h & 15)) * 4)
+                                 : 0x7f7f7f7fu;
+          sa[q][2 * c] = (dw >> (8 * a)) & 0xffu;
+          sa[q][2 * c + 1] = (dw >> (8 * (2 + a))) & 0xffu;
+        }
+      }
     } else {
       const uint8_t* ss = (const uint8_t*)s;
 #pragma unroll
@@ -1847,7 +1942,7 @@ struct DownTile {
 
   // w: row 0 of the weight; s: its scales (FP8 [H / 128][KD / 128] fp32, MXFP4 [H][KD / 32])
   __device__ __forceinline__ void load(const uint8_t* w, const void* s, int hb, int nv, int lane) {
-    static_assert(NA == 1, "register units are one 16-row block");
+    static_assert(NA == 1 && !SH, "register units are one row-major 16-row block");
     const int m = lane & 15, j = lane >> 4;
     const bool ok = m < nv;
     const size_t h = (size_t)hb + (ok ? m : 0);
@@ -1960,7 +2055,7 @@ __device__ __forceinline__ void build_union(const Params& p, Union<C>& un, bool 
   static_assert(kRowsMax <= 64, "row bitmaps");
   const int tid = threadIdx.x;
   const int npk = p.rows * C::K;
-  const int tgs = p.rows >= p.mfma_gate ? kMfmaPicks : kTokGroup;  // picks a token group
+  const int tgs = gate_on_mfma<C>(p.rows, p.mfma_gate) ? kMfmaPicks : kTokGroup;  // picks a token group
   const auto rs = ws_rsrc(p);
   __syncthreads();
   // one pick a thread; its expert is kept for the placement below. local: the routing left
@@ -2451,7 +2546,7 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
   {
     const uint32_t qoff = C::FMT == kFp4 ? p.off[3] : p.off[1];
     const uint32_t soff = C::FMT == kFp4 ? p.off[4] : p.off[2];
-    gu_mfma<C, kFp8, HALF>(
+    gu_mfma<C, kFp8, HALF, false>(
         sm, C::S, lo, min(hi, HU * n_sh), false,
         [&](int tg, const uint8_t*& w, const void*& s, int& np) {
           w = p.sgu;
@@ -2469,7 +2564,7 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
     const int slot = un.tg_slot[tg];
     return un.slot_start[slot] + (tg - un.tg_start[slot]) * kMfmaPicks;
   };
-  gu_mfma<C, C::FMT, HALF>(
+  gu_mfma<C, C::FMT, HALF, C::SHUF>(
       sm, C::I, max(lo, HU * n_sh) - HU * n_sh, hi - HU * n_sh, C::FMT == kFp4 && p.mx_scaled,
       [&](int tg, const uint8_t*& w, const void*& s, int& np) {
         const int slot = un.tg_slot[tg];
@@ -2496,7 +2591,7 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
 
 template <class C>
 __device__ __forceinline__ void stage_c(const Params& p, const Union<C>& un, GuSmem<C>& sm, int b, int nwg) {
-  if (p.rows >= p.mfma_gate) gate_up_mfma<C>(p, un, sm, b, nwg);
+  if (gate_on_mfma<C>(p.rows, p.mfma_gate)) gate_up_mfma<C>(p, un, sm, b, nwg);
   else gate_up_valu<C>(p, un, sm.x, b, nwg);
 }
 
@@ -2534,7 +2629,7 @@ __device__ __forceinline__ void batch_slots(const Union<C>& un, int pb0, int pbn
 template <class C>
 using DownRowsOf = DownRows<C::FMT, C::I>;
 template <class C>
-using DownTileOf = DownTile<C::FMT, C::I, C::DNA>;
+using DownTileOf = DownTile<C::FMT, C::I, C::DNA, C::SHUF>;
 // the down stage's batch of units: MFMA (MF) or VALU
 // the MFMA down's unit in flight: its rows in the wave's LDS slot, its scales in nxt
 template <class C>
@@ -2814,7 +2909,7 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   TL(kTlGateUp);
   arrive(p, kCtlC);
   TL(kTlCArrived);
-  if (p.rows >= p.mfma_down) wait_then_d<C, true>(p, un, sm.d, b, nwg);
+  if (down_on_mfma<C>(p.rows, p.mfma_down)) wait_then_d<C, true>(p, un, sm.d, b, nwg);
   else wait_then_d<C, false>(p, un, sm.d, b, nwg);
   TL(kTlEnd);
   TL_DUMP(p);
@@ -2848,7 +2943,7 @@ __global__ __launch_bounds__(kThreads) void k_d(Params p) {
   __shared__ Union<C> un;
   __shared__ DownSmem<C> sm;
   build_union<C>(p, un, false);
-  if (p.rows >= p.mfma_down) {
+  if (down_on_mfma<C>(p.rows, p.mfma_down)) {
     DownBatchOf<C, true> bt;
     stage_d<C, true>(p, un, sm, blockIdx.x, gridDim.x, bt, false);
   } else {
@@ -2942,10 +3037,18 @@ MKMOE_LAUNCHER(2, CfgTp4Fp4)
 #if !defined(MKMOE_UNIT) || MKMOE_UNIT == 3
 MKMOE_LAUNCHER(3, CfgTp2Fp4Norm)
 #endif
+#if !defined(MKMOE_UNIT) || MKMOE_UNIT == 4
+MKMOE_LAUNCHER(4, CfgTp4Fp4Aiter)
+#endif
+#if !defined(MKMOE_UNIT) || MKMOE_UNIT == 5
+MKMOE_LAUNCHER(5, CfgTp2Fp4NormAiter)
+#endif
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg0(const Params&, int, hipStream_t, bool);
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg1(const Params&, int, hipStream_t, bool);
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg2(const Params&, int, hipStream_t, bool);
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg3(const Params&, int, hipStream_t, bool);
+__attribute__((visibility("hidden"))) int mkmoe_launch_cfg4(const Params&, int, hipStream_t, bool);
+__attribute__((visibility("hidden"))) int mkmoe_launch_cfg5(const Params&, int, hipStream_t, bool);
 
 #if !defined(MKMOE_UNIT) || MKMOE_UNIT == MKMOE_UNIT_HOST
 namespace {
@@ -3027,13 +3130,13 @@ int device_info(int dev, DevInfo* out) {
   return MKMOE_OK;
 }
 
-enum CfgId { kNone = -1, kIdPlumbing = 0, kIdTp4Fp8, kIdTp4Fp4, kIdTp2Fp4Norm };
+enum CfgId { kNone = -1, kIdPlumbing = 0, kIdTp4Fp8, kIdTp4Fp4, kIdTp2Fp4Norm, kIdTp4Fp4Aiter, kIdTp2Fp4NormAiter };
 
 template <class C>
 bool shape_is(const mkmoe_shape* s) {
   return s->hidden == C::H && s->experts == C::E && s->topk == C::K && s->n_group == C::NG &&
          s->topk_group == C::TG && s->inter == C::I && s->shared_inter == C::S &&
-         s->routed_fmt == C::FMT && s->router_parts == C::P && (s->use_norm != 0) == C::NORM;
+         s->routed_fmt == (C::SHUF ? kFp4Aiter : C::FMT) && s->router_parts == C::P && (s->use_norm != 0) == C::NORM;
 }
 
 int cfg_id(const mkmoe_shape* s) {
@@ -3042,6 +3145,8 @@ int cfg_id(const mkmoe_shape* s) {
   if (shape_is<CfgTp4Fp8>(s)) return kIdTp4Fp8;
   if (shape_is<CfgTp4Fp4>(s)) return kIdTp4Fp4;
   if (shape_is<CfgTp2Fp4Norm>(s)) return kIdTp2Fp4Norm;
+  if (shape_is<CfgTp4Fp4Aiter>(s)) return kIdTp4Fp4Aiter;
+  if (shape_is<CfgTp2Fp4NormAiter>(s)) return kIdTp2Fp4NormAiter;
   return kNone;
 }
 
@@ -3053,7 +3158,8 @@ int check_shape(const mkmoe_shape* s) {
 }
 
 Layout layout_of(const mkmoe_shape* s) {
-  return make_layout(s->hidden, s->experts, s->topk, s->inter, s->shared_inter, s->routed_fmt,
+  return make_layout(s->hidden, s->experts, s->topk, s->inter, s->shared_inter,
+                     s->routed_fmt == kFp4Aiter ? kFp4 : s->routed_fmt,
                      s->router_parts, s->use_norm, s->max_rows);
 }
 
@@ -3068,6 +3174,8 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
   double dl;
   int mfma_gate, mfma_down, mx_scaled;
   if ((rc = options_of(opts, dl, mfma_gate, mfma_down, mx_scaled))) return rc;
+  // the VALU GEMVs read row-major expert rows: SGLang's shuffled layout runs on MFMA alone
+  if (s->routed_fmt == kFp4Aiter && (mfma_gate > 1 || mfma_down > 1)) return MKMOE_ERR_ARG;
   if (static_ws) {
     int cur = 0;
     if (hipGetDevice(&cur) != hipSuccess) return MKMOE_ERR_HIP;
@@ -3138,6 +3246,8 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
     case kIdTp4Fp8: return mkmoe_launch_cfg1(p, nwg, st, staged);
     case kIdTp4Fp4: return mkmoe_launch_cfg2(p, nwg, st, staged);
     case kIdTp2Fp4Norm: return mkmoe_launch_cfg3(p, nwg, st, staged);
+    case kIdTp4Fp4Aiter: return mkmoe_launch_cfg4(p, nwg, st, staged);
+    case kIdTp2Fp4NormAiter: return mkmoe_launch_cfg5(p, nwg, st, staged);
   }
   return MKMOE_ERR_SHAPE;
 }

@@ -23,6 +23,7 @@ TL_NAMES = (
 ABI_VERSION = 2  # MKMOE_ABI_VERSION of include/mkmoe.h that this binding follows
 FMT_FP8_B128 = 1
 FMT_MXFP4 = 2
+FMT_MXFP4_AITER = 3  # MXFP4 in SGLang's loaded gfx950 layout (aiter's shuffles), read in place
 ERRW_WORDS = 8
 ERRW_CODE, ERRW_STAGE, ERRW_BLOCK, ERRW_COUNT = 0, 1, 2, 3
 REGIONS = {
@@ -164,9 +165,18 @@ def check(rc: int, what: str) -> None:
         raise RuntimeError(f"{what}: {status_string(rc)} ({rc})")
 
 
-def shape_of(preset, max_rows: int | None = None) -> Shape:
-    """The C shape of a ``presets.MoePreset``."""
+LAYOUTS = ("row_major", "aiter")
+
+
+def shape_of(preset, max_rows: int | None = None, layout: str = "row_major") -> Shape:
+    """The C shape of a ``presets.MoePreset`` whose routed experts are in ``layout``: row-major
+    (include/mkmoe.h), or SGLang's loaded gfx950 layout of MXFP4 experts ("aiter")."""
     from .presets import FMT_CODES
+
+    if layout not in LAYOUTS:
+        raise ValueError(f"layout {layout!r}: one of {LAYOUTS}")
+    if layout == "aiter" and preset.routed_fmt != "mxfp4":
+        raise ValueError("the aiter layout is MXFP4's")
 
     return Shape(
         hidden=preset.hidden,
@@ -176,7 +186,7 @@ def shape_of(preset, max_rows: int | None = None) -> Shape:
         topk_group=preset.topk_group,
         inter=preset.inter,
         shared_inter=preset.shared_inter,
-        routed_fmt=FMT_CODES[preset.routed_fmt],
+        routed_fmt=FMT_MXFP4_AITER if layout == "aiter" else FMT_CODES[preset.routed_fmt],
         router_parts=preset.router_parts,
         renorm=1 if preset.renorm else 0,
         use_norm=0 if preset.norm_eps is None else 1,

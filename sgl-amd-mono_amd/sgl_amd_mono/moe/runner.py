@@ -38,6 +38,17 @@ def _bytes_dtype(t: torch.Tensor, allowed: tuple) -> bool:
     return t.dtype in allowed
 
 
+def shape_ok(name: str, t: torch.Tensor, shape: tuple) -> bool:
+    """``t`` has ``shape``, or (MXFP4 scales) the same bytes as SGLang holds them: one
+    [E * rows][cols] matrix a tensor (``deepseek_v41/gfx950/runner.py:169-172``)."""
+    if tuple(t.shape) == shape:
+        return True
+    return name in ("w13_s", "w2_s") and len(shape) == 3 and t.dtype == torch.uint8 and tuple(t.shape) == (
+        shape[0] * shape[1],
+        shape[2],
+    )
+
+
 @dataclass
 class MoeWeights:
     """One layer's MoE tensors on this rank, as the kernel reads them (in place).
@@ -103,7 +114,7 @@ class MoeWeights:
             if t is None:
                 raise RuntimeError(f"MoE {name}: missing, want {shape} {dtypes[0]}")
             dev_ok = t.is_cuda and (device is None or t.device == torch.device(device))
-            if not (tuple(t.shape) == shape and t.dtype in dtypes and t.is_contiguous() and dev_ok):
+            if not (shape_ok(name, t, shape) and t.dtype in dtypes and t.is_contiguous() and dev_ok):
                 raise RuntimeError(
                     f"MoE {name}: {tuple(t.shape)} {t.dtype} {t.device} contiguous={t.is_contiguous()}, "
                     f"want {shape} {dtypes[0]} contiguous on the GPU"
@@ -132,7 +143,9 @@ class MoeRunner:
 
     ``deadline_s``, ``mfma_rows`` (gate_up rows, down rows) and ``mxfp4_scaled_rows``
     are this runner's per-call options (``mkmoe_options``); ``moe(...)`` overrides
-    the GEMM choices for one call. Nothing is process-global."""
+    the GEMM choices for one call. Nothing is process-global. ``layout``: the routed
+    experts' layout, "row_major" or (MXFP4) "aiter", SGLang's loaded gfx950 layout
+    (``check_ffn.py:169-173``), read in place; with it every GEMM runs on MFMA."""
 
     def __init__(
         self,
@@ -142,8 +155,10 @@ class MoeRunner:
         deadline_s: float = DEADLINE_S,
         mfma_rows: tuple[int, int] = (MFMA_GATE_ROWS, MFMA_DOWN_ROWS),
         mxfp4_scaled_rows: int = MXFP4_SCALED_ROWS,
+        layout: str = "row_major",
     ):
         self.preset = PRESETS[preset] if isinstance(preset, str) else preset
+        self.layout = layout
         self.deadline_s = float(deadline_s)
         self.mfma_rows = (int(mfma_rows[0]), int(mfma_rows[1]))
         self.mxfp4_scaled_rows = int(mxfp4_scaled_rows)
@@ -152,7 +167,7 @@ class MoeRunner:
             raise RuntimeError(f"mkmoe: {dev} is not a GPU")
         self.device = torch.device("cuda", torch.cuda.current_device() if dev.index is None else dev.index)
         self.lib = _lib.lib()
-        self.shape = _lib.shape_of(self.preset, max_rows)
+        self.shape = _lib.shape_of(self.preset, max_rows, layout)
         if not self.lib.mkmoe_shape_supported(ctypes.byref(self.shape)):
             raise RuntimeError(f"mkmoe: no compiled specialisation for {self.preset}")
         n = ctypes.c_size_t()

@@ -21,6 +21,7 @@ installed here, so they are pinned only by the fake-model tests
 from __future__ import annotations
 
 import dataclasses
+import logging
 import math
 
 from .. import monospec as _local
@@ -28,6 +29,7 @@ from .presets import PRESETS, MoePreset
 
 MAX_ROWS = 48
 BLOCKS = 256
+_log = logging.getLogger(__name__)
 
 
 def _reg():
@@ -152,14 +154,23 @@ def _weights(layer, preset: MoePreset, copies: dict, i: int):
     )
 
 
+def weight_layout(experts) -> str:
+    """The routed experts' layout as SGLang loaded them: "aiter" when its gfx950 processing
+    shuffled them (the ``is_shuffled`` mark of mxfp4.py, spec.py:195 of the reference, which
+    requires it: spec.py:369-370), else "row_major"."""
+    return "aiter" if getattr(experts.w13_weight, "is_shuffled", False) else "row_major"
+
+
 def _shape_reasons(w, preset: MoePreset, i: int) -> list[str]:
     """Each tensor against the preset's shape and dtype (no device needed)."""
+    from .runner import shape_ok
+
     reasons = []
     for name, (shape, dtypes) in w.expected(preset).items():
         t = getattr(w, name)
         if t is None:
             reasons.append(f"layer {i}: MoE {name} missing")
-        elif tuple(t.shape) != shape or t.dtype not in dtypes or not t.is_contiguous():
+        elif not shape_ok(name, t, shape) or t.dtype not in dtypes or not t.is_contiguous():
             reasons.append(f"layer {i}: MoE {name} is {tuple(t.shape)} {t.dtype}, want {shape} {dtypes[0]} contiguous")
     return reasons
 
@@ -181,8 +192,9 @@ def _config_disable_reasons(cfg, hf_config) -> list[str]:
 
 def _model_disable_reasons(model, hf_config, copies: dict, tp_size: int | None = None, fuse_norm: bool = False) -> list[str]:
     """Why the loaded model cannot run on these kernels (empty: it can): per MoE layer,
-    the routed format, a row-major layout, one shared expert, a compiled shape at this
-    TP size, and every tensor's shape and dtype."""
+    the routed format, its layout (row-major, or for MXFP4 SGLang's shuffled gfx950 layout,
+    read in place; one layout for every layer), one shared expert, a compiled shape at this TP
+    size, and every tensor's shape and dtype."""
     if tp_size is None:
         from sglang.srt.runtime_context import get_parallel  # type: ignore[import-not-found]
 
@@ -191,6 +203,7 @@ def _model_disable_reasons(model, hf_config, copies: dict, tp_size: int | None =
     layers = _moe_layers(model)
     if not layers:
         return ["no routed-MoE layers"]
+    layouts = set()
     for i in layers:
         layer = model.model.layers[i]
         mlp = layer.mlp
@@ -198,8 +211,10 @@ def _model_disable_reasons(model, hf_config, copies: dict, tp_size: int | None =
         if fmt is None:
             reasons.append(f"layer {i}: routed experts neither FP8 128 x 128 nor MXFP4")
             continue
-        if getattr(mlp.experts.w13_weight, "is_shuffled", False):
-            reasons.append(f"layer {i}: MoE weights in a shuffled layout; the kernel reads them row-major")
+        layout = weight_layout(mlp.experts)
+        layouts.add(layout)
+        if layout == "aiter" and fmt != MXFP4:
+            reasons.append(f"layer {i}: {fmt} MoE weights in a shuffled layout; the kernel reads those row-major")
         if getattr(mlp, "shared_experts", None) is None:
             reasons.append(f"layer {i}: needs one shared expert")
             continue
@@ -208,6 +223,8 @@ def _model_disable_reasons(model, hf_config, copies: dict, tp_size: int | None =
             reasons.append(f"layer {i}: no compiled MoE shape for {fmt} experts at TP {tp_size}")
             continue
         reasons += _shape_reasons(_weights(layer, preset, copies, i), preset, i)
+    if len(layouts) > 1:
+        reasons.append("MoE layers in both the row-major and the shuffled layout")
     return reasons
 
 
@@ -243,8 +260,10 @@ def _build(model, hf_config, ctx) -> _Built:
     fuse_norm = bool(getattr(ctx, "fuse_norm", False))
     layers = {}
     preset = None
+    layout = "row_major"
     for i in _moe_layers(model):
         layer = model.model.layers[i]
+        layout = weight_layout(layer.mlp.experts)
         preset = preset_for(hf_config, tp, routed_format(layer.mlp.experts), fuse_norm)
         if preset is None:
             raise RuntimeError(f"layer {i}: no compiled MoE shape (model_disable_reasons refuses this model)")
@@ -252,7 +271,11 @@ def _build(model, hf_config, ctx) -> _Built:
         w.check(preset)
         layers[i] = w
     device = next(iter(layers.values())).gate_w.device
-    runner = MoeRunner(preset, device, max_rows=MAX_ROWS, deadline_s=getattr(ctx, "deadline_s", None) or DEADLINE_S)
+    runner = MoeRunner(
+        preset, device, max_rows=MAX_ROWS, deadline_s=getattr(ctx, "deadline_s", None) or DEADLINE_S, layout=layout
+    )
+    if layout == "aiter":
+        _log.info("mkmoe: MoE experts read in place in SGLang's shuffled gfx950 layout")
     return _Built(runner, layers)
 
 

@@ -202,6 +202,45 @@ def test_parity_mxfp4_scaled(workload, rows):
         assert not e["nan"] and e["rel_l2"] <= REL_L2 and e["cos"] >= 0.9999, e
 
 
+@pytest.mark.parametrize(
+    "workload,rows",
+    [
+        ("cfg3_tp4_mxfp4", 1),
+        ("cfg3_tp4_mxfp4", 8),
+        ("cfg3_tp4_mxfp4", 48),
+        ("cfg4_tp4_mxfp4_zipf", 48),
+        ("cfg5_tp2_mxfp4_norm", 8),
+        ("tp2_mxfp4_norm_zipf", 48),
+    ],
+)
+def test_parity_aiter_layout(workload, rows):
+    """SGLang's loaded gfx950 MXFP4 layout (aiter's shuffles, check_ffn.py:169-173), read in
+    place: the case's experts shuffled (oracle.shuffle, restated from the reference kernel's
+    addressing), scales as SGLang's flat [E rows][cols] views, give the row-major launch's
+    output bit for bit (persistent, staged, and on the scaled MFMA), and so the oracle's
+    parity, checked again here; the VALU GEMVs (row-major rows only) are refused."""
+    import dataclasses
+
+    from oracle import shuffle as sh
+
+    c = _case(workload, rows)
+    print(f"\n{workload} R={rows} (aiter layout)", flush=True)
+    w13, w13_s, w2, w2_s = sh.to_aiter(c.w.w13, c.w.w13_s, c.w.w2, c.w.w2_s)
+    e = c.p["experts"]
+    ws = dataclasses.replace(c.w, w13=w13, w13_s=w13_s.view(-1, w13_s.shape[-1]), w2=w2, w2_s=w2_s.view(-1, w2_s.shape[-1]))
+    assert not torch.equal(w13, c.w.w13) and w13_s.shape[0] == e
+    _check(dataclasses.replace(c, w=ws), rows, _runner(c, layout="aiter"), exact=False)
+    for kw, opts in (({}, {}), ({"staged": True}, {}), ({}, {"mxfp4_scaled_rows": 1})):
+        a = _runner(c, **opts).moe(c.w, c.x, **kw)
+        b = _runner(c, layout="aiter", **opts).moe(ws, c.x, **kw)
+        torch.cuda.synchronize()
+        n = int((a.view(torch.int16) != b.view(torch.int16)).sum())
+        print(f"  {kw or opts or 'default'}: {n} elements differ from the row-major launch", flush=True)
+        assert n == 0
+    with pytest.raises(RuntimeError):
+        _runner(c, (rows + 1, rows + 1), layout="aiter").moe(ws, c.x)
+
+
 @pytest.mark.parametrize("bias_kind", ["zero", "coarse"])
 @pytest.mark.parametrize("workload,rows", [("cfg1_plumbing_fp8", 4), ("cfg2_tp4_fp8", 1), ("cfg2_tp4_fp8", 16), ("cfg2_tp4_fp8", 24)])
 def test_routing_ties(workload, rows, bias_kind):

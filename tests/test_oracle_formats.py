@@ -213,3 +213,24 @@ def test_static_workspace_holds_every_compiled_shape():
         n = ctypes.c_size_t()
         assert _lib.lib().mkmoe_workspace_bytes(ctypes.byref(_lib.shape_of(p, 48)), ctypes.byref(n)) == 0
         assert n.value <= limit, (p.name, n.value, limit)
+
+
+def test_aiter_layout_shapes():
+    """SGLang's loaded MXFP4 layout is a compiled shape of each MXFP4 preset (same workspace
+    as the row-major one); the FP8 presets have none."""
+    from sgl_amd_mono.moe import _lib
+    from sgl_amd_mono.moe.presets import PRESETS
+
+    L = _lib.lib()
+    for p in PRESETS.values():
+        if p.routed_fmt != "mxfp4":
+            with pytest.raises(ValueError):
+                _lib.shape_of(p, 48, "aiter")
+            continue
+        a, r = _lib.shape_of(p, 48, "aiter"), _lib.shape_of(p, 48)
+        assert a.routed_fmt == _lib.FMT_MXFP4_AITER
+        assert L.mkmoe_shape_supported(ctypes.byref(a)) == 1
+        na, nr = ctypes.c_size_t(), ctypes.c_size_t()
+        assert L.mkmoe_workspace_bytes(ctypes.byref(a), ctypes.byref(na)) == 0
+        assert L.mkmoe_workspace_bytes(ctypes.byref(r), ctypes.byref(nr)) == 0
+        assert na.value == nr.value

@@ -49,6 +49,9 @@ def _moe_layer(tp=4, fmt="fp8_b128", e=256, h=7168, inter=2048, shuffled=False, 
     if shuffled:
         experts.w13_weight = experts.w13_weight.clone()
         experts.w13_weight.is_shuffled = True
+        if fmt != "fp8_b128":  # SGLang's views of the shuffled MXFP4 scales: [E * rows][cols]
+            experts.w13_weight_scale = _t((e * 2 * i, h // 32), torch.uint8)
+            experts.w2_weight_scale = _t((e * h, i // 32), torch.uint8)
     sh = None
     if shared:
         sh = SimpleNamespace(
@@ -130,6 +133,23 @@ def test_refusal_reasons():
     r = mspec._model_disable_reasons(_model([layer]), hf, {}, tp_size=4)
     assert any("neither FP8" in x for x in r)
     assert mspec._model_disable_reasons(_model([]), hf, {}, tp_size=4) == ["no routed-MoE layers"]
+
+
+def test_shuffled_mxfp4_is_read_in_place():
+    """SGLang's gfx950 processing shuffles MXFP4 experts (is_shuffled, flat scale views):
+    accepted and read in place in that layout (the reference requires it, spec.py:369-370);
+    shuffled FP8 experts and a mix of layouts are refused."""
+    hf = _hf()
+    for tp, fuse in ((4, False), (2, True)):
+        m = _model([_moe_layer(tp, "mxfp4", shuffled=True), _moe_layer(tp, "mxfp4", shuffled=True)])
+        assert mspec._model_disable_reasons(m, hf, {}, tp_size=tp, fuse_norm=fuse) == []
+        assert mspec.weight_layout(m.model.layers[1].mlp.experts) == "aiter"
+    assert mspec.weight_layout(_moe_layer(4, "mxfp4").mlp.experts) == "row_major"
+    mixed = _model([_moe_layer(4, "mxfp4", shuffled=True), _moe_layer(4, "mxfp4")])
+    assert any("both" in x for x in mspec._model_disable_reasons(mixed, hf, {}, tp_size=4))
+    layer = _moe_layer(4, "mxfp4", shuffled=True)
+    w = mspec._weights(layer, PRESETS["dsv3_tp4_mxfp4"], {}, 1)
+    assert w.w13 is layer.mlp.experts.w13_weight and w.w13_s is layer.mlp.experts.w13_weight_scale
 
 
 def test_weights_read_in_place():
