@@ -114,14 +114,23 @@ def router_logits(x: torch.Tensor, gate_w: torch.Tensor, parts: int) -> np.ndarr
 
 
 def exp_nonpos(y: np.ndarray) -> np.ndarray:
-    """exp(y) for fp64 y <= 0 from IEEE operations only (step 2)."""
+    """exp(y) for fp64 y <= 0 from IEEE operations only (step 2): Cody-Waite reduction, the
+    degree-13 Taylor polynomial in Estrin's order (pairs c_2k + c_2k+1 r, combined by r^2,
+    r^4, r^8), times 2^n."""
     y = np.asarray(y, np.float64)
     n = np.rint(y * INV_LN2)
     r = (y - n * LN2_HI) - n * LN2_LO
-    p = np.full_like(r, 1.0 / math.factorial(EXP_TERMS - 1))
-    for k in range(EXP_TERMS - 2, -1, -1):
-        p = p * r + 1.0 / math.factorial(k)
-    return np.ldexp(p, n.astype(np.int32))
+    c = [1.0 / math.factorial(k) for k in range(EXP_TERMS)]
+    r2 = r * r
+    r4 = r2 * r2
+    r8 = r4 * r4
+    q = [c[2 * k] + c[2 * k + 1] * r for k in range(EXP_TERMS // 2)]
+    s0 = q[0] + q[1] * r2
+    s1 = q[2] + q[3] * r2
+    s2 = q[4] + q[5] * r2
+    u0 = s0 + s1 * r4
+    u1 = s2 + q[6] * r4
+    return np.ldexp(u0 + u1 * r8, n.astype(np.int32))
 
 
 def sigmoid_exact(logit: np.ndarray) -> np.ndarray:

@@ -79,7 +79,9 @@ enum TlSlot {
   kTlGuFetch, kTlGuMma, kTlGuSync, kTlGuEmit, kTlGuSync2,
   // the routed down's parts (wave 0): quantizing the pick batches, the units' MFMAs
   kTlDQuant, kTlDMma,
-  kTlSlots = 24
+  // local routing (thread 0): its wave's part sums all landed, the scores of the step in LDS
+  kTlParts, kTlScores,
+  kTlSlots = 26
 };
 #ifdef MKMOE_TIMELINE
 static __shared__ unsigned long long s_tl[kTlSlots];
@@ -707,12 +709,29 @@ __device__ __forceinline__ float segment_max(float v) {
 // score weighs 0
 // POLL: the part sums are read before the router's hand-off, each reread until it holds a
 // value (kPartUnset marks a part sum not yet written in this launch)
+// the fp32 logits (parts added in order) and sigmoids of a thread's first NJ (row, expert) pairs
+template <int NJ, int MJ, int P>
+__device__ __forceinline__ void sigmoids(const float (&part)[MJ][P], float (&sg)[MJ]) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    float logit = 0.0f;
+#pragma unroll
+    for (int q = 0; q < P; ++q) logit = logit + part[j][q];
+    sg[j] = sigmoid_exact(logit);
+  }
+}
+
 template <class C, bool POLL = false>
 __device__ __forceinline__ void route_scores(const Params& p, RouteSmem<C>& sm, int r0, int n) {
 #pragma clang fp contract(off)
   constexpr int MJ = (kRouteRows * C::E + kThreads - 1) / kThreads;  // (row, expert) a thread
   const auto rs = ws_rsrc(p);
   const int tid = threadIdx.x;
+  // the bias of the thread's experts, requested before the part sums arrive
+  float bias[MJ];
+#pragma unroll
+  for (int j = 0; j < MJ; ++j) bias[j] = p.bias[(tid + j * kThreads) % C::E];
   // every part sum ([rows][P][E]) requested before the first is used
   float part[MJ][C::P];
   auto part_off = [&](int j, int q) {
@@ -748,18 +767,25 @@ __device__ __forceinline__ void route_scores(const Params& p, RouteSmem<C>& sm, 
         for (int q = 0; q < C::P; ++q)
           if (f2u(part[j][q]) == kPartUnset) part[j][q] = u2f(dld32(rs, part_off(j, q)));
     }
+    TL(kTlParts);
   }
+  // the thread's logits and sigmoids first, in one straight block for the live (row, expert)
+  // pairs (the first nj; the rest of a block score unused zeros), so that their fp64 chains
+  // overlap
+  float sgv[MJ];
+  const int nj = (n * C::E + kThreads - 1) / kThreads;
+  if (nj <= 1) sigmoids<1>(part, sgv);
+  else if (nj <= 2) sigmoids<(MJ < 2 ? MJ : 2)>(part, sgv);
+  else if (nj <= 4) sigmoids<(MJ < 4 ? MJ : 4)>(part, sgv);
+  else sigmoids<MJ>(part, sgv);
 #pragma unroll
   for (int j = 0; j < MJ; ++j) {
     const int idx = tid + j * kThreads;
     if (idx < n * C::E) {
       const int i = idx / C::E, e = idx - i * C::E;
-      float logit = 0.0f;
-#pragma unroll
-      for (int q = 0; q < C::P; ++q) logit = logit + part[j][q];
-      const float sg = sigmoid_exact(logit);
+      const float sg = sgv[j];
       const float s = sg != sg ? 0.0f : sg;  // the weight of a NaN score is 0
-      const float cv = sg + p.bias[e];
+      const float cv = sg + bias[j];
       const float ch = cv != cv ? -INFINITY : cv;  // and its choice -inf
       sm.sc[i][e] = s;
       sm.ch[i][e] = ch;
@@ -930,6 +956,7 @@ __device__ __forceinline__ void route_all(const Params& p, RouteSmem<C>& sm, int
     __syncthreads();  // the previous chunk's selections are done with the LDS
     route_scores<C, true>(p, sm, r0, n);
     __syncthreads();
+    TL(kTlScores);
     for (int i = wave; i < n; i += kWaves) {
       int id;
       float w;

@@ -9,7 +9,7 @@
 //     test/kernels/deepseek_v41/check_ffn.py:87-105)
 //   - sigmoid in fp64 from add / multiply / divide / rint / ldexp only, rounded
 //     once to fp32 (an exp by Cody-Waite reduction and a degree-13 Taylor
-//     polynomial; the input clamped to [-60, 60])
+//     polynomial in Estrin's order; the input clamped to [-60, 60])
 #pragma once
 
 #include <stdint.h>
@@ -86,7 +86,9 @@ MKMOE_HD inline float group_scale(float amax) {
   return a / kFp8Max;
 }
 
-// exp(y) for y <= 0 (fp64, IEEE steps only)
+// exp(y) for y <= 0 (fp64, IEEE steps only): n = rint(y / ln 2), r = y - n ln 2 (two-part
+// ln 2), the degree-13 Taylor polynomial of exp(r) in Estrin's order (pairs c_2k + c_2k+1 r,
+// then r^2, r^4 and r^8 combine them: 8 dependent steps instead of Horner's 26), times 2^n
 MKMOE_HD inline double exp_nonpos(double y) {
 #pragma clang fp contract(off)
   const double kInvLn2 = 1.4426950408889634;
@@ -94,21 +96,23 @@ MKMOE_HD inline double exp_nonpos(double y) {
   const double kLn2Lo = 0x1.a39ef35793c76p-33;
   double n = rint(y * kInvLn2);
   double r = (y - n * kLn2Hi) - n * kLn2Lo;
-  double p = 1.0 / 6227020800.0;  // 1/13!
-  p = p * r + 1.0 / 479001600.0;  // 1/12!
-  p = p * r + 1.0 / 39916800.0;
-  p = p * r + 1.0 / 3628800.0;
-  p = p * r + 1.0 / 362880.0;
-  p = p * r + 1.0 / 40320.0;
-  p = p * r + 1.0 / 5040.0;
-  p = p * r + 1.0 / 720.0;
-  p = p * r + 1.0 / 120.0;
-  p = p * r + 1.0 / 24.0;
-  p = p * r + 1.0 / 6.0;
-  p = p * r + 1.0 / 2.0;
-  p = p * r + 1.0;
-  p = p * r + 1.0;
-  return ldexp(p, (int)n);
+  const double r2 = r * r;
+  const double r4 = r2 * r2;
+  const double r8 = r4 * r4;
+  const double q0 = 1.0 + 1.0 * r;
+  const double q1 = 1.0 / 2.0 + (1.0 / 6.0) * r;
+  const double q2 = 1.0 / 24.0 + (1.0 / 120.0) * r;
+  const double q3 = 1.0 / 720.0 + (1.0 / 5040.0) * r;
+  const double q4 = 1.0 / 40320.0 + (1.0 / 362880.0) * r;
+  const double q5 = 1.0 / 3628800.0 + (1.0 / 39916800.0) * r;
+  const double q6 = 1.0 / 479001600.0 + (1.0 / 6227020800.0) * r;
+  const double s0 = q0 + q1 * r2;
+  const double s1 = q2 + q3 * r2;
+  const double s2 = q4 + q5 * r2;
+  const double u0 = s0 + s1 * r4;
+  const double u1 = s2 + q6 * r4;
+  const double pl = u0 + u1 * r8;
+  return ldexp(pl, (int)n);
 }
 
 MKMOE_HD inline float sigmoid_exact(float x) {
