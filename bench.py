@@ -330,6 +330,8 @@ def main() -> int:
     ap.add_argument("--staged", action="store_true", help="time the one-launch-per-stage variant")
     ap.add_argument("--mxfp4-scaled-rows", type=int, default=None,
                     help="MXFP4 launches with at least this many rows on the scaled fp4 x fp8 MFMA")
+    ap.add_argument("--mxfp4-scaled-down-rows", type=int, default=None,
+                    help="MXFP4 launches with at least this many rows run the down GEMM alone on the scaled MFMA")
     ap.add_argument("--layout", default="row_major", choices=("row_major", "aiter"),
                     help="the MXFP4 workloads' expert layout: row-major, or SGLang's loaded gfx950 layout "
                     "(aiter's shuffles; the random weight bytes are read as such)")
@@ -374,6 +376,8 @@ def main() -> int:
         layers = [make_layer(preset, g, device, zipf) for _ in range(args.layers)]
         torch.cuda.synchronize()
         kw = {} if args.mxfp4_scaled_rows is None else {"mxfp4_scaled_rows": args.mxfp4_scaled_rows}
+        if args.mxfp4_scaled_down_rows is not None:
+            kw["mxfp4_scaled_down_rows"] = args.mxfp4_scaled_down_rows
         if preset.routed_fmt == "mxfp4":
             kw["layout"] = args.layout
         runner = MoeRunner(preset, device, max_rows=max(48, max(rows_list)), **kw)

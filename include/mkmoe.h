@@ -148,7 +148,9 @@ typedef struct mkmoe_options {
                               * MFMA) run both expert GEMMs on the scaled fp4 x fp8 MFMA
                               * (v_mfma_scale_f32_16x16x128_f8f6f4), with no conversion of
                               * the codes; 0: the default (never) */
-  int32_t reserved[3];
+  int32_t mxfp4_scaled_down_rows; /* MXFP4 shapes: the down GEMM alone on the scaled MFMA from
+                                   * this many rows (and on MFMA); 0: the default (never) */
+  int32_t reserved[2];
 } mkmoe_options;
 
 /* One MoE block for rows bf16 rows x [rows][H] -> out bf16 [rows][H] (this

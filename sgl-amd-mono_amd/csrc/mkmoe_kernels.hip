@@ -198,7 +198,8 @@ struct Params {
   int tile_rows;
   int mfma_gate;  // launches with at least this many rows run the gate_up GEMMs on MFMA
   int mfma_down;  // ... and the down GEMMs
-  int mx_scaled;  // MXFP4 expert GEMMs on the scaled fp4 x fp8 MFMA (no converts)
+  int mx_scaled;       // the MXFP4 gate_up GEMMs on the scaled fp4 x fp8 MFMA (no converts)
+  int mx_scaled_down;  // and the MXFP4 down GEMMs
   float scale;
   float limit;
   float eps;
@@ -2790,7 +2791,7 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
       for (int jj = j0; jj < j1; jj += kMfmaPicks) {
         const int np = min(kMfmaPicks, j1 - jj);
         f32x4 acc[DT::NA];
-        cur.template mma<C::MQS, SST>(sm.q, sm.s, jj - pb0, np, lane, C::FMT == kFp4 && p.mx_scaled, acc);
+        cur.template mma<C::MQS, SST>(sm.q, sm.s, jj - pb0, np, lane, C::FMT == kFp4 && p.mx_scaled_down, acc);
         const int pk = n < np ? un.picks[jj + n] : 0;
 #pragma unroll
         for (int q = 0; q < DT::NA; ++q)
@@ -3124,16 +3125,19 @@ constexpr double kDeadlineDefault = 2.0;  // seconds
 constexpr int kMfmaGateDefault = 1;       // gate_up and down on MFMA at every row count
 constexpr int kMfmaDownDefault = 1;
 constexpr int kMxScaledDefault = 1 << 30;  // the MXFP4 GEMMs convert to bf16 at every row count
+constexpr int kMxScaledDownDefault = 1 << 30;
 
 // the options of one call (NULL: the defaults; a field left 0 takes its default)
-int options_of(const mkmoe_options* o, double& deadline_s, int& gate, int& down, int& scaled) {
+int options_of(const mkmoe_options* o, double& deadline_s, int& gate, int& down, int& scaled, int& scaled_down) {
   deadline_s = kDeadlineDefault;
   gate = kMfmaGateDefault;
   down = kMfmaDownDefault;
   scaled = kMxScaledDefault;
+  scaled_down = kMxScaledDownDefault;
   if (!o) return MKMOE_OK;
-  if (o->mxfp4_scaled_rows < 0) return MKMOE_ERR_ARG;
+  if (o->mxfp4_scaled_rows < 0 || o->mxfp4_scaled_down_rows < 0) return MKMOE_ERR_ARG;
   if (o->mxfp4_scaled_rows) scaled = o->mxfp4_scaled_rows;
+  if (o->mxfp4_scaled_down_rows) scaled_down = o->mxfp4_scaled_down_rows;
   if (o->deadline_s != 0.0) {
     if (!(o->deadline_s > 0.0) || o->deadline_s > 3600.0) return MKMOE_ERR_ARG;
     deadline_s = o->deadline_s;
@@ -3199,8 +3203,8 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
   int rc = check_shape(s);
   if (rc) return rc;
   double dl;
-  int mfma_gate, mfma_down, mx_scaled;
-  if ((rc = options_of(opts, dl, mfma_gate, mfma_down, mx_scaled))) return rc;
+  int mfma_gate, mfma_down, mx_scaled, mx_scaled_down;
+  if ((rc = options_of(opts, dl, mfma_gate, mfma_down, mx_scaled, mx_scaled_down))) return rc;
   // the VALU GEMVs read row-major expert rows: SGLang's shuffled layout runs on MFMA alone
   if (s->routed_fmt == kFp4Aiter && (mfma_gate > 1 || mfma_down > 1)) return MKMOE_ERR_ARG;
   if (static_ws) {
@@ -3260,6 +3264,7 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
   p.mfma_gate = mfma_gate;
   p.mfma_down = mfma_down;
   p.mx_scaled = rows >= mx_scaled && rows >= mfma_gate && rows >= mfma_down ? 1 : 0;
+  p.mx_scaled_down = (p.mx_scaled || rows >= mx_scaled_down) && rows >= mfma_down ? 1 : 0;
   for (int i = 0; i < kRegions; ++i) p.off[i] = (uint32_t)L.off[i];
   hipStream_t st = (hipStream_t)stream;
   if (static_ws) {

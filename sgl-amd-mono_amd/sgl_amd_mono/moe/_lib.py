@@ -92,7 +92,8 @@ class Options(ctypes.Structure):
         ("mfma_gate_rows", ctypes.c_int32),
         ("mfma_down_rows", ctypes.c_int32),
         ("mxfp4_scaled_rows", ctypes.c_int32),
-        ("reserved", ctypes.c_int32 * 3),
+        ("mxfp4_scaled_down_rows", ctypes.c_int32),
+        ("reserved", ctypes.c_int32 * 2),
     ]
 
 

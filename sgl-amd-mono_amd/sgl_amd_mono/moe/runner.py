@@ -136,6 +136,7 @@ DEADLINE_S = 2.0
 # MXFP4 shapes: launches with at least this many rows run the expert GEMMs on the scaled fp4 x
 # fp8 MFMA (0: the library's default, never)
 MXFP4_SCALED_ROWS = 0
+MXFP4_SCALED_DOWN_ROWS = 0  # the down GEMM alone on the scaled MFMA from this many rows (0: never)
 
 
 class MoeRunner:
@@ -156,12 +157,14 @@ class MoeRunner:
         mfma_rows: tuple[int, int] = (MFMA_GATE_ROWS, MFMA_DOWN_ROWS),
         mxfp4_scaled_rows: int = MXFP4_SCALED_ROWS,
         layout: str = "row_major",
+        mxfp4_scaled_down_rows: int = MXFP4_SCALED_DOWN_ROWS,
     ):
         self.preset = PRESETS[preset] if isinstance(preset, str) else preset
         self.layout = layout
         self.deadline_s = float(deadline_s)
         self.mfma_rows = (int(mfma_rows[0]), int(mfma_rows[1]))
         self.mxfp4_scaled_rows = int(mxfp4_scaled_rows)
+        self.mxfp4_scaled_down_rows = int(mxfp4_scaled_down_rows)
         dev = torch.device("cuda") if device is None else torch.device(device)
         if dev.type != "cuda":
             raise RuntimeError(f"mkmoe: {dev} is not a GPU")
@@ -229,7 +232,8 @@ class MoeRunner:
         gate, down = self.mfma_rows if mfma_rows is None else mfma_rows
         sc = self.mxfp4_scaled_rows if mxfp4_scaled_rows is None else int(mxfp4_scaled_rows)
         opts = _lib.Options(
-            deadline_s=self.deadline_s, mfma_gate_rows=int(gate), mfma_down_rows=int(down), mxfp4_scaled_rows=sc
+            deadline_s=self.deadline_s, mfma_gate_rows=int(gate), mfma_down_rows=int(down), mxfp4_scaled_rows=sc,
+            mxfp4_scaled_down_rows=self.mxfp4_scaled_down_rows,
         )
         rc = fn(
             ctypes.byref(self.shape),

@@ -176,19 +176,21 @@ def test_parity_mfma_forced(workload, rows):
         ("tp2_mxfp4_norm_zipf", 48),
     ],
 )
-def test_parity_mxfp4_scaled(workload, rows):
-    """Both MXFP4 expert GEMMs on the scaled fp4 x fp8 MFMA (no converts), an opt-in option.
+@pytest.mark.parametrize("mode", ["both", "down"])
+def test_parity_mxfp4_scaled(workload, rows, mode):
+    """Both MXFP4 expert GEMMs (or the down GEMM alone) on the scaled fp4 x fp8 MFMA (no
+    converts), opt-in options.
 
     Its internal sum keeps fewer bits than fp32 (test_gpu_scaled_mfma.py bounds it), so it is
     held to the reference's own bounds (cosine 0.9999 and relative error 0.015 of the golden,
     ffn.moe at spec.py:305-309, and the north_star's relative L2 1e-2), with routing bit for
-    bit; the elements beyond max-abs 2e-2 are reported (measured: 15 to 218 of 57344 to
-    688128), which is why the default launch converts the codes to bf16 instead."""
+    bit; the elements beyond max-abs 2e-2 are reported (measured, both: 1 to 218 of 7168 to
+    344064; down alone: 0 to 34), which is why the default launch converts the codes to bf16."""
     from gpu_case import errors
 
     c = _case(workload, rows)
-    print(f"\n{workload} R={rows} (scaled fp4 x fp8 MFMA)", flush=True)
-    run = _runner(c, mxfp4_scaled_rows=1)
+    print(f"\n{workload} R={rows} (scaled fp4 x fp8 MFMA: {mode})", flush=True)
+    run = _runner(c, **({"mxfp4_scaled_rows": 1} if mode == "both" else {"mxfp4_scaled_down_rows": 1}))
     ids = torch.zeros(rows, c.p["topk"], dtype=torch.int32, device="cuda")
     wts = torch.zeros(rows, c.p["topk"], dtype=torch.float32, device="cuda")
     out = run.moe(c.w, c.x, topk_ids=ids, topk_w=wts)
