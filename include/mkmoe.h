@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MKMOE_ABI_VERSION 2
+#define MKMOE_ABI_VERSION 3
 
 /* weight formats */
 #define MKMOE_FMT_FP8_B128 1 /* e4m3, fp32 scale per 128 x 128 block */
@@ -42,6 +42,11 @@ extern "C" {
  * FFNWeights hold (deepseek_v41/gfx950/runner.py:139-142: aiter's (16, 16) shuffle with the
  * gate/up interleave, scales in shuffle_scale order; made by check_ffn.py:169-173) */
 #define MKMOE_FMT_MXFP4_AITER 3
+
+/* router scores (mkmoe_shape.scoring) */
+#define MKMOE_SCORE_SIGMOID 0       /* DeepSeek-V3: sigmoid(logit) */
+#define MKMOE_SCORE_SQRT_SOFTPLUS 1 /* V4.1: sqrt(softplus(logit)) (check_ffn.py:201-206,
+                                     * deepseek_v41/gfx950/stages/moe.py:304-316) */
 
 /* status codes (negative: an error; the call enqueued nothing) */
 #define MKMOE_OK 0
@@ -83,7 +88,7 @@ typedef struct mkmoe_shape {
   float routed_scale;
   float swiglu_limit;
   float norm_eps;
-  float reserved;
+  int32_t scoring;       /* MKMOE_SCORE_* (0: sigmoid; the bytes ABI 2 left reserved) */
 } mkmoe_shape;
 
 /* Device pointers, read in place. Layouts (E experts, H hidden, I inter,
@@ -230,6 +235,7 @@ int mkmoe_device_mfma_scaled(const void* a, const void* b, const void* sa, const
 /* Host builds of the kernels' exact arithmetic (no device needed): */
 void mkmoe_host_e4m3_encode(const float* x, uint8_t* out, int64_t n);
 void mkmoe_host_sigmoid(const float* x, float* out, int64_t n);
+void mkmoe_host_sqrt_softplus(const float* x, float* out, int64_t n);
 /* grouped top-k of one row of fp32 scores [E] with fp32 bias */
 void mkmoe_host_topk(const mkmoe_shape* shape, const float* scores, const float* bias,
                      int32_t* ids, float* weights);

@@ -113,16 +113,27 @@ def code_ceil(v: torch.Tensor) -> torch.Tensor:
     return ((bits >> 23) & 0xFF) + ((bits & 0x7FFFFF) != 0).int()
 
 
-def mxfp8_quant(x: torch.Tensor):
-    """Per-32 MXFP8 with the "aiter" rule (check_ffn.py:93-105): -> (e4m3 codes, E8M0 codes).
+MX_RULES = ("aiter", "vllm")
 
-    The group amax is floored at 1e-10 and multiplied by fp32(1 / 448); the
-    code is clamped to [1, 254]; values are scaled by 2 ** (127 - code)
-    (exact), clamped to +-448 and rounded to nearest even.
+
+def mxfp8_quant(x: torch.Tensor, rule: str = "aiter"):
+    """Per-32 MXFP8 (check_ffn.py:93-105): -> (e4m3 codes, E8M0 codes).
+
+    "aiter" (the routed experts' activations): the group amax is floored at 1e-10
+    and multiplied by fp32(1 / 448), the code clamped to [1, 254]. "vllm" (the
+    V4.1 shared expert's): the amax is floored at the smallest normal fp32 and
+    divided by 448, the code clamped to [0, 254]. Either way the values are
+    scaled by 2 ** (127 - code) (exact), clamped to +-448 and rounded to nearest
+    even.
     """
+    if rule not in MX_RULES:
+        raise ValueError(rule)
     g = x.float().reshape(*x.shape[:-1], -1, 32)
     amax = g.abs().amax(-1, keepdim=True)
-    code = code_ceil(amax.clamp_min(AMAX_FLOOR) * torch.tensor(1.0 / FP8_MAX)).clamp(1, 254)
+    if rule == "aiter":
+        code = code_ceil(amax.clamp_min(AMAX_FLOOR) * torch.tensor(1.0 / FP8_MAX)).clamp(1, 254)
+    else:
+        code = code_ceil(amax.clamp_min(torch.finfo(torch.float32).tiny) / FP8_MAX).clamp(0, 254)
     inv = torch.exp2(127.0 - code.float())
     q = e4m3_codes_from_f32(g * inv)
     return q.reshape(x.shape), code.squeeze(-1).to(torch.uint8)
@@ -133,8 +144,8 @@ def mxfp8_dequant(q: torch.Tensor, code: torch.Tensor) -> torch.Tensor:
     return (g * torch.exp2(code.float() - 127.0)[..., None]).reshape(q.shape)
 
 
-def mxfp8_qdq(x: torch.Tensor) -> torch.Tensor:
-    return mxfp8_dequant(*mxfp8_quant(x))
+def mxfp8_qdq(x: torch.Tensor, rule: str = "aiter") -> torch.Tensor:
+    return mxfp8_dequant(*mxfp8_quant(x, rule))
 
 
 def group_fp8_quant(x: torch.Tensor, group: int = 128):

@@ -21,11 +21,13 @@ the kernel bit for bit, so every step below is a fixed sequence of IEEE fp32
    d = 32, 16, 8, 4, 2, 1); the logit is 0 + S_0 + S_1 + ... in part order.
    A bf16 x bf16 product is exact in fp32, so an FMA would give the same sum;
    the kernel still uses separate multiply and add.
-2. Scores (``sigmoid_exact``): sigmoid in fp64 from IEEE operations only
-   (Cody-Waite reduction by ln 2, a degree-13 Taylor polynomial, an exact
-   power-of-two scaling), rounded once to fp32; the input is clamped to
-   [-60, 60] first. The same steps run on the GPU with FP contraction off, so
-   the fp32 score is identical.
+2. Scores (``score_exact``): DeepSeek-V3's sigmoid (``sigmoid_exact``) in fp64
+   from IEEE operations only (Cody-Waite reduction by ln 2, a degree-13 Taylor
+   polynomial in Estrin's order, an exact power-of-two scaling), rounded once
+   to fp32, the input clamped to [-60, 60] first; or V4.1's sqrt(softplus)
+   (``sqrt_softplus_exact``): softplus in fp64 (the same exp, and log1p by an
+   atanh series) rounded to fp32, then the fp32 square root. The same steps
+   run on the GPU with FP contraction off, so the fp32 score is identical.
 3. Selection (``grouped_topk``): DeepSeek-V3's ``noaux_tc`` grouped top-k.
    choice = score + bias (fp32), and a NaN choice is -inf (the reference's
    ``max(sc + bias, -inf)``, ``stages/moe.py:346-347``); a NaN score weighs 0
@@ -47,8 +49,10 @@ the kernel bit for bit, so every step below is a fixed sequence of IEEE fp32
 Parity pins (tests/test_oracle_routing.py): the fixed-order logits against an
 fp64 matmul (within fp32 rounding) and against an independent scalar
 restatement on small shapes; the fp64 sigmoid against ``math.exp`` within 1
-fp64 ulp of the rounded fp32; the grouped top-k against brute-force
-enumeration of every group subset and expert subset at E = 16.
+fp64 ulp of the rounded fp32; sqrt(softplus) against ``math.log1p`` /
+``math.exp`` within its two fp32 roundings, and its closed forms (x past 20,
+x = 0, large negative x); the grouped and the global top-k against
+brute-force enumeration of every group subset and expert subset at E = 16.
 """
 
 from __future__ import annotations
@@ -133,6 +137,55 @@ def exp_nonpos(y: np.ndarray) -> np.ndarray:
     return np.ldexp(u0 + u1 * r8, n.astype(np.int32))
 
 
+SQRT2_M1 = 0.41421356237309503  # sqrt(2) - 1
+LN2 = 0.6931471805599453
+LOG1P_TERMS = 12  # atanh series terms z^(2k+1) / (2k+1), k = 0 .. 11: |z| <= 0.172 leaves < 1e-19
+SOFTPLUS_LINEAR = 20.0  # softplus(x) = x past this (torch's threshold)
+SOFTPLUS_FLOOR = -200.0
+
+
+def log1p_01(t: np.ndarray) -> np.ndarray:
+    """log(1 + t) for fp64 t in [0, 1] from IEEE operations only: t past sqrt(2) - 1 is
+    reduced to s = (t - 1) / 2 (log(1 + t) = ln 2 + log(1 + s)), then 2 atanh(s / (2 + s)) by
+    its series in Horner's order."""
+    t = np.asarray(t, np.float64)
+    big = t > SQRT2_M1
+    s = np.where(big, (t - 1.0) * 0.5, t)
+    z = s / (2.0 + s)
+    z2 = z * z
+    p = np.full_like(z, 1.0 / (2 * LOG1P_TERMS - 1))
+    for k in range(LOG1P_TERMS - 2, -1, -1):
+        p = p * z2 + 1.0 / (2 * k + 1)
+    lg = 2.0 * (z * p)
+    return np.where(big, LN2 + lg, lg)
+
+
+def sqrt_softplus_exact(logit: np.ndarray) -> np.ndarray:
+    """The V4.1 score sqrt(softplus(logit)) of fp32 logits (the golden's ``F.softplus(logits).sqrt()``,
+    check_ffn.py:203; the reference kernel's ``_score``, stages/moe.py:304-316): softplus in
+    fp64 from IEEE operations only, max(x, 0) + log1p(exp(-|x|)) (x itself past 20, the input
+    floored at -200), rounded to fp32; then its correctly rounded fp32 square root."""
+    x32 = np.asarray(logit, np.float32)
+    xd = np.maximum(x32.astype(np.float64), SOFTPLUS_FLOOR)
+    with np.errstate(invalid="ignore"):
+        t = exp_nonpos(-np.abs(xd))
+        sp = np.where(xd > SOFTPLUS_LINEAR, xd, np.maximum(xd, 0.0) + log1p_01(t))
+        sp = np.where(np.isnan(x32), np.nan, sp)
+    return np.sqrt(sp.astype(np.float32)).astype(np.float32)
+
+
+SCORERS = ("sigmoid", "sqrt_softplus")
+
+
+def score_exact(logit: np.ndarray, scoring: str = "sigmoid") -> np.ndarray:
+    """The preset's score of fp32 logits: DeepSeek-V3's sigmoid or V4.1's sqrt(softplus)."""
+    if scoring == "sigmoid":
+        return sigmoid_exact(logit)
+    if scoring == "sqrt_softplus":
+        return sqrt_softplus_exact(logit)
+    raise ValueError(scoring)
+
+
 def sigmoid_exact(logit: np.ndarray) -> np.ndarray:
     """fp32 sigmoid of fp32 logits via fp64 (step 2)."""
     xd = np.clip(np.asarray(logit, np.float32).astype(np.float64), -SIG_CLAMP, SIG_CLAMP)
@@ -192,7 +245,7 @@ def grouped_topk(
 def route(x, gate_w, bias, preset) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
     """Logits, then ids and weights, for a preset dict (see ``oracle.moe``)."""
     logit = router_logits(x, gate_w, preset["router_parts"])
-    sc = sigmoid_exact(logit)
+    sc = score_exact(logit, preset.get("scoring", "sigmoid"))
     ids, wts = grouped_topk(
         sc,
         np.asarray(bias, np.float32),

@@ -8,7 +8,7 @@
 The library holds the kernels and the C ABI of ``include/mkmoe.h``. It is built
 in place (not installed) so that the same file runs wherever the tree is copied.
 The source compiles in parts, in parallel: one object per compiled MoE shape
-(``MKMOE_UNIT`` 0 .. 5) and one for the host code (``MKMOE_UNIT`` 9), then one
+(``MKMOE_UNIT`` 0 .. 6) and one for the host code (``MKMOE_UNIT`` 9), then one
 link.
 """
 
@@ -27,7 +27,7 @@ CSRC = ROOT / "csrc"
 OUT = ROOT / "sgl_amd_mono" / "moe" / "libmkmoe.so"
 OUT_TIMELINE = ROOT / "sgl_amd_mono" / "moe" / "libmkmoe_tl.so"
 SOURCE = CSRC / "mkmoe_kernels.hip"
-UNITS = (0, 1, 2, 3, 4, 5, 9)  # the compiled shapes, then the host code
+UNITS = (0, 1, 2, 3, 4, 5, 6, 9)  # the compiled shapes, then the host code
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950",

@@ -38,7 +38,7 @@
 #include "../../include/mkmoe.h"
 #include "mkmoe_numerics.h"
 
-// Built whole, or in parts (MKMOE_UNIT = 0 .. 5: one compiled shape's kernels and launcher;
+// Built whole, or in parts (MKMOE_UNIT = 0 .. 6: one compiled shape's kernels and launcher;
 // MKMOE_UNIT_HOST: the host code and the C ABI), so that the parts compile in parallel.
 #define MKMOE_UNIT_HOST 9
 
@@ -51,6 +51,7 @@ constexpr int kTileMax = 32;   // output rows of a down tile, at most
 constexpr int kFp8 = MKMOE_FMT_FP8_B128;
 constexpr int kFp4 = MKMOE_FMT_MXFP4;
 constexpr int kFp4Aiter = MKMOE_FMT_MXFP4_AITER;  // MXFP4 in SGLang's loaded (aiter-shuffled) layout
+constexpr int kScoreSigmoid = MKMOE_SCORE_SIGMOID, kScoreSqrtSoftplus = MKMOE_SCORE_SQRT_SOFTPLUS;
 constexpr int kAuxDev = 16;  // sc1: device-coherent access
 constexpr int kAuxNt = 2;    // nt: streamed once
 
@@ -100,8 +101,10 @@ __device__ __forceinline__ unsigned long long tl_now() { return 0ull; }
 #define TL_DUMP(p) do {} while (0)
 #endif
 
-template <int H_, int E_, int K_, int NG_, int TG_, int I_, int S_, int FMT_, int P_, bool NORM_, bool SHUF_ = false>
+template <int H_, int E_, int K_, int NG_, int TG_, int I_, int S_, int FMT_, int P_, bool NORM_, bool SHUF_ = false,
+          int SCORE_ = kScoreSigmoid>
 struct Cfg {
+  static constexpr int SCORE = SCORE_;  // the router's score (sigmoid or V4.1's sqrt(softplus))
   static constexpr int H = H_, E = E_, K = K_, NG = NG_, TG = TG_, I = I_, S = S_, FMT = FMT_,
                        P = P_;
   static constexpr bool NORM = NORM_;
@@ -130,6 +133,8 @@ using CfgTp4Fp4 = Cfg<7168, 256, 8, 8, 4, 512, 512, kFp4, 7, false>;
 using CfgTp2Fp4Norm = Cfg<7168, 256, 8, 8, 4, 1024, 1024, kFp4, 7, true>;
 using CfgTp4Fp4Aiter = Cfg<7168, 256, 8, 8, 4, 512, 512, kFp4, 7, false, true>;
 using CfgTp2Fp4NormAiter = Cfg<7168, 256, 8, 8, 4, 1024, 1024, kFp4, 7, true, true>;
+// the plumbing shape routed as V4.1 routes (sqrt(softplus) scores, one group)
+using CfgPlumbingSoftplus = Cfg<1024, 16, 4, 1, 1, 512, 512, kFp8, 2, false, false, kScoreSqrtSoftplus>;
 
 // the expert GEMMs of a launch on MFMA (else the VALU GEMVs)
 template <class C>
@@ -710,8 +715,8 @@ __device__ __forceinline__ float segment_max(float v) {
 // score weighs 0
 // POLL: the part sums are read before the router's hand-off, each reread until it holds a
 // value (kPartUnset marks a part sum not yet written in this launch)
-// the fp32 logits (parts added in order) and sigmoids of a thread's first NJ (row, expert) pairs
-template <int NJ, int MJ, int P>
+// the fp32 logits (parts added in order) and scores of a thread's first NJ (row, expert) pairs
+template <class C, int NJ, int MJ, int P>
 __device__ __forceinline__ void sigmoids(const float (&part)[MJ][P], float (&sg)[MJ]) {
 #pragma clang fp contract(off)
 #pragma unroll
@@ -719,7 +724,7 @@ __device__ __forceinline__ void sigmoids(const float (&part)[MJ][P], float (&sg)
     float logit = 0.0f;
 #pragma unroll
     for (int q = 0; q < P; ++q) logit = logit + part[j][q];
-    sg[j] = sigmoid_exact(logit);
+    sg[j] = C::SCORE == kScoreSqrtSoftplus ? sqrt_softplus_exact(logit) : sigmoid_exact(logit);
   }
 }
 
@@ -775,10 +780,10 @@ __device__ __forceinline__ void route_scores(const Params& p, RouteSmem<C>& sm, 
   // overlap
   float sgv[MJ];
   const int nj = (n * C::E + kThreads - 1) / kThreads;
-  if (nj <= 1) sigmoids<1>(part, sgv);
-  else if (nj <= 2) sigmoids<(MJ < 2 ? MJ : 2)>(part, sgv);
-  else if (nj <= 4) sigmoids<(MJ < 4 ? MJ : 4)>(part, sgv);
-  else sigmoids<MJ>(part, sgv);
+  if (nj <= 1) sigmoids<C, 1>(part, sgv);
+  else if (nj <= 2) sigmoids<C, (MJ < 2 ? MJ : 2)>(part, sgv);
+  else if (nj <= 4) sigmoids<C, (MJ < 4 ? MJ : 4)>(part, sgv);
+  else sigmoids<C, MJ>(part, sgv);
 #pragma unroll
   for (int j = 0; j < MJ; ++j) {
     const int idx = tid + j * kThreads;
@@ -3071,12 +3076,16 @@ MKMOE_LAUNCHER(4, CfgTp4Fp4Aiter)
 #if !defined(MKMOE_UNIT) || MKMOE_UNIT == 5
 MKMOE_LAUNCHER(5, CfgTp2Fp4NormAiter)
 #endif
+#if !defined(MKMOE_UNIT) || MKMOE_UNIT == 6
+MKMOE_LAUNCHER(6, CfgPlumbingSoftplus)
+#endif
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg0(const Params&, int, hipStream_t, bool);
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg1(const Params&, int, hipStream_t, bool);
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg2(const Params&, int, hipStream_t, bool);
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg3(const Params&, int, hipStream_t, bool);
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg4(const Params&, int, hipStream_t, bool);
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg5(const Params&, int, hipStream_t, bool);
+__attribute__((visibility("hidden"))) int mkmoe_launch_cfg6(const Params&, int, hipStream_t, bool);
 
 #if !defined(MKMOE_UNIT) || MKMOE_UNIT == MKMOE_UNIT_HOST
 namespace {
@@ -3161,13 +3170,17 @@ int device_info(int dev, DevInfo* out) {
   return MKMOE_OK;
 }
 
-enum CfgId { kNone = -1, kIdPlumbing = 0, kIdTp4Fp8, kIdTp4Fp4, kIdTp2Fp4Norm, kIdTp4Fp4Aiter, kIdTp2Fp4NormAiter };
+enum CfgId {
+  kNone = -1, kIdPlumbing = 0, kIdTp4Fp8, kIdTp4Fp4, kIdTp2Fp4Norm, kIdTp4Fp4Aiter, kIdTp2Fp4NormAiter,
+  kIdPlumbingSoftplus
+};
 
 template <class C>
 bool shape_is(const mkmoe_shape* s) {
   return s->hidden == C::H && s->experts == C::E && s->topk == C::K && s->n_group == C::NG &&
          s->topk_group == C::TG && s->inter == C::I && s->shared_inter == C::S &&
-         s->routed_fmt == (C::SHUF ? kFp4Aiter : C::FMT) && s->router_parts == C::P && (s->use_norm != 0) == C::NORM;
+         s->routed_fmt == (C::SHUF ? kFp4Aiter : C::FMT) && s->router_parts == C::P && (s->use_norm != 0) == C::NORM &&
+         s->scoring == C::SCORE;
 }
 
 int cfg_id(const mkmoe_shape* s) {
@@ -3178,6 +3191,7 @@ int cfg_id(const mkmoe_shape* s) {
   if (shape_is<CfgTp2Fp4Norm>(s)) return kIdTp2Fp4Norm;
   if (shape_is<CfgTp4Fp4Aiter>(s)) return kIdTp4Fp4Aiter;
   if (shape_is<CfgTp2Fp4NormAiter>(s)) return kIdTp2Fp4NormAiter;
+  if (shape_is<CfgPlumbingSoftplus>(s)) return kIdPlumbingSoftplus;
   return kNone;
 }
 
@@ -3280,6 +3294,7 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
     case kIdTp2Fp4Norm: return mkmoe_launch_cfg3(p, nwg, st, staged);
     case kIdTp4Fp4Aiter: return mkmoe_launch_cfg4(p, nwg, st, staged);
     case kIdTp2Fp4NormAiter: return mkmoe_launch_cfg5(p, nwg, st, staged);
+    case kIdPlumbingSoftplus: return mkmoe_launch_cfg6(p, nwg, st, staged);
   }
   return MKMOE_ERR_SHAPE;
 }
@@ -3402,6 +3417,10 @@ void mkmoe_host_e4m3_encode(const float* x, uint8_t* out, int64_t n) {
 
 void mkmoe_host_sigmoid(const float* x, float* out, int64_t n) {
   for (int64_t i = 0; i < n; ++i) out[i] = sigmoid_exact(x[i]);
+}
+
+void mkmoe_host_sqrt_softplus(const float* x, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = sqrt_softplus_exact(x[i]);
 }
 
 void mkmoe_host_topk(const mkmoe_shape* s, const float* scores, const float* bias, int32_t* ids,

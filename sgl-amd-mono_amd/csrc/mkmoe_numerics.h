@@ -10,6 +10,8 @@
 //   - sigmoid in fp64 from add / multiply / divide / rint / ldexp only, rounded
 //     once to fp32 (an exp by Cody-Waite reduction and a degree-13 Taylor
 //     polynomial in Estrin's order; the input clamped to [-60, 60])
+//   - V4.1's sqrt(softplus): softplus in fp64 from the same exp and an atanh-series
+//     log1p, rounded to fp32, then the correctly rounded fp32 sqrt
 #pragma once
 
 #include <stdint.h>
@@ -123,6 +125,51 @@ MKMOE_HD inline float sigmoid_exact(float x) {
   double den = 1.0 + t;
   double s = d >= 0.0 ? 1.0 / den : t / den;
   return (float)s;
+}
+
+// log(1 + t) for t in [0, 1] (fp64, IEEE steps only): t past sqrt(2) - 1 reduced to
+// s = (t - 1) / 2 (log(1 + t) = ln 2 + log(1 + s)), then 2 atanh(s / (2 + s)) by its series,
+// terms z^(2k+1) / (2k+1) for k = 0 .. 11, in Horner's order
+MKMOE_HD inline double log1p_01(double t) {
+#pragma clang fp contract(off)
+  const double kSqrt2M1 = 0.41421356237309503;
+  const double kLn2 = 0.6931471805599453;
+  const bool big = t > kSqrt2M1;
+  const double s = big ? (t - 1.0) * 0.5 : t;
+  const double z = s / (2.0 + s);
+  const double z2 = z * z;
+  double p = 1.0 / 23.0;
+  p = p * z2 + 1.0 / 21.0;
+  p = p * z2 + 1.0 / 19.0;
+  p = p * z2 + 1.0 / 17.0;
+  p = p * z2 + 1.0 / 15.0;
+  p = p * z2 + 1.0 / 13.0;
+  p = p * z2 + 1.0 / 11.0;
+  p = p * z2 + 1.0 / 9.0;
+  p = p * z2 + 1.0 / 7.0;
+  p = p * z2 + 1.0 / 5.0;
+  p = p * z2 + 1.0 / 3.0;
+  p = p * z2 + 1.0;
+  const double lg = 2.0 * (z * p);
+  return big ? kLn2 + lg : lg;
+}
+
+// V4.1's score sqrt(softplus(x)): softplus in fp64 (x itself past 20, else
+// max(x, 0) + log1p(exp(-|x|)), the input floored at -200), rounded to fp32, then the
+// correctly rounded fp32 square root; NaN stays NaN
+MKMOE_HD inline float sqrt_softplus_exact(float x) {
+#pragma clang fp contract(off)
+  if (x != x) return x;
+  double d = (double)x;
+  d = d < -200.0 ? -200.0 : d;
+  double sp;
+  if (d > 20.0) {
+    sp = d;
+  } else {
+    const double t = exp_nonpos(-fabs(d));
+    sp = (d > 0.0 ? d : 0.0) + log1p_01(t);
+  }
+  return sqrtf((float)sp);
 }
 
 // a > b in the selection order: larger value, or equal value and lower index

@@ -20,10 +20,11 @@ TL_NAMES = (
     "down quant", "down mfma", "parts landed", "scores",
 )  # fmt: skip
 
-ABI_VERSION = 2  # MKMOE_ABI_VERSION of include/mkmoe.h that this binding follows
+ABI_VERSION = 3  # MKMOE_ABI_VERSION of include/mkmoe.h that this binding follows
 FMT_FP8_B128 = 1
 FMT_MXFP4 = 2
 FMT_MXFP4_AITER = 3  # MXFP4 in SGLang's loaded gfx950 layout (aiter's shuffles), read in place
+SCORE_CODES = {"sigmoid": 0, "sqrt_softplus": 1}  # MKMOE_SCORE_*
 ERRW_WORDS = 8
 ERRW_CODE, ERRW_STAGE, ERRW_BLOCK, ERRW_COUNT = 0, 1, 2, 3
 REGIONS = {
@@ -59,6 +60,7 @@ EXPORTS = (
     "mkmoe_device_mfma_scaled",
     "mkmoe_host_e4m3_encode",
     "mkmoe_host_sigmoid",
+    "mkmoe_host_sqrt_softplus",
     "mkmoe_host_topk",
 )
 
@@ -80,7 +82,7 @@ class Shape(ctypes.Structure):
         ("routed_scale", ctypes.c_float),
         ("swiglu_limit", ctypes.c_float),
         ("norm_eps", ctypes.c_float),
-        ("reserved", ctypes.c_float),
+        ("scoring", ctypes.c_int32),
     ]
 
 
@@ -147,6 +149,8 @@ def lib() -> ctypes.CDLL:
         L.mkmoe_host_e4m3_encode.restype = None
         L.mkmoe_host_sigmoid.argtypes = [vp, vp, ctypes.c_int64]
         L.mkmoe_host_sigmoid.restype = None
+        L.mkmoe_host_sqrt_softplus.argtypes = [vp, vp, ctypes.c_int64]
+        L.mkmoe_host_sqrt_softplus.restype = None
         L.mkmoe_host_topk.argtypes = [sp, vp, vp, vp, vp]
         L.mkmoe_host_topk.restype = None
         if L.mkmoe_abi_version() != ABI_VERSION:
@@ -195,5 +199,5 @@ def shape_of(preset, max_rows: int | None = None, layout: str = "row_major") -> 
         routed_scale=preset.routed_scale,
         swiglu_limit=preset.swiglu_limit,
         norm_eps=0.0 if preset.norm_eps is None else preset.norm_eps,
-        reserved=0.0,
+        scoring=SCORE_CODES[preset.scoring],
     )

@@ -17,6 +17,8 @@ Fields:
 - router_parts: contiguous K parts of the router GEMV summed in order (the
   reference's ``PARTS`` at ``stages/router.py:18``)
 - norm_eps: RMSNorm before the block (None: no norm)
+- scoring: the router's score, "sigmoid" (DeepSeek-V3) or "sqrt_softplus" (V4.1:
+  sqrt(softplus(logit)) with the bias for selection, ``check_ffn.py:201-206``)
 - max_rows: the decode rows a launch takes at most (``spec.py:64``: 48)
 """
 
@@ -44,6 +46,7 @@ class MoePreset:
     norm_eps: float | None = None
     max_rows: int = 48
     renorm: bool = True
+    scoring: str = "sigmoid"
 
     def as_dict(self) -> dict:
         return asdict(self)
@@ -99,12 +102,20 @@ PRESETS = {
         inter=1024, shared_inter=1024, routed_fmt="mxfp4", routed_scale=2.5,
         swiglu_limit=10.0, router_parts=7, norm_eps=1e-6,
     ),
+    # the plumbing layer routed as V4.1 routes (sqrt(softplus) scores over one group, the
+    # routed scale 1.5 of check_ffn.py:14)
+    "plumbing_fp8_softplus": MoePreset(
+        "plumbing_fp8_softplus", hidden=1024, experts=16, topk=4, n_group=1, topk_group=1,
+        inter=512, shared_inter=512, routed_fmt="fp8_b128", routed_scale=1.5,
+        swiglu_limit=10.0, router_parts=2, scoring="sqrt_softplus",
+    ),
 }  # fmt: skip
 
 # The workloads the tests and the benchmark run: a preset, the input
 # distribution and the decode row counts
 WORKLOADS = {
     "cfg1_plumbing_fp8": dict(preset="plumbing_fp8", rows=(4,)),
+    "plumbing_fp8_softplus": dict(preset="plumbing_fp8_softplus", rows=(1, 4, 16, 24)),
     "cfg2_tp4_fp8": dict(preset="dsv3_tp4_fp8", rows=(1, 8, 48)),
     "cfg3_tp4_mxfp4": dict(preset="dsv3_tp4_mxfp4", rows=(1, 8, 48)),
     "cfg4_tp4_mxfp4_zipf": dict(preset="dsv3_tp4_mxfp4", rows=(48,), zipf_s=1.2),

@@ -30,7 +30,7 @@ from oracle import gen  # noqa: E402
 from oracle import moe as om  # noqa: E402
 from sgl_amd_mono.moe.presets import workload_dict  # noqa: E402
 
-CASES = [("cfg1_plumbing_fp8", 4), ("cfg2_tp4_fp8", 1), ("cfg3_tp4_mxfp4", 1), ("cfg5_tp2_mxfp4_norm", 1)]
+CASES = [("cfg1_plumbing_fp8", 4), ("cfg2_tp4_fp8", 1), ("cfg3_tp4_mxfp4", 1), ("cfg5_tp2_mxfp4_norm", 1), ("plumbing_fp8_softplus", 4)]
 HERE = Path(__file__).resolve().parent
 
 

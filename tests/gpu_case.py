@@ -73,7 +73,7 @@ def _cpu_side(workload: str, rows: int, seed: int):
         dense = gen.make_dense(p, seed)
         xin = rt.rmsnorm_exact(x, dense["norm"], p["norm_eps"]) if p["norm_eps"] is not None else x
         parts = rt.router_part_sums(xin, dense["gate_w"], p["router_parts"])
-        scores = rt.sigmoid_exact(rt.logits_from_parts(parts))
+        scores = rt.score_exact(rt.logits_from_parts(parts), p.get("scoring", "sigmoid"))
         ids, wts = rt.grouped_topk(
             scores, dense["bias"].numpy(), p["topk"], p["n_group"], p["topk_group"], p["routed_scale"]
         )

@@ -33,6 +33,12 @@ CASES = [
     ("tp4_fp8_zipf", 16),
     ("tp4_fp8_zipf", 48),
     ("tp2_mxfp4_norm_zipf", 48),
+    # V4.1's router scores (sqrt(softplus), one group, check_ffn.py:201-206) on the plumbing
+    # shape: local routing (up to 16 rows) and the routing hand-off (24)
+    ("plumbing_fp8_softplus", 1),
+    ("plumbing_fp8_softplus", 4),
+    ("plumbing_fp8_softplus", 16),
+    ("plumbing_fp8_softplus", 24),
 ]
 _cache = {}
 
@@ -137,6 +143,8 @@ def test_parity(workload, rows):
         ("cfg5_tp2_mxfp4_norm", 1),
         ("cfg5_tp2_mxfp4_norm", 48),
         ("cfg4_tp4_mxfp4_zipf", 48),
+        ("plumbing_fp8_softplus", 4),
+        ("plumbing_fp8_softplus", 24),
     ],
 )
 def test_parity_valu_forced(workload, rows):

@@ -234,3 +234,33 @@ def test_aiter_layout_shapes():
         assert L.mkmoe_workspace_bytes(ctypes.byref(a), ctypes.byref(na)) == 0
         assert L.mkmoe_workspace_bytes(ctypes.byref(r), ctypes.byref(nr)) == 0
         assert na.value == nr.value
+
+
+def test_mxfp8_vllm_rule_closed_form():
+    """The "vllm" rule (check_ffn.py:99-101): the code of each 32-group is the smallest c in
+    [0, 254] with fp32(max(amax, smallest normal) / 448) <= 2^(c - 127) (1 for a subnormal
+    quotient, as code_ceil reads its exponent field); the values scaled by
+    2^(127 - c), clamped to +-448, nearest even; quantize-dequantize is a projection."""
+    from oracle import formats as fm
+
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(64, 256, generator=g) * torch.exp2(torch.randint(-30, 30, (64, 1), generator=g).float())
+    x[0, :32] = 0.0
+    x[1, :32] = 448.0 * 2.0**-3  # amax / 448 a power of two
+    q, code = fm.mxfp8_quant(x, "vllm")
+    amax = x.reshape(64, -1, 32).abs().amax(-1).clamp_min(torch.finfo(torch.float32).tiny)
+    t = (amax / 448.0).double()
+    for c, tv in zip(code.reshape(-1).tolist(), t.reshape(-1).tolist()):
+        if tv < 2.0**-126:  # a subnormal quotient (the floored zero group): code_ceil gives 1
+            assert c == 1
+        else:
+            assert 0 <= c <= 254 and tv <= 2.0 ** (c - 127) and tv > 2.0 ** (c - 128)
+    assert code[1, 0] == 124
+    d = fm.mxfp8_dequant(q, code)
+    # a projection: the dequantized values quantize to themselves (the codes may drop by one
+    # where a group's largest value rounded down to 224, whose quotient by 448 is a power of two)
+    assert torch.equal(fm.mxfp8_qdq(d, "vllm"), d)
+    qa, ca = fm.mxfp8_quant(x, "aiter")
+    assert ca.min() >= 1 and code.min() == 1  # the zero group: vllm code 1 from the floor, too
+    with pytest.raises(ValueError):
+        fm.mxfp8_quant(x, "other")

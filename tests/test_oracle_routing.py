@@ -265,3 +265,80 @@ def test_part_sums_never_take_the_unset_marker():
     xb[r - 1, 9], wb[1, 9] = -128, 0x3F80  # ... and -inf in one sum
     ps = rt.router_part_sums(x, w, parts)
     assert np.isnan(ps).any() and not (ps.view(np.uint32) == 0xFFFFFFFF).any()
+
+
+def test_sqrt_softplus_against_math():
+    """V4.1's score: softplus rounded to fp32, then the fp32 square root (the golden's
+    ``F.softplus(logits).sqrt()``, check_ffn.py:203), against math.log1p / math.exp: equal to
+    those two roundings of the true values but for a rare last-place tie, and never more than
+    one fp32 ulp off."""
+    rng = np.random.default_rng(5)
+    x = np.concatenate([rng.standard_normal(20000) * 6, np.linspace(-120, 40, 4001)]).astype(np.float32)
+    got = rt.sqrt_softplus_exact(x)
+    sp = np.array([v if v > 20 else math.log1p(math.exp(v)) for v in x.astype(np.float64)], np.float64)
+    ref = np.sqrt(sp.astype(np.float32)).astype(np.float32)
+    ulp = np.spacing(ref)
+    assert np.all(np.abs(got.astype(np.float64) - ref.astype(np.float64)) <= ulp)
+    assert np.mean(got == ref) > 0.9999
+
+
+def test_sqrt_softplus_closed_forms():
+    x = np.array([20.5, 33.0, 1e6, 0.0, -0.0, np.nan, -1000.0], np.float32)
+    got = rt.sqrt_softplus_exact(x)
+    assert np.array_equal(got[:3], np.sqrt(x[:3]))  # softplus(x) = x past 20
+    assert got[3] == got[4] == np.sqrt(np.float32(math.log(2.0)))
+    assert np.isnan(got[5]) and got[6] == 0.0
+    # log1p against math.log1p over [0, 1]
+    t = np.linspace(0.0, 1.0, 10001)
+    ref = np.array([math.log1p(v) for v in t])
+    assert np.max(np.abs(rt.log1p_01(t) - ref) / np.maximum(ref, 1e-300)) < 1e-15
+
+
+def test_host_sqrt_softplus_bitexact():
+    from sgl_amd_mono.moe import _lib
+
+    rng = np.random.default_rng(6)
+    x = np.concatenate([rng.standard_normal(100000) * 8, rng.uniform(-250, 60, 20000),
+                        [0.0, -0.0, 20.0, 20.000002, -200.0, -1e-30]]).astype(np.float32)  # fmt: skip
+    out = np.zeros_like(x)
+    _lib.lib().mkmoe_host_sqrt_softplus(x.ctypes.data, out.ctypes.data, x.size)
+    assert np.array_equal(out.view(np.uint32), rt.sqrt_softplus_exact(x).view(np.uint32))
+
+
+def test_global_topk_brute_force():
+    """One group (V4.1): the top-k of choice = score + bias over every expert (a tie to the
+    lower id) in that order, weights score * scale / their sum in that order; against every
+    k-subset at E = 16."""
+    rng = np.random.default_rng(7)
+    e, k, scale = 16, 4, 1.5
+    for trial in range(40):
+        sc = rt.sqrt_softplus_exact(rng.standard_normal((1, e)).astype(np.float32))
+        bias = (rng.integers(-2, 3, e) * 0.25).astype(np.float32) if trial % 2 else np.zeros(e, np.float32)
+        if trial % 4 == 3:
+            sc[0, 5] = sc[0, 9]  # a tie of choices
+            bias[5] = bias[9]
+        ids, wts = rt.grouped_topk(sc, bias, k, 1, 1, scale)
+        ch = (sc[0] + bias).astype(np.float32)
+        best = max(itertools.combinations(range(e), k), key=lambda s: sorted(((ch[i], -i) for i in s), reverse=True))
+        want = sorted(best, key=lambda i: (-ch[i], i))
+        assert ids[0].tolist() == want
+        tot = np.float32(0.0)
+        for i in want:
+            tot = np.float32(tot + sc[0, i])
+        f = np.float32(scale) / max(tot, np.float32(1e-20))
+        assert np.array_equal(wts[0], (sc[0, want] * f).astype(np.float32))
+
+
+def test_route_v41_scoring():
+    """``route`` takes the preset's scorer."""
+    import torch
+
+    rng = np.random.default_rng(8)
+    x = torch.from_numpy(rng.standard_normal((3, 1024)).astype(np.float32)).to(torch.bfloat16)
+    gw = torch.from_numpy((rng.standard_normal((16, 1024)) / 32).astype(np.float32)).to(torch.bfloat16)
+    p = dict(router_parts=2, topk=4, n_group=1, topk_group=1, routed_scale=1.5, scoring="sqrt_softplus")
+    logit, ids, wts = rt.route(x, gw, np.zeros(16, np.float32), p)
+    sc = rt.sqrt_softplus_exact(logit)
+    want, ww = rt.grouped_topk(sc, np.zeros(16, np.float32), 4, 1, 1, 1.5)
+    assert np.array_equal(ids, want) and np.array_equal(wts, ww)
+    assert np.allclose(wts.sum(1), 1.5, rtol=1e-6)
