@@ -18,6 +18,7 @@ HERE = Path(__file__).resolve().parent / "golden"
 sys.path.insert(0, str(HERE))
 
 import make_golden as mg  # noqa: E402
+from sgl_amd_mono.moe.presets import workload_dict  # noqa: E402
 
 
 @pytest.mark.parametrize("workload,rows", mg.CASES)
@@ -40,7 +41,7 @@ def test_fixture_invariants():
         assert all(len(set(r)) == len(r) for r in ids.tolist()), "distinct experts a row"
         assert set(np.unique(ids).tolist()) == set(f["experts"].tolist()), "the experts read are the ones picked"
         w = f["weights_bits"].view(np.float32)
-        scale = 1.0 if workload.startswith("cfg1") else 2.5
+        scale = workload_dict(workload)["routed_scale"]
         np.testing.assert_allclose(w.sum(axis=1), scale, rtol=1e-6)
 
 
