@@ -169,8 +169,9 @@ int mkmoe_forward(const mkmoe_shape* shape, const mkmoe_weights* w, const void* 
                   const mkmoe_options* opts, void* stream);
 
 /* The same results in one launch per stage (norm, router + quantize, route,
- * gate_up (routed and shared), down (shared and routed) + combine); for
- * diagnosis and per-stage profiles. */
+ * gate_up (routed and shared), the intermediates quantized, down (shared and
+ * routed) + combine); for diagnosis and per-stage profiles. Stage codes (error
+ * word MKMOE_ERRW_STAGE): 1 norm, 2 router, 3 route, 4 gate_up, 5 down, 6 quantize. */
 int mkmoe_forward_staged(const mkmoe_shape* shape, const mkmoe_weights* w, const void* x,
                          int32_t rows, void* out, int32_t* topk_ids, float* topk_w, void* ws,
                          size_t ws_bytes, const mkmoe_options* opts, void* stream);
@@ -211,8 +212,11 @@ int mkmoe_clear_errors(const mkmoe_shape* shape, void* ws, size_t ws_bytes, void
  * [rows][topk], 8 shared intermediate bf16 [rows][S], 9 routed intermediate
  * bf16 [rows * topk][I], 10 the router part sums as routing polls them (every
  * word 0xFFFFFFFF between launches), 11 the phase stamps of a diagnostic build
- * compiled with MKMOE_TIMELINE (u64 s_memrealtime ticks [workgroup][24]; other
- * builds leave it untouched). */
+ * compiled with MKMOE_TIMELINE (u64 s_memrealtime ticks [workgroup][28]; other
+ * builds leave it untouched), 12 / 13 the routed intermediates quantized once
+ * (codes [rows * topk][I + 16] in the union's pick order, E8M0 [..][I / 32] or
+ * fp32 [..][I / 128] scales), 14 / 15 the shared intermediate quantized (codes
+ * [rows][S + 16], fp32 scales [rows][S / 128]). */
 int mkmoe_workspace_region(const mkmoe_shape* shape, int32_t region, size_t* offset,
                            size_t* bytes);
 

@@ -58,14 +58,16 @@ constexpr int kAuxNt = 2;    // nt: streamed once
 // control words at the start of the workspace: the exit count, the error words; then, from
 // byte kCtlFlags, a flag array per hand-off (a word per workgroup: set on arrival, clear
 // between launches)
-constexpr int kCtlNorm = 0, kCtlA = 1, kCtlB = 2, kCtlC = 3;  // hand-offs (flag arrays; C last)
+// hand-offs (flag arrays): N normed x, A router and x codes, B routing, C the gate_up, Q the
+// intermediates quantized (the last)
+constexpr int kCtlNorm = 0, kCtlA = 1, kCtlB = 2, kCtlC = 3, kCtlQ = 4;
 constexpr int kCtlExit = 5;
 constexpr int kCtlErr = 8;  // MKMOE_ERRW_WORDS error words from here
 constexpr int kFlagWgs = 256;  // workgroups a persistent launch has at most
 constexpr int kCtlFlags = 256;
-constexpr int kCtlBytes = kCtlFlags + 4 * kFlagWgs * 4;
+constexpr int kCtlBytes = kCtlFlags + 5 * kFlagWgs * 4;
 
-enum Stage { kStageNorm = 1, kStageA = 2, kStageB = 3, kStageC = 4, kStageD = 5 };
+enum Stage { kStageNorm = 1, kStageA = 2, kStageB = 3, kStageC = 4, kStageD = 5, kStageQ = 6 };
 
 // ---------------------------------------------------------------- timeline (diagnostic build)
 // Built with MKMOE_TIMELINE, the persistent launch stamps s_memrealtime (100 MHz) into LDS at
@@ -82,7 +84,9 @@ enum TlSlot {
   kTlDQuant, kTlDMma,
   // local routing (thread 0): its wave's part sums all landed, the scores of the step in LDS
   kTlParts, kTlScores,
-  kTlSlots = 26
+  // the workgroup's share of the quantize stage done, and the Q hand-off passed
+  kTlQDone, kTlQAwaited,
+  kTlSlots = 28
 };
 #ifdef MKMOE_TIMELINE
 static __shared__ unsigned long long s_tl[kTlSlots];
@@ -113,6 +117,9 @@ struct Cfg {
   // every expert GEMM on MFMA (the VALU GEMVs read row-major rows)
   static constexpr bool SHUF = SHUF_;
   static_assert(!SHUF || FMT == kFp4, "the shuffled layout is MXFP4's");
+  // the intermediates quantized once by stage Q from kGlobalQuantRows rows (else in every
+  // workgroup's down stage); not at MXFP4 with I = 1024, whose persistent launch would spill
+  static constexpr bool GQ = !(FMT == kFp4 && I > 512);
   static constexpr int CH512 = H / 512;  // router / quantize chunks of a row
   static_assert(H % 1024 == 0 && CH512 % P == 0, "router chunks, K split over 8 waves");
   static_assert(I % 128 == 0 && S % 128 == 0, "widths");
@@ -143,7 +150,7 @@ template <class C>
 __device__ __forceinline__ bool down_on_mfma(int rows, int mfma_down) { return C::SHUF || rows >= mfma_down; }
 
 // ---------------------------------------------------------------- workspace layout
-constexpr int kRegions = 12;
+constexpr int kRegions = 16;
 
 struct Layout {
   size_t off[kRegions];
@@ -169,6 +176,13 @@ MKMOE_HD inline Layout make_layout(int H, int E, int K, int I, int S, int fmt, i
   sz[9] = (size_t)rm * K * I * 2;                                     // routed mid, bf16
   sz[10] = sz[5];  // the part sums as routing polls them (kPartUnset between launches)
   sz[11] = (size_t)kFlagWgs * kTlSlots * 8;  // the timeline build's stamps
+  // the intermediates quantized once (stage Q), in the rows' LDS layout: the routed picks in
+  // the union's order, codes [R k][I + 16] and scales (MXFP8: E8M0 [R k][I / 32]; FP8: fp32
+  // [R k][I / 128]); the shared rows, codes [R][S + 16] and fp32 scales [R][S / 128]
+  sz[12] = (size_t)rm * K * (I + 16);
+  sz[13] = (size_t)rm * K * (fmt == kFp4 ? I / 32 : (I / 128) * 4);
+  sz[14] = (size_t)rm * (S + 16);
+  sz[15] = (size_t)rm * (S / 128) * 4;
   size_t off = kCtlBytes;
   for (int i = 0; i < kRegions; ++i) {
     L.off[i] = off;
@@ -461,9 +475,9 @@ __device__ __forceinline__ void await_all(const Params& p, int which, int nwg, i
 }
 
 // leave the launch with its flags clear for the next (graph replay safe): every workgroup
-// here has passed the C hand-off, so every workgroup has passed the earlier ones and a
-// workgroup clears its own flags of those; the last workgroup out clears the C flags (all
-// have passed that wait) and the exit count
+// here has passed the C hand-off (and Q, where the launch has one), so every workgroup has
+// passed the earlier ones and a workgroup clears its own flags of those; the last workgroup
+// out clears the C and Q flags (all have passed those waits) and the exit count
 __device__ __forceinline__ void leave(const Params& p) {
   __syncthreads();
   if (threadIdx.x < 64) {
@@ -476,6 +490,7 @@ __device__ __forceinline__ void leave(const Params& p) {
     n = __builtin_amdgcn_readfirstlane(n);
     if (n == gridDim.x - 1) {
       dst128(rs, kCtlFlags + (kCtlC * kFlagWgs + 4 * lane) * 4, u32x4{0u, 0u, 0u, 0u});
+      dst128(rs, kCtlFlags + (kCtlQ * kFlagWgs + 4 * lane) * 4, u32x4{0u, 0u, 0u, 0u});
       if (lane == 0) __hip_atomic_store(ctl(p) + kCtlExit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
@@ -2399,6 +2414,68 @@ __device__ __forceinline__ void quant_rows_lds(const Params& p, RowFn src_row, i
   }
 }
 
+// launches of at least this many rows quantize the intermediates once (stage Q, a hand-off
+// of its own) instead of in every workgroup's down stage: measured 7-8 % faster at 48 rows,
+// even at 8, and 2.4-4.4 us slower at 1 row (the hand-off costs more than the work it saves)
+constexpr int kGlobalQuantRows = 16;
+
+// quantize one bf16 row of W values (workspace byte src) into the workspace by one wave: codes
+// at dq (8 bytes a chunk of 8 values), scales at ds; group-128 fp8 (fp32 scales) or MXFP8
+// (E8M0 bytes), the arithmetic of quant_rows_lds
+template <int FMT, int W>
+__device__ __forceinline__ void quant_row_ws(const Params& p, uint32_t src, uint32_t dq, uint32_t ds, int lane) {
+#pragma clang fp contract(off)
+  constexpr int PER = W / 8;  // 8-value chunks a row
+  constexpr int CPL = PER / 64;
+  static_assert(CPL * 64 == PER, "a lane takes whole chunks");
+  const auto rs = ws_rsrc(p);
+#pragma unroll 1
+  for (int t = 0; t < CPL; ++t) {
+    const int c = lane + 64 * t;
+    const u32x4 xv = dld128(rs, src + c * 16);
+    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+    float v[8];
+    float am = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[2 * j] = bf_lo(xw[j]);
+      v[2 * j + 1] = bf_hi(xw[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) am = fabsf(v[j]) > am ? fabsf(v[j]) : am;
+    if constexpr (FMT == kFp8) {
+      const float g = group_max<16>(am);
+      const float sc = group_scale(g);
+      const uint32_t lo = e4m3_pack4(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
+      const uint32_t hi = e4m3_pack4(v[4] / sc, v[5] / sc, v[6] / sc, v[7] / sc);
+      dst64(rs, dq + c * 8, u32x2{lo, hi});
+      if ((c & 15) == 0) dst32(rs, ds + (c / 16) * 4, f2u(sc));
+    } else {
+      const float g = group_max<4>(am);
+      const int code = mx_code(g);
+      const float inv = mx_inv(code);
+      const uint32_t lo = e4m3_pack4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+      const uint32_t hi = e4m3_pack4(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
+      dst64(rs, dq + c * 8, u32x2{lo, hi});
+      if ((c & 3) == 0) dst8(rs, ds + c / 4, (uint8_t)code);
+    }
+  }
+}
+
+// workspace bytes [src, src + n) (hand-off data: device-coherent loads) into LDS at dst, by
+// 16-byte LDS-direct loads, a wave a KB in turn; n and the addresses 16-byte aligned. The
+// caller waits (vmcnt) and syncs before the rows are read.
+__device__ __forceinline__ void ws_to_lds(const Params& p, uint32_t src, uint32_t n, uint8_t* dst) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const auto rs = ws_rsrc(p);
+  for (uint32_t kb = wave; kb * 1024 < n; kb += kWaves) {
+    const uint32_t off = kb * 1024 + lane * 16;
+    if (off < n)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + kb * 1024), 16,
+                                               src + off, 0, 0, kAuxDev);
+  }
+}
+
 // row blocks of 8 in a down tile (rows past the tile masked)
 constexpr int kRowBlocks = kTileMax / kDownLanes;
 
@@ -2460,9 +2537,16 @@ __device__ __forceinline__ void shared_down_tile(const Params& p, SharedDownSmem
   auto load = shared_down_loader<C, MF>(p, h0, hn);
   if (!first_ready || (threadIdx.x >> 6) == 0) bt.load(shared_down_vwave(), n_units, load);
   __syncthreads();  // the previous user of the LDS is done
-  // (2 chunks a thread at once with MXFP4 routed experts: 4 spill the persistent launch there)
-  quant_rows_lds<kFp8, C::S, C::SQS, C::FMT == kFp4 ? 2 : kQuantBatch>(
-      p, [&](int i) { return p.off[8] + (uint32_t)i * C::S * 2; }, R, sm.q, sm.s);
+  if (C::GQ && R >= kGlobalQuantRows) {
+    // the step's shared rows, quantized once (stage Q), copied in as they lie
+    ws_to_lds(p, p.off[14], (uint32_t)R * C::SQS, sm.q);
+    ws_to_lds(p, p.off[15], (uint32_t)R * (C::S / 128) * 4, (uint8_t*)sm.s);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  } else {
+    // (2 chunks a thread at once with MXFP4 routed experts: 4 spill the persistent launch there)
+    quant_rows_lds<kFp8, C::S, C::SQS, C::FMT == kFp4 ? 2 : kQuantBatch>(
+        p, [&](int i) { return p.off[8] + (uint32_t)i * C::S * 2; }, R, sm.q, sm.s);
+  }
   __syncthreads();
   if constexpr (MF) {
     using DT = Batched<DownTile<kFp8, C::S>>;
@@ -2710,6 +2794,17 @@ __device__ __forceinline__ void mfma_issue(const Params& p, const Union<C>& un, 
     nx.load_scales((const uint8_t*)p.w2_s + (size_t)e * C::H * (C::I / 32), hb, nv, lane);
 }
 
+// picks [pb0, pb0 + pbn) of the union's order, quantized once (stage Q), into the LDS rows of
+// the down stage as they lie (codes [pick][MQS], scales [pick][MSC words]); waited for here
+template <class C>
+__device__ __forceinline__ void copy_pick_batch(const Params& p, int pb0, int pbn, DownSmem<C>& sm) {
+  constexpr uint32_t SST = C::FMT == kFp4 ? C::I / 32 : (C::I / 128) * 4;  // scale bytes of a pick
+  static_assert(C::MQS % 16 == 0 && SST % 16 == 0, "16-byte pieces");
+  ws_to_lds(p, p.off[12] + (uint32_t)pb0 * C::MQS, (uint32_t)pbn * C::MQS, sm.q);
+  ws_to_lds(p, p.off[13] + (uint32_t)pb0 * SST, (uint32_t)pbn * SST, (uint8_t*)sm.s);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 template <class C>
 __device__ __forceinline__ void down_valu(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
                                           DownBatch<DownRowsOf<C>>& bt, bool first_ready) {
@@ -2723,11 +2818,14 @@ __device__ __forceinline__ void down_valu(const Params& p, const Union<C>& un, D
     batch_slots(un, pb0, pbn, s_lo, s_hi);
     const int n_units = (s_hi - s_lo + 1) * kRowBlocks;
     auto load = valu_down_loader<C>(p, un, h0, hn, s_lo);
-    // the first batch's weights are requested before the picks' rows are quantized
+    // the first batch's weights are requested before the picks' rows are copied in
     if (pb0 > 0 || !first_ready || threadIdx.x < 64) bt.load(threadIdx.x >> 6, n_units, load);
     __syncthreads();  // the previous batch is done with the LDS rows
-    quant_rows_lds<C::FMT, C::I, C::MQS>(
-        p, [&](int i) { return p.off[9] + (uint32_t)un.picks[pb0 + i] * C::I * 2; }, pbn, sm.q, sm.s);
+    if (C::GQ && p.rows >= kGlobalQuantRows)
+      copy_pick_batch<C>(p, pb0, pbn, sm);
+    else
+      quant_rows_lds<C::FMT, C::I, C::MQS>(
+          p, [&](int i) { return p.off[9] + (uint32_t)un.picks[pb0 + i] * C::I * 2; }, pbn, sm.q, sm.s);
     __syncthreads();
     down_pipeline<DR>(bt, n_units, load, [&](int v, const DR& wr) {
       const int slot = s_lo + v / kRowBlocks, rb = v % kRowBlocks;
@@ -2774,10 +2872,13 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
       mfma_issue<C>(p, un, h0, hn, s_lo, wave, slot, bt.nxt, lane);
     __syncthreads();  // the previous batch is done with the LDS rows
     const unsigned long long tq0 = tl_now();
-    // the quantize requests 8 chunks a thread at once (4 where a unit's scales take more
-    // registers: MXFP4, whose 8 spill there)
-    quant_rows_lds<C::FMT, C::I, C::MQS, (C::FMT == kFp4 ? 1 : 2) * kQuantBatch>(
-        p, [&](int i) { return p.off[9] + (uint32_t)un.picks[pb0 + i] * C::I * 2; }, pbn, sm.q, sm.s);
+    if (C::GQ && p.rows >= kGlobalQuantRows)
+      copy_pick_batch<C>(p, pb0, pbn, sm);
+    else
+      // the quantize requests 8 chunks a thread at once (4 where a unit's scales take more
+      // registers: MXFP4, whose 8 spill there)
+      quant_rows_lds<C::FMT, C::I, C::MQS, (C::FMT == kFp4 ? 1 : 2) * kQuantBatch>(
+          p, [&](int i) { return p.off[9] + (uint32_t)un.picks[pb0 + i] * C::I * 2; }, pbn, sm.q, sm.s);
     __syncthreads();
     TL_ADD(kTlDQuant, tl_now() - tq0);
     DT cur;
@@ -2878,6 +2979,27 @@ __device__ __forceinline__ void stage_d(const Params& p, const Union<C>& un, Dow
   }
 }
 
+// stage Q: the step's intermediates quantized once, a wave a row (the arithmetic of the down
+// stage's LDS rows): the routed picks in the union's order into regions 12 / 13 (the routed
+// rule), the shared rows into 14 / 15 (group-128 FP8); the down stage copies a pick batch's
+// rows into LDS as they lie, instead of every workgroup quantizing every row
+template <class C>
+__device__ __forceinline__ void stage_q(const Params& p, const Union<C>& un, int b, int nwg) {
+  constexpr uint32_t SST = C::FMT == kFp4 ? C::I / 32 : (C::I / 128) * 4;
+  const int lane = threadIdx.x & 63;
+  const int npk = p.rows * C::K;
+  for (int j = wave_slot(b, nwg); j < npk + p.rows; j += nwg * kWaves) {
+    if (j < npk) {
+      quant_row_ws<C::FMT, C::I>(p, p.off[9] + (uint32_t)un.picks[j] * C::I * 2, p.off[12] + (uint32_t)j * C::MQS,
+                                 p.off[13] + (uint32_t)j * SST, lane);
+    } else {
+      const int r = j - npk;
+      quant_row_ws<kFp8, C::S>(p, p.off[8] + (uint32_t)r * C::S * 2, p.off[14] + (uint32_t)r * C::SQS,
+                               p.off[15] + (uint32_t)r * (C::S / 128) * 4, lane);
+    }
+  }
+}
+
 // the persistent launch past its C arrival: the down stage's first weights depend on the
 // union alone, so they are requested before the wait for the other workgroups' gate_up
 template <class C, bool MF>
@@ -2889,6 +3011,13 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
   await_all(p, kCtlC, nwg, kStageC);
   TL(kTlCAwaited);
   reset_parts<C>(p, b, nwg);  // every workgroup is past its routing
+  if (C::GQ && p.rows >= kGlobalQuantRows) {
+    stage_q<C>(p, un, b, nwg);
+    TL(kTlQDone);
+    arrive(p, kCtlQ);
+    await_all(p, kCtlQ, nwg, kStageQ);
+    TL(kTlQAwaited);
+  }
   __syncthreads();  // the tile's readers are done before the down stage reuses its LDS
   stage_d<C, MF>(p, un, sm, b, nwg, bt, first);
 }
@@ -2972,6 +3101,12 @@ __global__ __launch_bounds__(kThreads) void k_c(Params p) {
   stage_c<C>(p, un, sm, blockIdx.x, gridDim.x);
 }
 template <class C>
+__global__ __launch_bounds__(kThreads) void k_q(Params p) {
+  __shared__ Union<C> un;
+  build_union<C>(p, un, false);
+  if (C::GQ && p.rows >= kGlobalQuantRows) stage_q<C>(p, un, blockIdx.x, gridDim.x);
+}
+template <class C>
 __global__ __launch_bounds__(kThreads) void k_d(Params p) {
   __shared__ Union<C> un;
   __shared__ DownSmem<C> sm;
@@ -3044,6 +3179,7 @@ int launch(const Params& p, int nwg, hipStream_t st, bool staged) {
     hipLaunchKernelGGL(k_a<C>, grid, block, 0, st, p);
     hipLaunchKernelGGL(k_b<C>, grid, block, 0, st, p);
     hipLaunchKernelGGL(k_c<C>, grid, block, 0, st, p);
+    hipLaunchKernelGGL(k_q<C>, grid, block, 0, st, p);
     hipLaunchKernelGGL(k_d<C>, grid, block, 0, st, p);
   }
   return hipGetLastError() == hipSuccess ? MKMOE_OK : MKMOE_ERR_LAUNCH;

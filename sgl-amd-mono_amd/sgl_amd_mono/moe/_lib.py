@@ -12,12 +12,12 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libmkmoe.so"
 # the diagnostic build with the persistent launch's phase stamps (build.py --timeline)
 TIMELINE_LIB_PATH = Path(__file__).resolve().parent / "libmkmoe_tl.so"
-TL_SLOTS = 26
+TL_SLOTS = 28
 TL_NAMES = (
     "start", "A done", "A arrived", "routed", "union", "A awaited", "gate_up", "C arrived",
     "C awaited", "D routed", "D shared", "end", "gate_up first unit", "gate_up wait", "down wait",
     "gate_up units", "gate_up fetch", "gate_up mfma", "gate_up sync", "gate_up emit", "gate_up sync2",
-    "down quant", "down mfma", "parts landed", "scores",
+    "down quant", "down mfma", "parts landed", "scores", "Q done", "Q awaited",
 )  # fmt: skip
 
 ABI_VERSION = 3  # MKMOE_ABI_VERSION of include/mkmoe.h that this binding follows
@@ -40,8 +40,12 @@ REGIONS = {
     "mid": 9,
     "router_parts_polled": 10,
     "timeline": 11,
+    "mid_codes": 12,
+    "mid_scales": 13,
+    "shared_mid_codes": 14,
+    "shared_mid_scales": 15,
 }
-STAGES = {1: "norm", 2: "router + quantize", 3: "route", 4: "gate_up (routed + shared)", 5: "down (shared + routed) + combine"}
+STAGES = {1: "norm", 2: "router + quantize", 3: "route", 4: "gate_up (routed + shared)", 5: "down (shared + routed) + combine", 6: "quantize the intermediates"}
 
 # every symbol include/mkmoe.h declares
 EXPORTS = (
