@@ -68,9 +68,10 @@ extern "C" {
 #define MKMOE_ERRW_WORDS 8
 #define MKMOE_DEVERR_DEADLINE 1
 
-/* One TP rank's MoE block. Routing is DeepSeek-V3's grouped top-k on sigmoid
- * scores: choice = score + bias; groups ranked by the sum of their top two
- * choices; topk experts chosen from the topk_group best groups; weights =
+/* One TP rank's MoE block. Routing is a grouped top-k on the scores `scoring`
+ * names (sigmoid, DeepSeek-V3; sqrt(softplus), V4.1): choice = score + bias;
+ * groups ranked by the sum of their top two choices; topk experts chosen from
+ * the topk_group best groups (n_group 1: a global top-k); weights =
  * score * routed_scale / sum (renorm) or score * routed_scale. */
 typedef struct mkmoe_shape {
   int32_t hidden;        /* H */
