@@ -301,11 +301,11 @@ def timeline(runner, rb: RowsBench, reps: int = 8) -> dict:
     out = {"total_us": round(total * tick_us, 2), "workgroups": int(st.shape[0]), "phases": {}}
     for k, name in enumerate(_lib.TL_NAMES):
         col = st[:, k]
-        if name in ("gate_up wait", "down wait", "down quant", "down mfma") or name.startswith(
-            "gate_up "
-        ) and name not in ("gate_up first unit", "gate_up units"):
-            v = col * tick_us  # time a workgroup's wave 0 spent waiting for its loads
-        elif name == "gate_up units":
+        counts = ("gate_up units", "down units")
+        ends = ("gate_up first unit", "down first unit")
+        if name.startswith(("gate_up ", "down ")) and name not in counts + ends:
+            v = col * tick_us  # time a workgroup's wave 0 spent in that part of its loop
+        elif name in counts:
             v = col
         else:
             v = (col - t0) * tick_us

@@ -213,7 +213,7 @@ int mkmoe_clear_errors(const mkmoe_shape* shape, void* ws, size_t ws_bytes, void
  * [rows][topk], 8 shared intermediate bf16 [rows][S], 9 routed intermediate
  * bf16 [rows * topk][I], 10 the router part sums as routing polls them (every
  * word 0xFFFFFFFF between launches), 11 the phase stamps of a diagnostic build
- * compiled with MKMOE_TIMELINE (u64 s_memrealtime ticks [workgroup][28]; other
+ * compiled with MKMOE_TIMELINE (u64 s_memrealtime ticks [workgroup][32]; other
  * builds leave it untouched), 12 / 13 the routed intermediates quantized once
  * (codes [rows * topk][I + 16] in the union's pick order, E8M0 [..][I / 32] or
  * fp32 [..][I / 128] scales), 14 / 15 the shared intermediate quantized (codes

@@ -86,7 +86,10 @@ enum TlSlot {
   kTlParts, kTlScores,
   // the workgroup's share of the quantize stage done, and the Q hand-off passed
   kTlQDone, kTlQAwaited,
-  kTlSlots = 28
+  // the routed down's other parts (wave 0): a unit read out of its slot, the next unit
+  // requested, the units counted; and the end of its first unit
+  kTlDFetch, kTlDIssue, kTlDUnits, kTlDFirst,
+  kTlSlots = 32
 };
 #ifdef MKMOE_TIMELINE
 static __shared__ unsigned long long s_tl[kTlSlots];
@@ -1850,7 +1853,7 @@ struct DownTile {
       (WFMT == kFp4 && KS >= 8) || BYTES >= 16384 ? 1 : (16384 / BYTES > 4 ? 4 : 16384 / BYTES);
   static_assert(NA == 1 || WFMT == kFp4, "FP8 units are one 16-row block");
   u32x4 a[NA][KS][NW];
-  uint32_t sa[NA][KS];   // MXFP4: the E8M0 byte of the lane's row and block
+  uint32_t sa[NA][KS];   // MXFP4: the E8M0 byte of the lane's row and block (load_scales<true>: the loaded dwords)
   float s0[KS], s1[KS];  // FP8: block scales of the lane's first and last C row
   int split;             // FP8: C elements v < split take s0, the rest s1
 
@@ -1919,7 +1922,11 @@ struct DownTile {
   }
   // the unit's scales alone (as load() sets them). FP8: the 128 x 128 block scales of the
   // lane's C rows; MXFP4: the lane's row's KD / 32 E8M0 bytes in 16-byte loads (byte j of
-  // dword ks is its block's), rows past nv unit scales
+  // dword ks is its block's), rows past nv unit scales. RAW (MXFP4): sa keeps the loaded
+  // dwords as they are and take_scales picks the lane's bytes out of them, so that nothing
+  // waits for the loads here: a wave's loads complete in order, so a wait for the scales
+  // would wait for the unit's weight rows requested just before them
+  template <bool RAW = false>
   __device__ __forceinline__ void load_scales(const void* s, int hb, int nv, int lane) {
     const int m = lane & 15, j = lane >> 4;
     if constexpr (WFMT == kFp8) {
@@ -1946,8 +1953,12 @@ struct DownTile {
           const uint32_t dw = ok ? *(const uint32_t*)(ss + (size_t)(h / 32) * (KD / 32) * 32 + c * 256 +
                                                       (16 * j + (h & 15)) * 4)
                                  : 0x7f7f7f7fu;
-          sa[q][2 * c] = (dw >> (8 * a)) & 0xffu;
-          sa[q][2 * c + 1] = (dw >> (8 * (2 + a))) & 0xffu;
+          if constexpr (RAW) {
+            sa[q][2 * c] = dw;
+          } else {
+            sa[q][2 * c] = (dw >> (8 * a)) & 0xffu;
+            sa[q][2 * c + 1] = (dw >> (8 * (2 + a))) & 0xffu;
+          }
         }
       }
     } else {
@@ -1961,7 +1972,7 @@ struct DownTile {
           const u32x4 d = ok ? ld16(ss + h * (KD / 32) + k4 * 4) : u32x4{0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu};
           const uint32_t dw[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
-          for (int t = 0; t < 4; ++t) sa[q][k4 + t] = (dw[t] >> (8 * j)) & 0xffu;
+          for (int t = 0; t < 4; ++t) sa[q][k4 + t] = RAW ? dw[t] : (dw[t] >> (8 * j)) & 0xffu;
         }
       }
     }
@@ -1977,13 +1988,31 @@ struct DownTile {
 #pragma unroll
         for (int w = 0; w < NW; ++w) asm volatile("" : "+v"(a[q][ks][w]));
   }
-  __device__ __forceinline__ void take_scales(const DownTile& o) {
+  // the scales o requested with load_scales<true> for the unit of first row hb, once they
+  // have landed
+  __device__ __forceinline__ void take_scales(const DownTile& o, int hb, int lane) {
+    const int m = lane & 15, j = lane >> 4;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       s0[ks] = o.s0[ks];
       s1[ks] = o.s1[ks];
+    }
+    if constexpr (WFMT == kFp4 && SH) {
 #pragma unroll
-      for (int q = 0; q < NA; ++q) sa[q][ks] = o.sa[q][ks];
+      for (int q = 0; q < NA; ++q) {
+        const int a = ((hb + q * 16 + m) >> 4) & 1;  // rows past nv: 0x7f in every byte
+#pragma unroll
+        for (int c = 0; c < KS / 2; ++c) {
+          const uint32_t dw = o.sa[q][2 * c];
+          sa[q][2 * c] = (dw >> (8 * a)) & 0xffu;
+          sa[q][2 * c + 1] = (dw >> (8 * (2 + a))) & 0xffu;
+        }
+      }
+    } else if constexpr (WFMT == kFp4) {
+#pragma unroll
+      for (int q = 0; q < NA; ++q)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) sa[q][ks] = (o.sa[q][ks] >> (8 * j)) & 0xffu;
     }
     split = o.split;
   }
@@ -2791,7 +2820,7 @@ __device__ __forceinline__ void mfma_issue(const Params& p, const Union<C>& un, 
   if constexpr (C::FMT == kFp8)
     nx.load_scales((const float*)p.w2_s + (size_t)e * (C::H / 128) * (C::I / 128), hb, nv, lane);
   else
-    nx.load_scales((const uint8_t*)p.w2_s + (size_t)e * C::H * (C::I / 32), hb, nv, lane);
+    nx.template load_scales<true>((const uint8_t*)p.w2_s + (size_t)e * C::H * (C::I / 32), hb, nv, lane);
 }
 
 // picks [pb0, pb0 + pbn) of the union's order, quantized once (stage Q), into the LDS rows of
@@ -2885,12 +2914,17 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
     for (int v = wave; v < n_units; v += kWaves) {
       const unsigned long long tw0 = tl_now();
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the unit's rows are in the slot
-      TL_ADD(kTlDWait, tl_now() - tw0);
-      cur.fetch(slot, lane);
-      cur.take_scales(bt.nxt);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // and read out of it
-      if (v + kWaves < n_units) mfma_issue<C>(p, un, h0, hn, s_lo, v + kWaves, slot, bt.nxt, lane);
+      const unsigned long long tf0 = tl_now();
+      TL_ADD(kTlDWait, tf0 - tw0);
+      TL_ADD(kTlDUnits, 1ull);
       const int slot_i = s_lo + v / nb, rb = v % nb;
+      cur.fetch(slot, lane);
+      cur.take_scales(bt.nxt, h0 + rb * UR, lane);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // and read out of it
+      const unsigned long long tf1 = tl_now();
+      TL_ADD(kTlDFetch, tf1 - tf0);
+      if (v + kWaves < n_units) mfma_issue<C>(p, un, h0, hn, s_lo, v + kWaves, slot, bt.nxt, lane);
+      TL_ADD(kTlDIssue, tl_now() - tf1);
       const int j0 = max(un.slot_start[slot_i], pb0), j1 = min(un.slot_start[slot_i + 1], pb0 + pbn);
       const int n = lane & 15;
       const unsigned long long tm0 = tl_now();
@@ -2908,6 +2942,7 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
           }
       }
       TL_ADD(kTlDMma, tl_now() - tm0);
+      if (pb0 == 0 && v == wave) TL(kTlDFirst);
     }
   }
 }

@@ -12,12 +12,13 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libmkmoe.so"
 # the diagnostic build with the persistent launch's phase stamps (build.py --timeline)
 TIMELINE_LIB_PATH = Path(__file__).resolve().parent / "libmkmoe_tl.so"
-TL_SLOTS = 28
+TL_SLOTS = 32
 TL_NAMES = (
     "start", "A done", "A arrived", "routed", "union", "A awaited", "gate_up", "C arrived",
     "C awaited", "D routed", "D shared", "end", "gate_up first unit", "gate_up wait", "down wait",
     "gate_up units", "gate_up fetch", "gate_up mfma", "gate_up sync", "gate_up emit", "gate_up sync2",
-    "down quant", "down mfma", "parts landed", "scores", "Q done", "Q awaited",
+    "down quant", "down mfma", "parts landed", "scores", "Q done", "Q awaited", "down fetch", "down issue",
+    "down units", "down first unit",
 )  # fmt: skip
 
 ABI_VERSION = 3  # MKMOE_ABI_VERSION of include/mkmoe.h that this binding follows
