@@ -120,9 +120,11 @@ struct Cfg {
   // every expert GEMM on MFMA (the VALU GEMVs read row-major rows)
   static constexpr bool SHUF = SHUF_;
   static_assert(!SHUF || FMT == kFp4, "the shuffled layout is MXFP4's");
-  // the intermediates quantized once by stage Q from kGlobalQuantRows rows (else in every
-  // workgroup's down stage); not at MXFP4 with I = 1024, whose persistent launch would spill
-  static constexpr bool GQ = !(FMT == kFp4 && I > 512);
+  // launches of at least QROWS rows quantize the intermediates once (stage Q, a hand-off of
+  // its own) instead of in every workgroup's down stage. Measured: 7-8 % faster at 48 rows;
+  // at 8 rows 1.4 us faster with FP8 experts, even at I = 1024, 1.5 us slower with MXFP4 at
+  // I = 512; 2.4-4.4 us slower at 1 row (the hand-off costs more than the work it saves)
+  static constexpr int QROWS = FMT == kFp8 || I > 512 ? 8 : 16;
   static constexpr int CH512 = H / 512;  // router / quantize chunks of a row
   static_assert(H % 1024 == 0 && CH512 % P == 0, "router chunks, K split over 8 waves");
   static_assert(I % 128 == 0 && S % 128 == 0, "widths");
@@ -499,8 +501,11 @@ __device__ __forceinline__ void leave(const Params& p) {
   }
 }
 
+// this thread's wave, as a uniform (scalar) value: it then takes no vector register, which the
+// persistent launch's loops need for their operands
+__device__ __forceinline__ int wave_index() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 // wave units spread over workgroups first: this wave is slot b + nwg * wave
-__device__ __forceinline__ int wave_slot(int b, int nwg) { return b + nwg * (int)(threadIdx.x >> 6); }
+__device__ __forceinline__ int wave_slot(int b, int nwg) { return b + nwg * wave_index(); }
 
 // ---------------------------------------------------------------- stage N: RMSNorm
 template <class C>
@@ -672,7 +677,7 @@ __device__ __forceinline__ void reset_parts(const Params& p, int b, int nwg) {
 
 template <class C>
 __device__ __forceinline__ void stage_a(const Params& p, RouterSmem<C>& sm, int b, int nwg) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = (int)(threadIdx.x >> 6);
   constexpr int EB = (C::E + kWaves - 1) / kWaves;
   constexpr int n_router = C::P * EB;
   const int n = n_router + p.rows;
@@ -972,7 +977,7 @@ __device__ __forceinline__ void route_row(const Params& p, RouteSmem<C>& sm, int
 template <class C>
 __device__ __forceinline__ void route_all(const Params& p, RouteSmem<C>& sm, int* ids, float* wts,
                                           uint32_t (*rows_of)[2], int b) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = (int)(threadIdx.x >> 6);
   const auto rs = ws_rsrc(p);
   for (int e = threadIdx.x; e < C::E; e += kThreads) rows_of[e][0] = rows_of[e][1] = 0u;
   for (int r0 = 0; r0 < p.rows; r0 += kRouteRows) {
@@ -1338,7 +1343,7 @@ __device__ __forceinline__ float lane_pick(const float (&a)[kTokGroup]) {
 template <class C, int FMT, class WFn, class XFn, class EmitFn>
 __device__ __forceinline__ void gu_unit(const Params& p, XTile<C>& xt, int np, int W, int c0, int cb, WFn weights,
                         XFn load_x, EmitFn emit) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = (int)(threadIdx.x >> 6);
   using GU = GateUpCol<FMT, C::H>;
   const uint8_t* wb;
   const void* sb;
@@ -1487,7 +1492,7 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, void* lds,
 template <class C, class TokFn>
 __device__ __forceinline__ void stage_x_lds(const Params& p, XTile<C>& xt, int np, uint32_t qoff, uint32_t soff, TokFn tok,
                                             const float* wsc, int nw) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = (int)(threadIdx.x >> 6);
   const auto rs = ws_rsrc(p);
   constexpr int IPR = C::H / 1024;  // 1 KB loads a row of codes
   constexpr int RB = C::H / 32;     // scale bytes a row
@@ -1743,7 +1748,7 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
       nc = T::NC;
     }
   };
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = (int)(threadIdx.x >> 6);
   const int nb = W / T::NC;
   constexpr uint32_t WB = WFMT == kFp8 ? C::H : C::H / 2;  // bytes a weight row
   uint8_t* slot = sm.m.wslot[wave];
@@ -2443,10 +2448,6 @@ __device__ __forceinline__ void quant_rows_lds(const Params& p, RowFn src_row, i
   }
 }
 
-// launches of at least this many rows quantize the intermediates once (stage Q, a hand-off
-// of its own) instead of in every workgroup's down stage: measured 7-8 % faster at 48 rows,
-// even at 8, and 2.4-4.4 us slower at 1 row (the hand-off costs more than the work it saves)
-constexpr int kGlobalQuantRows = 16;
 
 // quantize one bf16 row of W values (workspace byte src) into the workspace by one wave: codes
 // at dq (8 bytes a chunk of 8 values), scales at ds; group-128 fp8 (fp32 scales) or MXFP8
@@ -2495,7 +2496,7 @@ __device__ __forceinline__ void quant_row_ws(const Params& p, uint32_t src, uint
 // 16-byte LDS-direct loads, a wave a KB in turn; n and the addresses 16-byte aligned. The
 // caller waits (vmcnt) and syncs before the rows are read.
 __device__ __forceinline__ void ws_to_lds(const Params& p, uint32_t src, uint32_t n, uint8_t* dst) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = (int)(threadIdx.x >> 6);
   const auto rs = ws_rsrc(p);
   for (uint32_t kb = wave; kb * 1024 < n; kb += kWaves) {
     const uint32_t off = kb * 1024 + lane * 16;
@@ -2552,21 +2553,22 @@ __device__ __forceinline__ int shared_down_units(int R, int hn) {
 }
 // the wave that takes the shared down's unit v first: wave 1 unit 0 and so on, wave 0 last (its
 // unit is requested after the hand-off it polls)
-__device__ __forceinline__ int shared_down_vwave() { return ((threadIdx.x >> 6) + kWaves - 1) % kWaves; }
+__device__ __forceinline__ int shared_down_vwave() { return ((int)(threadIdx.x >> 6) + kWaves - 1) % kWaves; }
 
 
 // the shared down of tile rows [h0, h0 + hn) into out[t * hn + hl] (bf16); first_ready: the
-// first units of waves 1-7 are already requested into bt (shared_down_first)
-template <class C, bool MF>
+// first units of waves 1-7 are already requested into bt (shared_down_first); GQ: the step's
+// rows were quantized by stage Q (launches of C::QROWS rows or more)
+template <class C, bool MF, bool GQ>
 __device__ __forceinline__ void shared_down_tile(const Params& p, SharedDownSmem<C>& sm, uint16_t* out, int h0, int hn,
                                                  SharedDownBatch<C, MF>& bt, bool first_ready) {
   const int lane = threadIdx.x & 63, g = lane / kDownLanes, l = lane % kDownLanes;
   const int R = p.rows;
   const int n_units = shared_down_units<C, MF>(R, hn);
   auto load = shared_down_loader<C, MF>(p, h0, hn);
-  if (!first_ready || (threadIdx.x >> 6) == 0) bt.load(shared_down_vwave(), n_units, load);
+  if (!first_ready || (int)(threadIdx.x >> 6) == 0) bt.load(shared_down_vwave(), n_units, load);
   __syncthreads();  // the previous user of the LDS is done
-  if (C::GQ && R >= kGlobalQuantRows) {
+  if constexpr (GQ) {
     // the step's shared rows, quantized once (stage Q), copied in as they lie
     ws_to_lds(p, p.off[14], (uint32_t)R * C::SQS, sm.q);
     ws_to_lds(p, p.off[15], (uint32_t)R * (C::S / 128) * 4, (uint8_t*)sm.s);
@@ -2700,7 +2702,7 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
           np = min(kMfmaPicks, p.rows - tg * kMfmaPicks);
         },
         [&](int tg, int np, GuX<C, kFp8>& x) {
-          x.load(p, np, qoff, soff, [&](int r) { return tg * kMfmaPicks + r; }, threadIdx.x & 63, threadIdx.x >> 6);
+          x.load(p, np, qoff, soff, [&](int r) { return tg * kMfmaPicks + r; }, threadIdx.x & 63, (int)(threadIdx.x >> 6));
         },
         [&](int tg, int q, int col, float g, float u) {
           dst16(rs, p.off[8] + ((uint32_t)(tg * kMfmaPicks + q) * C::S + col) * 2, f2bf(swiglu_shared(g, u, p.limit)));
@@ -2727,7 +2729,7 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
       [&](int tg, int np, GuX<C, C::FMT>& x) {
         const int j0 = first(tg);
         x.load(p, np, p.off[1], p.off[2], [&](int r) { return un.picks[j0 + r] / C::K; }, threadIdx.x & 63,
-               threadIdx.x >> 6);
+               (int)(threadIdx.x >> 6));
       },
       [&](int tg, int q, int col, float g, float u) {
         const int pk = un.picks[first(tg) + q];
@@ -2834,7 +2836,7 @@ __device__ __forceinline__ void copy_pick_batch(const Params& p, int pb0, int pb
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-template <class C>
+template <class C, bool GQ>
 __device__ __forceinline__ void down_valu(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
                                           DownBatch<DownRowsOf<C>>& bt, bool first_ready) {
   const int lane = threadIdx.x & 63, l = lane % kDownLanes, g = lane / kDownLanes;
@@ -2848,9 +2850,9 @@ __device__ __forceinline__ void down_valu(const Params& p, const Union<C>& un, D
     const int n_units = (s_hi - s_lo + 1) * kRowBlocks;
     auto load = valu_down_loader<C>(p, un, h0, hn, s_lo);
     // the first batch's weights are requested before the picks' rows are copied in
-    if (pb0 > 0 || !first_ready || threadIdx.x < 64) bt.load(threadIdx.x >> 6, n_units, load);
+    if (pb0 > 0 || !first_ready || threadIdx.x < 64) bt.load((int)(threadIdx.x >> 6), n_units, load);
     __syncthreads();  // the previous batch is done with the LDS rows
-    if (C::GQ && p.rows >= kGlobalQuantRows)
+    if constexpr (GQ)
       copy_pick_batch<C>(p, pb0, pbn, sm);
     else
       quant_rows_lds<C::FMT, C::I, C::MQS>(
@@ -2882,10 +2884,10 @@ __device__ __forceinline__ void down_valu(const Params& p, const Union<C>& un, D
 // the same on MFMA: units (slot, 16-row block), each against its slot's picks 16 at a time. A
 // wave keeps one unit in flight: once a unit's rows are read out of its LDS slot, the wave's
 // next unit is requested into the slot, and the unit is computed while those rows stream in.
-template <class C>
+template <class C, bool GQ>
 __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
                                           LdsUnit<C>& bt, bool first_ready) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = (int)(threadIdx.x >> 6);
   const int npk = p.rows * C::K;
   using DT = DownTileOf<C>;
   constexpr int SST = C::FMT == kFp4 ? C::I / 32 : (C::I / 128) * 4;  // scale bytes of a pick
@@ -2901,7 +2903,7 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
       mfma_issue<C>(p, un, h0, hn, s_lo, wave, slot, bt.nxt, lane);
     __syncthreads();  // the previous batch is done with the LDS rows
     const unsigned long long tq0 = tl_now();
-    if (C::GQ && p.rows >= kGlobalQuantRows)
+    if constexpr (GQ)
       copy_pick_batch<C>(p, pb0, pbn, sm);
     else
       // the quantize requests 8 chunks a thread at once (4 where a unit's scales take more
@@ -2955,7 +2957,7 @@ __device__ __forceinline__ void down_first(const Params& p, const Union<C>& un, 
   const int npk = p.rows * C::K;
   int s_lo, s_hi;
   batch_slots(un, 0, min(C::PB, npk), s_lo, s_hi);
-  const int wave = threadIdx.x >> 6;
+  const int wave = (int)(threadIdx.x >> 6);
   // not wave 0, which polls the hand-off next: its flag reads would return only after
   // these weights (a wave's loads return in order)
   if (wave == 0) return;
@@ -2971,17 +2973,17 @@ __device__ __forceinline__ void down_first(const Params& p, const Union<C>& un, 
 // tile rows [h0, h0 + hn): the routed down GEMVs (MFMA or VALU, as MF), the shared expert's
 // down, then the combine; first_ready: the routed down's first units are already requested
 // into bt (waves 1-7)
-template <class C, bool MF>
+template <class C, bool MF, bool GQ>
 __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
                                           DownBatchOf<C, MF>& bt, bool first_ready) {
   const int tid = threadIdx.x;
   const int R = p.rows;
-  if constexpr (MF) down_mfma<C>(p, un, sm, h0, hn, bt, first_ready);
-  else down_valu<C>(p, un, sm, h0, hn, bt, first_ready);
+  if constexpr (MF) down_mfma<C, GQ>(p, un, sm, h0, hn, bt, first_ready);
+  else down_valu<C, GQ>(p, un, sm, h0, hn, bt, first_ready);
   TL(kTlDRouted);
   {
     SharedDownBatch<C, MF> bs;
-    shared_down_tile<C, MF>(p, sm.sd, sm.shv, h0, hn, bs, false);
+    shared_down_tile<C, MF, GQ>(p, sm.sd, sm.shv, h0, hn, bs, false);
   }
   __syncthreads();
   TL(kTlDShared);
@@ -2999,18 +3001,19 @@ __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, D
   __syncthreads();
 }
 
-// this workgroup's tiles; first_ready: its first tile's first routed units are already requested
-template <class C, bool MF>
+// this workgroup's tiles; first_ready: its first tile's first routed units are already
+// requested; GQ: stage Q has quantized the step's intermediates
+template <class C, bool MF, bool GQ>
 __device__ __forceinline__ void stage_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg,
                                         DownBatchOf<C, MF>& bt, bool first_ready) {
   const int tr = p.tile_rows;
   const int n_tiles = (C::H + tr - 1) / tr;
-  if (b < n_tiles) down_tile<C, MF>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt, first_ready);
+  if (b < n_tiles) down_tile<C, MF, GQ>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt, first_ready);
   // further tiles (fewer workgroups than tiles) start from batches of their own, so that bt
   // is free once the first tile's routed down is done
   for (int tile = b + nwg; tile < n_tiles; tile += nwg) {
     DownBatchOf<C, MF> bl;
-    down_tile<C, MF>(p, un, sm, tile * tr, min(tr, C::H - tile * tr), bl, false);
+    down_tile<C, MF, GQ>(p, un, sm, tile * tr, min(tr, C::H - tile * tr), bl, false);
   }
 }
 
@@ -3036,8 +3039,10 @@ __device__ __forceinline__ void stage_q(const Params& p, const Union<C>& un, int
 }
 
 // the persistent launch past its C arrival: the down stage's first weights depend on the
-// union alone, so they are requested before the wait for the other workgroups' gate_up
-template <class C, bool MF>
+// union alone, so they are requested before the wait for the other workgroups' gate_up. GQ
+// (launches of C::QROWS rows or more): stage Q first. Each combination is a code path
+// of its own, so that neither path's registers are allocated around the other's
+template <class C, bool MF, bool GQ>
 __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg) {
   DownBatchOf<C, MF> bt;
   const int tr = p.tile_rows;
@@ -3046,7 +3051,7 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
   await_all(p, kCtlC, nwg, kStageC);
   TL(kTlCAwaited);
   reset_parts<C>(p, b, nwg);  // every workgroup is past its routing
-  if (C::GQ && p.rows >= kGlobalQuantRows) {
+  if constexpr (GQ) {
     stage_q<C>(p, un, b, nwg);
     TL(kTlQDone);
     arrive(p, kCtlQ);
@@ -3054,7 +3059,7 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
     TL(kTlQAwaited);
   }
   __syncthreads();  // the tile's readers are done before the down stage reuses its LDS
-  stage_d<C, MF>(p, un, sm, b, nwg, bt, first);
+  stage_d<C, MF, GQ>(p, un, sm, b, nwg, bt, first);
 }
 
 // ---------------------------------------------------------------- kernels
@@ -3106,8 +3111,14 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   TL(kTlGateUp);
   arrive(p, kCtlC);
   TL(kTlCArrived);
-  if (down_on_mfma<C>(p.rows, p.mfma_down)) wait_then_d<C, true>(p, un, sm.d, b, nwg);
-  else wait_then_d<C, false>(p, un, sm.d, b, nwg);
+  const bool gq = p.rows >= C::QROWS;
+  if (down_on_mfma<C>(p.rows, p.mfma_down)) {
+    if (gq) wait_then_d<C, true, true>(p, un, sm.d, b, nwg);
+    else wait_then_d<C, true, false>(p, un, sm.d, b, nwg);
+  } else {
+    if (gq) wait_then_d<C, false, true>(p, un, sm.d, b, nwg);
+    else wait_then_d<C, false, false>(p, un, sm.d, b, nwg);
+  }
   TL(kTlEnd);
   TL_DUMP(p);
   leave(p);
@@ -3139,19 +3150,22 @@ template <class C>
 __global__ __launch_bounds__(kThreads) void k_q(Params p) {
   __shared__ Union<C> un;
   build_union<C>(p, un, false);
-  if (C::GQ && p.rows >= kGlobalQuantRows) stage_q<C>(p, un, blockIdx.x, gridDim.x);
+  if (p.rows >= C::QROWS) stage_q<C>(p, un, blockIdx.x, gridDim.x);
 }
 template <class C>
 __global__ __launch_bounds__(kThreads) void k_d(Params p) {
   __shared__ Union<C> un;
   __shared__ DownSmem<C> sm;
   build_union<C>(p, un, false);
+  const bool gq = p.rows >= C::QROWS;
   if (down_on_mfma<C>(p.rows, p.mfma_down)) {
     DownBatchOf<C, true> bt;
-    stage_d<C, true>(p, un, sm, blockIdx.x, gridDim.x, bt, false);
+    if (gq) stage_d<C, true, true>(p, un, sm, blockIdx.x, gridDim.x, bt, false);
+    else stage_d<C, true, false>(p, un, sm, blockIdx.x, gridDim.x, bt, false);
   } else {
     DownBatchOf<C, false> bt;
-    stage_d<C, false>(p, un, sm, blockIdx.x, gridDim.x, bt, false);
+    if (gq) stage_d<C, false, true>(p, un, sm, blockIdx.x, gridDim.x, bt, false);
+    else stage_d<C, false, false>(p, un, sm, blockIdx.x, gridDim.x, bt, false);
   }
 }
 
