@@ -89,6 +89,8 @@ enum TlSlot {
   // the routed down's other parts (wave 0): a unit read out of its slot, the next unit
   // requested, the units counted; and the end of its first unit
   kTlDFetch, kTlDIssue, kTlDUnits, kTlDFirst,
+  // the routed down's waits at the pick batches' first barrier (wave 0)
+  kTlDBar,
   kTlSlots = 32
 };
 #ifdef MKMOE_TIMELINE
@@ -2894,15 +2896,24 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
   constexpr int UR = 16 * DT::NA;  // rows a unit
   const int nb = (hn + UR - 1) / UR;
   uint8_t* slot = sm.wslot[wave];
+  int s_lo, s_hi;
+  batch_slots(un, 0, min(C::PB, npk), s_lo, s_hi);
+  bool ahead = false;  // this wave's first unit of the batch was requested in the batch before
   for (int pb0 = 0; pb0 < npk; pb0 += C::PB) {
     const int pbn = min(C::PB, npk - pb0);
-    int s_lo, s_hi;
-    batch_slots(un, pb0, pbn, s_lo, s_hi);
     const int n_units = (s_hi - s_lo + 1) * nb;
-    if ((pb0 > 0 || !first_ready || wave == 0) && wave < n_units)
+    // the next batch's slots: a wave's last unit of this batch requests its first unit there,
+    // so that the batch change waits for no weight rows
+    int nx_lo = 0, nx_hi = -1;
+    if (pb0 + C::PB < npk) batch_slots(un, pb0 + C::PB, min(C::PB, npk - pb0 - C::PB), nx_lo, nx_hi);
+    const int nx_units = (nx_hi - nx_lo + 1) * nb;
+    if (!ahead && (pb0 > 0 || !first_ready || wave == 0) && wave < n_units)
       mfma_issue<C>(p, un, h0, hn, s_lo, wave, slot, bt.nxt, lane);
+    ahead = false;
+    const unsigned long long tb0 = tl_now();
     __syncthreads();  // the previous batch is done with the LDS rows
     const unsigned long long tq0 = tl_now();
+    TL_ADD(kTlDBar, tq0 - tb0);
     if constexpr (GQ)
       copy_pick_batch<C>(p, pb0, pbn, sm);
     else
@@ -2925,7 +2936,12 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // and read out of it
       const unsigned long long tf1 = tl_now();
       TL_ADD(kTlDFetch, tf1 - tf0);
-      if (v + kWaves < n_units) mfma_issue<C>(p, un, h0, hn, s_lo, v + kWaves, slot, bt.nxt, lane);
+      if (v + kWaves < n_units) {
+        mfma_issue<C>(p, un, h0, hn, s_lo, v + kWaves, slot, bt.nxt, lane);
+      } else if (wave < nx_units) {
+        mfma_issue<C>(p, un, h0, hn, nx_lo, wave, slot, bt.nxt, lane);
+        ahead = true;
+      }
       TL_ADD(kTlDIssue, tl_now() - tf1);
       const int j0 = max(un.slot_start[slot_i], pb0), j1 = min(un.slot_start[slot_i + 1], pb0 + pbn);
       const int n = lane & 15;
@@ -2946,6 +2962,8 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
       TL_ADD(kTlDMma, tl_now() - tm0);
       if (pb0 == 0 && v == wave) TL(kTlDFirst);
     }
+    s_lo = nx_lo;
+    s_hi = nx_hi;
   }
 }
 

@@ -18,7 +18,7 @@ TL_NAMES = (
     "C awaited", "D routed", "D shared", "end", "gate_up first unit", "gate_up wait", "down wait",
     "gate_up units", "gate_up fetch", "gate_up mfma", "gate_up sync", "gate_up emit", "gate_up sync2",
     "down quant", "down mfma", "parts landed", "scores", "Q done", "Q awaited", "down fetch", "down issue",
-    "down units", "down first unit",
+    "down units", "down first unit", "down barrier",
 )  # fmt: skip
 
 ABI_VERSION = 3  # MKMOE_ABI_VERSION of include/mkmoe.h that this binding follows
