@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MKMOE_ABI_VERSION 3
+#define MKMOE_ABI_VERSION 4
 
 /* weight formats */
 #define MKMOE_FMT_FP8_B128 1 /* e4m3, fp32 scale per 128 x 128 block */
@@ -65,6 +65,7 @@ extern "C" {
 #define MKMOE_ERRW_STAGE 1   /* the stage whose wait ran past its deadline */
 #define MKMOE_ERRW_BLOCK 2   /* the workgroup that saw it */
 #define MKMOE_ERRW_COUNT 3   /* how many waits ran past their deadline */
+#define MKMOE_ERRW_FAULT 4   /* 1: a wait stalled by mkmoe_options.fault_stage ran to its deadline */
 #define MKMOE_ERRW_WORDS 8
 #define MKMOE_DEVERR_DEADLINE 1
 
@@ -156,7 +157,17 @@ typedef struct mkmoe_options {
                               * the codes; 0: the default (never) */
   int32_t mxfp4_scaled_down_rows; /* MXFP4 shapes: the down GEMM alone on the scaled MFMA from
                                    * this many rows (and on MFMA); 0: the default (never) */
-  int32_t reserved[2];
+  /* Test fault injection, the reference's SGLANG_AMD_MONO_FAULT_INJECT (common/guard.py:69-89:
+   * a wait that stalls and times out). fault_stage 0: none; else workgroup fault_workgroup's
+   * wait at that stage (the MKMOE_ERRW_STAGE codes of the persistent launch's waits: 1 norm,
+   * 2 router part sums and x codes, 3 route, 4 gate_up, 6 quantize) ignores what it waits for
+   * and runs to the deadline, then records the error words with MKMOE_ERRW_FAULT set and the
+   * launch goes on, as after any deadline. A stage the launch does not wait at (3 up to 16
+   * rows, 6 below the shape's stage-Q rows, 1 without the norm) and the staged launches (no
+   * waits) stall nothing. The faulted launch's output is not valid; mkmoe_clear_errors
+   * restores the workspace. */
+  int32_t fault_stage;
+  int32_t fault_workgroup; /* 0 .. 255 */
 } mkmoe_options;
 
 /* One MoE block for rows bf16 rows x [rows][H] -> out bf16 [rows][H] (this

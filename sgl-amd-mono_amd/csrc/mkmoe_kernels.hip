@@ -230,6 +230,8 @@ struct Params {
   float limit;
   float eps;
   unsigned long long deadline;  // s_memrealtime ticks (100 MHz)
+  int fault_stage;              // test fault injection: the stage whose wait workgroup fault_wg
+  int fault_wg;                 // stalls to its deadline (0: none)
   uint32_t off[kRegions];
 };
 
@@ -436,14 +438,19 @@ __device__ __forceinline__ float dot32_fp4(u32x4 w, u32x4 xa, u32x4 xb) {
 }
 
 // ---------------------------------------------------------------- hand-offs
-__device__ __forceinline__ void record_error(const Params& p, int stage) {
+__device__ __forceinline__ void record_error(const Params& p, int stage, bool fault = false) {
   uint32_t* e = ctl(p) + kCtlErr;
   uint32_t prev = atomicCAS(&e[MKMOE_ERRW_CODE], 0u, (uint32_t)MKMOE_DEVERR_DEADLINE);
   if (prev == 0u) {
     atomicExch(&e[MKMOE_ERRW_STAGE], (uint32_t)stage);
     atomicExch(&e[MKMOE_ERRW_BLOCK], (uint32_t)blockIdx.x);
   }
+  if (fault) atomicExch(&e[MKMOE_ERRW_FAULT], 1u);
   atomicAdd(&e[MKMOE_ERRW_COUNT], 1u);
+}
+// test fault injection: this workgroup's wait at ``stage`` stalls to its deadline
+__device__ __forceinline__ bool stalls(const Params& p, int stage) {
+  return stage == p.fault_stage && (int)blockIdx.x == p.fault_wg;
 }
 
 // this workgroup is done with a stage: its sc1 stores acknowledged, then its flag set (an
@@ -465,15 +472,16 @@ __device__ __forceinline__ void await_all(const Params& p, int which, int nwg, i
     const auto rs = ws_rsrc(p);
     const int lane = threadIdx.x;
     const uint32_t off = kCtlFlags + (which * kFlagWgs + 4 * lane) * 4;
+    const bool stall = stalls(p, stage);
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
     while (true) {
       const u32x4 f = dld128(rs, off);
       const int i = 4 * lane, own = blockIdx.x;
       const bool ok = (f.x != 0u || i == own || i >= nwg) && (f.y != 0u || i + 1 == own || i + 1 >= nwg) &&
                       (f.z != 0u || i + 2 == own || i + 2 >= nwg) && (f.w != 0u || i + 3 == own || i + 3 >= nwg);
-      if (__ballot(!ok) == 0ull) break;
+      if (__ballot(!ok) == 0ull && !stall) break;
       if (__builtin_amdgcn_s_memrealtime() - t0 > p.deadline) {
-        if (lane == 0) record_error(p, stage);
+        if (lane == 0) record_error(p, stage, stall);
         break;
       }
     }
@@ -780,6 +788,7 @@ __device__ __forceinline__ void route_scores(const Params& p, RouteSmem<C>& sm, 
     // wave-uniform: a wave polls until none of its lanes' part sums is unset, or gives up
     // at the deadline (s_memrealtime is a scalar read, the same in every lane), and then
     // records the error once (lane 0)
+    const bool stall = stalls(p, kStageA);
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
     while (true) {
       bool unset = false;
@@ -787,9 +796,9 @@ __device__ __forceinline__ void route_scores(const Params& p, RouteSmem<C>& sm, 
       for (int j = 0; j < MJ; ++j)
 #pragma unroll
         for (int q = 0; q < C::P; ++q) unset |= f2u(part[j][q]) == kPartUnset;
-      if (__ballot(unset) == 0ull) break;
+      if (__ballot(unset) == 0ull && !stall) break;
       if (__builtin_amdgcn_s_memrealtime() - t0 > p.deadline) {
-        if ((tid & 63) == 0) record_error(p, kStageA);
+        if ((tid & 63) == 0) record_error(p, kStageA, stall);
         break;
       }
 #pragma unroll
@@ -3340,13 +3349,23 @@ constexpr int kMxScaledDefault = 1 << 30;  // the MXFP4 GEMMs convert to bf16 at
 constexpr int kMxScaledDownDefault = 1 << 30;
 
 // the options of one call (NULL: the defaults; a field left 0 takes its default)
-int options_of(const mkmoe_options* o, double& deadline_s, int& gate, int& down, int& scaled, int& scaled_down) {
+int options_of(const mkmoe_options* o, double& deadline_s, int& gate, int& down, int& scaled, int& scaled_down,
+               int& fault_stage, int& fault_wg) {
   deadline_s = kDeadlineDefault;
   gate = kMfmaGateDefault;
   down = kMfmaDownDefault;
   scaled = kMxScaledDefault;
   scaled_down = kMxScaledDownDefault;
+  fault_stage = 0;
+  fault_wg = 0;
   if (!o) return MKMOE_OK;
+  // a stage the persistent launch waits at (kStageD has no wait), a workgroup of the grid
+  const int fs = o->fault_stage;
+  if (fs != 0 && fs != kStageNorm && fs != kStageA && fs != kStageB && fs != kStageC && fs != kStageQ)
+    return MKMOE_ERR_ARG;
+  if (o->fault_workgroup < 0 || o->fault_workgroup >= kFlagWgs) return MKMOE_ERR_ARG;
+  fault_stage = fs;
+  fault_wg = o->fault_workgroup;
   if (o->mxfp4_scaled_rows < 0 || o->mxfp4_scaled_down_rows < 0) return MKMOE_ERR_ARG;
   if (o->mxfp4_scaled_rows) scaled = o->mxfp4_scaled_rows;
   if (o->mxfp4_scaled_down_rows) scaled_down = o->mxfp4_scaled_down_rows;
@@ -3420,8 +3439,8 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
   int rc = check_shape(s);
   if (rc) return rc;
   double dl;
-  int mfma_gate, mfma_down, mx_scaled, mx_scaled_down;
-  if ((rc = options_of(opts, dl, mfma_gate, mfma_down, mx_scaled, mx_scaled_down))) return rc;
+  int mfma_gate, mfma_down, mx_scaled, mx_scaled_down, fault_stage, fault_wg;
+  if ((rc = options_of(opts, dl, mfma_gate, mfma_down, mx_scaled, mx_scaled_down, fault_stage, fault_wg))) return rc;
   // the VALU GEMVs read row-major expert rows: SGLang's shuffled layout runs on MFMA alone
   if (s->routed_fmt == kFp4Aiter && (mfma_gate > 1 || mfma_down > 1)) return MKMOE_ERR_ARG;
   if (static_ws) {
@@ -3478,6 +3497,8 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
   p.limit = s->swiglu_limit;
   p.eps = s->norm_eps;
   p.deadline = (unsigned long long)(dl * 1e8);
+  p.fault_stage = fault_stage;
+  p.fault_wg = fault_wg;
   p.mfma_gate = mfma_gate;
   p.mfma_down = mfma_down;
   p.mx_scaled = rows >= mx_scaled && rows >= mfma_gate && rows >= mfma_down ? 1 : 0;

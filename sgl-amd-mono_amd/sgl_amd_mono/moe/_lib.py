@@ -21,13 +21,13 @@ TL_NAMES = (
     "down units", "down first unit", "down barrier",
 )  # fmt: skip
 
-ABI_VERSION = 3  # MKMOE_ABI_VERSION of include/mkmoe.h that this binding follows
+ABI_VERSION = 4  # MKMOE_ABI_VERSION of include/mkmoe.h that this binding follows
 FMT_FP8_B128 = 1
 FMT_MXFP4 = 2
 FMT_MXFP4_AITER = 3  # MXFP4 in SGLang's loaded gfx950 layout (aiter's shuffles), read in place
 SCORE_CODES = {"sigmoid": 0, "sqrt_softplus": 1}  # MKMOE_SCORE_*
 ERRW_WORDS = 8
-ERRW_CODE, ERRW_STAGE, ERRW_BLOCK, ERRW_COUNT = 0, 1, 2, 3
+ERRW_CODE, ERRW_STAGE, ERRW_BLOCK, ERRW_COUNT, ERRW_FAULT = 0, 1, 2, 3, 4
 REGIONS = {
     "x_normed": 0,
     "x_codes": 1,
@@ -100,7 +100,8 @@ class Options(ctypes.Structure):
         ("mfma_down_rows", ctypes.c_int32),
         ("mxfp4_scaled_rows", ctypes.c_int32),
         ("mxfp4_scaled_down_rows", ctypes.c_int32),
-        ("reserved", ctypes.c_int32 * 2),
+        ("fault_stage", ctypes.c_int32),  # test fault injection: a stage code (STAGES), 0: none
+        ("fault_workgroup", ctypes.c_int32),
     ]
 
 

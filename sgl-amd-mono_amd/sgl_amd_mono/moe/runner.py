@@ -204,8 +204,14 @@ class MoeRunner:
         staged: bool = False,
         mfma_rows: tuple[int, int] | None = None,
         mxfp4_scaled_rows: int | None = None,
+        fault: tuple[int, int] | None = None,
     ) -> torch.Tensor:
-        """This rank's MoE partial of bf16 rows ``x`` [R, H] (before the all-reduce) -> bf16 [R, H]."""
+        """This rank's MoE partial of bf16 rows ``x`` [R, H] (before the all-reduce) -> bf16 [R, H].
+
+        ``fault=(stage, workgroup)``: test fault injection for this call, as the reference's
+        ``SGLANG_AMD_MONO_FAULT_INJECT`` (``common/guard.py:69-89``): that workgroup's wait at
+        that stage (a code of ``_lib.STAGES``) runs to the deadline; the call's output is then
+        not valid and ``clear_errors()`` restores the workspace."""
         p = self.preset
         rows = x.shape[0]
         if not self.supports(rows):
@@ -231,9 +237,10 @@ class MoeRunner:
         ws_ = w.c_struct()
         gate, down = self.mfma_rows if mfma_rows is None else mfma_rows
         sc = self.mxfp4_scaled_rows if mxfp4_scaled_rows is None else int(mxfp4_scaled_rows)
+        fs, fw = (0, 0) if fault is None else (int(fault[0]), int(fault[1]))
         opts = _lib.Options(
             deadline_s=self.deadline_s, mfma_gate_rows=int(gate), mfma_down_rows=int(down), mxfp4_scaled_rows=sc,
-            mxfp4_scaled_down_rows=self.mxfp4_scaled_down_rows,
+            mxfp4_scaled_down_rows=self.mxfp4_scaled_down_rows, fault_stage=fs, fault_workgroup=fw,
         )
         rc = fn(
             ctypes.byref(self.shape),

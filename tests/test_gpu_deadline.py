@@ -55,3 +55,50 @@ def test_deadline_gives_up_then_clear_restores(workload, rows):
     run.raise_on_device_error()
     assert torch.equal(out2.view(torch.int16), ref.view(torch.int16)), "launch after clear_errors"
     assert bool((run.region("router_parts_polled") == 0xFF).all()), "polled part sums left unset"
+
+
+@pytest.mark.parametrize(
+    "workload,rows,stage,wg",
+    [
+        ("cfg2_tp4_fp8", 8, 4, 5),  # the gate_up hand-off (C)
+        ("cfg2_tp4_fp8", 24, 3, 17),  # the routing hand-off (above 16 rows)
+        ("cfg3_tp4_mxfp4", 16, 6, 200),  # stage Q's hand-off
+        ("cfg3_tp4_mxfp4", 1, 2, 0),  # the polled router part sums and the x codes
+        ("cfg5_tp2_mxfp4_norm", 8, 1, 255),  # the RMSNorm's hand-off
+    ],
+)
+def test_fault_injection_stalls_one_wait(workload, rows, stage, wg):
+    """A wait stalled by the test fault injection (one workgroup, one stage: the reference's
+    SGLANG_AMD_MONO_FAULT_INJECT, common/guard.py:69-89) runs to its deadline: the first error
+    recorded is that wait's (its stage and workgroup, the fault word set), the launch ends, and
+    clear_errors restores a launch bit-identical to a fresh workspace's."""
+    from test_gpu_parity import _case, _runner
+
+    from sgl_amd_mono.moe import _lib
+
+    c = _case(workload, rows)
+    x = c.x[:rows].contiguous()
+    ref_run = _runner(c)
+    ref = ref_run.moe(c.w, x).clone()
+    torch.cuda.synchronize()
+    ref_run.raise_on_device_error()
+    assert ref_run.read_errors() == [0] * _lib.ERRW_WORDS
+
+    print(f"\n{workload} R={rows}: workgroup {wg}'s wait at stage {stage} stalled (deadline 1 ms)", flush=True)
+    run = _runner(c, deadline_s=1e-3)
+    run.moe(c.w, x, fault=(stage, wg))
+    torch.cuda.synchronize()
+    e = run.read_errors()
+    print(f"  error words {e}", flush=True)
+    assert e[_lib.ERRW_CODE] == 1, e  # MKMOE_DEVERR_DEADLINE
+    assert e[_lib.ERRW_FAULT] == 1, e
+    assert (e[_lib.ERRW_STAGE], e[_lib.ERRW_BLOCK]) == (stage, wg), e
+    assert e[_lib.ERRW_COUNT] >= 1, e
+
+    run.deadline_s = 2.0
+    run.clear_errors()
+    assert run.read_errors() == [0] * _lib.ERRW_WORDS
+    out2 = run.moe(c.w, x)
+    torch.cuda.synchronize()
+    run.raise_on_device_error()
+    assert torch.equal(out2.view(torch.int16), ref.view(torch.int16)), "launch after clear_errors"

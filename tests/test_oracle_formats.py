@@ -264,3 +264,32 @@ def test_mxfp8_vllm_rule_closed_form():
     assert ca.min() >= 1 and code.min() == 1  # the zero group: vllm code 1 from the floor, too
     with pytest.raises(ValueError):
         fm.mxfp8_quant(x, "other")
+
+
+def test_host_rejects_bad_options_before_any_device_call():
+    """mkmoe_forward checks its options on the host first: a fault-injection stage the launch
+    has no wait at, or a workgroup past the flag arrays, is MKMOE_ERR_ARG; valid options get
+    as far as the pointer checks (MKMOE_ERR_NULL here). No GPU is touched."""
+    from sgl_amd_mono.moe import _lib
+    from sgl_amd_mono.moe.presets import PRESETS
+
+    L = _lib.lib()
+    shape = _lib.shape_of(PRESETS["dsv3_tp4_fp8"], 48)
+    w = _lib.Weights()
+
+    def fwd(**opts):
+        o = _lib.Options(**opts)
+        return L.mkmoe_forward(ctypes.byref(shape), ctypes.byref(w), None, 1, None, None, None, None, 0,
+                               ctypes.byref(o), None)
+
+    err_arg, err_null = -8, -1
+    assert fwd() == err_null
+    for stage in (1, 2, 3, 4, 6):
+        assert fwd(fault_stage=stage, fault_workgroup=255) == err_null, stage
+    assert fwd(fault_stage=5) == err_arg  # the down stage has no wait
+    assert fwd(fault_stage=7) == err_arg
+    assert fwd(fault_stage=-1) == err_arg
+    assert fwd(fault_stage=4, fault_workgroup=256) == err_arg
+    assert fwd(fault_stage=4, fault_workgroup=-1) == err_arg
+    assert fwd(mfma_gate_rows=-1) == err_arg
+    assert fwd(deadline_s=-1.0) == err_arg
