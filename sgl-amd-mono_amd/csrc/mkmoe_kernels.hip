@@ -489,6 +489,24 @@ __device__ __forceinline__ void await_all(const Params& p, int which, int nwg, i
   __syncthreads();
 }
 
+// one look at a hand-off's flags (wave 0, before the workgroup requests anything behind it):
+// how many are set (this workgroup's own counts as set), in every thread
+__device__ __forceinline__ int flags_set_count(const Params& p, int which, int nwg) {
+  __shared__ int s_n;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const u32x4 f = dld128(ws_rsrc(p), kCtlFlags + (which * kFlagWgs + 4 * lane) * 4);
+    const int i = 4 * lane, own = blockIdx.x;
+    const int n = __popcll(__ballot(i < nwg && (f.x != 0u || i == own))) +
+                  __popcll(__ballot(i + 1 < nwg && (f.y != 0u || i + 1 == own))) +
+                  __popcll(__ballot(i + 2 < nwg && (f.z != 0u || i + 2 == own))) +
+                  __popcll(__ballot(i + 3 < nwg && (f.w != 0u || i + 3 == own)));
+    if (lane == 0) s_n = n;
+  }
+  __syncthreads();
+  return s_n;
+}
+
 // leave the launch with its flags clear for the next (graph replay safe): every workgroup
 // here has passed the C hand-off (and Q, where the launch has one), so every workgroup has
 // passed the earlier ones and a workgroup clears its own flags of those; the last workgroup
@@ -3074,7 +3092,12 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
   DownBatchOf<C, MF> bt;
   const int tr = p.tile_rows;
   const bool first = b * tr < C::H;
-  if (first) down_first<C, MF>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt);
+  // from 8 rows the first units are requested across the wait only by the workgroups that
+  // arrive among the first three quarters: a late one's requests would hold up its own sight
+  // of the last flags (its CU's loads queue behind them), by up to 5 us at 8 rows, and the Q
+  // hand-off with it. (Below 8 rows the wait is short and the look costs more than it saves.)
+  const bool early = first && (p.rows < 8 || 4 * flags_set_count(p, kCtlC, nwg) < 3 * nwg);
+  if (early) down_first<C, MF>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt);
   await_all(p, kCtlC, nwg, kStageC);
   TL(kTlCAwaited);
   reset_parts<C>(p, b, nwg);  // every workgroup is past its routing
@@ -3086,7 +3109,7 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
     TL(kTlQAwaited);
   }
   __syncthreads();  // the tile's readers are done before the down stage reuses its LDS
-  stage_d<C, MF, GQ>(p, un, sm, b, nwg, bt, first);
+  stage_d<C, MF, GQ>(p, un, sm, b, nwg, bt, early);
 }
 
 // ---------------------------------------------------------------- kernels
