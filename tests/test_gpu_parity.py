@@ -30,6 +30,9 @@ CASES = [
     ("cfg5_tp2_mxfp4_norm", 1),
     ("cfg5_tp2_mxfp4_norm", 8),
     ("cfg5_tp2_mxfp4_norm", 48),
+    # 12 rows: stage Q with the shared expert's down inside its hand-off, pick batch whole
+    ("cfg2_tp4_fp8", 12),
+    ("cfg3_tp4_mxfp4", 12),
     ("tp4_fp8_zipf", 16),
     ("tp4_fp8_zipf", 48),
     ("tp2_mxfp4_norm_zipf", 48),
