@@ -141,3 +141,40 @@ def expert_shapes(p: dict) -> dict:
         "w2": ((e, h, i // 2), torch.uint8),
         "w2_s": ((e, h, i // 32), torch.uint8),
     }
+
+
+# ---------------------------------------------------------------- the FFN seam (mHC) inputs
+T_SEAM_X, T_SEAM_RES, T_SEAM_COMB, T_SEAM_POST, T_SEAM_PRE = 11, 12, 13, 14, 15
+T_SEAM_FN, T_SEAM_SCALE, T_SEAM_BASE, T_SEAM_NORM = 16, 17, 18, 19
+SEAM_HC = 4
+SEAM_MIX = 24
+
+
+def seam_inputs(tokens: int, hidden: int, seed: int) -> dict:
+    """One step's seam inputs, with the distributions of the reference test's
+    ``seam_inputs`` (check_ffn.py:236-251) on one rank: residual streams of RMS 1 (bf16), a
+    Sinkhorn-normalised comb, post = 2 sigmoid(N), pre = sigmoid(N) + 1e-6, the attention
+    output N(0, 0.5) (bf16)."""
+    hc = SEAM_HC
+    res = torch.randn(tokens, hc, hidden, generator=_gen(seed + T_SEAM_RES))
+    res = (res * torch.rsqrt(res.pow(2).mean(-1, keepdim=True))).to(torch.bfloat16)
+    comb = torch.rand(tokens, hc, hc, generator=_gen(seed + T_SEAM_COMB)) + 0.1
+    for _ in range(20):
+        comb = comb / comb.sum(-1, keepdim=True)
+        comb = comb / comb.sum(-2, keepdim=True)
+    post = torch.sigmoid(torch.randn(tokens, hc, generator=_gen(seed + T_SEAM_POST))) * 2
+    pre = torch.sigmoid(torch.randn(tokens, hc, generator=_gen(seed + T_SEAM_PRE))) + 1e-6
+    a = (torch.randn(tokens, hidden, generator=_gen(seed + T_SEAM_X)) * 0.5).to(torch.bfloat16)
+    return dict(a=a, res=res, post=post.contiguous(), comb=comb.contiguous(), pre=pre.contiguous())
+
+
+def seam_weights(hidden: int, seed: int) -> dict:
+    """The seam's weights as the reference test draws them (check_ffn.py:149-152): fn
+    N(0, 0.01) [24, 4 H] fp32, scale |N(0, 0.5)| + 0.5 [3], base N(0, 0.1) [24], the norm
+    weight 1 + N(0, 0.1) bf16."""
+    return dict(
+        fn=randn((SEAM_MIX, SEAM_HC * hidden), seed + T_SEAM_FN, 0.01),
+        scale=randn((3,), seed + T_SEAM_SCALE, 0.5).abs() + 0.5,
+        base=randn((SEAM_MIX,), seed + T_SEAM_BASE, 0.1),
+        norm=(1.0 + randn((hidden,), seed + T_SEAM_NORM, 0.1)).to(torch.bfloat16),
+    )

@@ -7,9 +7,9 @@
 
 The library holds the kernels and the C ABI of ``include/mkmoe.h``. It is built
 in place (not installed) so that the same file runs wherever the tree is copied.
-The source compiles in parts, in parallel: one object per compiled MoE shape
-(``MKMOE_UNIT`` 0 .. 6) and one for the host code (``MKMOE_UNIT`` 9), then one
-link.
+The MoE source compiles in parts, in parallel: one object per compiled MoE shape
+(``MKMOE_UNIT`` 0 .. 6) and one for the host code (``MKMOE_UNIT`` 9); the FFN
+seam's source (``csrc/mkmoe_seam.hip``) is one more object; then one link.
 """
 
 from __future__ import annotations
@@ -27,6 +27,7 @@ CSRC = ROOT / "csrc"
 OUT = ROOT / "sgl_amd_mono" / "moe" / "libmkmoe.so"
 OUT_TIMELINE = ROOT / "sgl_amd_mono" / "moe" / "libmkmoe_tl.so"
 SOURCE = CSRC / "mkmoe_kernels.hip"
+SEAM_SOURCE = CSRC / "mkmoe_seam.hip"
 UNITS = (0, 1, 2, 3, 4, 5, 6, 9)  # the compiled shapes, then the host code
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -51,13 +52,14 @@ def build(check: bool = False, verbose: bool = False, timeline: bool = False) ->
     out = OUT_TIMELINE if timeline else OUT
     defs = ["-DMKMOE_TIMELINE"] if timeline else []
     with tempfile.TemporaryDirectory(prefix="mkmoe_build_") as tmpd:
-        objs = [Path(tmpd) / f"unit{u}.o" for u in UNITS]
+        objs = [Path(tmpd) / f"unit{u}.o" for u in UNITS] + [Path(tmpd) / "seam.o"]
         cmds = []
         for u, o in zip(UNITS, objs):
-            cmd = [HIPCC, *FLAGS, *defs, f"-DMKMOE_UNIT={u}", "-c", str(SOURCE), "-o", str(o)]
-            if check:
+            cmds.append([HIPCC, *FLAGS, *defs, f"-DMKMOE_UNIT={u}", "-c", str(SOURCE), "-o", str(o)])
+        cmds.append([HIPCC, *FLAGS, "-c", str(SEAM_SOURCE), "-o", str(objs[-1])])
+        if check:
+            for cmd in cmds:
                 cmd.append("-Rpass-analysis=kernel-resource-usage")
-            cmds.append(cmd)
         if verbose:
             print(" ".join(cmds[0]), flush=True)
         jobs = min(len(cmds), max(1, int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))

@@ -1,4 +1,5 @@
-"""ctypes binding of the in-tree HIP library (the C ABI of ``include/mkmoe.h``).
+"""ctypes binding of the in-tree HIP library (the C ABI of ``include/mkmoe.h`` and
+``include/mkmoe_seam.h``).
 
 The library is loaded from this directory only. There is no fallback: a missing
 or unloadable library raises, so a GPU run can never silently take another path.
@@ -48,7 +49,7 @@ REGIONS = {
 }
 STAGES = {1: "norm", 2: "router + quantize", 3: "route", 4: "gate_up (routed + shared)", 5: "down (shared + routed) + combine", 6: "quantize the intermediates"}
 
-# every symbol include/mkmoe.h declares
+# every symbol include/mkmoe.h and include/mkmoe_seam.h declare
 EXPORTS = (
     "mkmoe_abi_version",
     "mkmoe_shape_supported",
@@ -67,6 +68,8 @@ EXPORTS = (
     "mkmoe_host_sigmoid",
     "mkmoe_host_sqrt_softplus",
     "mkmoe_host_topk",
+    "mkmoe_seam_workspace_bytes",
+    "mkmoe_seam_forward",
 )
 
 
@@ -111,6 +114,28 @@ class Weights(ctypes.Structure):
         for n in ("gate_w", "bias", "w13", "w13_s", "w2", "w2_s", "sgu", "sgu_s", "sw2", "sw2_s", "norm")
     ]
 
+
+class SeamIO(ctypes.Structure):
+    """mkmoe_seam_io of include/mkmoe_seam.h."""
+
+    _fields_ = [
+        ("hidden", ctypes.c_int32),
+        ("tokens", ctypes.c_int32),
+        ("norm_eps", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
+    ] + [
+        (n, ctypes.c_void_p)
+        for n in (
+            "a", "res", "post", "comb", "pre", "hc_fn", "hc_scale", "hc_base", "norm_w",
+            "res_out", "normed", "post_out", "comb_out", "pre_out",
+        )
+    ]  # fmt: skip
+
+
+SEAM_HC = 4
+SEAM_MIX = 24
+SEAM_HIDDEN = 5120
+SEAM_MAX_TOKENS = 64
 
 _lib = None
 
@@ -159,6 +184,8 @@ def lib() -> ctypes.CDLL:
         L.mkmoe_host_sqrt_softplus.restype = None
         L.mkmoe_host_topk.argtypes = [sp, vp, vp, vp, vp]
         L.mkmoe_host_topk.restype = None
+        L.mkmoe_seam_workspace_bytes.argtypes = [i32, i32, ctypes.POINTER(sz)]
+        L.mkmoe_seam_forward.argtypes = [ctypes.POINTER(SeamIO), vp, sz, vp]
         if L.mkmoe_abi_version() != ABI_VERSION:
             raise RuntimeError(
                 f"{LIB_PATH} has ABI {L.mkmoe_abi_version()}, this binding wants {ABI_VERSION}: rebuild it"

@@ -190,8 +190,9 @@ def test_host_library_exports():
 
     L = _lib.lib()
     assert L.mkmoe_abi_version() == _lib.ABI_VERSION
-    header = (Path(__file__).resolve().parents[1] / "include" / "mkmoe.h").read_text()
-    declared = set(re.findall(r"^(?:int|void|const char\*)\s+(mkmoe_\w+)\(", header, re.M))
+    declared = set()
+    for header in sorted((Path(__file__).resolve().parents[1] / "include").glob("*.h")):
+        declared |= set(re.findall(r"^(?:int|void|const char\*)\s+(mkmoe_\w+)\(", header.read_text(), re.M))
     assert declared == set(_lib.EXPORTS), declared ^ set(_lib.EXPORTS)
     for name in _lib.EXPORTS:
         assert hasattr(L, name), name
