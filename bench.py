@@ -3,6 +3,7 @@
     python bench.py [--gpus 1] [--steps 200] [--warmup 20]
                     [--workloads cfg2_tp4_fp8,cfg3_tp4_mxfp4,...] [--rows 1,8,48]
     python bench.py --timeline --workloads cfg3_tp4_mxfp4 --rows 8   # phase timeline
+    python bench.py --seam-only [--seam-tokens 1,8,48]               # the FFN seam alone
 
 A step is one MoE layer (one persistent launch) over one batch of decode rows.
 Each workload rotates over ``--layers`` distinct weight sets (each with its own
@@ -29,6 +30,12 @@ its roofline fraction (of 8 TB/s) and, where a committed counter pass exists
 (profiles/traffic_<workload>_r<rows>.json), its HBM bytes per launch. The CPU
 baseline times the oracle (the PyTorch restatement of the reference's golden
 MoE) on the host cores on a bounded sample of the headline workload.
+
+The FFN seam before the MoE block (DeepSeek-V4.1's mHC update, H 5120, two launches) is
+timed the same way at 1, 8 and 48 tokens (``workloads["v41_ffn_seam"]``), rotating over 144
+layers of its weights (283 MB of projection weights, more than the infinity cache holds).
+Its algorithmic bytes per call: the attention output and the residual streams in, the new
+streams and the normed input out, the mixes, and one layer's projection (1.97 MB fp32).
 """
 
 from __future__ import annotations
@@ -50,6 +57,9 @@ HBM_PEAK_GBPS = 8000.0
 HEADLINE = ("cfg2_tp4_fp8", 8)
 DEFAULT_WORKLOADS = "cfg2_tp4_fp8,cfg3_tp4_mxfp4,cfg4_tp4_mxfp4_zipf,cfg5_tp2_mxfp4_norm"
 MIN_TIMED = 200
+SEAM_TOKENS = "1,8,48"
+SEAM_LAYERS = 144
+SEAM_H, SEAM_HC, SEAM_MIX = 5120, 4, 24
 
 
 def log(msg: str) -> None:
@@ -201,6 +211,97 @@ def summarize(preset, rb: RowsBench, reps) -> dict:
     }
 
 
+def seam_alg_bytes(tokens: int) -> int:
+    """Bytes one seam call must move: a, res, the mixes in; res_out, normed, the mixes out; the
+    projection, scales, bias and norm weight."""
+    h, hc, t = SEAM_H, SEAM_HC, tokens
+    io = 2 * t * h + 2 * hc * t * h + t * SEAM_MIX * 4 + 2 * hc * t * h + 2 * t * h + t * SEAM_MIX * 4
+    return io + SEAM_MIX * hc * h * 4 + (3 + SEAM_MIX) * 4 + 2 * h
+
+
+def bench_seam(device, tokens_list, timed_n: int, layers: int = SEAM_LAYERS) -> dict:
+    """The FFN seam's µs per call at each token count: a captured graph of one call per layer
+    (two launches each), replayed; HIP events bracket each replay."""
+    import torch
+
+    from sgl_amd_mono.moe.seam import SeamRunner, SeamWeights
+
+    h, hc = SEAM_H, SEAM_HC
+    g = torch.Generator(device=device).manual_seed(4101)
+    run = SeamRunner(device)
+    ws = []
+    for _ in range(layers):
+        ws.append(
+            SeamWeights(
+                hc_ffn_fn=torch.randn(SEAM_MIX, hc * h, generator=g, device=device) * 0.01,
+                hc_ffn_scale=torch.rand(3, generator=g, device=device) * 0.5 + 0.5,
+                hc_ffn_base=torch.randn(SEAM_MIX, generator=g, device=device) * 0.1,
+                ffn_norm=(1 + 0.1 * torch.randn(h, generator=g, device=device)).to(torch.bfloat16),
+            )
+        )
+    out = {}
+    for t in tokens_list:
+        ins, outs = [], []
+        for _ in range(layers):
+            res = torch.randn(t, hc, h, generator=g, device=device)
+            res = (res * torch.rsqrt(res.pow(2).mean(-1, keepdim=True))).to(torch.bfloat16)
+            comb = torch.rand(t, hc, hc, generator=g, device=device) + 0.1
+            comb = comb / comb.sum(-2, keepdim=True)
+            post = torch.sigmoid(torch.randn(t, hc, 1, generator=g, device=device)) * 2
+            pre = torch.sigmoid(torch.randn(t, hc, generator=g, device=device)) + 1e-6
+            a = (torch.randn(t, h, generator=g, device=device) * 0.5).to(torch.bfloat16)
+            ins.append((a, res, post, comb, pre))
+            outs.append((
+                torch.empty(t, h, dtype=torch.bfloat16, device=device), torch.empty_like(res),
+                torch.empty_like(post), torch.empty_like(comb), torch.empty_like(pre),
+            ))  # fmt: skip
+        for j in range(layers):
+            run.ffn_seam(ws[j], *ins[j], outs=outs[j])
+        torch.cuda.synchronize()
+
+        def timed(gate_later: bool) -> list[float]:
+            gr = torch.cuda.CUDAGraph()
+            cap = torch.cuda.Stream()
+            cap.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(cap):
+                with torch.cuda.graph(gr, stream=cap):
+                    for j in range(layers):
+                        run.ffn_seam(ws[j], *ins[j], outs=outs[j], gate_later=gate_later)
+            torch.cuda.current_stream().wait_stream(cap)
+            gr.replay()
+            torch.cuda.synchronize()
+            reps = max(2, -(-timed_n // layers))
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+            ev[0].record()
+            for k in range(reps):
+                gr.replay()
+                ev[k + 1].record()
+            torch.cuda.synchronize()
+            return [ev[k].elapsed_time(ev[k + 1]) * 1e3 / layers for k in range(reps)]
+
+        per = timed(False)
+        us = statistics.median(per)
+        # the path to the MoE block's input: the slice launch and the norm, the gate left out
+        us_normed = statistics.median(timed(True))
+        reps = len(per)
+        b = seam_alg_bytes(t)
+        gbps = b / (us * 1e-6) / 1e9
+        out[str(t)] = {
+            "us_per_layer": round(us, 2),
+            "us_mean": round(sum(per) / len(per), 2),
+            "us_to_normed": round(us_normed, 2),
+            "GBps": round(gbps, 1),
+            "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+            "alg_MB_per_layer": round(b / 1e6, 3),
+            "launches_timed": 2 * reps * layers,
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+        }  # fmt: skip
+        log(f"v41_ffn_seam tokens={t}: {out[str(t)]}")
+        del ins, outs
+    return {"preset": f"DeepSeek-V4.1 FFN seam (hidden {h}, {hc} streams, {SEAM_MIX} mixes)", "rows": out}
+
+
 def cpu_baseline(workload: str, rows: int, budget_s: float = 25.0):
     """The oracle's MoE partial on the host cores: µs per layer on a bounded sample."""
     import numpy as np
@@ -337,6 +438,8 @@ def main() -> int:
                     "(aiter's shuffles; the random weight bytes are read as such)")
     ap.add_argument("--timeline", action="store_true",
                     help="phase timeline of the diagnostic build (build.py --timeline); no JSON line")
+    ap.add_argument("--seam-tokens", default=SEAM_TOKENS, help="the FFN seam's token counts ('' : none)")
+    ap.add_argument("--seam-only", action="store_true", help="time the FFN seam alone and print its results")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain copy of MIB MiB (counter calibration) and exit")
     args = ap.parse_args()
@@ -363,6 +466,10 @@ def main() -> int:
 
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
+    seam_tokens = [int(v) for v in args.seam_tokens.split(",") if v]
+    if args.seam_only:
+        print(json.dumps({"v41_ffn_seam": bench_seam(device, seam_tokens, max(args.steps, MIN_TIMED))}), flush=True)
+        return 0
     names = [args.workload] if args.workload else args.workloads.split(",")
     timed_n = max(args.steps, MIN_TIMED)
     results, head = {}, None
@@ -418,6 +525,8 @@ def main() -> int:
         torch.cuda.empty_cache()
     if args.timeline:
         return 0
+    if seam_tokens:
+        results["v41_ffn_seam"] = bench_seam(device, seam_tokens, timed_n)
 
     hname, hrows = HEADLINE
     if hname in results and str(hrows) in results[hname]["rows"]:

@@ -37,6 +37,9 @@ extern "C" {
 #define MKMOE_SEAM_MIX 24        /* projections: pre 4 | post 4 | comb 16 */
 #define MKMOE_SEAM_HIDDEN 5120   /* the one compiled hidden width (V4.1's) */
 #define MKMOE_SEAM_MAX_TOKENS 64 /* decode tokens a call takes at most */
+/* mkmoe_seam_io.flags: mkmoe_seam_forward leaves the gate (post_out, comb_out, pre_out) to
+ * a later mkmoe_seam_gate call, so that the next block's input (normed) is ready first */
+#define MKMOE_SEAM_GATE_LATER 1
 
 /* One call's tensors: device pointers, row-major, every bf16 and fp32 [.][hidden] array
  * 16-byte aligned, the small fp32 arrays 4-byte aligned. The mixes are those of
@@ -45,7 +48,7 @@ typedef struct mkmoe_seam_io {
   int32_t hidden;        /* MKMOE_SEAM_HIDDEN */
   int32_t tokens;        /* 1 .. MKMOE_SEAM_MAX_TOKENS */
   float norm_eps;        /* the RMSNorm's epsilon (the reference: 1e-20) */
-  int32_t reserved;      /* 0 */
+  int32_t flags;         /* 0, or MKMOE_SEAM_GATE_LATER */
   const void* a;         /* [tokens][hidden] bf16: the all-reduced attention output ("part" at TP 1) */
   const void* res;       /* [tokens][4][hidden] bf16: the residual streams */
   const float* post;     /* [tokens][4]: the attention seam's post mix */
@@ -69,9 +72,16 @@ int mkmoe_seam_workspace_bytes(int32_t hidden, int32_t tokens, size_t* bytes);
 /* Run the seam on `stream` (a hipStream_t; NULL: the default stream). Every argument is
  * checked on the host before anything is launched: MKMOE_ERR_NULL, MKMOE_ERR_SHAPE
  * (hidden), MKMOE_ERR_ROWS (tokens), MKMOE_ERR_ALIGN, MKMOE_ERR_WORKSPACE,
- * MKMOE_ERR_ARG (reserved != 0, norm_eps not finite or negative), MKMOE_ERR_LAUNCH.
- * Graph-capture safe: two kernel launches, no allocation, no host synchronisation. */
+ * MKMOE_ERR_ARG (unknown flags, norm_eps not finite or negative), MKMOE_ERR_LAUNCH.
+ * Graph-capture safe: two kernel launches, no allocation, no host synchronisation.
+ * With MKMOE_SEAM_GATE_LATER the second launch is the norm alone. */
 int mkmoe_seam_forward(const mkmoe_seam_io* io, void* ws, size_t ws_bytes, void* stream);
+
+/* The gate of a mkmoe_seam_forward call made with MKMOE_SEAM_GATE_LATER: the same io and
+ * workspace, whose mix partials must be untouched in between (stream order). One launch.
+ * The reference runs its gates this late too, inside its MoE stage (gfx950/layer.py:579-586).
+ * MKMOE_ERR_ARG without the flag; the other checks as mkmoe_seam_forward's. */
+int mkmoe_seam_gate(const mkmoe_seam_io* io, void* ws, size_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -3,14 +3,16 @@
 //
 // Two launches on the caller's stream:
 //   k_seam_slice  a 256-thread workgroup per 32-column slice of the hidden width (160 at
-//                 H = 5120). For every token at its columns: the new residual streams R
-//                 (bf16, to res_out), the collapse lin = sum_h pre[h] R[h] (bf16, to the
-//                 workspace), and the slice's partials of the 24 mix projections and of the
-//                 sum of squares of R (to the workspace). The slice's projection weights
-//                 (12 KB) are read once, into registers, for all tokens.
+//                 H = 5120) and group of 8 tokens. For each token at its columns: the new
+//                 residual streams R (bf16, to res_out), the collapse lin = sum_h pre[h] R[h]
+//                 (bf16, to the workspace), and the slice's partials of the 24 mix projections
+//                 and of the sum of squares of R (to the workspace). The slice's projection
+//                 weights (12 KB) go into registers first, and a slice's token groups share
+//                 an XCD, so its L2 serves them after the first read.
 //   k_seam_gate   a workgroup per token. Wave 0: the partials summed in groups of 8 slices,
-//                 then the gate (pre, post and the Sinkhorn-normalised comb) on 24 lanes.
-//                 Wave 1: the RMSNorm of lin, the MoE block's input.
+//                 then the gate: pre and post on 8 lanes, the comb's 4 x 4 Sinkhorn rounds
+//                 on 16 lanes by DPP exchanges. Wave 1: the RMSNorm of lin, the MoE block's
+//                 input.
 // Every value is a fixed sequence of IEEE fp32 / fp64 operations with contraction off (the
 // residual's last term and the gate's affine steps are explicit fmas), and the sigmoid and
 // exp are the exact fp64 ones of mkmoe_numerics.h, so a CPU restatement gives the same bits.
@@ -69,7 +71,7 @@ struct SeamParams {
   float* comb_out;
   float* pre_out;
   uint16_t* lin;  // workspace: [T][H] bf16
-  float* part;    // workspace: [T][kPart][H / kCols]
+  float* part;    // workspace: [H / kCols][T][kPart] (a slice's workgroups write whole rows)
   int T;
   float norm_eps;
 };
@@ -78,17 +80,36 @@ __device__ __forceinline__ float bf_lo(uint32_t w) { return mkmoe::u2f(w << 16);
 __device__ __forceinline__ float bf_hi(uint32_t w) { return mkmoe::u2f(w & 0xffff0000u); }
 
 // ---------------------------------------------------------------- slice launch
+// grid (slices, token groups of kTokGroup): the token groups of slice s are blocks s + NS g,
+// all on XCD s % 8 (NS is a multiple of 8 and blocks go round-robin over the 8 XCDs), so
+// the slice's projection weights come from HBM once into that XCD's L2
+constexpr int kTokGroup = 8;
+
 template <int H>
 __global__ __launch_bounds__(kThreads) void k_seam_slice(SeamParams p) {
 #pragma clang fp contract(off)
   constexpr int NS = H / kCols;
-  __shared__ __align__(16) float rl[kTokMax * kHC * kRStride];
-  __shared__ float qs[kTokMax * kTasks];
-  const int s = blockIdx.x, c0 = s * kCols, tid = threadIdx.x, T = p.T;
+  static_assert(NS % 8 == 0, "a slice's token groups on one XCD");
+  __shared__ __align__(16) float rl[kTokGroup * kHC * kRStride];
+  __shared__ float qs[kTokGroup * kTasks];
+  const int s = blockIdx.x, c0 = s * kCols, tid = threadIdx.x;
+  const int t0 = blockIdx.y * kTokGroup;
+  const int nt = min(kTokGroup, p.T - t0);
+
+  // the (projection j, stream o) task of this thread (j = 24: the sum of squares), its 32
+  // weights requested first, into registers
+  const int k = tid % 128, half = tid / 128;
+  const int j = k / kHC, o = k % kHC;
+  f32x4 f[kCols / 4];
+  if (k < kTasks && j < kMix) {
+    const f32x4* src = (const f32x4*)(p.fn + (size_t)j * kHC * H + (size_t)o * H + c0);
+#pragma unroll
+    for (int q = 0; q < kCols / 4; ++q) f[q] = src[q];
+  }
 
   // R, res_out and lin: a thread per (token, column pair)
-  for (int i = tid; i < T * (kCols / 2); i += kThreads) {
-    const int t = i / (kCols / 2), cp = i % (kCols / 2), col = c0 + 2 * cp;
+  if (tid < nt * (kCols / 2)) {
+    const int tl = tid / (kCols / 2), cp = tid % (kCols / 2), col = c0 + 2 * cp, t = t0 + tl;
     const uint32_t av = *(const uint32_t*)(p.a + (size_t)t * H + col);
     uint32_t rv[kHC];
 #pragma unroll
@@ -99,7 +120,7 @@ __global__ __launch_bounds__(kThreads) void k_seam_slice(SeamParams p) {
       po[h] = p.post[t * kHC + h];
       pr[h] = p.pre[t * kHC + h];
 #pragma unroll
-      for (int o = 0; o < kHC; ++o) cm[h][o] = p.comb[(t * kHC + h) * kHC + o];
+      for (int oo = 0; oo < kHC; ++oo) cm[h][oo] = p.comb[(t * kHC + h) * kHC + oo];
     }
     uint32_t ro[kHC] = {0u, 0u, 0u, 0u}, lo = 0u;
 #pragma unroll
@@ -110,39 +131,30 @@ __global__ __launch_bounds__(kThreads) void k_seam_slice(SeamParams p) {
       for (int h = 0; h < kHC; ++h) r[h] = d ? bf_hi(rv[h]) : bf_lo(rv[h]);
       float lin = 0.0f;
 #pragma unroll
-      for (int o = 0; o < kHC; ++o) {
-        float v = po[o] * x + r[0] * cm[0][o];
-        v = v + cm[1][o] * r[1];
-        v = v + cm[2][o] * r[2];
-        v = __builtin_fmaf(cm[3][o], r[3], v);
+      for (int oo = 0; oo < kHC; ++oo) {
+        float v = po[oo] * x + r[0] * cm[0][oo];
+        v = v + cm[1][oo] * r[1];
+        v = v + cm[2][oo] * r[2];
+        v = __builtin_fmaf(cm[3][oo], r[3], v);
         const uint16_t b = f2bf(v);
         const float R = bf2f(b);
-        ro[o] |= (uint32_t)b << (16 * d);
-        rl[(t * kHC + o) * kRStride + 2 * cp + d] = R;
-        lin = lin + pr[o] * R;
+        ro[oo] |= (uint32_t)b << (16 * d);
+        rl[(tl * kHC + oo) * kRStride + 2 * cp + d] = R;
+        lin = lin + pr[oo] * R;
       }
       lo |= (uint32_t)f2bf(lin) << (16 * d);
     }
 #pragma unroll
-    for (int o = 0; o < kHC; ++o) *(uint32_t*)(p.res_out + ((size_t)t * kHC + o) * H + col) = ro[o];
+    for (int oo = 0; oo < kHC; ++oo) *(uint32_t*)(p.res_out + ((size_t)t * kHC + oo) * H + col) = ro[oo];
     *(uint32_t*)(p.lin + (size_t)t * H + col) = lo;
   }
-
-  // the (projection j, stream o) sums over the slice's 32 columns, in column order from 0:
-  // task k = j * 4 + o (j = 24: the sum of squares), tokens split over the two halves of the
-  // workgroup; the task's 32 weights stay in registers for every token
-  const int k = tid % 128, half = tid / 128;
-  const int j = k / kHC, o = k % kHC;
-  f32x4 f[kCols / 4];
-  if (k < kTasks && j < kMix) {
-    const f32x4* src = (const f32x4*)(p.fn + (size_t)j * kHC * H + (size_t)o * H + c0);
-#pragma unroll
-    for (int q = 0; q < kCols / 4; ++q) f[q] = src[q];
-  }
   __syncthreads();
+
+  // the task's sums over the slice's 32 columns, in column order from 0, for the group's
+  // tokens (split over the two halves of the workgroup)
   if (k < kTasks) {
-    for (int t = half; t < T; t += 2) {
-      const f32x4* rr = (const f32x4*)(rl + (t * kHC + o) * kRStride);
+    for (int tl = half; tl < nt; tl += 2) {
+      const f32x4* rr = (const f32x4*)(rl + (tl * kHC + o) * kRStride);
       float acc = 0.0f;
       if (j < kMix) {
 #pragma unroll
@@ -163,82 +175,121 @@ __global__ __launch_bounds__(kThreads) void k_seam_slice(SeamParams p) {
           acc = acc + r4.w * r4.w;
         }
       }
-      qs[t * kTasks + k] = acc;
+      qs[tl * kTasks + k] = acc;
     }
   }
   __syncthreads();
-  // the slice's partial of (token, projection): the streams added in order
-  for (int i = tid; i < T * kPart; i += kThreads) {
-    const int t = i / kPart, jj = i % kPart;
-    const float* q = qs + t * kTasks + jj * kHC;
-    p.part[((size_t)t * kPart + jj) * NS + s] = ((q[0] + q[1]) + q[2]) + q[3];
+  // the slice's partial of (token, projection): the streams added in order; the group's
+  // tokens are one contiguous run of the slice's row
+  if (tid < nt * kPart) {
+    const int tl = tid / kPart, jj = tid % kPart;
+    const float* q = qs + tl * kTasks + jj * kHC;
+    p.part[((size_t)s * p.T + t0) * kPart + tid] = ((q[0] + q[1]) + q[2]) + q[3];
   }
 }
 
 // ---------------------------------------------------------------- gate and norm launch
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+// lanes 4 r + c of each 16-lane row hold a 4 x 4 matrix (row r, column c). Row sums as
+// (x0 + x1) + (x2 + x3) by quad permutes; column sums as (x_r0 + x_r1) + (x_r2 + x_r3) by row
+// rotations (a lane receives lane (i - n) mod 16 under row_ror:n): the partner 4 lanes up for
+// rows 0 and 2, 4 lanes down for rows 1 and 3, then the one 8 lanes away. Every lane of a row
+// (column) ends with the same bits, since each add is of the same two values in either order.
+__device__ __forceinline__ float quad_sum(float x) {
+  const float a = x + dpp<0xB1>(x);  // quad_perm 1, 0, 3, 2
+  return a + dpp<0x4E>(a);           // quad_perm 2, 3, 0, 1
+}
+__device__ __forceinline__ float col_sum(float x, bool even_row) {
+  const float up = dpp<0x12C>(x), down = dpp<0x124>(x);  // row_ror:12 (lane + 4), row_ror:4 (lane - 4)
+  const float a = x + (even_row ? up : down);
+  return a + dpp<0x128>(a);  // row_ror:8
+}
+__device__ __forceinline__ float quad_max(float x) {
+  const float a = fmaxf(x, dpp<0xB1>(x));
+  return fmaxf(a, dpp<0x4E>(a));
+}
+
 // lane l < d receives lane l + d's value (other lanes: unspecified)
 __device__ __forceinline__ float from_above(float v, int d) { return __shfl_down(v, d, 64); }
 
-template <int H>
+// GATE: the gate (wave 0, after all 4 waves' group sums); NORM: the norm (wave 1 with the
+// gate, else a one-wave launch)
+template <int H, bool GATE, bool NORM>
 __global__ __launch_bounds__(kThreads) void k_seam_gate(SeamParams p) {
 #pragma clang fp contract(off)
   constexpr int NS = H / kCols;
   constexpr int NG = NS / kGroup;
   constexpr int CH = H / 512;
+  constexpr int kNormWave = GATE ? 1 : 0;
+  __shared__ float pl[kPart * NS];  // this token's partials, [projection][slice]
   __shared__ float red[kPart * NG];
   const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-  // group sums: 8 slices in order from the first
-  for (int i = tid; i < kPart * NG; i += kThreads) {
-    const int jj = i / NG, g = i % NG;
-    const float* q = p.part + ((size_t)t * kPart + jj) * NS + g * kGroup;
-    float acc = q[0];
+  // the norm wave's inputs, requested first: lin rows (written by the slice launch) and weights
+  u32x4 xv[CH], nw[CH];
+  if (NORM && wave == kNormWave) {
+    const uint16_t* x = p.lin + (size_t)t * H;
 #pragma unroll
-    for (int kk = 1; kk < kGroup; ++kk) acc = acc + q[kk];
-    red[jj * NG + g] = acc;
+    for (int c = 0; c < CH; ++c) {
+      xv[c] = *(const u32x4*)(x + c * 512 + lane * 8);
+      nw[c] = *(const u32x4*)(p.norm_w + c * 512 + lane * 8);
+    }
   }
-  __syncthreads();
 
-  if (wave == 0) {
-    // projection j = lane (lane 24: the sum of squares): the groups in order from the first
-    const int jj = lane < kPart ? lane : kPart - 1;
+  // this token's 25 partials of each slice into LDS, then the group sums: 8 slices in order
+  // from the first
+  if (GATE) {
+    for (int sl = tid; sl < NS; sl += kThreads) {
+      const float* q = p.part + ((size_t)sl * p.T + t) * kPart;
+      float v[kPart];
+#pragma unroll
+      for (int jj = 0; jj < kPart; ++jj) v[jj] = q[jj];
+#pragma unroll
+      for (int jj = 0; jj < kPart; ++jj) pl[jj * NS + sl] = v[jj];
+    }
+    __syncthreads();
+    for (int i = tid; i < kPart * NG; i += kThreads) {
+      const int jj = i / NG, g = i % NG;
+      const float* q = pl + jj * NS + g * kGroup;
+      float acc = q[0];
+#pragma unroll
+      for (int kk = 1; kk < kGroup; ++kk) acc = acc + q[kk];
+      red[jj * NG + g] = acc;
+    }
+    __syncthreads();
+  }
+
+  if (GATE && wave == 0) {
+    // lane l < 16: comb element (l / 4, l % 4), projection 8 + l; lanes 16 .. 23: pre and post,
+    // projections 0 .. 7; lane 24 and up: the sum of squares
+    const int jj = lane < 16 ? 2 * kHC + lane : (lane < kMix ? lane - 16 : kMix);
     float mix = red[jj * NG];
 #pragma unroll
     for (int g = 1; g < NG; ++g) mix = mix + red[jj * NG + g];
-    const float sq = __shfl(mix, kMix, 64);
+    const float sq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mix), kMix));
     const float dn = __builtin_fmaf(sq, 1.0f / (float)(kHC * H), kMixEps);
     const float rstd = 1.0f / sqrtf(dn);
     const float v = mix * rstd;
-    const int which = lane < kHC ? 0 : (lane < 2 * kHC ? 1 : 2);
-    const float z = __builtin_fmaf(v, p.scale[which], p.base[lane < kMix ? lane : kMix - 1]);
-    if (lane < kHC) p.pre_out[t * kHC + lane] = mkmoe::sigmoid_exact(z) + kHcEps;
-    if (lane >= kHC && lane < 2 * kHC) p.post_out[t * kHC + lane - kHC] = mkmoe::sigmoid_exact(z) * kPostMult;
-    // comb: lane 8 + 4 r + c holds element (r, c); other lanes shadow lanes 8 or 23
-    const int cl = lane < 2 * kHC ? 2 * kHC : (lane >= kMix ? kMix - 1 : lane);
-    const int rowl = 2 * kHC + ((cl - 2 * kHC) & ~3), coll = 2 * kHC + ((cl - 2 * kHC) & 3);
-    auto rsum = [&](float x) {
-      return (__shfl(x, rowl, 64) + __shfl(x, rowl + 1, 64)) + (__shfl(x, rowl + 2, 64) + __shfl(x, rowl + 3, 64));
-    };
-    auto csum = [&](float x) {
-      return (__shfl(x, coll, 64) + __shfl(x, coll + 4, 64)) + (__shfl(x, coll + 8, 64) + __shfl(x, coll + 12, 64));
-    };
-    const float m = fmaxf(fmaxf(__shfl(z, rowl, 64), __shfl(z, rowl + 1, 64)),
-                          fmaxf(__shfl(z, rowl + 2, 64), __shfl(z, rowl + 3, 64)));
+    const int which = jj < kHC ? 0 : (jj < 2 * kHC ? 1 : 2);
+    const float z = __builtin_fmaf(v, p.scale[which], p.base[jj < kMix ? jj : kMix - 1]);
+    if (lane >= 16 && lane < 16 + kHC) p.pre_out[t * kHC + jj] = mkmoe::sigmoid_exact(z) + kHcEps;
+    if (lane >= 16 + kHC && lane < kMix) p.post_out[t * kHC + jj - kHC] = mkmoe::sigmoid_exact(z) * kPostMult;
+    const bool even_row = ((lane >> 2) & 1) == 0;
+    const float m = quad_max(z);
     const float e = (float)mkmoe::exp_nonpos((double)(z - m));
-    float cv = __builtin_fmaf(e, 1.0f / rsum(e), kHcEps);
-    cv = cv * (1.0f / (csum(cv) + kHcEps));
+    float cv = __builtin_fmaf(e, 1.0f / quad_sum(e), kHcEps);
+    cv = cv * (1.0f / (col_sum(cv, even_row) + kHcEps));
     for (int it = 1; it < kSinkhorn; ++it) {
-      cv = cv * (1.0f / (rsum(cv) + kHcEps));
-      cv = cv * (1.0f / (csum(cv) + kHcEps));
+      cv = cv * (1.0f / (quad_sum(cv) + kHcEps));
+      cv = cv * (1.0f / (col_sum(cv, even_row) + kHcEps));
     }
-    if (lane >= 2 * kHC && lane < kMix) p.comb_out[t * kHC * kHC + lane - 2 * kHC] = cv;
-  } else if (wave == 1) {
+    if (lane < 16) p.comb_out[t * kHC * kHC + lane] = cv;
+  } else if (NORM && wave == kNormWave) {
     // RMSNorm of lin: lane l holds the 8 values from 512 c + 8 l of each chunk c; squares summed
     // in chunk then element order, the lanes by a halving tree
-    const uint16_t* x = p.lin + (size_t)t * H;
-    u32x4 xv[CH];
-#pragma unroll
-    for (int c = 0; c < CH; ++c) xv[c] = *(const u32x4*)(x + c * 512 + lane * 8);
     float acc = 0.0f;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
@@ -257,8 +308,7 @@ __global__ __launch_bounds__(kThreads) void k_seam_gate(SeamParams p) {
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       const uint32_t w4[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
-      const u32x4 nw = *(const u32x4*)(p.norm_w + c * 512 + lane * 8);
-      const uint32_t n4[4] = {nw.x, nw.y, nw.z, nw.w};
+      const uint32_t n4[4] = {nw[c].x, nw[c].y, nw[c].z, nw[c].w};
       uint32_t ov[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -292,8 +342,10 @@ extern "C" int mkmoe_seam_workspace_bytes(int32_t hidden, int32_t tokens, size_t
   return MKMOE_OK;
 }
 
-extern "C" int mkmoe_seam_forward(const mkmoe_seam_io* io, void* ws, size_t ws_bytes, void* stream) {
-  using namespace mkmoe_seam;
+namespace mkmoe_seam {
+
+// the checks every entry point makes, then the kernel parameters
+inline int prepare(const mkmoe_seam_io* io, void* ws, size_t ws_bytes, SeamParams* p) {
   if (!io || !ws) return MKMOE_ERR_NULL;
   const void* need[] = {io->a,        io->res,     io->post,    io->comb,     io->pre,
                         io->hc_fn,    io->hc_scale, io->hc_base, io->norm_w,  io->res_out,
@@ -302,7 +354,8 @@ extern "C" int mkmoe_seam_forward(const mkmoe_seam_io* io, void* ws, size_t ws_b
     if (!q) return MKMOE_ERR_NULL;
   if (io->hidden != kHidden) return MKMOE_ERR_SHAPE;
   if (io->tokens < 1 || io->tokens > kTokMax) return MKMOE_ERR_ROWS;
-  if (io->reserved != 0 || !(io->norm_eps >= 0.0f) || !isfinite(io->norm_eps)) return MKMOE_ERR_ARG;
+  if ((io->flags & ~MKMOE_SEAM_GATE_LATER) != 0 || !(io->norm_eps >= 0.0f) || !isfinite(io->norm_eps))
+    return MKMOE_ERR_ARG;
   const void* wide[] = {io->a, io->res, io->hc_fn, io->norm_w, io->res_out, io->normed, ws};
   for (const void* q : wide)
     if (!aligned(q, 16)) return MKMOE_ERR_ALIGN;
@@ -310,30 +363,53 @@ extern "C" int mkmoe_seam_forward(const mkmoe_seam_io* io, void* ws, size_t ws_b
   for (const void* q : narrow)
     if (!aligned(q, 4)) return MKMOE_ERR_ALIGN;
   if (ws_bytes < lin_bytes(io->tokens) + part_bytes(io->tokens)) return MKMOE_ERR_WORKSPACE;
+  p->a = (const uint16_t*)io->a;
+  p->res = (const uint16_t*)io->res;
+  p->post = io->post;
+  p->comb = io->comb;
+  p->pre = io->pre;
+  p->fn = io->hc_fn;
+  p->scale = io->hc_scale;
+  p->base = io->hc_base;
+  p->norm_w = (const uint16_t*)io->norm_w;
+  p->res_out = (uint16_t*)io->res_out;
+  p->normed = (uint16_t*)io->normed;
+  p->post_out = io->post_out;
+  p->comb_out = io->comb_out;
+  p->pre_out = io->pre_out;
+  p->lin = (uint16_t*)ws;
+  p->part = (float*)((char*)ws + lin_bytes(io->tokens));
+  p->T = io->tokens;
+  p->norm_eps = io->norm_eps;
+  return MKMOE_OK;
+}
 
+}  // namespace mkmoe_seam
+
+extern "C" int mkmoe_seam_forward(const mkmoe_seam_io* io, void* ws, size_t ws_bytes, void* stream) {
+  using namespace mkmoe_seam;
   SeamParams p;
-  p.a = (const uint16_t*)io->a;
-  p.res = (const uint16_t*)io->res;
-  p.post = io->post;
-  p.comb = io->comb;
-  p.pre = io->pre;
-  p.fn = io->hc_fn;
-  p.scale = io->hc_scale;
-  p.base = io->hc_base;
-  p.norm_w = (const uint16_t*)io->norm_w;
-  p.res_out = (uint16_t*)io->res_out;
-  p.normed = (uint16_t*)io->normed;
-  p.post_out = io->post_out;
-  p.comb_out = io->comb_out;
-  p.pre_out = io->pre_out;
-  p.lin = (uint16_t*)ws;
-  p.part = (float*)((char*)ws + lin_bytes(io->tokens));
-  p.T = io->tokens;
-  p.norm_eps = io->norm_eps;
+  const int rc = prepare(io, ws, ws_bytes, &p);
+  if (rc != MKMOE_OK) return rc;
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(k_seam_slice<kHidden>, dim3(kHidden / kCols), dim3(kThreads), 0, st, p);
+  const int groups = (io->tokens + kTokGroup - 1) / kTokGroup;
+  hipLaunchKernelGGL(k_seam_slice<kHidden>, dim3(kHidden / kCols, groups), dim3(kThreads), 0, st, p);
   if (hipGetLastError() != hipSuccess) return MKMOE_ERR_LAUNCH;
-  hipLaunchKernelGGL(k_seam_gate<kHidden>, dim3(io->tokens), dim3(kThreads), 0, st, p);
+  if (io->flags & MKMOE_SEAM_GATE_LATER)
+    hipLaunchKernelGGL((k_seam_gate<kHidden, false, true>), dim3(io->tokens), dim3(64), 0, st, p);
+  else
+    hipLaunchKernelGGL((k_seam_gate<kHidden, true, true>), dim3(io->tokens), dim3(kThreads), 0, st, p);
+  if (hipGetLastError() != hipSuccess) return MKMOE_ERR_LAUNCH;
+  return MKMOE_OK;
+}
+
+extern "C" int mkmoe_seam_gate(const mkmoe_seam_io* io, void* ws, size_t ws_bytes, void* stream) {
+  using namespace mkmoe_seam;
+  SeamParams p;
+  const int rc = prepare(io, ws, ws_bytes, &p);
+  if (rc != MKMOE_OK) return rc;
+  if (!(io->flags & MKMOE_SEAM_GATE_LATER)) return MKMOE_ERR_ARG;
+  hipLaunchKernelGGL((k_seam_gate<kHidden, true, false>), dim3(io->tokens), dim3(kThreads), 0, (hipStream_t)stream, p);
   if (hipGetLastError() != hipSuccess) return MKMOE_ERR_LAUNCH;
   return MKMOE_OK;
 }

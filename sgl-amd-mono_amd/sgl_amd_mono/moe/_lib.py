@@ -70,6 +70,7 @@ EXPORTS = (
     "mkmoe_host_topk",
     "mkmoe_seam_workspace_bytes",
     "mkmoe_seam_forward",
+    "mkmoe_seam_gate",
 )
 
 
@@ -122,7 +123,7 @@ class SeamIO(ctypes.Structure):
         ("hidden", ctypes.c_int32),
         ("tokens", ctypes.c_int32),
         ("norm_eps", ctypes.c_float),
-        ("reserved", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
     ] + [
         (n, ctypes.c_void_p)
         for n in (
@@ -136,6 +137,7 @@ SEAM_HC = 4
 SEAM_MIX = 24
 SEAM_HIDDEN = 5120
 SEAM_MAX_TOKENS = 64
+SEAM_GATE_LATER = 1
 
 _lib = None
 
@@ -186,6 +188,7 @@ def lib() -> ctypes.CDLL:
         L.mkmoe_host_topk.restype = None
         L.mkmoe_seam_workspace_bytes.argtypes = [i32, i32, ctypes.POINTER(sz)]
         L.mkmoe_seam_forward.argtypes = [ctypes.POINTER(SeamIO), vp, sz, vp]
+        L.mkmoe_seam_gate.argtypes = [ctypes.POINTER(SeamIO), vp, sz, vp]
         if L.mkmoe_abi_version() != ABI_VERSION:
             raise RuntimeError(
                 f"{LIB_PATH} has ABI {L.mkmoe_abi_version()}, this binding wants {ABI_VERSION}: rebuild it"

@@ -12,6 +12,9 @@ Mirrors the seam half of the reference's FFN launch:
   rank's own), since the reduce itself needs peers.
 Two launches on the current stream (include/mkmoe_seam.h), no host synchronisation; the
 workspace for a token count is allocated on its first call, never inside a graph capture.
+With ``gate_later`` the second launch is the norm alone and ``gate()`` runs the gate later,
+off the path to the MoE block, as the reference runs its gates inside its MoE stage
+(``gfx950/layer.py:579-586``).
 """
 
 from __future__ import annotations
@@ -87,8 +90,13 @@ class SeamRunner:
         res_mix: torch.Tensor,  # [M, 4, 4] fp32
         pre_mix: torch.Tensor,  # [M, 4] fp32
         outs: tuple | None = None,
+        gate_later: bool = False,
     ) -> tuple:
-        """-> (normed [M, H] bf16, res_out [M, 4, H] bf16, post_out [M, 4, 1], comb_out [M, 4, 4], pre_out [M, 4])."""
+        """-> (normed [M, H] bf16, res_out [M, 4, H] bf16, post_out [M, 4, 1], comb_out [M, 4, 4], pre_out [M, 4]).
+
+        ``gate_later``: post_out, comb_out and pre_out are written by the next ``gate()`` call
+        (after, say, the MoE launch), so that ``normed`` is ready first; until then the tensors
+        must stay alive and the workspace of this token count must not serve another call."""
         M = part.shape[0]
         if not self.supports(M):
             raise RuntimeError(f"mkmoe seam: {M} rows, want 1 .. {_lib.SEAM_MAX_TOKENS}")
@@ -125,15 +133,28 @@ class SeamRunner:
                 )
         ws = self.workspace(M)
         io = _lib.SeamIO(
-            hidden=HIDDEN, tokens=M, norm_eps=self.norm_eps, reserved=0,
+            hidden=HIDDEN, tokens=M, norm_eps=self.norm_eps, flags=_lib.SEAM_GATE_LATER if gate_later else 0,
             a=part.data_ptr(), res=residual.data_ptr(), post=post_mix.data_ptr(), comb=res_mix.data_ptr(),
             pre=pre_mix.data_ptr(), hc_fn=w.hc_ffn_fn.data_ptr(), hc_scale=w.hc_ffn_scale.data_ptr(),
             hc_base=w.hc_ffn_base.data_ptr(), norm_w=w.ffn_norm.data_ptr(), res_out=res_out.data_ptr(),
             normed=normed.data_ptr(), post_out=post_out.data_ptr(), comb_out=comb_out.data_ptr(),
             pre_out=pre_out.data_ptr(),
         )  # fmt: skip
+        self._io = io  # the later gate's arguments
         rc = self.lib.mkmoe_seam_forward(
             ctypes.byref(io), ws.data_ptr(), ws.numel(), torch.cuda.current_stream(self.device).cuda_stream
         )
         _lib.check(rc, "mkmoe seam forward")
         return outs
+
+    def gate(self) -> None:
+        """The gate of the last ``ffn_seam(..., gate_later=True)`` call (its outputs filled in)."""
+        io = getattr(self, "_io", None)
+        if io is None or not (io.flags & _lib.SEAM_GATE_LATER):
+            raise RuntimeError("mkmoe seam gate: no ffn_seam(..., gate_later=True) call to finish")
+        ws = self._ws[io.tokens]
+        rc = self.lib.mkmoe_seam_gate(
+            ctypes.byref(io), ws.data_ptr(), ws.numel(), torch.cuda.current_stream(self.device).cuda_stream
+        )
+        _lib.check(rc, "mkmoe seam gate")
+        self._io = None

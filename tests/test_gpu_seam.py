@@ -92,6 +92,31 @@ def test_seam_reference_bounds_against_fp64():
     assert cos.item() > 0.9999
 
 
+@pytest.mark.parametrize("tokens", [1, 8, 48])
+def test_seam_gate_later_equals_one_call(tokens):
+    """The norm first and the gate after other work on the stream give the one call's bits."""
+    from sgl_amd_mono.moe.seam import SeamRunner
+
+    print(f"\nseam gate_later tokens={tokens}", flush=True)
+    i, w = _inputs(tokens, 5000 + tokens)
+    sw, ins = _device(i, w)
+    run = SeamRunner()
+    one = [t.clone() for t in run.ffn_seam(sw, *ins)]
+    torch.cuda.synchronize()
+    outs = tuple(torch.full_like(t, -7) for t in one)
+    run.ffn_seam(sw, *ins, outs=outs, gate_later=True)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int16), one[0].view(torch.int16))  # normed
+    assert torch.equal(outs[1].view(torch.int16), one[1].view(torch.int16))  # res_out
+    assert bool((outs[2] == -7).all() and (outs[3] == -7).all() and (outs[4] == -7).all())
+    filler = torch.randn(1 << 20, device="cuda").sum()  # other work in between
+    run.gate()
+    torch.cuda.synchronize()
+    assert torch.isfinite(filler)
+    for a, b in zip(outs[2:], one[2:]):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
 def test_seam_graph_replays_bitwise():
     from sgl_amd_mono.moe.seam import SeamRunner
 

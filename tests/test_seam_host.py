@@ -11,7 +11,7 @@ import torch
 def _io(**over):
     from sgl_amd_mono.moe import _lib
 
-    io = _lib.SeamIO(hidden=_lib.SEAM_HIDDEN, tokens=8, norm_eps=1e-20, reserved=0)
+    io = _lib.SeamIO(hidden=_lib.SEAM_HIDDEN, tokens=8, norm_eps=1e-20, flags=0)
     for n, _ in _lib.SeamIO._fields_[4:]:
         setattr(io, n, 0x100000)
     for k, v in over.items():
@@ -41,7 +41,8 @@ def test_seam_workspace_bytes():
         (dict(hidden=7168), -2),
         (dict(tokens=0), -3),
         (dict(tokens=65), -3),
-        (dict(reserved=1), -8),
+        (dict(flags=2), -8),
+        (dict(flags=-1), -8),
         (dict(norm_eps=-1.0), -8),
         (dict(norm_eps=float("nan")), -8),
         (dict(res=0x100008), -4),
@@ -70,6 +71,17 @@ def test_seam_forward_rejects_small_workspace_and_null():
     assert L.mkmoe_seam_forward(ctypes.byref(io), 0x200008, n.value, None) == -4
     assert L.mkmoe_seam_forward(ctypes.byref(io), None, n.value, None) == -1
     assert L.mkmoe_seam_forward(None, 0x200000, n.value, None) == -1
+
+
+def test_seam_gate_needs_the_gate_later_flag():
+    from sgl_amd_mono.moe import _lib
+
+    L = _lib.lib()
+    n = ctypes.c_size_t()
+    assert L.mkmoe_seam_workspace_bytes(5120, 8, ctypes.byref(n)) == 0
+    assert L.mkmoe_seam_gate(ctypes.byref(_io(flags=0)), 0x200000, n.value, None) == -8
+    assert L.mkmoe_seam_gate(ctypes.byref(_io(flags=1, tokens=0)), 0x200000, n.value, None) == -3
+    assert L.mkmoe_seam_gate(ctypes.byref(_io(flags=1)), 0x200000, n.value - 1, None) == -5
 
 
 def test_seam_weights_check_names_the_tensor():
