@@ -239,6 +239,14 @@ const char* mkmoe_status_string(int status);
  * the same hardware converts the kernels use (for tests of those converts). */
 int mkmoe_device_decode(const uint8_t* codes, float* fp8, float* fp4, int32_t n, void* stream);
 
+/* Device sweep of the fp32 bit patterns [first, first + count) (inf and NaN skipped) through
+ * the e4m3 convert the activation quantizers use, against the integer-step encoder of
+ * mkmoe_numerics.h that the CPU oracle restates; adds the number of differing codes to *bad
+ * and lowers *first_bad to the lowest differing pattern (device pointers the caller set). A
+ * test hook with no counterpart in the reference, whose quantizer is torch's conversion
+ * (check_ffn.py:104). MKMOE_ERR_ARG for count 0 or a range past 2^32. */
+int mkmoe_device_e4m3_sweep(uint32_t first, uint32_t count, uint32_t* bad, uint32_t* first_bad, void* stream);
+
 /* Device run of the scaled MFMA the MXFP4 option uses (v_mfma_scale_f32_16x16x128_f8f6f4,
  * C = 0), for its known-answer tests; no counterpart in the reference, which calls the
  * instruction through FlyDSL (common/mx.py:60-66). tiles waves, one 16x16x128 tile each: a

@@ -388,8 +388,8 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
 __device__ __forceinline__ float clampf(float v, float lim) { return fminf(fmaxf(v, -lim), lim); }
 
 // four e4m3 codes (a in the low byte) by the gfx950 convert after the clamp to +-448: for
-// every finite input the convert's nearest-even code equals e4m3_encode's (checked over all
-// finite fp32 on the device)
+// every finite input the convert's nearest-even code equals e4m3_encode's (k_e4m3_sweep checks
+// all finite fp32 on the device)
 __device__ __forceinline__ float clamp448(float v) { return v > kFp8Max ? kFp8Max : (v < -kFp8Max ? -kFp8Max : v); }
 __device__ __forceinline__ uint32_t e4m3_pack4(float a, float b, float c, float d) {
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(clamp448(a), clamp448(b), 0, false);
@@ -3321,6 +3321,28 @@ __global__ void k_mfma_scaled(const uint32_t* a, const uint32_t* b, const uint32
   for (int v = 0; v < 4; ++v) d[base * 4 + v] = c[v];
 }
 
+// every finite fp32 bit pattern of [first, first + count) through the gfx950 e4m3 convert the
+// activation quantizers use (e4m3_pack4: clamp to +-448, then the convert) against
+// e4m3_encode (the integer-step encoder the CPU oracle restates): the count of differing codes
+// and the lowest differing pattern
+__global__ void k_e4m3_sweep(uint32_t first, uint32_t count, uint32_t* bad, uint32_t* first_bad) {
+  uint32_t n_bad = 0, lo_bad = 0xffffffffu;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x) {
+    const uint32_t bits = first + i;
+    if ((bits & 0x7f800000u) == 0x7f800000u) continue;  // inf, NaN
+    const float x = u2f(bits);
+    const uint32_t hw = e4m3_pack4(x, 0.0f, 0.0f, 0.0f) & 0xffu;
+    if (hw != e4m3_encode(x)) {
+      ++n_bad;
+      lo_bad = bits < lo_bad ? bits : lo_bad;
+    }
+  }
+  if (n_bad) {
+    atomicAdd(bad, n_bad);
+    atomicMin(first_bad, lo_bad);
+  }
+}
+
 // decode byte i as e4m3 (the fp8 convert the GEMVs use) and as two e2m1 (the fp4 convert)
 __global__ void k_decode(const uint8_t* codes, float* fp8, float* fp4, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -3735,6 +3757,13 @@ int mkmoe_device_decode(const uint8_t* codes, float* fp8, float* fp4, int32_t n,
   if (n < 1) return MKMOE_ERR_ARG;
   hipLaunchKernelGGL(k_decode, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, codes, fp8,
                      fp4, n);
+  return hipGetLastError() == hipSuccess ? MKMOE_OK : MKMOE_ERR_LAUNCH;
+}
+
+int mkmoe_device_e4m3_sweep(uint32_t first, uint32_t count, uint32_t* bad, uint32_t* first_bad, void* stream) {
+  if (!bad || !first_bad) return MKMOE_ERR_NULL;
+  if (count == 0 || (uint64_t)first + count > (1ull << 32)) return MKMOE_ERR_ARG;
+  hipLaunchKernelGGL(k_e4m3_sweep, dim3(2048), dim3(256), 0, (hipStream_t)stream, first, count, bad, first_bad);
   return hipGetLastError() == hipSuccess ? MKMOE_OK : MKMOE_ERR_LAUNCH;
 }
 

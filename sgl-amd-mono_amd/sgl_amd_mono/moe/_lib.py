@@ -63,6 +63,7 @@ EXPORTS = (
     "mkmoe_workspace_region",
     "mkmoe_status_string",
     "mkmoe_device_decode",
+    "mkmoe_device_e4m3_sweep",
     "mkmoe_device_mfma_scaled",
     "mkmoe_host_e4m3_encode",
     "mkmoe_host_sigmoid",
@@ -177,6 +178,7 @@ def lib() -> ctypes.CDLL:
         L.mkmoe_status_string.argtypes = [ctypes.c_int]
         L.mkmoe_status_string.restype = ctypes.c_char_p
         L.mkmoe_device_decode.argtypes = [vp, vp, vp, i32, vp]
+        L.mkmoe_device_e4m3_sweep.argtypes = [ctypes.c_uint32, ctypes.c_uint32, vp, vp, vp]
         L.mkmoe_device_mfma_scaled.argtypes = [vp, vp, vp, vp, vp, i32, i32, vp]
         L.mkmoe_host_e4m3_encode.argtypes = [vp, vp, ctypes.c_int64]
         L.mkmoe_host_e4m3_encode.restype = None

@@ -403,6 +403,52 @@ def test_graph_replay_bitwise():
     run.raise_on_device_error()
 
 
+def test_device_e4m3_convert_equals_encoder_on_every_float():
+    """The hardware e4m3 convert of the activation quantizers (after the +-448 clamp) against the
+    integer-step encoder (host-pinned by the oracle tests) on all 2^32 fp32 patterns but inf and
+    NaN, on the device: no code differs."""
+    from sgl_amd_mono.moe import _lib
+
+    L = _lib.lib()
+    bad = torch.zeros(1, dtype=torch.int32, device="cuda")
+    first_bad = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    for k in range(16):
+        _lib.check(L.mkmoe_device_e4m3_sweep(k << 28, 1 << 28, bad.data_ptr(), first_bad.data_ptr(), None), "sweep")
+    torch.cuda.synchronize()
+    assert int(bad.item()) == 0, f"{int(bad.item())} codes differ, first at {int(first_bad.item()) & 0xffffffff:#010x}"
+
+
+def test_graph_replay_bitwise_routing_handoff():
+    """Rows 24 and 48 (the routing hand-off, stage Q) in one graph, replayed with eager work between."""
+    c = _case("cfg2_tp4_fp8", 48)
+    run = _runner(c)
+    rows = (24, 48)
+    xs = [c.x[:r].contiguous() for r in rows]
+    outs = [torch.empty(r, c.p["hidden"], dtype=torch.bfloat16, device="cuda") for r in rows]
+    for x, o in zip(xs, outs):
+        run.moe(c.w, x, out=o)
+    torch.cuda.synchronize()
+    ref = [o.clone() for o in outs]
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for x, o in zip(xs, outs):
+                run.moe(c.w, x, out=o)
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(4):
+        for o in outs:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, r in zip(outs, ref):
+            assert torch.equal(o.view(torch.int16), r.view(torch.int16)), f"replay {i}"
+        run.moe(c.w, xs[0], out=outs[0])  # eager work between replays
+        torch.cuda.synchronize()
+    run.raise_on_device_error()
+
+
 def test_host_validation_errors():
     c = _case("cfg1_plumbing_fp8", 4)
     run = _runner(c)
