@@ -95,8 +95,9 @@ class SeamRunner:
         """-> (normed [M, H] bf16, res_out [M, 4, H] bf16, post_out [M, 4, 1], comb_out [M, 4, 4], pre_out [M, 4]).
 
         ``gate_later``: post_out, comb_out and pre_out are written by the next ``gate()`` call
-        (after, say, the MoE launch), so that ``normed`` is ready first; until then the tensors
-        must stay alive and the workspace of this token count must not serve another call."""
+        (after, say, the MoE launch), so that ``normed`` is ready first; the runner holds the
+        call's tensors until then, and the workspace of this token count must not serve another
+        call in between."""
         M = part.shape[0]
         if not self.supports(M):
             raise RuntimeError(f"mkmoe seam: {M} rows, want 1 .. {_lib.SEAM_MAX_TOKENS}")
@@ -140,7 +141,9 @@ class SeamRunner:
             normed=normed.data_ptr(), post_out=post_out.data_ptr(), comb_out=comb_out.data_ptr(),
             pre_out=pre_out.data_ptr(),
         )  # fmt: skip
-        self._io = io  # the later gate's arguments
+        # the later gate's arguments, and the tensors they point into (kept alive until then)
+        self._io = io
+        self._keep = (w, part, residual, post_mix, res_mix, pre_mix, outs) if gate_later else None
         rc = self.lib.mkmoe_seam_forward(
             ctypes.byref(io), ws.data_ptr(), ws.numel(), torch.cuda.current_stream(self.device).cuda_stream
         )
@@ -158,3 +161,4 @@ class SeamRunner:
         )
         _lib.check(rc, "mkmoe seam gate")
         self._io = None
+        self._keep = None
