@@ -257,6 +257,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t weight_rsrc(const void* w, uin
 }
 constexpr uint32_t kNoLoad = 0xF0000000u;  // an offset past every weight resource
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+// A wait for all of the wave's vector memory loads (vmcnt 0), placed as the compiler's own
+// wait, so that it knows every register loaded before it is ready. Its own waits for loads
+// issued before an asm wait would count the loads issued after it as well (they complete in
+// order): a register loaded before a unit's wait, used after the next unit's rows are
+// requested, would then wait for those rows.
+__device__ __forceinline__ void wait_vm0() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // gfx9 fields: vmcnt 0, expcnt 7 (none), lgkmcnt 15 (none)
+  asm volatile("" ::: "memory");
+}
+
 // a weight of n bytes as the four scalar words of a buffer resource (for lds_dma16)
 __device__ __forceinline__ i32x4 weight_rsrc_words(const void* w, uint32_t n) {
   const unsigned long long a = (unsigned long long)w;
@@ -1549,7 +1560,7 @@ __device__ __forceinline__ void stage_x_lds(const Params& p, XTile<C>& xt, int n
       lds_load16(wr, (uint8_t*)xt.wsc + k * 1024, off < nw * 4 ? off : 0, 0);
     }
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  wait_vm0();
   __syncthreads();
 }
 
@@ -1609,8 +1620,11 @@ struct GuTile {
   // ([2W][H / 32] bytes); the unit's columns j0 .. j0 + nc - 1 (nc = NC, or NC / 2 at a
   // share's ends: the other rows are requested past the resource, so the slot holds zeros
   // there and no memory is read)
+  // (part [b0, b1) of the unit's 1 KB blocks alone, and its scales with block 0: a wave can
+  // spread its request over the current unit's K steps)
+  static constexpr int kBlocks = SLOT / 1024;
   __device__ __forceinline__ void issue(i32x4 wr, i32x4 sr, int W, int j0, int nc, uint8_t* slot, uint8_t* sslot,
-                                        int lane, int wave) {
+                                        int lane, int wave, int b0 = 0, int b1 = kBlocks) {
     const int s0 = wave * SPW;
     constexpr int ROWB = WFMT == kFp8 ? C::H : C::H / 2;  // bytes a weight row
     if constexpr (SH) {
@@ -1622,19 +1636,21 @@ struct GuTile {
       const int b = j0 / 16;
 #pragma unroll
       for (int blk = 0; blk < 2 * SPW; ++blk) {
+        if (blk < b0 || blk >= b1) continue;
         const int q = blk / SPW, i = blk % SPW;
         lds_dma16(wr, slot + blk * 1024, (uint32_t)(2 * b + q) * 16 * ROWB + (s0 + i) * 1024 + lane * 16);
       }
-      lds_dma16_cached(sr, sslot, (uint32_t)b * C::H + (s0 / 2) * 256 + lane * 16);
+      if (b0 == 0) lds_dma16_cached(sr, sslot, (uint32_t)b * C::H + (s0 / 2) * 256 + lane * 16);
       return;
     }
 #pragma unroll
     for (int i = 0; i < SLOT / 1024; ++i) {
+      if (i < b0 || i >= b1) continue;
       const int pos = i * 64 + lane, r = pos / CPW, c = (pos % CPW) ^ key(r);
       const bool live = (WFMT == kFp8 ? (r & 7) : (r & 15)) < nc;
       lds_dma16(wr, slot + i * 1024, live ? (uint32_t)wrow(W, j0, r) * ROWB + s0 * (RB / SPW) + c * 16 : kNoLoad);
     }
-    if constexpr (WFMT == kFp4) {
+    if (WFMT == kFp4 && b0 == 0) {
       // the scales of the wave's K steps (4 SPW bytes a row, from byte 4 s0) in one LDS-direct
       // load: lane 2 r + h takes 16 bytes of row r from byte 16 h of its slice, to sslot + 32 r +
       // 16 h (the 32 - 4 SPW bytes past the slice are never read; past the resource the load
@@ -1727,9 +1743,10 @@ struct GuX {
 
 // this wave's partial C tiles of unit j0 over its K steps: t's weights against x's picks;
 // wsc the FP8 weight's block scales in LDS
-template <class C, int WFMT, bool SH>
+template <class C, int WFMT, bool SH, class StepFn>
 __device__ __forceinline__ void gu_mma(const GuTile<C, WFMT, SH>& t, const GuX<C, WFMT>& x, const float* wsc, int W,
-                                       int j0, int lane, int wave, bool scaled, f32x4 (&acc)[GuTile<C, WFMT, SH>::NA]) {
+                                       int j0, int lane, int wave, bool scaled, f32x4 (&acc)[GuTile<C, WFMT, SH>::NA],
+                                       StepFn after_step) {
   using T = GuTile<C, WFMT, SH>;
   const int s0 = wave * T::SPW;
 #pragma unroll
@@ -1754,6 +1771,7 @@ __device__ __forceinline__ void gu_mma(const GuTile<C, WFMT, SH>& t, const GuX<C
                       e8m0(x.ex[i]), acc[0], acc[1]);
       }
     }
+    after_step(i);
   }
 }
 
@@ -1824,7 +1842,7 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
       }
     }
     const unsigned long long tw0 = tl_now();
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the unit's slot, the activations, the scales
+    wait_vm0();  // the unit's slot, the activations, the scales
     TL_ADD(kTlGuWait, tl_now() - tw0);
     TL_ADD(kTlGuUnits, 1ull);
     if (u == lo) TL(kTlGuFirst);
@@ -1832,21 +1850,38 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
     const unsigned long long tf0 = tl_now();
     t.fetch(slot, sslot, lane, wave);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // read out of the slot
-    if (u + 1 < hi) {
+    // the next unit's request: spread over this unit's K steps (a share of its 1 KB blocks
+    // after each), so that its address work overlaps the MFMAs, where registers allow (not
+    // in the row-major MXFP4 shapes, whose conversions need them: 20-28 B spill); else whole
+    // before them
+    constexpr bool spread = C::FMT == kFp8 || SH;
+    const bool more = u + 1 < hi;
+    int c1 = 0, nc1 = 0;
+    if (more) {
       const int tn = (u + 1) / nb;
       if (tn != tg_w) {
         tg_w = tn;
         group(tg_w, wb, sb, np_w);
       }
-      int c1, nc1;
       half(u + 1, c1, nc1);
-      t.issue(weight_rsrc_words(wb, 2u * W * WB), srsc(sb), W, ((u + 1) % nb) * T::NC + c1, nc1, slot, sslot, lane,
-              wave);
+      if (!spread)
+        t.issue(weight_rsrc_words(wb, 2u * W * WB), srsc(sb), W, ((u + 1) % nb) * T::NC + c1, nc1, slot, sslot,
+                lane, wave);
     }
     const unsigned long long tf1 = tl_now();
     TL_ADD(kTlGuFetch, tf1 - tf0);
     f32x4 acc[T::NA];
-    gu_mma<C, WFMT, SH>(t, x, sm.m.wsc, W, j0, lane, wave, scaled, acc);
+    if constexpr (spread) {
+      const i32x4 wr1 = weight_rsrc_words(wb, 2u * W * WB), sr1 = srsc(sb);
+      const int j1 = ((u + 1) % nb) * T::NC + c1;
+      gu_mma<C, WFMT, SH>(t, x, sm.m.wsc, W, j0, lane, wave, scaled, acc, [&](int i) {
+        if (more)
+          t.issue(wr1, sr1, W, j1, nc1, slot, sslot, lane, wave, i * T::kBlocks / T::SPW,
+                  (i + 1) * T::kBlocks / T::SPW);
+      });
+    } else {
+      gu_mma<C, WFMT, SH>(t, x, sm.m.wsc, W, j0, lane, wave, scaled, acc, [](int) {});
+    }
 #pragma unroll
     for (int q = 0; q < T::NA; ++q) sm.red[q][wave][lane] = acc[q];
     const unsigned long long tf2 = tl_now();
@@ -2605,7 +2640,7 @@ __device__ __forceinline__ void shared_down_tile(const Params& p, SharedDownSmem
     // the step's shared rows, quantized once (stage Q), copied in as they lie
     ws_to_lds(p, p.off[14], (uint32_t)R * C::SQS, sm.q);
     ws_to_lds(p, p.off[15], (uint32_t)R * (C::S / 128) * 4, (uint8_t*)sm.s);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    wait_vm0();
   } else {
     // (2 chunks a thread at once with MXFP4 routed experts: 4 spill the persistent launch there)
     quant_rows_lds<kFp8, C::S, C::SQS, C::FMT == kFp4 ? 2 : kQuantBatch>(
@@ -2866,7 +2901,7 @@ __device__ __forceinline__ void copy_pick_batch(const Params& p, int pb0, int pb
   static_assert(C::MQS % 16 == 0 && SST % 16 == 0, "16-byte pieces");
   ws_to_lds(p, p.off[12] + (uint32_t)pb0 * C::MQS, (uint32_t)pbn * C::MQS, sm.q);
   ws_to_lds(p, p.off[13] + (uint32_t)pb0 * SST, (uint32_t)pbn * SST, (uint8_t*)sm.s);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  wait_vm0();
 }
 
 template <class C, bool GQ>
@@ -2958,7 +2993,7 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
     DT cur;
     for (int v = wave; v < n_units; v += kWaves) {
       const unsigned long long tw0 = tl_now();
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the unit's rows are in the slot
+      wait_vm0();  // the unit's rows are in the slot
       const unsigned long long tf0 = tl_now();
       TL_ADD(kTlDWait, tf0 - tw0);
       TL_ADD(kTlDUnits, 1ull);
@@ -3121,7 +3156,7 @@ __device__ __forceinline__ void shared_first_run(const Params& p, DownSmem<C>& s
       p, [&](int i) { return p.off[8] + (uint32_t)i * C::S * 2; }, R, sm.sd.q, sm.sd.s);
   __syncthreads();
   if (v >= 0 && v < 2 && v * 16 < hn) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the unit's rows are in the slot
+    wait_vm0();  // the unit's rows are in the slot
     DT cur;
     cur.fetch(sm.wslot[wave], lane);
     cur.take_scales(sh, h0 + v * 16, lane);
