@@ -1643,10 +1643,15 @@ struct GuTile {
       if (b0 == 0) lds_dma16_cached(sr, sslot, (uint32_t)b * C::H + (s0 / 2) * 256 + lane * 16);
       return;
     }
+    // (MXFP4: a lane index the compiler cannot see through, so that a request spread over the
+    // K steps computes each block's address where it is issued instead of holding them all,
+    // which spilled 20-28 B)
+    int ln = lane;
+    if (WFMT == kFp4 && (b0 > 0 || b1 < kBlocks)) asm volatile("" : "+v"(ln));
 #pragma unroll
     for (int i = 0; i < SLOT / 1024; ++i) {
       if (i < b0 || i >= b1) continue;
-      const int pos = i * 64 + lane, r = pos / CPW, c = (pos % CPW) ^ key(r);
+      const int pos = i * 64 + ln, r = pos / CPW, c = (pos % CPW) ^ key(r);
       const bool live = (WFMT == kFp8 ? (r & 7) : (r & 15)) < nc;
       lds_dma16(wr, slot + i * 1024, live ? (uint32_t)wrow(W, j0, r) * ROWB + s0 * (RB / SPW) + c * 16 : kNoLoad);
     }
@@ -1850,11 +1855,8 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
     const unsigned long long tf0 = tl_now();
     t.fetch(slot, sslot, lane, wave);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // read out of the slot
-    // the next unit's request: spread over this unit's K steps (a share of its 1 KB blocks
-    // after each), so that its address work overlaps the MFMAs, where registers allow (not
-    // in the row-major MXFP4 shapes, whose conversions need them: 20-28 B spill); else whole
-    // before them
-    constexpr bool spread = C::FMT == kFp8 || SH;
+    // the next unit's request, spread over this unit's K steps (a share of its 1 KB blocks
+    // after each step's MFMAs), so that the wave's loads queue behind one another less
     const bool more = u + 1 < hi;
     int c1 = 0, nc1 = 0;
     if (more) {
@@ -1864,24 +1866,16 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
         group(tg_w, wb, sb, np_w);
       }
       half(u + 1, c1, nc1);
-      if (!spread)
-        t.issue(weight_rsrc_words(wb, 2u * W * WB), srsc(sb), W, ((u + 1) % nb) * T::NC + c1, nc1, slot, sslot,
-                lane, wave);
     }
+    const i32x4 wr1 = weight_rsrc_words(wb, 2u * W * WB), sr1 = srsc(sb);
+    const int j1 = ((u + 1) % nb) * T::NC + c1;
     const unsigned long long tf1 = tl_now();
     TL_ADD(kTlGuFetch, tf1 - tf0);
     f32x4 acc[T::NA];
-    if constexpr (spread) {
-      const i32x4 wr1 = weight_rsrc_words(wb, 2u * W * WB), sr1 = srsc(sb);
-      const int j1 = ((u + 1) % nb) * T::NC + c1;
-      gu_mma<C, WFMT, SH>(t, x, sm.m.wsc, W, j0, lane, wave, scaled, acc, [&](int i) {
-        if (more)
-          t.issue(wr1, sr1, W, j1, nc1, slot, sslot, lane, wave, i * T::kBlocks / T::SPW,
-                  (i + 1) * T::kBlocks / T::SPW);
-      });
-    } else {
-      gu_mma<C, WFMT, SH>(t, x, sm.m.wsc, W, j0, lane, wave, scaled, acc, [](int) {});
-    }
+    gu_mma<C, WFMT, SH>(t, x, sm.m.wsc, W, j0, lane, wave, scaled, acc, [&](int i) {
+      if (more)
+        t.issue(wr1, sr1, W, j1, nc1, slot, sslot, lane, wave, i * T::kBlocks / T::SPW, (i + 1) * T::kBlocks / T::SPW);
+    });
 #pragma unroll
     for (int q = 0; q < T::NA; ++q) sm.red[q][wave][lane] = acc[q];
     const unsigned long long tf2 = tl_now();
