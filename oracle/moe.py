@@ -27,10 +27,21 @@ restatement (the kernel's order) rather than the golden's unordered fp32
 matmul; the golden's own routing is kept as ``routing_golden`` for the
 cross-check the reference makes (check_ffn.py:321-322,341).
 
-Parity pins (tests/test_oracle_moe.py): each expert GEMM against an fp64
-matmul of the dequantized operands; the combine order against a
-hand-computed two-pick case; invariants (a zero shared expert leaves the
-routed sum; an expert picked by no token is never read).
+Parity pins:
+- tests/test_oracle_moe.py: the whole partial (both forms) on a crafted layer
+  whose every value is a short dyadic number, against output bits worked out by
+  hand: the routed SwiGLU rounded once after the product, the shared one at
+  gate, up and product, the clamp, the combine in top-k order with bf16 at every
+  add, then the shared output added; each misplaced rounding point or order,
+  planted in the oracle, changes those bits (``combine``,
+  ``swiglu_*_golden``, ``oracle.exact.swiglu_*``). Also the block against an
+  fp64 evaluation of the same quantized operands, and an unpicked expert never
+  read.
+- tests/test_oracle_routing_golden.py: ``routing_golden`` (the golden's fp32
+  matmul and torch's score) against the fixed-order routing on every benchmark
+  workload's seeds: the same ids everywhere (a disagreement would be allowed
+  only between choices within the two routings' measured logit errors), the
+  weights within 1e-4; the fixed-order logits within their order's error bound.
 """
 
 from __future__ import annotations
@@ -67,14 +78,54 @@ def silu(x: torch.Tensor) -> torch.Tensor:
     return F.silu(x)
 
 
+def swiglu_routed_golden(g: torch.Tensor, u: torch.Tensor, lim: float) -> torch.Tensor:
+    """A routed expert's SwiGLU as the golden rounds it: bf16 once, after the product
+    (``mid = bf(F.silu(gate.clamp(max=LIMIT)) * up.clamp(-LIMIT, LIMIT))``, check_ffn.py:220)."""
+    return fm.bf(silu(g.clamp(max=lim)) * u.clamp(-lim, lim))
+
+
+def swiglu_shared_golden(g: torch.Tensor, u: torch.Tensor, lim: float) -> torch.Tensor:
+    """The shared expert's SwiGLU as the golden rounds it: bf16 at the clamped gate, at the
+    clamped up and at the product (check_ffn.py:227-230)."""
+    return fm.bf(silu(fm.bf(g.clamp(max=lim))) * fm.bf(u.clamp(-lim, lim)))
+
+
+def combine(per_k: torch.Tensor, shared: torch.Tensor):
+    """The weighted combine (check_ffn.py:223-225,232): the picks' bf16 contributions
+    ``per_k`` [R, k, H] added in top-k order from 0 with bf16 at every add, then the shared
+    expert's bf16 output added and rounded once more -> (out bf16 [R, H], the largest
+    magnitude the bf16 chain held, fp32 [R, H])."""
+    r, topk, h = per_k.shape
+    routed = torch.zeros(r, h)
+    chain = torch.zeros(r, h)
+    for k in range(topk):
+        routed = fm.bf(routed + per_k[:, k])
+        chain = torch.maximum(chain, routed.abs())
+    out = fm.bf(routed + shared).to(torch.bfloat16)
+    return out, torch.maximum(chain, out.float().abs())
+
+
 def routing_golden(x: torch.Tensor, gate_w: torch.Tensor, bias: torch.Tensor, p: dict):
-    """The golden's unordered fp32 routing (check_ffn.py:201-206), sigmoid grouped form."""
+    """The golden's own routing (check_ffn.py:201-206): logits by an fp32 matmul of
+    unspecified order, the score by torch (``F.softplus(l).sqrt()`` for V4.1, ``torch.sigmoid``
+    for the grouped DeepSeek-V3 presets), selection on score + bias (``topk`` of torch over one
+    group; ``rt.grouped_topk`` over several), weights score * (scale / sum) -> (ids int32
+    [R, k], weights fp32 [R, k], logits fp32 [R, E])."""
     logits = x.float() @ gate_w.float().T
-    sc = torch.sigmoid(logits)
-    ids, _ = rt.grouped_topk(
-        sc.numpy(), bias.float().numpy(), p["topk"], p["n_group"], p["topk_group"], p["routed_scale"]
+    if p.get("scoring", "sigmoid") == "sqrt_softplus":
+        sc = F.softplus(logits).sqrt()
+    else:
+        sc = torch.sigmoid(logits)
+    scale = float(p["routed_scale"])
+    if p["n_group"] == 1:
+        ids = (sc + bias.float()).topk(p["topk"], dim=1).indices
+        wt = sc.gather(1, ids)
+        wts = wt * (scale / wt.sum(1, keepdim=True)) if p.get("renorm", True) else wt * scale
+        return ids.numpy().astype(np.int32), wts.numpy().astype(np.float32), logits.numpy()
+    ids, wts = rt.grouped_topk(
+        sc.numpy(), bias.float().numpy(), p["topk"], p["n_group"], p["topk_group"], scale, p.get("renorm", True)
     )
-    return ids
+    return ids, wts, logits.numpy()
 
 
 class ExpertSource:
@@ -121,7 +172,7 @@ def expert_contrib(tensors, xin_rows: torch.Tensor, w_rows: torch.Tensor, p: dic
         xr = act_qdq(xin_rows, fmt)
         hh = xr @ deq_weight(w13, w13_s, fmt).T
         gate, up = hh[:, :inter], hh[:, inter:]
-        mid = fm.bf(silu(gate.clamp(max=lim)) * up.clamp(-lim, lim))
+        mid = swiglu_routed_golden(gate, up, lim)
         y = act_qdq(mid, fmt) @ deq_weight(w2, w2_s, fmt).T
     return fm.bf(y * w_rows[:, None])
 
@@ -199,11 +250,6 @@ def moe_partial(x: torch.Tensor, w: dict, p: dict, experts=None, exact: bool = T
             per_k[rows, ks] = expert_contrib(experts.get(e), xin[rows], wts[rows, ks], p, exact)
     if exact:
         xq2, xs2 = fm.group_fp8_quant(xin, 128)
-    routed = torch.zeros(r, h)
-    chain = torch.zeros(r, h)  # the largest magnitude the combine's bf16 chain holds
-    for k in range(topk):
-        routed = fm.bf(routed + per_k[:, k])
-        chain = torch.maximum(chain, routed.abs())
     if ish > 0 and exact:
         hs = ex.gemv_fp8_b128(w["sgu"], w["sgu_s"], xq2, xs2)
         smid = ex.swiglu_shared(hs[:, :ish], hs[:, ish:], lim)
@@ -212,12 +258,11 @@ def moe_partial(x: torch.Tensor, w: dict, p: dict, experts=None, exact: bool = T
     elif ish > 0:
         xs_ = act_qdq(xin, FP8_B128)
         hs = xs_ @ fm.deq_fp8_b128(w["sgu"], w["sgu_s"]).T
-        smid = fm.bf(silu(fm.bf(hs[:, :ish].clamp(max=lim))) * fm.bf(hs[:, ish:].clamp(-lim, lim)))
+        smid = swiglu_shared_golden(hs[:, :ish], hs[:, ish:], lim)
         shared = fm.bf(act_qdq(smid, FP8_B128) @ fm.deq_fp8_b128(w["sw2"], w["sw2_s"]).T)
     else:
         shared = torch.zeros(r, h)
-    out = fm.bf(routed + shared).to(torch.bfloat16)
-    chain = torch.maximum(chain, out.float().abs())
+    out, chain = combine(per_k, shared)
     return {
         "chain_max": chain,
         "ids": ids_np,

@@ -52,26 +52,185 @@ def test_golden_against_fp64(fmt):
     assert rel < 2e-2, rel
 
 
-def test_combine_order_two_picks():
-    """bf16 at every add, in top-k order: each step rounds, unlike the fp32 sum rounded once."""
-    a = torch.tensor([1.0])
-    b = torch.tensor([3 * 2.0**-10])  # exact in bf16; below half a bf16 ulp of 1.0 (2^-8)
-    routed = torch.zeros(1)
-    for v in (a, b, b):
-        routed = fm.bf(routed + fm.bf(v))
-    assert float(routed) == 1.0  # each add rounds back to 1.0
-    assert float(fm.bf(a + 2 * b)) == 1.0078125  # the one-shot sum crosses half an ulp
+# ---------------------------------------------------------------- moe_partial, crafted bits
+# A layer built so that every value moe_partial computes is a short dyadic number: the
+# router weight is zero (every logit 0, every score sigmoid(0) = 1/2, so the bias -e / 1000
+# picks experts 0, 1, 2, 3 in that order, each weighing 1/2 * 2.0 / 2.0 = 1/2); x rows are
+# (448, v, t, 0, ...), whose group-128 FP8 scale is 448 / 448 = 1 exactly, so the codes are x;
+# every weight and block scale is an e4m3 value or 1. A gate row holds (A, B) at K 0, 1 and
+# its up row (C, 0, D) at K 0..2, so gate = 448 A + v B and up = 448 C + t D exactly; the
+# intermediate is nonzero in column 0 only, its requantized code is 448 and the down row
+# (1 at K 0, for output columns 0..7) gives it back: each pick contributes bf16(mid / 2), the
+# shared expert its smid. The values were searched so that each plausible misplacement of a
+# rounding point (test_moe_partial_crafted_catches) changes at least one row's bits.
+CRAFT = dict(
+    hidden=1024, experts=16, topk=4, n_group=1, topk_group=1, inter=128, shared_inter=128,
+    routed_fmt="fp8_b128", routed_scale=2.0, swiglu_limit=10.0, router_parts=2, norm_eps=None,
+    renorm=True, scoring="sigmoid",
+)  # fmt: skip
+CRAFT_ROWS = ((0.3125, 0.875), (2.25, 4.0), (0.46875, 0.6875), (0.029296875, 1.875))  # (v, t)
+CRAFT_SHARED = (0.0078125, -0.8125, 0.01953125, -0.4375)  # (A, B, C, D)
+CRAFT_ROUTED = (  # experts 0..3
+    (-0.015625, 0.0546875, -0.017578125, -7.0),
+    (0.005859375, -2.5, -0.029296875, -0.03515625),
+    (0.021484375, -0.021484375, 0.02734375, 1.125),
+    (0.04296875, 0.001953125, -0.05078125, -0.234375),
+)
+# Worked by hand, row 0 (v 0.3125, t 0.875):
+#   shared: g = 448 * 2^-7 - 0.3125 * 0.8125 = 3.24609375, bf16 3.25; u = 448 * 0.01953125 -
+#     0.875 * 0.4375 = 8.3671875, bf16 8.375; smid = bf16(silu(3.25) * 8.375) = bf16(26.2028) = 26.25
+#   expert 0: g = -6.98291015625, u = -14 (clamps to -10): mid = bf16(silu(g) * -10) = bf16(0.064713)
+#     = 0.06494140625
+#   expert 1: g = 1.84375, u = -13.15576171875 (-10): mid = bf16(-15.91878) = -15.9375
+#   expert 2: g = 9.6182861328125, u = 13.234375 (10): mid = bf16(96.1765) = 96
+#   expert 3: g = 19.25... (10), u = -22.95... (-10): mid = bf16(-99.99546) = -100
+#   contributions mid / 2 in top-k order: 0.032470703125, -7.96875, 48, -50
+#   chain: 0.032470703125; bf16(-7.936279296875) = -7.9375; bf16(40.0625) = 40 (the 0.25 grid of
+#     [32, 64)); bf16(40 - 50) = -10; out = bf16(-10 + 26.25) = 16.25
+#   rows 1-3 likewise: 8.625, 17.5, 13. Each mistake of MISTAKES changes at least one row.
+CRAFT_OUT_BITS = (0x4182, 0x410A, 0x418C, 0x4150)  # out[r, 0:8] (16.25, 8.625, 17.5, 13); 0 elsewhere
 
 
-def test_zero_shared_expert_leaves_routed():
-    p = dict(TINY, routed_fmt="fp8_b128")
-    x, w, ex = _inputs(p, 3, seed=2)
-    w0 = dict(w, sw2=torch.zeros_like(w["sw2"]))
-    res = om.moe_partial(x, w0, p, experts=ex)
-    routed = torch.zeros(3, p["hidden"])
-    for k in range(p["topk"]):
-        routed = fm.bf(routed + res["per_k"][:, k])
-    assert torch.equal(res["out"].float(), routed)
+def _craft_layer():
+    from oracle import formats as fm
+
+    p = dict(CRAFT)
+    h, e, i, s = p["hidden"], p["experts"], p["inter"], p["shared_inter"]
+    x = torch.zeros(len(CRAFT_ROWS), h)
+    x[:, 0] = 448.0
+    for r, (v, t) in enumerate(CRAFT_ROWS):
+        x[r, 1], x[r, 2] = v, t
+
+    def gate_up(a, b, c, d, n):
+        w = torch.zeros(2 * n, h)
+        w[0, 0], w[0, 1], w[n, 0], w[n, 2] = a, b, c, d
+        return fm.e4m3_codes_from_f32(w)
+
+    down = torch.zeros(h, i)
+    down[:8, 0] = 1.0
+    w = {
+        "gate_w": torch.zeros(e, h, dtype=torch.bfloat16),
+        "bias": -torch.arange(e, dtype=torch.float32) / 1000,
+        "sgu": gate_up(*CRAFT_SHARED, s),
+        "sgu_s": torch.ones(2 * s // 128, h // 128),
+        "sw2": fm.e4m3_codes_from_f32(down),
+        "sw2_s": torch.ones(h // 128, s // 128),
+    }
+    w13 = torch.zeros(e, 2 * i, h, dtype=torch.uint8)
+    for k, abcd in enumerate(CRAFT_ROUTED):
+        w13[k] = gate_up(*abcd, i)
+    w2 = fm.e4m3_codes_from_f32(down)[None].repeat(e, 1, 1)
+    src = om.ExpertSource(w13, torch.ones(e, 2 * i // 128, h // 128), w2, torch.ones(e, h // 128, i // 128))
+    return p, x.to(torch.bfloat16), w, src
+
+
+def _craft_bits(out):
+    return [int(v) & 0xFFFF for v in out.view(torch.int16)[:, 0].tolist()]
+
+
+@pytest.mark.parametrize("exact", [True, False])
+def test_moe_partial_crafted_bits(exact):
+    """moe_partial on the crafted layer: routing, and every output element's bits, as worked
+    out by hand (CRAFT_OUT_BITS): the routed SwiGLU rounds once after the product, the shared
+    SwiGLU at gate, up and product, the combine adds in top-k order with bf16 at every add and
+    then adds the shared output (check_ffn.py:216-232)."""
+    p, x, w, src = _craft_layer()
+    res = om.moe_partial(x, w, p, experts=src, exact=exact)
+    assert res["ids"].tolist() == [[0, 1, 2, 3]] * len(CRAFT_ROWS)
+    assert np.all(res["weights"] == np.float32(0.5))
+    out = res["out"]
+    assert _craft_bits(out) == list(CRAFT_OUT_BITS)
+    assert torch.equal(out[:, :8], out[:, :1].expand(-1, 8)) and not out[:, 8:].float().any()
+    assert res["per_k"][0, :, 0].tolist() == [0.032470703125, -7.96875, 48.0, -50.0]
+
+
+def _one_shot(per_k, shared):
+    routed = per_k.sum(1)
+    return om.fm.bf(routed + shared).to(torch.bfloat16), routed.abs()
+
+
+_COMBINE = om.combine
+
+
+def _reversed(per_k, shared):
+    return _COMBINE(per_k.flip(1), shared)
+
+
+def _shared_first(per_k, shared):
+    acc = shared.clone()
+    for k in range(per_k.shape[1]):
+        acc = om.fm.bf(acc + per_k[:, k])
+    return acc.to(torch.bfloat16), acc.abs()
+
+
+def _no_per_add_round(per_k, shared):
+    routed = torch.zeros_like(shared)
+    for k in range(per_k.shape[1]):
+        routed = routed + per_k[:, k]
+    return om.fm.bf(routed + shared).to(torch.bfloat16), routed.abs()
+
+
+def _np_bf(a):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16).float().numpy()
+
+
+MISTAKES = {
+    # the combine
+    "one_shot_sum": ("combine", _one_shot),
+    "reversed_order": ("combine", _reversed),
+    "shared_added_first": ("combine", _shared_first),
+    "no_bf16_per_add": ("combine", _no_per_add_round),
+    # the shared SwiGLU (exact path: oracle.exact; golden path: oracle.moe)
+    "shared_as_routed_rule": ("swiglu_shared", lambda g, u, lim: _routed_rule(g, u, lim)),
+    "shared_gate_not_rounded": ("swiglu_shared", lambda g, u, lim: _shared_rule(g, u, lim, gate=False)),
+    "shared_up_not_rounded": ("swiglu_shared", lambda g, u, lim: _shared_rule(g, u, lim, up=False)),
+    "shared_silu_rounded": ("swiglu_shared", lambda g, u, lim: _shared_rule(g, u, lim, silu_bf=True)),
+    # the routed SwiGLU
+    "routed_as_shared_rule": ("swiglu_routed", lambda g, u, lim: _shared_rule(g, u, lim)),
+    "routed_silu_rounded": ("swiglu_routed", lambda g, u, lim: _routed_rule(g, u, lim, silu_bf=True)),
+    "routed_no_clamp": ("swiglu_routed", lambda g, u, lim: _routed_rule(g, u, 1e30)),
+}
+
+
+def _silu_np(z):
+    z = np.asarray(z, np.float32)
+    return (z / (np.float32(1) + np.exp(-z.astype(np.float64)))).astype(np.float32)
+
+
+def _routed_rule(g, u, lim, silu_bf=False):
+    g, u = np.asarray(g, np.float32), np.asarray(u, np.float32)
+    s = _silu_np(np.minimum(g, np.float32(lim)))
+    s = _np_bf(s) if silu_bf else s
+    return _np_bf(s * np.clip(u, -np.float32(lim), np.float32(lim)))
+
+
+def _shared_rule(g, u, lim, gate=True, up=True, silu_bf=False):
+    g, u = np.asarray(g, np.float32), np.asarray(u, np.float32)
+    gg = np.minimum(g, np.float32(lim))
+    uu = np.clip(u, -np.float32(lim), np.float32(lim))
+    s = _silu_np(_np_bf(gg) if gate else gg)
+    s = _np_bf(s) if silu_bf else s
+    return _np_bf(s * (_np_bf(uu) if up else uu))
+
+
+@pytest.mark.parametrize("exact", [True, False])
+@pytest.mark.parametrize("mistake", sorted(MISTAKES))
+def test_moe_partial_crafted_catches(mistake, exact, monkeypatch):
+    """Each plausible misplacement of a rounding point, planted in the oracle, changes the
+    crafted layer's bits: the crafted case pins moe_partial's combine and both SwiGLU rules."""
+    from oracle import exact as ex
+
+    what, fn = MISTAKES[mistake]
+    if what == "combine":
+        monkeypatch.setattr(om, "combine", fn)
+    elif exact:
+        monkeypatch.setattr(ex, what, fn)
+    else:
+        golden = {"swiglu_shared": "swiglu_shared_golden", "swiglu_routed": "swiglu_routed_golden"}[what]
+        monkeypatch.setattr(om, golden, lambda g, u, lim: torch.from_numpy(fn(g.numpy(), u.numpy(), lim)))
+    p, x, w, src = _craft_layer()
+    out = om.moe_partial(x, w, p, experts=src, exact=exact)["out"]
+    assert _craft_bits(out) != list(CRAFT_OUT_BITS)
 
 
 def test_unpicked_experts_never_read():
