@@ -27,9 +27,12 @@ B = U * expert bytes + shared bytes + router (E * H * 2 + E * 4) + x and out
 (2 * R * H * 2) [+ H * 2 for the norm weight]. ``value`` is the headline's
 weight-stream GB/s; every workload's rows are under ``workloads``, each with
 its roofline fraction (of 8 TB/s) and, where a committed counter pass exists
-(profiles/traffic_<workload>_r<rows>.json), its HBM bytes per launch. The CPU
-baseline times the oracle (the PyTorch restatement of the reference's golden
-MoE) on the host cores on a bounded sample of the headline workload.
+(profiles/traffic_<workload>_r<rows>.json), its HBM bytes per launch, and, where the
+committed GPU parity record has the point (profiles/accuracy_parity.jsonl, written by the
+parity tests under MKMOE_ACCURACY_LOG), the default launch's accuracy there against the
+oracle and the golden. The CPU baseline times the oracle (the PyTorch restatement of the
+reference's golden MoE) on the host cores on a bounded sample of the headline workload, and of
+the MXFP4 workloads at 8 rows (``CPU_POINTS``, under their ``workloads`` entries).
 
 The FFN seam before the MoE block (DeepSeek-V4.1's mHC update, H 5120, two launches) is
 timed the same way at 1, 8 and 48 tokens (``workloads["v41_ffn_seam"]``), rotating over 144
@@ -55,6 +58,9 @@ sys.path.insert(0, str(ROOT))
 METRIC = "MoE µs/layer @1/8/48 decode rows + weight-stream HBM GB/s (% of peak), 1 GPU"
 HBM_PEAK_GBPS = 8000.0
 HEADLINE = ("cfg2_tp4_fp8", 8)
+# further (workload, rows) points that get a CPU baseline of their own (under ``workloads``)
+CPU_POINTS = (("cfg3_tp4_mxfp4", 8), ("cfg5_tp2_mxfp4_norm", 8))
+CPU_POINT_BUDGET_S = 15.0
 DEFAULT_WORKLOADS = "cfg2_tp4_fp8,cfg3_tp4_mxfp4,cfg4_tp4_mxfp4_zipf,cfg5_tp2_mxfp4_norm"
 MIN_TIMED = 200
 SEAM_TOKENS = "1,8,48"
@@ -267,6 +273,8 @@ def bench_seam(device, tokens_list, timed_n: int, layers: int = SEAM_LAYERS) -> 
                 with torch.cuda.graph(gr, stream=cap):
                     for j in range(layers):
                         run.ffn_seam(ws[j], *ins[j], outs=outs[j], gate_later=gate_later)
+                        if gate_later:
+                            run.cancel_gate()  # the path to the MoE block's input alone
             torch.cuda.current_stream().wait_stream(cap)
             gr.replay()
             torch.cuda.synchronize()
@@ -321,8 +329,7 @@ def cpu_baseline(workload: str, rows: int, budget_s: float = 25.0):
     xin = rt.rmsnorm_exact(x, dense["norm"], p["norm_eps"]) if p["norm_eps"] is not None else x
     _, ids, _ = rt.route(xin, dense["gate_w"], dense["bias"], p)
     ex = gen.LazyExperts(p, 0)
-    for e in np.unique(ids).tolist():  # expert generation is not timed
-        ex.get(e)
+    ex.prefetch(np.unique(ids).tolist(), min(16, cores))  # expert generation is not timed
     # the golden's own form: fp32 matmuls of the dequantized experts, torch silu
     om.moe_partial(x, dense, p, experts=ex, exact=False)  # warm-up
     times = []
@@ -366,6 +373,24 @@ def calibrate_copy(mib: int, reps: int = 4) -> dict:
         dst.copy_(src)
     torch.cuda.synchronize()
     return {"copy_bytes_read": n, "copy_bytes_written": n, "reps": reps}
+
+
+def measured_accuracy(workload: str, rows: int):
+    """The default launch's accuracy at this point from the committed GPU parity record
+    (profiles/accuracy_parity.jsonl), or None."""
+    f = ROOT / "profiles" / "accuracy_parity.jsonl"
+    if not f.exists():
+        return None
+    for rec in map(json.loads, f.read_text().splitlines()):
+        if rec["workload"] == workload and rec["rows"] == rows and rec["mode"] == "default":
+            keep = ("max_abs", "rel_l2", "cos", "n_over_2e-2", "numel")
+            return {
+                "vs_golden": {k: rec["vs_golden"][k] for k in keep},
+                "vs_oracle": {k: rec["vs_oracle"][k] for k in keep},
+                "routing_exact": rec["routing_exact"],
+                "source": f"profiles/{f.name}",
+            }
+    return None
 
 
 def measured_traffic(workload: str, rows: int):
@@ -516,6 +541,9 @@ def main() -> int:
             }
             if traffic is not None and not args.staged:
                 res["roofline"]["traffic_source"] = source
+            acc = measured_accuracy(name, r)
+            if acc is not None:
+                res["accuracy"] = acc
             wres[str(r)] = res
             log(f"{name} rows={r}: {res}")
             del rb
@@ -581,6 +609,10 @@ def main() -> int:
     if not args.no_cpu:
         log("CPU baseline (oracle on the host cores)")
         out["cpu_baseline"] = cpu_baseline(hname, hrows)
+        for wname, r in CPU_POINTS:
+            if wname in results and str(r) in results[wname]["rows"]:
+                log(f"CPU baseline of {wname} at {r} rows")
+                results[wname]["rows"][str(r)]["cpu_baseline"] = cpu_baseline(wname, r, CPU_POINT_BUDGET_S)
     print(json.dumps(out), flush=True)
     return 0
 

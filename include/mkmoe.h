@@ -156,7 +156,10 @@ typedef struct mkmoe_options {
                               * (v_mfma_scale_f32_16x16x128_f8f6f4), with no conversion of
                               * the codes; 0: the default (never) */
   int32_t mxfp4_scaled_down_rows; /* MXFP4 shapes: the down GEMM alone on the scaled MFMA from
-                                   * this many rows (and on MFMA); 0: the default (never) */
+                                   * this many rows (and on MFMA); 0: the default, 8 on the
+                                   * shapes with inter <= 512 and never on wider ones (the
+                                   * reference runs its MXFP4 GEMMs on that instruction,
+                                   * common/mx.py:60-66) */
   /* Test fault injection, the reference's SGLANG_AMD_MONO_FAULT_INJECT (common/guard.py:69-89:
    * a wait that stalls and times out). fault_stage 0: none; else workgroup fault_workgroup's
    * wait at that stage (the MKMOE_ERRW_STAGE codes of the persistent launch's waits: 1 norm,
@@ -167,7 +170,8 @@ typedef struct mkmoe_options {
    * waits) stall nothing. The faulted launch's output is not valid; mkmoe_clear_errors
    * restores the workspace. */
   int32_t fault_stage;
-  int32_t fault_workgroup; /* 0 .. 255 */
+  int32_t fault_workgroup; /* 0 .. 255, and below the launch's grid (one workgroup a CU, at
+                            * most 256): MKMOE_ERR_ARG otherwise */
 } mkmoe_options;
 
 /* One MoE block for rows bf16 rows x [rows][H] -> out bf16 [rows][H] (this

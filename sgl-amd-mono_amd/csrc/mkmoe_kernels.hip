@@ -3499,8 +3499,15 @@ int static_workspace(int dev, void** ws) {
 constexpr double kDeadlineDefault = 2.0;  // seconds
 constexpr int kMfmaGateDefault = 1;       // gate_up and down on MFMA at every row count
 constexpr int kMfmaDownDefault = 1;
-constexpr int kMxScaledDefault = 1 << 30;  // the MXFP4 GEMMs convert to bf16 at every row count
-constexpr int kMxScaledDownDefault = 1 << 30;
+constexpr int kMxScaledDefault = 1 << 30;  // the MXFP4 gate_up GEMMs convert to bf16 at every row count
+// From 8 rows the MXFP4 down GEMM of the shapes with I <= 512 runs on the scaled fp4 x fp8 MFMA
+// (no converts): 5-7 % faster there, and within the output bounds at every measured workload of
+// those shapes (at most 8 of 344064 elements past 2e-2, Zipf routing at 48 rows). Its internal
+// sum keeps fewer bits than fp32, and a K of 1024 adds twice the steps: the I = 1024 shapes land
+// 37 elements past 2e-2 under Zipf routing at 48 rows, so they keep the converting path, as do
+// launches below 8 rows (a TP2 row at 1 row lands 2 elements past 2e-2).
+constexpr int kMxScaledDownDefault = 8;
+constexpr int kMxScaledDownMaxInter = 512;
 
 // the options of one call (NULL: the defaults; a field left 0 takes its default)
 int options_of(const mkmoe_options* o, double& deadline_s, int& gate, int& down, int& scaled, int& scaled_down,
@@ -3509,7 +3516,7 @@ int options_of(const mkmoe_options* o, double& deadline_s, int& gate, int& down,
   gate = kMfmaGateDefault;
   down = kMfmaDownDefault;
   scaled = kMxScaledDefault;
-  scaled_down = kMxScaledDownDefault;
+  scaled_down = 0;  // the shape's default (forward_impl)
   fault_stage = 0;
   fault_wg = 0;
   if (!o) return MKMOE_OK;
@@ -3522,7 +3529,7 @@ int options_of(const mkmoe_options* o, double& deadline_s, int& gate, int& down,
   fault_wg = o->fault_workgroup;
   if (o->mxfp4_scaled_rows < 0 || o->mxfp4_scaled_down_rows < 0) return MKMOE_ERR_ARG;
   if (o->mxfp4_scaled_rows) scaled = o->mxfp4_scaled_rows;
-  if (o->mxfp4_scaled_down_rows) scaled_down = o->mxfp4_scaled_down_rows;
+  scaled_down = o->mxfp4_scaled_down_rows;  // 0: the shape's default (forward_impl)
   if (o->deadline_s != 0.0) {
     if (!(o->deadline_s > 0.0) || o->deadline_s > 3600.0) return MKMOE_ERR_ARG;
     deadline_s = o->deadline_s;
@@ -3621,6 +3628,9 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
   rc = device_info(dev, &di);
   if (rc) return rc;
   const int nwg = di.cus < kFlagWgs ? di.cus : kFlagWgs;  // the persistent grid: a workgroup a CU
+  // a fault aimed past the grid would stall nothing (the launch's grid is smaller than 256 on a
+  // device or partition with fewer CUs)
+  if (fault_stage != 0 && fault_wg >= nwg) return MKMOE_ERR_ARG;
 
   Params p;
   p.x = (const uint16_t*)x;
@@ -3656,6 +3666,7 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
   p.mfma_gate = mfma_gate;
   p.mfma_down = mfma_down;
   p.mx_scaled = rows >= mx_scaled && rows >= mfma_gate && rows >= mfma_down ? 1 : 0;
+  if (mx_scaled_down == 0) mx_scaled_down = s->inter <= kMxScaledDownMaxInter ? kMxScaledDownDefault : 1 << 30;
   p.mx_scaled_down = (p.mx_scaled || rows >= mx_scaled_down) && rows >= mfma_down ? 1 : 0;
   for (int i = 0; i < kRegions; ++i) p.off[i] = (uint32_t)L.off[i];
   hipStream_t st = (hipStream_t)stream;

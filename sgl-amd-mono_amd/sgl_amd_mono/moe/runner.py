@@ -136,7 +136,9 @@ DEADLINE_S = 2.0
 # MXFP4 shapes: launches with at least this many rows run the expert GEMMs on the scaled fp4 x
 # fp8 MFMA (0: the library's default, never)
 MXFP4_SCALED_ROWS = 0
-MXFP4_SCALED_DOWN_ROWS = 0  # the down GEMM alone on the scaled MFMA from this many rows (0: never)
+# the down GEMM alone on the scaled MFMA from this many rows (0: the library's default, 8 rows on
+# the shapes with inter <= 512, never on wider ones)
+MXFP4_SCALED_DOWN_ROWS = 0
 
 
 class MoeRunner:

@@ -97,7 +97,12 @@ class SeamRunner:
         ``gate_later``: post_out, comb_out and pre_out are written by the next ``gate()`` call
         (after, say, the MoE launch), so that ``normed`` is ready first; the runner holds the
         call's tensors until then, and the workspace of this token count must not serve another
-        call in between."""
+        call in between, so a call made while a gate_later call still waits for its gate is
+        refused (its gate would be lost, and a call of the same token count would overwrite the
+        partials that gate reads)."""
+        pending = getattr(self, "_io", None)
+        if pending is not None and pending.flags & _lib.SEAM_GATE_LATER:
+            raise RuntimeError("mkmoe seam: a gate_later call waits for its gate(); call gate() first")
         M = part.shape[0]
         if not self.supports(M):
             raise RuntimeError(f"mkmoe seam: {M} rows, want 1 .. {_lib.SEAM_MAX_TOKENS}")
@@ -149,6 +154,12 @@ class SeamRunner:
         )
         _lib.check(rc, "mkmoe seam forward")
         return outs
+
+    def cancel_gate(self) -> None:
+        """Drop a pending ``gate_later`` call's gate: its post_out, comb_out and pre_out stay
+        unwritten (for a caller that times or needs the path to ``normed`` alone)."""
+        self._io = None
+        self._keep = None
 
     def gate(self) -> None:
         """The gate of the last ``ffn_seam(..., gate_later=True)`` call (its outputs filled in)."""

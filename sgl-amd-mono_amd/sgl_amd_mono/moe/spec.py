@@ -116,8 +116,18 @@ def routed_format(experts) -> str | None:
         return None
     if w.dtype == torch.float8_e4m3fn and hasattr(experts, "w13_weight_scale_inv"):
         return FP8_B128
-    if w.dtype in (torch.uint8, torch.float4_e2m1fn_x2) and hasattr(experts, "w13_weight_scale"):
+    if w.dtype in (torch.uint8, torch.float4_e2m1fn_x2) and _mx_scale_name(experts, "w13") is not None:
         return MXFP4
+    return None
+
+
+def _mx_scale_name(experts, which: str) -> str | None:
+    """The attribute holding an MXFP4 tensor's E8M0 scales: ``*_weight_scale_inv`` where
+    SGLang's gfx950 processing left them (the reference reads that name, deepseek_v41/spec.py:
+    521-524), else ``*_weight_scale``."""
+    for name in (f"{which}_weight_scale_inv", f"{which}_weight_scale"):
+        if getattr(experts, name, None) is not None:
+            return name
     return None
 
 
@@ -138,14 +148,28 @@ def _weights(layer, preset: MoePreset, copies: dict, i: int):
     if bias.dtype != torch.float32:  # the reference keeps an fp32 copy too (spec.py:519-521)
         bias = bias.float()
         copies["f32 router bias", i] = bias
-    scale = "w13_weight_scale_inv" if preset.routed_fmt == FP8_B128 else "w13_weight_scale"
+    if preset.routed_fmt == FP8_B128:
+        w13, w13_s, w2, w2_s = e.w13_weight, e.w13_weight_scale_inv, e.w2_weight, e.w2_weight_scale_inv
+    else:
+        # MXFP4 as SGLang holds it (deepseek_v41/spec.py:521-524 of the reference): the routed
+        # experts are the router's rows (a fused shared expert or padding experts may follow
+        # them in the tensors), the scales' bytes viewed as uint8, and a shuffled layout's flat
+        # [E' rows][cols] scale matrix cut to the routed experts' rows. Views, not copies.
+        n = mlp.gate.weight.shape[0]
+        w13, w2 = e.w13_weight[:n], e.w2_weight[:n]
+        w13_s = getattr(e, _mx_scale_name(e, "w13")).view(torch.uint8)
+        w2_s = getattr(e, _mx_scale_name(e, "w2")).view(torch.uint8)
+        if w13_s.dim() == 2:
+            w13_s, w2_s = w13_s[: n * w13.shape[1]], w2_s[: n * w2.shape[1]]
+        else:
+            w13_s, w2_s = w13_s[:n], w2_s[:n]
     return MoeWeights(
         gate_w=mlp.gate.weight,
         bias=bias,
-        w13=e.w13_weight,
-        w13_s=getattr(e, scale),
-        w2=e.w2_weight,
-        w2_s=getattr(e, scale.replace("w13", "w2")),
+        w13=w13,
+        w13_s=w13_s,
+        w2=w2,
+        w2_s=w2_s,
         sgu=sh.gate_up_proj.weight,
         sgu_s=sh.gate_up_proj.weight_scale_inv,
         sw2=sh.down_proj.weight,

@@ -131,6 +131,24 @@ def within_bar(e: dict, numel: int) -> bool:
     )
 
 
+def record_accuracy(workload: str, rows: int, mode: str, vs_oracle: dict, vs_golden: dict, routing_exact: bool,
+                    bits_differ: int | None = None) -> None:
+    """Append one case's accuracy to the JSON-lines file MKMOE_ACCURACY_LOG names (if set): the
+    per-case table the benchmark line and the committed profile read."""
+    path = os.environ.get("MKMOE_ACCURACY_LOG")
+    if not path:
+        return
+    import json
+
+    rec = {
+        "workload": workload, "rows": rows, "mode": mode, "routing_exact": bool(routing_exact),
+        "vs_oracle": vs_oracle, "vs_golden": vs_golden, "bits_differ_from_oracle": bits_differ,
+        "numel": int(vs_golden.get("numel", 0)),
+    }  # fmt: skip
+    with open(path, "a") as f:
+        f.write(json.dumps(rec) + "\n")
+
+
 def errors(out: torch.Tensor, ref: torch.Tensor, chain: torch.Tensor | None = None) -> dict:
     """max-abs, relative L2, cosine, and the largest difference in bf16 ulps of the reference
     (of the largest magnitude the combine chain held, when ``chain`` is given)."""
@@ -148,4 +166,5 @@ def errors(out: torch.Tensor, ref: torch.Tensor, chain: torch.Tensor | None = No
         "max_ulp": float((d / ulp).max()),
         "n_over_2e-2": int((d > 2e-2).sum()),
         "nan": bool(torch.isnan(a).any()),
+        "numel": int(d.numel()),
     }

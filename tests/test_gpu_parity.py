@@ -87,9 +87,9 @@ def test_device_decode_matches_tables():
     assert np.array_equal(f4.cpu().numpy(), want4)
 
 
-def _check(c, rows, run, exact):
+def _check(c, rows, run, exact, mode="default"):
     """Run the launch; routing bit for bit, the output within the bounds (and, exact: bit for bit)."""
-    from gpu_case import errors, within_bar
+    from gpu_case import errors, record_accuracy, within_bar
 
     ids = torch.zeros(rows, c.p["topk"], dtype=torch.int32, device="cuda")
     wts = torch.zeros(rows, c.p["topk"], dtype=torch.float32, device="cuda")
@@ -120,6 +120,7 @@ def _check(c, rows, run, exact):
     # and the reference's own cosine bound (ffn.moe.cosine, spec.py:305-309)
     g = errors(out.cpu(), c.golden, c.chain)
     print(f"  all {rows} rows vs fp32-matmul golden: {g}", flush=True)
+    record_accuracy(c.workload, rows, mode, e, g, True, n_diff)
     assert within_bar(g, out.numel()) and g["cos"] >= 0.9999, g
     assert out.numel() == c.golden.numel() == rows * c.p["hidden"]
 
@@ -132,7 +133,7 @@ def test_parity(workload, rows):
     c = _case(workload, rows)
     mode = f"gate_up {'MFMA' if rows >= MFMA_GATE_ROWS else 'VALU'}, down {'MFMA' if rows >= MFMA_DOWN_ROWS else 'VALU'}"
     print(f"\n{workload} R={rows} ({mode})", flush=True)
-    _check(c, rows, _runner(c), exact=rows < min(MFMA_GATE_ROWS, MFMA_DOWN_ROWS))
+    _check(c, rows, _runner(c), exact=rows < min(MFMA_GATE_ROWS, MFMA_DOWN_ROWS), mode="default")
 
 
 @pytest.mark.parametrize(
@@ -154,7 +155,7 @@ def test_parity_valu_forced(workload, rows):
     """Large launches held on the VALU GEMVs: bit for bit against the oracle."""
     c = _case(workload, rows)
     print(f"\n{workload} R={rows} (VALU forced)", flush=True)
-    _check(c, rows, _runner(c, (rows + 1, rows + 1)), exact=True)
+    _check(c, rows, _runner(c, (rows + 1, rows + 1)), exact=True, mode="valu")
 
 
 @pytest.mark.parametrize(
@@ -173,7 +174,7 @@ def test_parity_mfma_forced(workload, rows):
     """Every expert GEMM on MFMA (gate_up included): within the bounds, routing bit for bit."""
     c = _case(workload, rows)
     print(f"\n{workload} R={rows} (MFMA forced)", flush=True)
-    _check(c, rows, _runner(c, (1, 1)), exact=False)
+    _check(c, rows, _runner(c, (1, 1)), exact=False, mode="mfma")
 
 
 @pytest.mark.parametrize(
@@ -197,7 +198,7 @@ def test_parity_mxfp4_scaled(workload, rows, mode):
     ffn.moe at spec.py:305-309, and the north_star's relative L2 1e-2), with routing bit for
     bit; the elements beyond max-abs 2e-2 are reported (measured, both: 1 to 218 of 7168 to
     344064; down alone: 0 to 34), which is why the default launch converts the codes to bf16."""
-    from gpu_case import errors
+    from gpu_case import errors, record_accuracy
 
     c = _case(workload, rows)
     print(f"\n{workload} R={rows} (scaled fp4 x fp8 MFMA: {mode})", flush=True)
@@ -209,10 +210,12 @@ def test_parity_mxfp4_scaled(workload, rows, mode):
     run.raise_on_device_error()
     assert np.array_equal(ids.cpu().numpy(), c.ids), "expert ids"
     assert np.array_equal(wts.cpu().numpy().view(np.uint32), c.wts.view(np.uint32)), "routing weights"
+    res = {}
     for name, ref in (("oracle", c.ref), ("golden", c.golden)):
-        e = errors(out.cpu(), ref, c.chain)
+        e = res[name] = errors(out.cpu(), ref, c.chain)
         print(f"  all {rows} rows vs {name}: {e}", flush=True)
         assert not e["nan"] and e["rel_l2"] <= REL_L2 and e["cos"] >= 0.9999, e
+    record_accuracy(c.workload, rows, f"scaled_{mode}", res["oracle"], res["golden"], True)
 
 
 @pytest.mark.parametrize(

@@ -96,3 +96,20 @@ def test_seam_weights_check_names_the_tensor():
     w.hc_ffn_fn = None
     with pytest.raises(RuntimeError, match="hc_ffn_fn: missing"):
         w.check()
+
+
+def test_seam_call_refused_while_a_gate_is_pending():
+    """A second ffn_seam call while a gate_later call waits for gate() would lose that gate (and,
+    at the same token count, overwrite the partials it reads): refused before any launch."""
+    from sgl_amd_mono.moe import _lib
+    from sgl_amd_mono.moe.seam import SeamRunner
+
+    run = object.__new__(SeamRunner)  # the host checks alone: no device
+    run._io = _io(flags=_lib.SEAM_GATE_LATER)
+    z = torch.zeros(1)
+    with pytest.raises(RuntimeError, match="waits for its gate"):
+        run.ffn_seam(None, z, z, z, z, z)
+    run.cancel_gate()
+    with pytest.raises(Exception) as e:  # no pending gate: on to the argument checks
+        run.ffn_seam(None, z, z, z, z, z)
+    assert "waits for its gate" not in str(e.value)

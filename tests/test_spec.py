@@ -30,8 +30,10 @@ def _t(shape, dtype):
     return torch.empty(shape, dtype=dtype, device=META)
 
 
-def _moe_layer(tp=4, fmt="fp8_b128", e=256, h=7168, inter=2048, shuffled=False, shared=True, gate_dtype=torch.bfloat16):
+def _moe_layer(tp=4, fmt="fp8_b128", e=256, h=7168, inter=2048, shuffled=False, shared=True, gate_dtype=torch.bfloat16,
+               pad_experts=0):
     i = inter // tp
+    n = e  # the router's experts; the fused-MoE tensors may hold pad_experts more
     if fmt == "fp8_b128":
         experts = SimpleNamespace(
             w13_weight=_t((e, 2 * i, h), FP8),
@@ -40,6 +42,7 @@ def _moe_layer(tp=4, fmt="fp8_b128", e=256, h=7168, inter=2048, shuffled=False, 
             w2_weight_scale_inv=_t((e, h // 128, i // 128), torch.float32),
         )
     else:
+        e += pad_experts
         experts = SimpleNamespace(
             w13_weight=_t((e, 2 * i, h // 2), torch.uint8),
             w13_weight_scale=_t((e, 2 * i, h // 32), torch.uint8),
@@ -49,16 +52,23 @@ def _moe_layer(tp=4, fmt="fp8_b128", e=256, h=7168, inter=2048, shuffled=False, 
     if shuffled:
         experts.w13_weight = experts.w13_weight.clone()
         experts.w13_weight.is_shuffled = True
-        if fmt != "fp8_b128":  # SGLang's views of the shuffled MXFP4 scales: [E * rows][cols]
-            experts.w13_weight_scale = _t((e * 2 * i, h // 32), torch.uint8)
-            experts.w2_weight_scale = _t((e * h, i // 32), torch.uint8)
+        if fmt != "fp8_b128":
+            # SGLang's gfx950 processing, as the reference reads it (deepseek_v41/spec.py:
+            # 521-524): fp4x2 weights, E8M0 scales as one flat [E' rows][cols] matrix a tensor,
+            # under the name w13_weight_scale_inv
+            experts.w13_weight = _t((e, 2 * i, h // 2), torch.float4_e2m1fn_x2)
+            experts.w13_weight.is_shuffled = True
+            experts.w2_weight = _t((e, h, i // 2), torch.float4_e2m1fn_x2)
+            del experts.w13_weight_scale, experts.w2_weight_scale
+            experts.w13_weight_scale_inv = _t((e * 2 * i, h // 32), torch.float8_e8m0fnu)
+            experts.w2_weight_scale_inv = _t((e * h, i // 32), torch.float8_e8m0fnu)
     sh = None
     if shared:
         sh = SimpleNamespace(
             gate_up_proj=SimpleNamespace(weight=_t((2 * i, h), FP8), weight_scale_inv=_t((2 * i // 128, h // 128), torch.float32)),
             down_proj=SimpleNamespace(weight=_t((h, i), FP8), weight_scale_inv=_t((h // 128, i // 128), torch.float32)),
         )
-    gate = SimpleNamespace(weight=_t((e, h), gate_dtype), e_score_correction_bias=_t((e,), torch.float32))
+    gate = SimpleNamespace(weight=_t((n, h), gate_dtype), e_score_correction_bias=_t((n,), torch.float32))
     return SimpleNamespace(
         mlp=SimpleNamespace(gate=gate, experts=experts, shared_experts=sh),
         post_attention_layernorm=SimpleNamespace(weight=_t((h,), torch.bfloat16)),
@@ -148,14 +158,36 @@ def test_shuffled_mxfp4_is_read_in_place():
     mixed = _model([_moe_layer(4, "mxfp4", shuffled=True), _moe_layer(4, "mxfp4")])
     assert any("both" in x for x in mspec._model_disable_reasons(mixed, hf, {}, tp_size=4))
     layer = _moe_layer(4, "mxfp4", shuffled=True)
+    ex = layer.mlp.experts
     w = mspec._weights(layer, PRESETS["dsv3_tp4_mxfp4"], {}, 1)
-    assert w.w13 is layer.mlp.experts.w13_weight and w.w13_s is layer.mlp.experts.w13_weight_scale
+    assert w.w13.shape == ex.w13_weight.shape and w.w13.dtype == torch.float4_e2m1fn_x2
+    assert w.w13_s.dtype == torch.uint8 and tuple(w.w13_s.shape) == (256 * 1024, 224)
+    assert tuple(w.w2_s.shape) == (256 * 7168, 16)
+
+
+def test_shuffled_mxfp4_with_padding_experts():
+    """Fused-MoE tensors that hold more experts than the router (a fused shared expert or
+    padding): the routed experts' rows are read (views, no copy), as the reference does
+    (``e.w13_weight[:n]``, ``w13_weight_scale_inv.view(u8)[: n * rows]``)."""
+    hf = _hf()
+    layer = _moe_layer(4, "mxfp4", shuffled=True, pad_experts=1)
+    ex = layer.mlp.experts
+    assert ex.w13_weight.shape[0] == 257 and ex.w13_weight_scale_inv.shape[0] == 257 * 1024
+    assert mspec._model_disable_reasons(_model([layer]), hf, {}, tp_size=4) == []
+    w = mspec._weights(layer, PRESETS["dsv3_tp4_mxfp4"], {}, 1)
+    assert w.w13.shape[0] == 256 and w.w2.shape[0] == 256
+    assert tuple(w.w13_s.shape) == (256 * 1024, 224) and tuple(w.w2_s.shape) == (256 * 7168, 16)
+    # row-major MXFP4 with a padding expert: its stacked tensors are cut alike
+    layer = _moe_layer(4, "mxfp4", pad_experts=1)
+    w = mspec._weights(layer, PRESETS["dsv3_tp4_mxfp4"], {}, 1)
+    assert w.w13.shape[0] == 256 and w.w13_s.shape[0] == 256 and w.w2_s.shape[0] == 256
+    assert mspec._model_disable_reasons(_model([layer]), hf, {}, tp_size=4) == []
 
 
 def test_weights_read_in_place():
     layer = _moe_layer(4, "mxfp4")
     w = mspec._weights(layer, PRESETS["dsv3_tp4_mxfp4"], {}, 1)
-    assert w.w13 is layer.mlp.experts.w13_weight and w.w2_s is layer.mlp.experts.w2_weight_scale
+    assert w.w13.data_ptr() == layer.mlp.experts.w13_weight.data_ptr() and w.w2_s.shape == layer.mlp.experts.w2_weight_scale.shape
     assert w.sgu is layer.mlp.shared_experts.gate_up_proj.weight and w.norm is None
     # a bf16 bias becomes an fp32 copy, kept in the copy table
     layer.mlp.gate.e_score_correction_bias = torch.zeros(256, dtype=torch.bfloat16)
