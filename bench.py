@@ -61,7 +61,7 @@ HEADLINE = ("cfg2_tp4_fp8", 8)
 # further (workload, rows) points that get a CPU baseline of their own (under ``workloads``)
 CPU_POINTS = (("cfg3_tp4_mxfp4", 8), ("cfg5_tp2_mxfp4_norm", 8))
 CPU_POINT_BUDGET_S = 15.0
-DEFAULT_WORKLOADS = "cfg2_tp4_fp8,cfg3_tp4_mxfp4,cfg4_tp4_mxfp4_zipf,cfg5_tp2_mxfp4_norm"
+DEFAULT_WORKLOADS = "cfg2_tp4_fp8,cfg3_tp4_mxfp4,cfg4_tp4_mxfp4_zipf,cfg5_tp2_mxfp4_norm,v41_tp4_mxfp4"
 MIN_TIMED = 200
 SEAM_TOKENS = "1,8,48"
 SEAM_LAYERS = 144
@@ -73,31 +73,28 @@ def log(msg: str) -> None:
 
 
 def make_layer(preset, g, device, zipf_s=None):
-    """One layer's weights with random contents (GPU-generated), in the kernel's layouts."""
+    """One layer's weights with random contents (GPU-generated), in the kernel's layouts: every
+    tensor of the preset's weight contract (``MoeWeights.expected``) with its shape and dtype;
+    e4m3 and e2m1 bytes uniform (no e4m3 NaN codes), E8M0 codes 118..122, fp32 block scales
+    small, the router N(0, 1/H) (logits ~N(0, 1)), the bias N(0, 0.02), the norm weight
+    1 + N(0, 0.1)."""
     import torch
 
     from sgl_amd_mono.moe.runner import MoeWeights
 
-    e, h, i, s = preset.experts, preset.hidden, preset.inter, preset.shared_inter
-
-    def fp8(*shape):
-        t = torch.randint(0, 256, shape, generator=g, device=device, dtype=torch.uint8)
-        return torch.where((t & 0x7F) == 0x7F, t ^ 1, t)
-
-    def f32s(*shape):
-        return torch.rand(*shape, generator=g, device=device) * 1e-4 + 5e-5
-
-    def e8m0(*shape):
-        return torch.randint(118, 123, shape, generator=g, device=device, dtype=torch.uint8)
-
-    if preset.routed_fmt == "fp8_b128":
-        w13, w13_s = fp8(e, 2 * i, h), f32s(e, 2 * i // 128, h // 128)
-        w2, w2_s = fp8(e, h, i), f32s(e, h // 128, i // 128)
-    else:
-        w13 = torch.randint(0, 256, (e, 2 * i, h // 2), generator=g, device=device, dtype=torch.uint8)
-        w13_s = e8m0(e, 2 * i, h // 32)
-        w2 = torch.randint(0, 256, (e, h, i // 2), generator=g, device=device, dtype=torch.uint8)
-        w2_s = e8m0(e, h, i // 32)
+    e, h = preset.experts, preset.hidden
+    want = MoeWeights.expected(preset)
+    t = {}
+    for name, (shape, dtypes) in want.items():
+        if name in ("gate_w", "bias", "norm"):
+            continue
+        if dtypes[0] == torch.float32:  # fp32 block scales
+            t[name] = torch.rand(*shape, generator=g, device=device) * 1e-4 + 5e-5
+        elif name.endswith("_s"):  # E8M0
+            t[name] = torch.randint(118, 123, shape, generator=g, device=device, dtype=torch.uint8)
+        else:
+            b = torch.randint(0, 256, shape, generator=g, device=device, dtype=torch.uint8)
+            t[name] = torch.where((b & 0x7F) == 0x7F, b ^ 1, b)
     gate = torch.randn(e, h, generator=g, device=device) / h**0.5
     if zipf_s:
         # expert popularity p_e ~ rank(e)^-s over a seeded permutation: with x[:, 0] = 1 the
@@ -111,13 +108,8 @@ def make_layer(preset, g, device, zipf_s=None):
     if preset.norm_eps is not None:
         norm = (1 + 0.1 * torch.randn(h, generator=g, device=device)).to(torch.bfloat16)
     return MoeWeights(
-        gate_w=gate.to(torch.bfloat16),
-        bias=torch.randn(e, generator=g, device=device) * 0.02,
-        w13=w13, w13_s=w13_s, w2=w2, w2_s=w2_s,
-        sgu=fp8(2 * s, h), sgu_s=f32s(2 * s // 128, h // 128),
-        sw2=fp8(h, s), sw2_s=f32s(h // 128, s // 128),
-        norm=norm,
-    )  # fmt: skip
+        gate_w=gate.to(torch.bfloat16), bias=torch.randn(e, generator=g, device=device) * 0.02, norm=norm, **t
+    )
 
 
 class RowsBench:
@@ -510,7 +502,7 @@ def main() -> int:
         kw = {} if args.mxfp4_scaled_rows is None else {"mxfp4_scaled_rows": args.mxfp4_scaled_rows}
         if args.mxfp4_scaled_down_rows is not None:
             kw["mxfp4_scaled_down_rows"] = args.mxfp4_scaled_down_rows
-        if preset.routed_fmt == "mxfp4":
+        if preset.routed_fmt == "mxfp4" and not preset.aiter_only:
             kw["layout"] = args.layout
         runner = MoeRunner(preset, device, max_rows=max(48, max(rows_list)), **kw)
         if args.staged:
@@ -591,7 +583,7 @@ def main() -> int:
             "rows": hrows,
             "layers_rotated": args.layers,
             "launch": "staged" if args.staged else "persistent",
-            "layout": args.layout if hpreset.routed_fmt == "mxfp4" else "row_major",
+            "layout": "aiter" if hpreset.aiter_only else (args.layout if hpreset.routed_fmt == "mxfp4" else "row_major"),
         },
         "roofline": {
             "bound": "hbm",

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MKMOE_ABI_VERSION 4
+#define MKMOE_ABI_VERSION 5
 
 /* weight formats */
 #define MKMOE_FMT_FP8_B128 1 /* e4m3, fp32 scale per 128 x 128 block */
@@ -42,6 +42,9 @@ extern "C" {
  * FFNWeights hold (deepseek_v41/gfx950/runner.py:139-142: aiter's (16, 16) shuffle with the
  * gate/up interleave, scales in shuffle_scale order; made by check_ffn.py:169-173) */
 #define MKMOE_FMT_MXFP4_AITER 3
+/* e4m3 with an E8M0 scale per 32 x 32 block, fed by MXFP8 activations of the "vllm" rule: the
+ * V4.1 shared expert (deepseek_v41/gfx950/runner.py:143-146, check_ffn.py:118-121,226-231) */
+#define MKMOE_FMT_FP8_MX32 4
 
 /* router scores (mkmoe_shape.scoring) */
 #define MKMOE_SCORE_SIGMOID 0       /* DeepSeek-V3: sigmoid(logit) */
@@ -81,7 +84,7 @@ typedef struct mkmoe_shape {
   int32_t n_group;       /* expert groups (1: no groups) */
   int32_t topk_group;    /* groups kept */
   int32_t inter;         /* a routed expert's intermediate width on this rank */
-  int32_t shared_inter;  /* the shared expert's (FP8 128 x 128) */
+  int32_t shared_inter;  /* the shared expert's (FP8, shared_fmt) */
   int32_t routed_fmt;    /* MKMOE_FMT_* */
   int32_t router_parts;  /* router K parts, summed in order */
   int32_t renorm;        /* 1: normalise the top-k scores */
@@ -91,6 +94,9 @@ typedef struct mkmoe_shape {
   float swiglu_limit;
   float norm_eps;
   int32_t scoring;       /* MKMOE_SCORE_* (0: sigmoid; the bytes ABI 2 left reserved) */
+  int32_t shared_fmt;    /* the shared expert's weights: MKMOE_FMT_FP8_B128 (0 taken as it: x
+                          * and its intermediate quantized per 128 with fp32 scales) or
+                          * MKMOE_FMT_FP8_MX32 (MXFP8 "vllm" rule); ABI 5 */
 } mkmoe_shape;
 
 /* Device pointers, read in place. Layouts (E experts, H hidden, I inter,
@@ -109,7 +115,10 @@ typedef struct mkmoe_shape {
  *             (c/4)%2) 2 + (r/16)%2 (common/mx.py:40-44). The GEMMs run on MFMA at every
  *             row count (mfma_*_rows above 1 are refused)
  *   sgu e4m3 [2S][H] (gate rows, then up rows), sgu_s fp32 [2S/128][H/128],
- *   sw2 e4m3 [H][S], sw2_s fp32 [H/128][S/128]
+ *   sw2 e4m3 [H][S], sw2_s fp32 [H/128][S/128]; with shared_fmt MKMOE_FMT_FP8_MX32 the
+ *   scales are E8M0 bytes, sgu_s [2S/32][H/32], sw2_s [H/32][S/32] (the V4.1 FFNWeights,
+ *   gfx950/runner.py:143-146). The MXFP4_AITER w2_s holds [E H][C] bytes with C = I/32 padded
+ *   to a multiple of 8 (stages/dims.py:54-56), read as the shuffle_scale order of that matrix
  * w13 holds each expert's gate rows [0, I) then its up rows [I, 2I). */
 typedef struct mkmoe_weights {
   const void* gate_w;

@@ -106,6 +106,14 @@ def deq_fp8_b128(q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
     return e4m3_to_f32(q) * sf
 
 
+def deq_fp8_mx32(q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    """[N, K] e4m3 with [N / 32, K / 32] E8M0 block scales -> [N, K] fp32: the reference's
+    ``deq_fp8_block`` (check_ffn.py:118-121), each weight times 2 ** (code - 127) of its block."""
+    n, k = q.shape
+    sf = e8m0_to_f32(s).repeat_interleave(32, 0)[:n].repeat_interleave(32, 1)[:, :k]
+    return e4m3_to_f32(q) * sf
+
+
 # ---------------------------------------------------------------- activation rules
 def code_ceil(v: torch.Tensor) -> torch.Tensor:
     """Biased exponent of the smallest power of two >= v (v > 0) (check_ffn.py:87-90)."""

@@ -21,6 +21,12 @@ Distributions (per workload):
 - the Zipf(1.2) stress: hidden element 0 of every row is 1.0 and router column
   0 holds bf16(log p_e) for p_e ~ rank(e)^-1.2 over a seeded permutation of the
   experts, so the logits are log p_e plus N(0, 1) noise.
+- the V4.1 shape (an MX shared expert, padded routed widths) follows the reference
+  test's ``make_weights`` (check_ffn.py:128-182) instead: router N(0, 0.02) bf16, bias
+  N(0, 0.02) held in bf16; routed experts as random e2m1 bytes with E8M0 codes 118..122 over
+  the rank's real columns and zeros in the loader's padding (gate and up rows I_real .. I, w2's
+  K columns and scales past I_real); the shared expert N(0, 1) clamped to +-6 in e4m3 with E8M0
+  32 x 32 codes 118..122.
 """
 
 from __future__ import annotations
@@ -59,9 +65,30 @@ def quant_weight(w: torch.Tensor, fmt: str):
     raise ValueError(fmt)
 
 
+def _e8m0(shape, g: torch.Generator) -> torch.Tensor:
+    return torch.randint(118, 123, shape, generator=g, dtype=torch.uint8)
+
+
+def _v41(p: dict) -> bool:
+    return p.get("shared_fmt") == "fp8_mx32"
+
+
 def make_dense(p: dict, seed: int) -> dict:
     """The router, bias, norm and shared expert (everything but the routed experts)."""
     h, e = p["hidden"], p["experts"]
+    if _v41(p):
+        ish = p["shared_inter"]
+        g = _gen(seed * 1000 + T_SGU)
+        sgu = torch.randn(2 * ish, h, generator=g).clamp(-6, 6)
+        sw2 = torch.randn(h, ish, generator=g).clamp(-6, 6)
+        return {
+            "gate_w": randn((e, h), seed * 1000 + T_GATE, 0.02).to(torch.bfloat16),
+            "bias": randn((e,), seed * 1000 + T_BIAS, 0.02).to(torch.bfloat16).float(),
+            "sgu": fm.e4m3_codes_from_f32(sgu),
+            "sgu_s": _e8m0((2 * ish // 32, h // 32), g),
+            "sw2": fm.e4m3_codes_from_f32(sw2),
+            "sw2_s": _e8m0((h // 32, ish // 32), g),
+        }
     std = 0.02 if h <= 1024 else 1.0 / math.sqrt(h)
     gate = randn((e, h), seed * 1000 + T_GATE, std)
     if p.get("zipf_s"):
@@ -115,6 +142,21 @@ class LazyExperts:
                 self.cache[e] = t
 
     def get(self, e: int):
+        if e not in self.cache and _v41(self.p):
+            p = self.p
+            h, i = p["hidden"], p["inter"]
+            ir = p.get("inter_real") or i
+            g = _gen(self.seed * 1000 + EXPERT_SEED + 4 * e)
+            w13 = torch.zeros(2 * i, h // 2, dtype=torch.uint8)
+            s13 = torch.zeros(2 * i, h // 32, dtype=torch.uint8)
+            for half in (0, i):
+                w13[half : half + ir] = torch.randint(0, 256, (ir, h // 2), generator=g, dtype=torch.uint8)
+                s13[half : half + ir] = _e8m0((ir, h // 32), g)
+            w2 = torch.zeros(h, i // 2, dtype=torch.uint8)
+            s2 = torch.zeros(h, i // 32, dtype=torch.uint8)
+            w2[:, : ir // 2] = torch.randint(0, 256, (h, ir // 2), generator=g, dtype=torch.uint8)
+            s2[:, : ir // 32] = _e8m0((h, ir // 32), g)
+            self.cache[e] = (w13, s13, w2, s2)
         if e not in self.cache:
             p = self.p
             h, i = p["hidden"], p["inter"]

@@ -57,18 +57,33 @@ FP8_B128 = "fp8_b128"
 MXFP4 = "mxfp4"
 
 
+FP8_MX32 = "fp8_mx32"  # e4m3 with E8M0 32 x 32 block scales (the V4.1 shared expert)
+
+
 def act_qdq(x: torch.Tensor, fmt: str) -> torch.Tensor:
-    """The activation rule that feeds an expert GEMM of weight format ``fmt``."""
+    """The activation rule that feeds an expert GEMM of weight format ``fmt``: MXFP8 "aiter"
+    (MXFP4 weights), MXFP8 "vllm" (MX FP8 weights: check_ffn.py:212,231), group-128 FP8."""
     if fmt == MXFP4:
         return fm.mxfp8_qdq(x)
+    if fmt == FP8_MX32:
+        return fm.mxfp8_qdq(x, "vllm")
     if fmt == FP8_B128:
         return fm.group_fp8_qdq(x, 128)
     raise ValueError(fmt)
 
 
+def has_exact(p: dict) -> bool:
+    """Whether the preset has the fixed-order restatement (``exact=True``): the shapes whose
+    GEMMs can run on the VALU GEMVs. The MX shared expert and the padded widths of the V4.1
+    shape run on MFMA alone and are held to the golden's fp32-matmul form."""
+    return p.get("shared_fmt", FP8_B128) == FP8_B128 and p.get("inter_real") is None
+
+
 def deq_weight(q: torch.Tensor, s: torch.Tensor, fmt: str) -> torch.Tensor:
     if fmt == MXFP4:
         return fm.deq_mxfp4(q, s)
+    if fmt == FP8_MX32:
+        return fm.deq_fp8_mx32(q, s)
     if fmt == FP8_B128:
         return fm.deq_fp8_b128(q, s)
     raise ValueError(fmt)
@@ -182,7 +197,8 @@ def _contrib_job(args):
 
     p, seed, e, xin_rows, w_rows = args
     t = gen.LazyExperts(p, seed).get(e)
-    return e, t, expert_contrib(t, xin_rows, w_rows, p, True), expert_contrib(t, xin_rows, w_rows, p, False)
+    g = expert_contrib(t, xin_rows, w_rows, p, False)
+    return e, t, expert_contrib(t, xin_rows, w_rows, p, True) if has_exact(p) else g, g
 
 
 def pool_contribs(p: dict, seed: int, xin: torch.Tensor, ids: np.ndarray, wts: np.ndarray, workers: int):
@@ -225,9 +241,16 @@ def moe_partial(x: torch.Tensor, w: dict, p: dict, experts=None, exact: bool = T
     matmuls and torch's silu. ``contribs``: the routed experts' contributions
     already computed (``pool_contribs``) in the same mode. Returns ids, weights,
     logits, the normed rows (if any), the per-pick contributions and the bf16 output.
+    The shared expert's format is ``p["shared_fmt"]`` (default FP8 128 x 128); with
+    "fp8_mx32" its activations and intermediate take the MXFP8 "vllm" rule and its
+    weights E8M0 32 x 32 scales (check_ffn.py:226-231); such presets have the golden's
+    form alone (``has_exact``).
     """
     from . import exact as ex
 
+    if exact and not has_exact(p):
+        raise ValueError(f"{p.get('name', p)}: no fixed-order restatement (MFMA-only shape); use exact=False")
+    sfmt = p.get("shared_fmt", FP8_B128)
     lim = float(p["swiglu_limit"])
     r = x.shape[0]
     h = p["hidden"]
@@ -256,10 +279,10 @@ def moe_partial(x: torch.Tensor, w: dict, p: dict, experts=None, exact: bool = T
         smq, sms = fm.group_fp8_quant(torch.from_numpy(smid), 128)
         shared = fm.bf(torch.from_numpy(ex.gemv_fp8_b128(w["sw2"], w["sw2_s"], smq, sms, ex.DOWN_LANES)))
     elif ish > 0:
-        xs_ = act_qdq(xin, FP8_B128)
-        hs = xs_ @ fm.deq_fp8_b128(w["sgu"], w["sgu_s"]).T
+        xs_ = act_qdq(xin, sfmt)
+        hs = xs_ @ deq_weight(w["sgu"], w["sgu_s"], sfmt).T
         smid = swiglu_shared_golden(hs[:, :ish], hs[:, ish:], lim)
-        shared = fm.bf(act_qdq(smid, FP8_B128) @ fm.deq_fp8_b128(w["sw2"], w["sw2_s"]).T)
+        shared = fm.bf(act_qdq(smid, sfmt) @ deq_weight(w["sw2"], w["sw2_s"], sfmt).T)
     else:
         shared = torch.zeros(r, h)
     out, chain = combine(per_k, shared)

@@ -106,21 +106,34 @@ def unshuffle_scales(s: torch.Tensor) -> torch.Tensor:
     return s.reshape(-1)[_scale_perm(rows, cols, s.device)].view(shape).contiguous()
 
 
+def pad_scale_cols(s: torch.Tensor, mult: int = 8) -> torch.Tensor:
+    """[..., C] E8M0 bytes with C padded to a multiple of ``mult`` by zero codes, as SGLang's
+    loader pads w2's scales (``down_scale_cols``: I / 32 padded to a multiple of 8,
+    ``stages/dims.py:54-56``)."""
+    c = s.shape[-1]
+    pad = -c % mult
+    if pad == 0:
+        return s
+    return torch.cat([s, torch.zeros(*s.shape[:-1], pad, dtype=s.dtype, device=s.device)], -1)
+
+
 def to_aiter(w13: torch.Tensor, w13_s: torch.Tensor, w2: torch.Tensor, w2_s: torch.Tensor):
-    """Row-major MXFP4 experts -> SGLang's loaded gfx950 layout (check_ffn.py:170-173)."""
+    """Row-major MXFP4 experts -> SGLang's loaded gfx950 layout (check_ffn.py:170-173); w2's
+    scale columns padded to a multiple of 8 first (``pad_scale_cols``)."""
     return (
         shuffle_16x16(interleave_gate_up(w13)),
         shuffle_scales(interleave_gate_up(w13_s)),
         shuffle_16x16(w2),
-        shuffle_scales(w2_s),
+        shuffle_scales(pad_scale_cols(w2_s)),
     )
 
 
-def from_aiter(w13: torch.Tensor, w13_s: torch.Tensor, w2: torch.Tensor, w2_s: torch.Tensor):
-    """The inverse of ``to_aiter``."""
+def from_aiter(w13: torch.Tensor, w13_s: torch.Tensor, w2: torch.Tensor, w2_s: torch.Tensor, w2_cols: int | None = None):
+    """The inverse of ``to_aiter`` (w2_cols: w2's scale columns before the padding)."""
+    s2 = unshuffle_scales(w2_s)
     return (
         deinterleave_gate_up(unshuffle_16x16(w13)),
         deinterleave_gate_up(unshuffle_scales(w13_s)),
         unshuffle_16x16(w2),
-        unshuffle_scales(w2_s),
+        s2 if w2_cols is None else s2[..., :w2_cols].contiguous(),
     )

@@ -38,7 +38,7 @@
 #include "../../include/mkmoe.h"
 #include "mkmoe_numerics.h"
 
-// Built whole, or in parts (MKMOE_UNIT = 0 .. 6: one compiled shape's kernels and launcher;
+// Built whole, or in parts (MKMOE_UNIT = 0 .. 7: one compiled shape's kernels and launcher;
 // MKMOE_UNIT_HOST: the host code and the C ABI), so that the parts compile in parallel.
 #define MKMOE_UNIT_HOST 9
 
@@ -51,6 +51,9 @@ constexpr int kTileMax = 32;   // output rows of a down tile, at most
 constexpr int kFp8 = MKMOE_FMT_FP8_B128;
 constexpr int kFp4 = MKMOE_FMT_MXFP4;
 constexpr int kFp4Aiter = MKMOE_FMT_MXFP4_AITER;  // MXFP4 in SGLang's loaded (aiter-shuffled) layout
+// e4m3 with E8M0 32 x 32 block scales (the V4.1 shared expert), fed by MXFP8 of the "vllm" rule;
+// as a quantizer's format argument it selects that rule
+constexpr int kFp8Mx = MKMOE_FMT_FP8_MX32;
 constexpr int kScoreSigmoid = MKMOE_SCORE_SIGMOID, kScoreSqrtSoftplus = MKMOE_SCORE_SQRT_SOFTPLUS;
 constexpr int kAuxDev = 16;  // sc1: device-coherent access
 constexpr int kAuxNt = 2;    // nt: streamed once
@@ -111,9 +114,14 @@ __device__ __forceinline__ unsigned long long tl_now() { return 0ull; }
 #endif
 
 template <int H_, int E_, int K_, int NG_, int TG_, int I_, int S_, int FMT_, int P_, bool NORM_, bool SHUF_ = false,
-          int SCORE_ = kScoreSigmoid>
+          int SCORE_ = kScoreSigmoid, int SFMT_ = kFp8>
 struct Cfg {
   static constexpr int SCORE = SCORE_;  // the router's score (sigmoid or V4.1's sqrt(softplus))
+  // the shared expert's weights: FP8 with fp32 128 x 128 scales (its activations and
+  // intermediate quantized per 128, fp32 scales), or with E8M0 32 x 32 scales (V4.1: MXFP8 of
+  // the "vllm" rule)
+  static constexpr int SFMT = SFMT_;
+  static_assert(SFMT == kFp8 || SFMT == kFp8Mx, "shared formats");
   static constexpr int H = H_, E = E_, K = K_, NG = NG_, TG = TG_, I = I_, S = S_, FMT = FMT_,
                        P = P_;
   static constexpr bool NORM = NORM_;
@@ -130,15 +138,17 @@ struct Cfg {
   static constexpr int QROWS = 8;
   // the persistent launch runs the shared expert's down before the routed one, its units
   // staged through two waves' LDS slots (where a 16-row shared unit fits a routed unit's slot)
-  static constexpr bool SF = 16 * S <= (FMT == kFp8 ? 16 * I : (I <= 512 ? 32 : 16) * (I / 2));
+  static constexpr bool SF = SFMT == kFp8 && 16 * S <= (FMT == kFp8 ? 16 * I : (I <= 512 ? 32 : 16) * (I / 2));
   static constexpr int CH512 = H / 512;  // router / quantize chunks of a row
   static_assert(H % 1024 == 0 && CH512 % P == 0, "router chunks, K split over 8 waves");
-  static_assert(I % 128 == 0 && S % 128 == 0, "widths");
+  // (an MX shared expert's width may end in half a 128-K step: V4.1's 2304 / 4 = 576)
+  static_assert(I % 128 == 0 && (SFMT == kFp8Mx ? S % 64 == 0 : S % 128 == 0), "widths");
   static_assert(E <= 1024 && (NG == 1 || (E % NG == 0)), "experts");
   // down-stage mid batch: picks whose quantized rows fit ~32 KB of LDS
   static constexpr int PB = 32768 / I;
   static constexpr int MQS = I + 16;  // LDS row stride of quantized mid (bank spread)
   static constexpr int SQS = S + 16;
+  static constexpr int SSC = SFMT == kFp8Mx ? S / 32 : (S / 128) * 4;  // scale bytes of a shared row
   static constexpr int MSC = FMT == kFp4 ? I / 32 : I / 128;  // mid scales a pick
   // 16-row blocks of a routed down unit: MXFP4 rows of 512 K are 256 bytes, so a unit of 32 rows
   // keeps 8 KB a wave in flight (as 16 rows do at FP8, or at MXFP4 with 1024 K)
@@ -153,6 +163,11 @@ using CfgTp4Fp4Aiter = Cfg<7168, 256, 8, 8, 4, 512, 512, kFp4, 7, false, true>;
 using CfgTp2Fp4NormAiter = Cfg<7168, 256, 8, 8, 4, 1024, 1024, kFp4, 7, true, true>;
 // the plumbing shape routed as V4.1 routes (sqrt(softplus) scores, one group)
 using CfgPlumbingSoftplus = Cfg<1024, 16, 4, 1, 1, 512, 512, kFp8, 2, false, false, kScoreSqrtSoftplus>;
+// DeepSeek-V4.1's MoE at TP4 (stages/moe_shape.py:24, stages/dims.py:13-56, check_ffn.py:13-18):
+// hidden 5120, 384 experts top-6 by sqrt(softplus) over one group, routed experts MXFP4 in
+// SGLang's aiter layout with the rank's 576 columns padded to 640 (zero weights), the shared
+// expert's 576 columns FP8 with E8M0 32 x 32 scales
+using CfgV41Tp4 = Cfg<5120, 384, 6, 1, 1, 640, 576, kFp4, 5, false, true, kScoreSqrtSoftplus, kFp8Mx>;
 
 // the expert GEMMs of a launch on MFMA (else the VALU GEMVs)
 template <class C>
@@ -172,7 +187,7 @@ struct Layout {
 MKMOE_HD inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 MKMOE_HD inline Layout make_layout(int H, int E, int K, int I, int S, int fmt, int P, int norm,
-                                   int rm) {
+                                   int rm, int sfmt = kFp8) {
   Layout L;
   size_t sz[kRegions];
   sz[0] = norm ? (size_t)rm * H * 2 : 0;                              // x normed, bf16
@@ -193,7 +208,7 @@ MKMOE_HD inline Layout make_layout(int H, int E, int K, int I, int S, int fmt, i
   sz[12] = (size_t)rm * K * (I + 16);
   sz[13] = (size_t)rm * K * (fmt == kFp4 ? I / 32 : (I / 128) * 4);
   sz[14] = (size_t)rm * (S + 16);
-  sz[15] = (size_t)rm * (S / 128) * 4;
+  sz[15] = (size_t)rm * (sfmt == kFp8Mx ? S / 32 : (S / 128) * 4);
   size_t off = kCtlBytes;
   for (int i = 0; i < kRegions; ++i) {
     L.off[i] = off;
@@ -679,8 +694,17 @@ __device__ __forceinline__ void quant_unit(const Params& p, int r, int c, int la
 #pragma unroll
   for (int j = 0; j < 8; ++j) am = fabsf(v[j]) > am ? fabsf(v[j]) : am;
   const uint32_t col = (uint32_t)r * C::H + c * 512 + lane * 8;
-  // group-128 fp8: 16 lanes a group
-  {
+  if constexpr (C::SFMT == kFp8Mx) {
+    // the shared expert's rule: MXFP8 per 32, the "vllm" code (4 lanes a group)
+    static_assert(C::FMT == kFp4, "the MX shared rule's codes in regions 3 / 4");
+    const int code = vllm_code(group_max<4>(am));
+    const float inv = mx_inv(code);
+    const uint32_t lo = e4m3_pack4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+    const uint32_t hi = e4m3_pack4(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
+    dst64(rs, p.off[3] + col, u32x2{lo, hi});
+    if ((lane & 3) == 0) dst8(rs, p.off[4] + (uint32_t)r * (C::H / 32) + c * 16 + lane / 4, (uint8_t)code);
+  } else {
+    // group-128 fp8: 16 lanes a group
     float g = group_max<16>(am);
     float s = group_scale(g);
     const uint32_t lo = e4m3_pack4(v[0] / s, v[1] / s, v[2] / s, v[3] / s);
@@ -927,6 +951,22 @@ __device__ __forceinline__ void select_row(const Params& p, const RouteSmem<C>& 
         const float v2 = sm.gv2[row][g];
         lb = ((gkeep >> g) & 1ull) && v2 < lb ? v2 : lb;
       }
+    }
+  } else if constexpr (C::E > 64) {
+    // one group over more experts than lanes: L is the topk-th largest of the lanes' own
+    // largest choices (topk rounds of a wave max, each taking out one lane's). At least topk
+    // experts reach it, so every pick does, and only experts at L or above are ranked: about
+    // topk of them, where ranking all E (each lane against every candidate in dependent chains)
+    // took 42 us at E = 384
+    static_assert(C::K <= 64, "picks from distinct lanes");
+    float m = ch[0];
+#pragma unroll
+    for (int i = 1; i < EPL; ++i) m = ch[i] > m ? ch[i] : m;
+#pragma unroll 1
+    for (int k = 0; k < C::K; ++k) {
+      lb = segment_max<64>(m);
+      const uint64_t at = __ballot(m == lb);
+      if (lane == (int)__ffsll((unsigned long long)at) - 1) m = -INFINITY;
     }
   }
   // candidates to LDS slots 0 .. nc - 1, in id order
@@ -1507,6 +1547,19 @@ __device__ __forceinline__ void mma_fp4_step2(u32x4 a0, float s0, u32x4 a1, floa
   }
 }
 
+// an FP8 x MXFP8 128-K step with E8M0 32 x 32 weight scales (the V4.1 shared expert),
+// accumulated into c: each lane's two 16-byte pieces (K 16 j .. and 64 + 16 j .. of the step)
+// lie in 32-K blocks j / 2 and 2 + j / 2, converted with their own block's scales folded in
+// (exact powers of two), so the products are exactly scaled whichever block they come from
+__device__ __forceinline__ f32x4 mma_fp8mx_step(u32x4 alo, u32x4 ahi, float swl, float swh, u32x4 blo, u32x4 bhi,
+                                                float sxl, float sxh, f32x4 c) {
+  c = mfma_bf16(fp8x8(alo.x, alo.y, swl), fp8x8(blo.x, blo.y, sxl), c);
+  c = mfma_bf16(fp8x8(alo.z, alo.w, swl), fp8x8(blo.z, blo.w, sxl), c);
+  c = mfma_bf16(fp8x8(ahi.x, ahi.y, swh), fp8x8(bhi.x, bhi.y, sxh), c);
+  c = mfma_bf16(fp8x8(ahi.z, ahi.w, swh), fp8x8(bhi.z, bhi.w, sxh), c);
+  return c;
+}
+
 // an MXFP4 x MXFP8 128-K step on the scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4), no
 // converts: A lane (m, j) holds row m's 32 e2m1 of K [32 j, 32 j + 32) (16 bytes), B lane
 // (n, j) column n's e4m3 of K [16 j, 16 j + 16) then [64 + 16 j, 64 + 16 j + 16) (blo, bhi);
@@ -1570,7 +1623,7 @@ __device__ __forceinline__ void stage_x_lds(const Params& p, XTile<C>& xt, int n
 template <class C>
 struct GuSmem {
   // MXFP4: a wave's slot of its K slice's E8M0 scales of a unit (32 rows x 32 bytes)
-  static constexpr int SSLOT = C::FMT == kFp4 ? 1024 : 16;
+  static constexpr int SSLOT = C::FMT == kFp4 || C::SFMT == kFp8Mx ? 1024 : 16;
   union {
     XTile<C> x;
     struct {
@@ -1591,11 +1644,15 @@ struct GuTile {
   static constexpr int KS = C::H / 128;
   static constexpr int SPW = KS / kWaves;
   static_assert(KS % kWaves == 0, "K steps split evenly over the waves");
-  static constexpr int NA = WFMT == kFp8 ? 1 : 2;   // A operands a K step
-  static constexpr int NC = WFMT == kFp8 ? 8 : 16;  // columns a unit
-  static constexpr int NW = WFMT == kFp8 ? 2 : 1;   // 16-byte words of a lane's step
+  // FP8 (fp32 128 x 128 scales, or E8M0 32 x 32: MX) or MXFP4 weights
+  static constexpr bool F8 = WFMT == kFp8 || WFMT == kFp8Mx;
+  static constexpr int NA = F8 ? 1 : 2;   // A operands a K step
+  static constexpr int NC = F8 ? 8 : 16;  // columns a unit
+  static constexpr int NW = F8 ? 2 : 1;   // 16-byte words of a lane's step
   u32x4 a[NA][SPW][NW];
-  uint32_t sa[NA][SPW];  // MXFP4: the E8M0 byte of the lane's row and block
+  // MXFP4: the E8M0 byte of the lane's row and block; MX FP8: the E8M0 bytes of the lane's
+  // row's blocks of its two pieces (low byte: K 16 j .., next: 64 + 16 j ..)
+  uint32_t sa[NA][SPW];
 
   // A unit's weight rows (FP8: gate rows j0 .. j0 + 7 then up rows W + j0 ..; MXFP4: 16 gate
   // rows then 16 up rows), this wave's K steps, go through the wave's LDS slot: LDS-direct
@@ -1603,18 +1660,19 @@ struct GuTile {
   // runs, which stream at about 5.1 against 6.6 TB/s: measured, loads alone). Chunk c (16 bytes)
   // of slot row r sits at position r * CPW + (c ^ key(r)), so that the 16 rows' reads of one
   // chunk fall in distinct banks.
-  static constexpr int RW = WFMT == kFp8 ? 16 : 32;              // slot rows
-  static constexpr int RB = WFMT == kFp8 ? SPW * 128 : SPW * 64;  // bytes a slot row
+  static constexpr int RW = F8 ? 16 : 32;              // slot rows
+  static constexpr int RB = F8 ? SPW * 128 : SPW * 64;  // bytes a slot row
   static constexpr int CPW = RB / 16;
   static constexpr int SLOT = RW * RB;
-  static_assert(SLOT == 2 * C::H && SLOT % 1024 == 0 && CPW % (WFMT == kFp8 ? 8 : 4) == 0, "slot layout");
+  static_assert(SLOT == 2 * C::H && SLOT % 1024 == 0 && CPW % (F8 ? 8 : 4) == 0, "slot layout");
   static_assert(!SH || (WFMT == kFp4 && SLOT == 2 * SPW * 1024), "shuffled: a 1 KB block a row group and K step");
-  // shuffled scales: the wave's K steps lie in four 256-byte chunks (two steps each) of the
-  // 32-row block, which end within it
-  static_assert(!SH || ((SPW + 2) / 2 <= 4 && ((kWaves - 1) * SPW / 2) * 256 + 1024 <= C::H), "scale chunks");
-  __device__ __forceinline__ static int key(int r) { return WFMT == kFp8 ? (r >> 1) : ((r & 15) >> 2); }
+  // shuffled scales: the wave's K steps lie in the first three of the four 256-byte chunks (two
+  // steps each) it loads from its first step's chunk (with an odd SPW the last wave's fourth
+  // chunk lies past the 32-row block: the next block's bytes, or zeros past the tensor, unread)
+  static_assert(!SH || (SPW + 2) / 2 <= 4, "scale chunks");
+  __device__ __forceinline__ static int key(int r) { return F8 ? (r >> 1) : ((r & 15) >> 2); }
   __device__ __forceinline__ static int wrow(int W, int j0, int r) {
-    return WFMT == kFp8 ? (r < 8 ? j0 + r : W + j0 + r - 8) : (r >> 4) * W + j0 + (r & 15);
+    return F8 ? (r < 8 ? j0 + r : W + j0 + r - 8) : (r >> 4) * W + j0 + (r & 15);
   }
   // w: the [2W][H] weight (wr: its resource words), sr: its MXFP4 scales' resource words
   // ([2W][H / 32] bytes); the unit's columns j0 .. j0 + nc - 1 (nc = NC, or NC / 2 at a
@@ -1626,7 +1684,7 @@ struct GuTile {
   __device__ __forceinline__ void issue(i32x4 wr, i32x4 sr, int W, int j0, int nc, uint8_t* slot, uint8_t* sslot,
                                         int lane, int wave, int b0 = 0, int b1 = kBlocks) {
     const int s0 = wave * SPW;
-    constexpr int ROWB = WFMT == kFp8 ? C::H : C::H / 2;  // bytes a weight row
+    constexpr int ROWB = F8 ? C::H : C::H / 2;  // bytes a weight row
     if constexpr (SH) {
       // SGLang's layout: the column block's gate tile is row group 2 b and its up tile 2 b + 1
       // (16 rows each), stored per K step as 1 KB in the MFMA operand's lane order; slot
@@ -1652,8 +1710,16 @@ struct GuTile {
     for (int i = 0; i < SLOT / 1024; ++i) {
       if (i < b0 || i >= b1) continue;
       const int pos = i * 64 + ln, r = pos / CPW, c = (pos % CPW) ^ key(r);
-      const bool live = (WFMT == kFp8 ? (r & 7) : (r & 15)) < nc;
+      const bool live = (F8 ? (r & 7) : (r & 15)) < nc;
       lds_dma16(wr, slot + i * 1024, live ? (uint32_t)wrow(W, j0, r) * ROWB + s0 * (RB / SPW) + c * 16 : kNoLoad);
+    }
+    if (WFMT == kFp8Mx && b0 == 0) {
+      // the E8M0 bytes of the wave's K steps (4 SPW from byte 4 s0) of the unit's two 32-row
+      // scale blocks, gate (rows j0 / 32) then up (rows (W + j0) / 32), in one LDS-direct load:
+      // lanes 0, 1 the gate row's 32 bytes from 4 s0, lanes 2, 3 the up row's, to sslot + 16 l
+      static_assert(4 * SPW <= 32, "a scale row's slice in two 16-byte pieces");
+      const int h = lane & 1, blk = (lane < 2 ? j0 : W + j0) / 32;
+      lds_dma16_cached(sr, sslot, lane < 4 ? (uint32_t)blk * (C::H / 32) + s0 * 4 + h * 16 : kNoLoad);
     }
     if (WFMT == kFp4 && b0 == 0) {
       // the scales of the wave's K steps (4 SPW bytes a row, from byte 4 s0) in one LDS-direct
@@ -1691,9 +1757,15 @@ struct GuTile {
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
           const int r = q * 16 + m;
-          const int c = WFMT == kFp8 ? i * 8 + j + 4 * w : i * 4 + j;
+          const int c = F8 ? i * 8 + j + 4 * w : i * 4 + j;
           a[q][i][w] = *(const u32x4*)(slot + (r * CPW + (c ^ key(r))) * 16);
         }
+    if constexpr (WFMT == kFp8Mx) {
+      // row m's scale row (gate rows 0..7, up rows 8..15), bytes 4 i + j / 2 and 4 i + 2 + j / 2
+      const uint8_t* row = sslot + (m < 8 ? 0 : 32);
+#pragma unroll
+      for (int i = 0; i < SPW; ++i) sa[0][i] = row[4 * i + (j >> 1)] | ((uint32_t)row[4 * i + 2 + (j >> 1)] << 8);
+    }
     if constexpr (WFMT == kFp4) {
       // byte j of dword i of row q 16 + m's slice: the E8M0 of the lane's row and block
 #pragma unroll
@@ -1716,7 +1788,7 @@ struct GuX {
   static constexpr int SPW = C::H / 128 / kWaves;
   u32x4 lo[SPW], hi[SPW];
   float sx[SPW];     // FP8: the pick's fp32 scale of the 128-block
-  uint32_t ex[SPW];  // MXFP8: the E8M0 byte of the lane's 32-block
+  uint32_t ex[SPW];  // MXFP8: the E8M0 byte of the lane's 32-block; MX FP8: the step's four codes
   template <class TokFn>
   __device__ __forceinline__ void load(const Params& p, int np, uint32_t qoff, uint32_t soff, TokFn tok, int lane,
                                        int wave) {
@@ -1731,6 +1803,11 @@ struct GuX {
         lo[i] = dld128(rs, qoff + t * C::H + k0 + 16 * j);
         hi[i] = dld128(rs, qoff + t * C::H + k0 + 64 + 16 * j);
         sx[i] = u2f(dld32(rs, soff + (t * (C::H / 128) + s0 + i) * 4));
+      } else if constexpr (WFMT == kFp8Mx) {
+        // the codes as FP8's; the step's four E8M0 bytes (blocks 4 ks .. 4 ks + 3) in one dword
+        lo[i] = dld128(rs, qoff + t * C::H + k0 + 16 * j);
+        hi[i] = dld128(rs, qoff + t * C::H + k0 + 64 + 16 * j);
+        ex[i] = dld32(rs, soff + t * (C::H / 32) + k0 / 32);
       } else {
         // the scaled MFMA takes K [16 j, 16 j + 16) and [64 + 16 j, ..); the converting path
         // the 32-K block j itself
@@ -1766,6 +1843,11 @@ __device__ __forceinline__ void gu_mma(const GuTile<C, WFMT, SH>& t, const GuX<C
       const f32x4 c = mma_fp8_step(t.a[0][i][0], t.a[0][i][1], x.lo[i], x.hi[i]);
 #pragma unroll
       for (int v = 0; v < 4; ++v) acc[0][v] = fmaf(c[v], f, acc[0][v]);
+    } else if constexpr (WFMT == kFp8Mx) {
+      const int jh = lane >> 5;  // (lane group j) / 2: the pieces' blocks are jh and 2 + jh
+      const uint32_t sw = t.sa[0][i], xe = x.ex[i];
+      acc[0] = mma_fp8mx_step(t.a[0][i][0], t.a[0][i][1], e8m0(sw & 0xffu), e8m0((sw >> 8) & 0xffu), x.lo[i], x.hi[i],
+                              e8m0((xe >> (8 * jh)) & 0xffu), e8m0((xe >> (8 * (2 + jh))) & 0xffu), acc[0]);
     } else {
       static_assert(T::NA == 2, "gate and up rows");
       if (scaled) {
@@ -1806,11 +1888,13 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
   };
   const int tid = threadIdx.x, lane = tid & 63, wave = (int)(threadIdx.x >> 6);
   const int nb = W / T::NC;
-  constexpr uint32_t WB = WFMT == kFp8 ? C::H : C::H / 2;  // bytes a weight row
+  constexpr uint32_t WB = T::F8 ? C::H : C::H / 2;  // bytes a weight row
   uint8_t* slot = sm.m.wslot[wave];
   uint8_t* sslot = sm.m.sslot[wave];
   // an MXFP4 weight's scales ([2W][H / 32] E8M0) as a resource (unused for FP8)
-  auto srsc = [&](const void* sp) { return weight_rsrc_words(sp, WFMT == kFp4 ? 2u * W * (C::H / 32) : 0u); };
+  auto srsc = [&](const void* sp) {
+    return weight_rsrc_words(sp, WFMT == kFp4 ? 2u * W * (C::H / 32) : WFMT == kFp8Mx ? 2u * W / 32 * (C::H / 32) : 0u);
+  };
   T t;
   GuX<C, WFMT> x;
   const uint8_t* wb;
@@ -1911,8 +1995,16 @@ struct DownTile {
   static constexpr int NA = NA_;  // 16-row A operands a unit
   static_assert(!SH || WFMT == kFp4, "the shuffled layout is MXFP4's");
   static constexpr bool kIsTile = true;
-  static constexpr int KS = KD / 128;
-  static constexpr int NW = WFMT == kFp8 ? 2 : 1;  // 16-byte words of a lane's step
+  // FP8 (fp32 128 x 128 scales, or E8M0 32 x 32: MX, whose K may end in half a step: the last
+  // step's K 64 .. 127 are zeros) or MXFP4 weights
+  static constexpr bool F8 = WFMT == kFp8 || WFMT == kFp8Mx;
+  static_assert(KD % 128 == 0 || (WFMT == kFp8Mx && KD % 64 == 0), "whole (MX FP8: half) steps");
+  static constexpr int KS = (KD + 127) / 128;
+  static constexpr bool HALF = KD % 128 != 0;  // the last step's second half is past the row
+  static constexpr int NW = F8 ? 2 : 1;  // 16-byte words of a lane's step
+  // MXFP4 in SGLang's layout: a scale row's E8M0 columns, padded to a multiple of 8
+  // (stages/dims.py:54-56, down_scale_cols)
+  static constexpr int SC = (KD / 32 + 7) / 8 * 8;
   static constexpr int BYTES = NA * NW * 16 * 64 * KS;  // registers' bytes a unit
   // units a wave requests at once: 16 KB of codes (MXFP4 rows of 1024 K: one unit, leaving
   // registers for the conversions)
@@ -1920,7 +2012,10 @@ struct DownTile {
       (WFMT == kFp4 && KS >= 8) || BYTES >= 16384 ? 1 : (16384 / BYTES > 4 ? 4 : 16384 / BYTES);
   static_assert(NA == 1 || WFMT == kFp4, "FP8 units are one 16-row block");
   u32x4 a[NA][KS][NW];
-  uint32_t sa[NA][KS];   // MXFP4: the E8M0 byte of the lane's row and block (load_scales<true>: the loaded dwords)
+  // MXFP4: the E8M0 byte of the lane's row and block (load_scales<true>: the loaded dwords); MX
+  // FP8: the lane's row block's codes of its two pieces' K blocks (low byte: 16 j .., next:
+  // 64 + 16 j ..)
+  uint32_t sa[NA][KS];
   float s0[KS], s1[KS];  // FP8: block scales of the lane's first and last C row
   int split;             // FP8: C elements v < split take s0, the rest s1
 
@@ -1931,11 +2026,12 @@ struct DownTile {
   // reads of one chunk fall in distinct banks. Rows past nv are requested past the resource
   // (zeros, no memory access). fetch() reads the slot into a[][] in the operand layout; the
   // scales travel in registers (load_scales, take_scales).
-  static constexpr int RB = WFMT == kFp8 ? KD : KD / 2;  // bytes a row
-  static constexpr int CPR = RB / 16;                   // chunks a row
-  static constexpr int SLOT = 16 * NA * RB;             // bytes a unit
-  static_assert(CPR >= 16 && (CPR & (CPR - 1)) == 0 && SLOT % 1024 == 0, "slot layout");
-  static_assert(WFMT == kFp8 || KS % 4 == 0, "MXFP4 scales in 16-byte loads");
+  static constexpr int RB = F8 ? KD : KD / 2;  // bytes a row
+  static constexpr int CPR = RB / 16;         // chunks a row
+  static constexpr int SLOT = 16 * NA * RB;   // bytes a unit
+  // (row-major units through LDS: the swizzle needs CPR a power of two of 16 or more; the
+  // shuffled layout's blocks go in whole)
+  static constexpr bool kRowMajorSlot = CPR >= 16 && (CPR & (CPR - 1)) == 0 && SLOT % 1024 == 0;
   // wr: a resource over the weight from row 0 (H x RB bytes a matrix); wrow: the unit's first
   // row's byte offset in it
   __device__ __forceinline__ static void issue(__amdgpu_buffer_rsrc_t wr, uint32_t wrow, int nv, uint8_t* slot,
@@ -1959,6 +2055,7 @@ struct DownTile {
       }
       return;
     }
+    static_assert(SH || kRowMajorSlot, "slot layout");
 #pragma unroll
     for (int i = 0; i < SLOT / 1024; ++i) {
       const int pos = i * 64 + lane;
@@ -1977,13 +2074,14 @@ struct DownTile {
         for (int ks = 0; ks < KS; ++ks) a[q][ks][0] = *(const u32x4*)(slot + (q * KS + ks) * 1024 + lane * 16);
       return;
     }
+    static_assert(SH || kRowMajorSlot, "slot layout");
 #pragma unroll
     for (int q = 0; q < NA; ++q)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-          const int c = WFMT == kFp8 ? ks * 8 + j + 4 * w : ks * 4 + j;
+          const int c = F8 ? ks * 8 + j + 4 * w : ks * 4 + j;
           a[q][ks][w] = *(const u32x4*)(slot + ((q * 16 + m) * CPR + (c ^ m)) * 16);
         }
   }
@@ -2005,6 +2103,16 @@ struct DownTile {
         s1[ks] = sp[(r3 / 128) * (KD / 128) + ks];
       }
       split = r0 / 128 == r3 / 128 ? 4 : 128 - (hb + 4 * j) % 128;
+    } else if constexpr (WFMT == kFp8Mx) {
+      // E8M0 [H / 32][KD / 32]: lane (m, j) supplies A row hb + m (a unit may straddle two
+      // 32-row blocks), its pieces of step ks in K blocks 4 ks + j / 2 and 4 ks + 2 + j / 2 (the
+      // second past the row in a half step)
+      const uint8_t* row = (const uint8_t*)s + (size_t)((hb + min(m, nv - 1)) / 32) * (KD / 32);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int b0 = 4 * ks + (j >> 1), b1 = b0 + 2;
+        sa[0][ks] = row[b0] | (b1 < KD / 32 ? (uint32_t)row[b1] << 8 : 0u);
+      }
     } else if constexpr (SH) {
       // shuffle_scale order (a [H][KD / 32] matrix of the expert): row h's bytes of K steps
       // 2 c and 2 c + 1, column j of each, are bytes 2 (step % 2) + (h / 16) % 2 of the dword
@@ -2015,20 +2123,23 @@ struct DownTile {
         const bool ok = q * 16 + m < nv;
         const int h = hb + (ok ? q * 16 + m : 0);
         const int a = (h >> 4) & 1;
+        // chunk c (256 bytes) holds steps 2 c and 2 c + 1 (with an odd KS the last holds one);
+        // a 32-row block's chunks are SC / 8 (the padded columns)
 #pragma unroll
-        for (int c = 0; c < KS / 2; ++c) {
-          const uint32_t dw = ok ? *(const uint32_t*)(ss + (size_t)(h / 32) * (KD / 32) * 32 + c * 256 +
+        for (int c = 0; c < (KS + 1) / 2; ++c) {
+          const uint32_t dw = ok ? *(const uint32_t*)(ss + (size_t)(h / 32) * SC * 32 + c * 256 +
                                                       (16 * j + (h & 15)) * 4)
                                  : 0x7f7f7f7fu;
           if constexpr (RAW) {
             sa[q][2 * c] = dw;
           } else {
             sa[q][2 * c] = (dw >> (8 * a)) & 0xffu;
-            sa[q][2 * c + 1] = (dw >> (8 * (2 + a))) & 0xffu;
+            if (2 * c + 1 < KS) sa[q][2 * c + 1] = (dw >> (8 * (2 + a))) & 0xffu;
           }
         }
       }
     } else {
+      static_assert(KS % 4 == 0, "MXFP4 scales in 16-byte loads");
       const uint8_t* ss = (const uint8_t*)s;
 #pragma unroll
       for (int q = 0; q < NA; ++q) {
@@ -2069,10 +2180,10 @@ struct DownTile {
       for (int q = 0; q < NA; ++q) {
         const int a = ((hb + q * 16 + m) >> 4) & 1;  // rows past nv: 0x7f in every byte
 #pragma unroll
-        for (int c = 0; c < KS / 2; ++c) {
+        for (int c = 0; c < (KS + 1) / 2; ++c) {
           const uint32_t dw = o.sa[q][2 * c];
           sa[q][2 * c] = (dw >> (8 * a)) & 0xffu;
-          sa[q][2 * c + 1] = (dw >> (8 * (2 + a))) & 0xffu;
+          if (2 * c + 1 < KS) sa[q][2 * c + 1] = (dw >> (8 * (2 + a))) & 0xffu;
         }
       }
     } else if constexpr (WFMT == kFp4) {
@@ -2080,6 +2191,9 @@ struct DownTile {
       for (int q = 0; q < NA; ++q)
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) sa[q][ks] = (o.sa[q][ks] >> (8 * j)) & 0xffu;
+    } else if constexpr (WFMT == kFp8Mx) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) sa[0][ks] = o.sa[0][ks];
     }
     split = o.split;
   }
@@ -2090,13 +2204,14 @@ struct DownTile {
     const int m = lane & 15, j = lane >> 4;
     const bool ok = m < nv;
     const size_t h = (size_t)hb + (ok ? m : 0);
-    if constexpr (WFMT == kFp8) {
+    if constexpr (F8) {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const uint8_t* p = w + h * KD + ks * 128 + 16 * j;
+        const bool tail = HALF && ks == KS - 1;  // K 64 .. 127 of the step: past the row
         if (ok) {
           a[0][ks][0] = ld16_nt(p);
-          a[0][ks][1] = ld16_nt(p + 64);
+          a[0][ks][1] = tail ? u32x4{0u, 0u, 0u, 0u} : ld16_nt(p + 64);
         } else {
           a[0][ks][0] = a[0][ks][1] = u32x4{0u, 0u, 0u, 0u};
         }
@@ -2123,7 +2238,17 @@ struct DownTile {
     for (int q = 0; q < NA; ++q) acc[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      if constexpr (WFMT == kFp8) {
+      if constexpr (WFMT == kFp8Mx) {
+        const bool tail = HALF && ks == KS - 1;
+        u32x4 blo = *(const u32x4*)(xr + ks * 128 + 16 * j);
+        u32x4 bhi = tail ? u32x4{0u, 0u, 0u, 0u} : *(const u32x4*)(xr + ks * 128 + 64 + 16 * j);
+        if (!live) blo = bhi = u32x4{0u, 0u, 0u, 0u};
+        const int b0 = 4 * ks + (j >> 1);
+        const float sxl = e8m0(xs[row * SST + b0]), sxh = tail ? 1.0f : e8m0(xs[row * SST + b0 + 2]);
+        const uint32_t sw = sa[0][ks];
+        acc[0] = mma_fp8mx_step(a[0][ks][0], a[0][ks][1], e8m0(sw & 0xffu), e8m0((sw >> 8) & 0xffu), blo, bhi, sxl, sxh,
+                                acc[0]);
+      } else if constexpr (WFMT == kFp8) {
         u32x4 blo = *(const u32x4*)(xr + ks * 128 + 16 * j), bhi = *(const u32x4*)(xr + ks * 128 + 64 + 16 * j);
         if (!live) blo = bhi = u32x4{0u, 0u, 0u, 0u};
         const float sx = ((const float*)(xs + row * SST))[ks];
@@ -2449,11 +2574,14 @@ __device__ __forceinline__ void down_pipeline(DownBatch<Rows>& bt, int n, LoadFn
 // A thread's chunks (8 values each) are requested NB at a time before any is
 // converted, so a batch costs one trip to memory.
 constexpr int kQuantBatch = 4;
+// The rule by FMT, the weight format the rows feed: group-128 fp8 with fp32 scales (kFp8), MXFP8
+// per 32 with the "aiter" code (kFp4) or the "vllm" code (kFp8Mx), E8M0 bytes
 template <int FMT, int W, int QS, int NB = kQuantBatch, class RowFn>
 __device__ __forceinline__ void quant_rows_lds(const Params& p, RowFn src_row, int n, uint8_t* q, void* s) {
 #pragma clang fp contract(off)
   constexpr int PER = W / 8;  // 8-value chunks a row
-  static_assert(kThreads % PER == 0, "a thread keeps its column chunk");
+  // a group's chunks lie in adjacent lanes of one wave (rows hold whole groups)
+  static_assert(PER % (FMT == kFp8 ? 16 : 4) == 0, "whole groups a row");
   const int tid = threadIdx.x;
   const auto rs = ws_rsrc(p);
   // a wave's lanes cover consecutive chunks so that a group's lanes are adjacent
@@ -2497,7 +2625,7 @@ __device__ __forceinline__ void quant_rows_lds(const Params& p, RowFn src_row, i
         }
       } else {
         float g = group_max<4>(am);
-        int code = mx_code(g);
+        int code = FMT == kFp8Mx ? vllm_code(g) : mx_code(g);
         float inv = mx_inv(code);
         const uint32_t lo = e4m3_pack4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
         const uint32_t hi = e4m3_pack4(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
@@ -2518,13 +2646,16 @@ template <int FMT, int W>
 __device__ __forceinline__ void quant_row_ws(const Params& p, uint32_t src, uint32_t dq, uint32_t ds, int lane) {
 #pragma clang fp contract(off)
   constexpr int PER = W / 8;  // 8-value chunks a row
-  constexpr int CPL = PER / 64;
-  static_assert(CPL * 64 == PER, "a lane takes whole chunks");
+  constexpr int CPL = (PER + 63) / 64;
+  // the chunks past the row (a last round of fewer than 64) are whole groups of lanes, which
+  // load and store nothing
+  static_assert(PER % (FMT == kFp8 ? 16 : 4) == 0, "whole groups a row");
   const auto rs = ws_rsrc(p);
 #pragma unroll 1
   for (int t = 0; t < CPL; ++t) {
     const int c = lane + 64 * t;
-    const u32x4 xv = dld128(rs, src + c * 16);
+    const bool ok = PER % 64 == 0 || c < PER;
+    const u32x4 xv = ok ? dld128(rs, src + c * 16) : u32x4{0u, 0u, 0u, 0u};
     const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
     float v[8];
     float am = 0.0f;
@@ -2540,16 +2671,16 @@ __device__ __forceinline__ void quant_row_ws(const Params& p, uint32_t src, uint
       const float sc = group_scale(g);
       const uint32_t lo = e4m3_pack4(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
       const uint32_t hi = e4m3_pack4(v[4] / sc, v[5] / sc, v[6] / sc, v[7] / sc);
-      dst64(rs, dq + c * 8, u32x2{lo, hi});
-      if ((c & 15) == 0) dst32(rs, ds + (c / 16) * 4, f2u(sc));
+      if (ok) dst64(rs, dq + c * 8, u32x2{lo, hi});
+      if (ok && (c & 15) == 0) dst32(rs, ds + (c / 16) * 4, f2u(sc));
     } else {
       const float g = group_max<4>(am);
-      const int code = mx_code(g);
+      const int code = FMT == kFp8Mx ? vllm_code(g) : mx_code(g);
       const float inv = mx_inv(code);
       const uint32_t lo = e4m3_pack4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
       const uint32_t hi = e4m3_pack4(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
-      dst64(rs, dq + c * 8, u32x2{lo, hi});
-      if ((c & 3) == 0) dst8(rs, ds + c / 4, (uint8_t)code);
+      if (ok) dst64(rs, dq + c * 8, u32x2{lo, hi});
+      if (ok && (c & 3) == 0) dst8(rs, ds + c / 4, (uint8_t)code);
     }
   }
 }
@@ -2578,7 +2709,7 @@ constexpr int kRowBlocks = kTileMax / kDownLanes;
 template <class C>
 struct SharedDownSmem {
   uint8_t q[kRowsMax * C::SQS];
-  float s[kRowsMax * (C::S / 128)];
+  float s[(kRowsMax * C::SSC + 3) / 4];  // fp32 per 128 or E8M0 per 32 (C::SSC bytes a row)
 };
 
 // the shared down's units a wave requests at once: one (MFMA: a 16-row block for every row of
@@ -2589,7 +2720,7 @@ struct Batched : Rows {
 };
 template <class C, bool MF>
 using SharedDownBatch =
-    DownBatch<Batched<typename std::conditional<MF, DownTile<kFp8, C::S>, DownRows<kFp8, C::S>>::type>>;
+    DownBatch<Batched<typename std::conditional<MF, DownTile<C::SFMT, C::S>, DownRows<kFp8, C::S>>::type>>;
 
 // loader of the shared down's units of tile rows [h0, h0 + hn) (MFMA: unit v is the 16-row
 // block v, for every row of the step; VALU: an 8-row block and kPickBlock rows)
@@ -2597,7 +2728,7 @@ template <class C, bool MF>
 __device__ __forceinline__ auto shared_down_loader(const Params& p, int h0, int hn) {
   const int lane = threadIdx.x & 63, g = lane / kDownLanes, l = lane % kDownLanes;
   if constexpr (MF) {
-    return [&p, h0, hn, lane](int v, DownTile<kFp8, C::S>& dt) {
+    return [&p, h0, hn, lane](int v, DownTile<C::SFMT, C::S>& dt) {
       dt.load(p.sw2, p.sw2_s, h0 + v * 16, min(16, hn - v * 16), lane);
     };
   } else {
@@ -2633,16 +2764,16 @@ __device__ __forceinline__ void shared_down_tile(const Params& p, SharedDownSmem
   if constexpr (GQ) {
     // the step's shared rows, quantized once (stage Q), copied in as they lie
     ws_to_lds(p, p.off[14], (uint32_t)R * C::SQS, sm.q);
-    ws_to_lds(p, p.off[15], (uint32_t)R * (C::S / 128) * 4, (uint8_t*)sm.s);
+    ws_to_lds(p, p.off[15], (uint32_t)R * C::SSC, (uint8_t*)sm.s);
     wait_vm0();
   } else {
     // (2 chunks a thread at once with MXFP4 routed experts: 4 spill the persistent launch there)
-    quant_rows_lds<kFp8, C::S, C::SQS, C::FMT == kFp4 ? 2 : kQuantBatch>(
+    quant_rows_lds<C::SFMT, C::S, C::SQS, C::FMT == kFp4 ? 2 : kQuantBatch>(
         p, [&](int i) { return p.off[8] + (uint32_t)i * C::S * 2; }, R, sm.q, sm.s);
   }
   __syncthreads();
   if constexpr (MF) {
-    using DT = Batched<DownTile<kFp8, C::S>>;
+    using DT = Batched<DownTile<C::SFMT, C::S>>;
     down_pipeline<DT>(bt, n_units, load, [&](int v, DT& dt) {
       const int n = lane & 15;
 #pragma unroll 1
@@ -2650,7 +2781,7 @@ __device__ __forceinline__ void shared_down_tile(const Params& p, SharedDownSmem
         const int np = min(kMfmaPicks, R - t0);
         f32x4 acc[1];
         dt.opaque();
-        dt.template mma<C::SQS, (C::S / 128) * 4>(sm.q, (const uint8_t*)sm.s, t0, np, lane, false, acc);
+        dt.template mma<C::SQS, C::SSC>(sm.q, (const uint8_t*)sm.s, t0, np, lane, false, acc);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const int hl = v * 16 + 4 * (lane >> 4) + k;
@@ -2659,6 +2790,7 @@ __device__ __forceinline__ void shared_down_tile(const Params& p, SharedDownSmem
       }
     });
   } else {
+    static_assert(C::SFMT == kFp8, "the VALU GEMVs read FP8 128 x 128 shared rows");
     using DR = Batched<DownRows<kFp8, C::S>>;
     down_pipeline<DR>(bt, n_units, load, [&](int v, const DR& wr) {
       const int rb = v % kRowBlocks, pb = v / kRowBlocks;
@@ -2744,7 +2876,7 @@ __device__ __forceinline__ void gate_up_valu(const Params& p, const Union<C>& un
 template <class C>
 __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un, GuSmem<C>& sm, int b, int nwg) {
   const auto rs = ws_rsrc(p);
-  const int n_sh = (p.rows + kMfmaPicks - 1) / kMfmaPicks * (C::S / GuTile<C, kFp8>::NC);
+  const int n_sh = (p.rows + kMfmaPicks - 1) / kMfmaPicks * (C::S / GuTile<C, C::SFMT>::NC);
   const int n_rt = un.ntg_r * (C::I / GuTile<C, C::FMT>::NC);
   // FP8: the share in half-units (a unit's first or last NC / 2 columns), so that shares
   // differ by half a unit at most (with MXFP4 weights the extra bookkeeping crowds the
@@ -2756,14 +2888,14 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
   {
     const uint32_t qoff = C::FMT == kFp4 ? p.off[3] : p.off[1];
     const uint32_t soff = C::FMT == kFp4 ? p.off[4] : p.off[2];
-    gu_mfma<C, kFp8, HALF, false>(
+    gu_mfma<C, C::SFMT, HALF, false>(
         sm, C::S, lo, min(hi, HU * n_sh), false,
         [&](int tg, const uint8_t*& w, const void*& s, int& np) {
           w = p.sgu;
           s = p.sgu_s;
           np = min(kMfmaPicks, p.rows - tg * kMfmaPicks);
         },
-        [&](int tg, int np, GuX<C, kFp8>& x) {
+        [&](int tg, int np, GuX<C, C::SFMT>& x) {
           x.load(p, np, qoff, soff, [&](int r) { return tg * kMfmaPicks + r; }, threadIdx.x & 63, (int)(threadIdx.x >> 6));
         },
         [&](int tg, int q, int col, float g, float u) {
@@ -2801,7 +2933,8 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
 
 template <class C>
 __device__ __forceinline__ void stage_c(const Params& p, const Union<C>& un, GuSmem<C>& sm, int b, int nwg) {
-  if (gate_on_mfma<C>(p.rows, p.mfma_gate)) gate_up_mfma<C>(p, un, sm, b, nwg);
+  if constexpr (C::SHUF) gate_up_mfma<C>(p, un, sm, b, nwg);  // (the VALU GEMVs read row-major rows)
+  else if (gate_on_mfma<C>(p.rows, p.mfma_gate)) gate_up_mfma<C>(p, un, sm, b, nwg);
   else gate_up_valu<C>(p, un, sm.x, b, nwg);
 }
 
@@ -2884,17 +3017,29 @@ __device__ __forceinline__ void mfma_issue(const Params& p, const Union<C>& un, 
   if constexpr (C::FMT == kFp8)
     nx.load_scales((const float*)p.w2_s + (size_t)e * (C::H / 128) * (C::I / 128), hb, nv, lane);
   else
-    nx.template load_scales<true>((const uint8_t*)p.w2_s + (size_t)e * C::H * (C::I / 32), hb, nv, lane);
+    // (SGLang's layout: the flat [E H][SC] scale matrix's columns are padded to a multiple of 8)
+    nx.template load_scales<true>((const uint8_t*)p.w2_s + (size_t)e * C::H * (C::SHUF ? DT::SC : C::I / 32), hb, nv,
+                                  lane);
 }
 
 // picks [pb0, pb0 + pbn) of the union's order, quantized once (stage Q), into the LDS rows of
 // the down stage as they lie (codes [pick][MQS], scales [pick][MSC words]); waited for here
+// (a pick's scale bytes need not be a multiple of 16: I / 32 = 20 at I = 640; the copy then
+// starts at the 16-byte boundary below the batch's first scale, and the batch's scales begin
+// pick_batch_scales() bytes into sm.s)
+template <class C>
+__device__ __forceinline__ uint32_t pick_batch_scales(int pb0) {
+  constexpr uint32_t SST = C::FMT == kFp4 ? C::I / 32 : (C::I / 128) * 4;
+  return (uint32_t)pb0 * SST % 16;
+}
 template <class C>
 __device__ __forceinline__ void copy_pick_batch(const Params& p, int pb0, int pbn, DownSmem<C>& sm) {
   constexpr uint32_t SST = C::FMT == kFp4 ? C::I / 32 : (C::I / 128) * 4;  // scale bytes of a pick
-  static_assert(C::MQS % 16 == 0 && SST % 16 == 0, "16-byte pieces");
+  static_assert(C::MQS % 16 == 0, "16-byte pieces");
+  static_assert(SST % 16 == 0 || sizeof(sm.s) >= C::PB * SST + 16, "room for the aligned copy");
   ws_to_lds(p, p.off[12] + (uint32_t)pb0 * C::MQS, (uint32_t)pbn * C::MQS, sm.q);
-  ws_to_lds(p, p.off[13] + (uint32_t)pb0 * SST, (uint32_t)pbn * SST, (uint8_t*)sm.s);
+  const uint32_t a = (uint32_t)pb0 * SST - pick_batch_scales<C>(pb0);
+  ws_to_lds(p, p.off[13] + a, (uint32_t)(pb0 + pbn) * SST - a, (uint8_t*)sm.s);
   wait_vm0();
 }
 
@@ -2929,7 +3074,8 @@ __device__ __forceinline__ void down_valu(const Params& p, const Union<C>& un, D
         const int np = min(kPickBlock, j1 - jj);
         const int lp = jj - pb0;
         float acc[kPickBlock];
-        wr.template dot<C::MQS, SST>(sm.q + (size_t)lp * C::MQS, sm.s + lp * SST, np, l, acc);
+        wr.template dot<C::MQS, SST>(sm.q + (size_t)lp * C::MQS, sm.s + (GQ ? pick_batch_scales<C>(pb0) : 0u) + lp * SST,
+                                     np, l, acc);
 #pragma unroll
         for (int q = 0; q < kPickBlock; ++q) {
           const float y = tree_sum<kDownLanes>(acc[q]);
@@ -3010,7 +3156,8 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
       for (int jj = j0; jj < j1; jj += kMfmaPicks) {
         const int np = min(kMfmaPicks, j1 - jj);
         f32x4 acc[DT::NA];
-        cur.template mma<C::MQS, SST>(sm.q, sm.s, jj - pb0, np, lane, C::FMT == kFp4 && p.mx_scaled_down, acc);
+        cur.template mma<C::MQS, SST>(sm.q, sm.s + (GQ ? pick_batch_scales<C>(pb0) : 0u), jj - pb0, np, lane,
+                                      C::FMT == kFp4 && p.mx_scaled_down, acc);
         const int pk = n < np ? un.picks[jj + n] : 0;
 #pragma unroll
         for (int q = 0; q < DT::NA; ++q)
@@ -3114,8 +3261,8 @@ __device__ __forceinline__ void stage_q(const Params& p, const Union<C>& un, int
                                  p.off[13] + (uint32_t)j * SST, lane);
     } else {
       const int r = j - npk;
-      quant_row_ws<kFp8, C::S>(p, p.off[8] + (uint32_t)r * C::S * 2, p.off[14] + (uint32_t)r * C::SQS,
-                               p.off[15] + (uint32_t)r * (C::S / 128) * 4, lane);
+      quant_row_ws<C::SFMT, C::S>(p, p.off[8] + (uint32_t)r * C::S * 2, p.off[14] + (uint32_t)r * C::SQS,
+                                  p.off[15] + (uint32_t)r * C::SSC, lane);
     }
   }
 }
@@ -3127,8 +3274,9 @@ constexpr int kSharedFirstRows = 16;
 // hold the units' block scales in sh
 template <class C>
 __device__ __forceinline__ void shared_first_issue(const Params& p, DownSmem<C>& sm, int h0, int hn,
-                                                   DownTile<kFp8, C::S>& sh) {
+                                                   DownTile<C::SFMT, C::S>& sh) {
   using DT = DownTile<kFp8, C::S>;
+  static_assert(C::SFMT == kFp8, "the shared down first: FP8 128 x 128 units");
   static_assert(DT::SLOT <= DownTileOf<C>::SLOT, "a shared unit fits a routed unit's slot");
   const int wave = (int)(threadIdx.x >> 6), v = wave - 1;
   if (v < 0 || v >= 2 || v * 16 >= hn) return;
@@ -3142,7 +3290,7 @@ __device__ __forceinline__ void shared_first_issue(const Params& p, DownSmem<C>&
 // complete and the LDS rows free
 template <class C>
 __device__ __forceinline__ void shared_first_run(const Params& p, DownSmem<C>& sm, int h0, int hn,
-                                                 DownTile<kFp8, C::S>& sh) {
+                                                 DownTile<C::SFMT, C::S>& sh) {
   using DT = DownTile<kFp8, C::S>;
   const int R = p.rows, lane = threadIdx.x & 63, wave = (int)(threadIdx.x >> 6), v = wave - 1;
   __syncthreads();  // the LDS's previous users are done
@@ -3161,7 +3309,7 @@ __device__ __forceinline__ void shared_first_run(const Params& p, DownSmem<C>& s
       const int np = min(kMfmaPicks, R - t0);
       f32x4 acc[1];
       cur.opaque();
-      cur.template mma<C::SQS, (C::S / 128) * 4>(sm.sd.q, (const uint8_t*)sm.sd.s, t0, np, lane, false, acc);
+      cur.template mma<C::SQS, C::SSC>(sm.sd.q, (const uint8_t*)sm.sd.s, t0, np, lane, false, acc);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int hl = v * 16 + 4 * (lane >> 4) + k;
@@ -3189,7 +3337,7 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
   const bool early = first && (p.rows < 8 || 4 * flags_set_count(p, kCtlC, nwg) < 3 * nwg);
   // SHF: the shared expert's down first, during the Q hand-off; its units are requested with
   // the routed ones
-  DownTile<kFp8, C::S> sh;
+  DownTile<C::SFMT, C::S> sh;
   if (early) {
     down_first<C, MF>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt, SHF);
     if constexpr (SHF) shared_first_issue<C>(p, sm, b * tr, min(tr, C::H - b * tr), sh);
@@ -3268,13 +3416,13 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   arrive(p, kCtlC);
   TL(kTlCArrived);
   const bool gq = p.rows >= C::QROWS;
-  if (down_on_mfma<C>(p.rows, p.mfma_down)) {
+  if (C::SHUF || down_on_mfma<C>(p.rows, p.mfma_down)) {
     // the shared down first, inside the Q hand-off, up to kSharedFirstRows rows (above, its
     // rows' quantize outlasts the hand-off)
     if (gq && C::SF && p.rows <= kSharedFirstRows) wait_then_d<C, true, true, C::SF>(p, un, sm.d, b, nwg);
     else if (gq) wait_then_d<C, true, true>(p, un, sm.d, b, nwg);
     else wait_then_d<C, true, false>(p, un, sm.d, b, nwg);
-  } else {
+  } else if constexpr (!C::SHUF) {
     if (gq) wait_then_d<C, false, true>(p, un, sm.d, b, nwg);
     else wait_then_d<C, false, false>(p, un, sm.d, b, nwg);
   }
@@ -3317,11 +3465,11 @@ __global__ __launch_bounds__(kThreads) void k_d(Params p) {
   __shared__ DownSmem<C> sm;
   build_union<C>(p, un, false);
   const bool gq = p.rows >= C::QROWS;
-  if (down_on_mfma<C>(p.rows, p.mfma_down)) {
+  if (C::SHUF || down_on_mfma<C>(p.rows, p.mfma_down)) {
     DownBatchOf<C, true> bt;
     if (gq) stage_d<C, true, true>(p, un, sm, blockIdx.x, gridDim.x, bt, false);
     else stage_d<C, true, false>(p, un, sm, blockIdx.x, gridDim.x, bt, false);
-  } else {
+  } else if constexpr (!C::SHUF) {
     DownBatchOf<C, false> bt;
     if (gq) stage_d<C, false, true>(p, un, sm, blockIdx.x, gridDim.x, bt, false);
     else stage_d<C, false, false>(p, un, sm, blockIdx.x, gridDim.x, bt, false);
@@ -3445,6 +3593,9 @@ MKMOE_LAUNCHER(5, CfgTp2Fp4NormAiter)
 #if !defined(MKMOE_UNIT) || MKMOE_UNIT == 6
 MKMOE_LAUNCHER(6, CfgPlumbingSoftplus)
 #endif
+#if !defined(MKMOE_UNIT) || MKMOE_UNIT == 7
+MKMOE_LAUNCHER(7, CfgV41Tp4)
+#endif
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg0(const Params&, int, hipStream_t, bool);
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg1(const Params&, int, hipStream_t, bool);
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg2(const Params&, int, hipStream_t, bool);
@@ -3452,6 +3603,7 @@ __attribute__((visibility("hidden"))) int mkmoe_launch_cfg3(const Params&, int, 
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg4(const Params&, int, hipStream_t, bool);
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg5(const Params&, int, hipStream_t, bool);
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg6(const Params&, int, hipStream_t, bool);
+__attribute__((visibility("hidden"))) int mkmoe_launch_cfg7(const Params&, int, hipStream_t, bool);
 
 #if !defined(MKMOE_UNIT) || MKMOE_UNIT == MKMOE_UNIT_HOST
 namespace {
@@ -3555,7 +3707,7 @@ int device_info(int dev, DevInfo* out) {
 
 enum CfgId {
   kNone = -1, kIdPlumbing = 0, kIdTp4Fp8, kIdTp4Fp4, kIdTp2Fp4Norm, kIdTp4Fp4Aiter, kIdTp2Fp4NormAiter,
-  kIdPlumbingSoftplus
+  kIdPlumbingSoftplus, kIdV41Tp4
 };
 
 template <class C>
@@ -3563,7 +3715,7 @@ bool shape_is(const mkmoe_shape* s) {
   return s->hidden == C::H && s->experts == C::E && s->topk == C::K && s->n_group == C::NG &&
          s->topk_group == C::TG && s->inter == C::I && s->shared_inter == C::S &&
          s->routed_fmt == (C::SHUF ? kFp4Aiter : C::FMT) && s->router_parts == C::P && (s->use_norm != 0) == C::NORM &&
-         s->scoring == C::SCORE;
+         s->scoring == C::SCORE && (s->shared_fmt == 0 ? kFp8 : s->shared_fmt) == C::SFMT;
 }
 
 int cfg_id(const mkmoe_shape* s) {
@@ -3575,6 +3727,7 @@ int cfg_id(const mkmoe_shape* s) {
   if (shape_is<CfgTp4Fp4Aiter>(s)) return kIdTp4Fp4Aiter;
   if (shape_is<CfgTp2Fp4NormAiter>(s)) return kIdTp2Fp4NormAiter;
   if (shape_is<CfgPlumbingSoftplus>(s)) return kIdPlumbingSoftplus;
+  if (shape_is<CfgV41Tp4>(s)) return kIdV41Tp4;
   return kNone;
 }
 
@@ -3588,7 +3741,7 @@ int check_shape(const mkmoe_shape* s) {
 Layout layout_of(const mkmoe_shape* s) {
   return make_layout(s->hidden, s->experts, s->topk, s->inter, s->shared_inter,
                      s->routed_fmt == kFp4Aiter ? kFp4 : s->routed_fmt,
-                     s->router_parts, s->use_norm, s->max_rows);
+                     s->router_parts, s->use_norm, s->max_rows, s->shared_fmt == kFp8Mx ? kFp8Mx : kFp8);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -3684,6 +3837,7 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
     case kIdTp4Fp4Aiter: return mkmoe_launch_cfg4(p, nwg, st, staged);
     case kIdTp2Fp4NormAiter: return mkmoe_launch_cfg5(p, nwg, st, staged);
     case kIdPlumbingSoftplus: return mkmoe_launch_cfg6(p, nwg, st, staged);
+    case kIdV41Tp4: return mkmoe_launch_cfg7(p, nwg, st, staged);
   }
   return MKMOE_ERR_SHAPE;
 }

@@ -77,7 +77,17 @@ MKMOE_HD inline int mx_code(float amax) {
   int c = code_ceil(a * kInv448);
   return c < 1 ? 1 : (c > 254 ? 254 : c);
 }
-// 2^(127 - code), exact for code in [1, 253]; code 254 gives 2^-127 (subnormal)
+// the MXFP8 "vllm" code of a group amax (vLLM's mxfp8_e4m3_quantize, the V4.1 shared expert's
+// activations and intermediate: stages/moe.py:234-245, check_ffn.py:99-101): the smallest power
+// of two >= fp32(max(amax, FLT_MIN) / 448) (a correctly rounded division), clamped to [0, 254]
+MKMOE_HD inline int vllm_code(float amax) {
+#pragma clang fp contract(off)
+  const float kFltMin = 1.17549435e-38f;
+  float a = amax > kFltMin ? amax : kFltMin;
+  int c = code_ceil(a / kFp8Max);
+  return c < 0 ? 0 : (c > 254 ? 254 : c);
+}
+// 2^(127 - code), exact for code in [0, 253]; code 254 gives 2^-127 (subnormal)
 MKMOE_HD inline float mx_inv(int code) {
   return code <= 253 ? u2f((uint32_t)(254 - code) << 23) : u2f(0x00200000u);
 }

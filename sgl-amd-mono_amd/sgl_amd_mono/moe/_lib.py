@@ -22,10 +22,11 @@ TL_NAMES = (
     "down units", "down first unit", "down barrier",
 )  # fmt: skip
 
-ABI_VERSION = 4  # MKMOE_ABI_VERSION of include/mkmoe.h that this binding follows
+ABI_VERSION = 5  # MKMOE_ABI_VERSION of include/mkmoe.h that this binding follows
 FMT_FP8_B128 = 1
 FMT_MXFP4 = 2
 FMT_MXFP4_AITER = 3  # MXFP4 in SGLang's loaded gfx950 layout (aiter's shuffles), read in place
+FMT_FP8_MX32 = 4  # FP8 with E8M0 32 x 32 scales (the V4.1 shared expert)
 SCORE_CODES = {"sigmoid": 0, "sqrt_softplus": 1}  # MKMOE_SCORE_*
 ERRW_WORDS = 8
 ERRW_CODE, ERRW_STAGE, ERRW_BLOCK, ERRW_COUNT, ERRW_FAULT = 0, 1, 2, 3, 4
@@ -93,6 +94,7 @@ class Shape(ctypes.Structure):
         ("swiglu_limit", ctypes.c_float),
         ("norm_eps", ctypes.c_float),
         ("scoring", ctypes.c_int32),
+        ("shared_fmt", ctypes.c_int32),
     ]
 
 
@@ -211,15 +213,21 @@ def check(rc: int, what: str) -> None:
 LAYOUTS = ("row_major", "aiter")
 
 
-def shape_of(preset, max_rows: int | None = None, layout: str = "row_major") -> Shape:
+def shape_of(preset, max_rows: int | None = None, layout: str | None = None) -> Shape:
     """The C shape of a ``presets.MoePreset`` whose routed experts are in ``layout``: row-major
-    (include/mkmoe.h), or SGLang's loaded gfx950 layout of MXFP4 experts ("aiter")."""
+    (include/mkmoe.h), or SGLang's loaded gfx950 layout of MXFP4 experts ("aiter"); by default
+    the preset's own (aiter for a preset compiled for that layout alone, else row-major)."""
     from .presets import FMT_CODES
+
+    if layout is None:
+        layout = "aiter" if preset.aiter_only else "row_major"
 
     if layout not in LAYOUTS:
         raise ValueError(f"layout {layout!r}: one of {LAYOUTS}")
     if layout == "aiter" and preset.routed_fmt != "mxfp4":
         raise ValueError("the aiter layout is MXFP4's")
+    if preset.aiter_only and layout != "aiter":
+        raise ValueError(f"{preset.name} is compiled for SGLang's loaded (aiter) layout alone")
 
     return Shape(
         hidden=preset.hidden,
@@ -238,4 +246,5 @@ def shape_of(preset, max_rows: int | None = None, layout: str = "row_major") -> 
         swiglu_limit=preset.swiglu_limit,
         norm_eps=0.0 if preset.norm_eps is None else preset.norm_eps,
         scoring=SCORE_CODES[preset.scoring],
+        shared_fmt=FMT_CODES[preset.shared_fmt],
     )

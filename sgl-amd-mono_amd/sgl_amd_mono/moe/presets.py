@@ -11,7 +11,13 @@ Fields:
 - inter / shared_inter: a routed / the shared expert's intermediate width on
   this rank (the TP share)
 - routed_fmt: "fp8_b128" (e4m3 with fp32 128 x 128 block scales) or "mxfp4"
-  (e2m1 with an E8M0 scale per 32 K); the shared expert is always fp8_b128
+  (e2m1 with an E8M0 scale per 32 K)
+- shared_fmt: the shared expert's, "fp8_b128" (its activations and intermediate quantized
+  per 128 with fp32 scales) or "fp8_mx32" (e4m3 with E8M0 32 x 32 block scales, fed by MXFP8
+  of the "vllm" rule: V4.1's, ``gfx950/runner.py:143-146``, ``check_ffn.py:118-121,226-231``)
+- inter_real: a routed expert's real width on this rank when the loader pads it with zero
+  weights to ``inter`` (V4.1: 2304 / 4 = 576 padded to 640, ``stages/dims.py:13-46``)
+- aiter_only: compiled for SGLang's loaded gfx950 layout of the MXFP4 experts alone
 - routed_scale, swiglu_limit: the weights' scale after normalisation and the
   SwiGLU clamp (the reference's 1.5 and 10.0 at ``stages/moe.py:96-97``)
 - router_parts: contiguous K parts of the router GEMV summed in order (the
@@ -26,7 +32,7 @@ from __future__ import annotations
 
 from dataclasses import asdict, dataclass
 
-FMT_CODES = {"fp8_b128": 1, "mxfp4": 2}
+FMT_CODES = {"fp8_b128": 1, "mxfp4": 2, "fp8_mx32": 4}
 
 
 @dataclass(frozen=True)
@@ -47,14 +53,19 @@ class MoePreset:
     max_rows: int = 48
     renorm: bool = True
     scoring: str = "sigmoid"
+    shared_fmt: str = "fp8_b128"
+    inter_real: int | None = None
+    aiter_only: bool = False
 
     def as_dict(self) -> dict:
         return asdict(self)
 
     @property
     def routed_expert_bytes(self) -> int:
-        """HBM bytes of one routed expert (gate_up + down, weights + scales)."""
-        h, i = self.hidden, self.inter
+        """HBM bytes of one routed expert (gate_up + down, weights + scales), at its real width
+        (a padded layout's zero columns are not counted: they need not be read)."""
+        h = self.hidden
+        i = self.inter if self.inter_real is None else self.inter_real
         if self.routed_fmt == "mxfp4":
             return 3 * i * h // 2 + 3 * i * h // 32
         return 3 * i * h + 4 * (-(-2 * i // 128) * -(-h // 128) + -(-h // 128) * -(-i // 128))
@@ -62,6 +73,8 @@ class MoePreset:
     @property
     def shared_bytes(self) -> int:
         h, i = self.hidden, self.shared_inter
+        if self.shared_fmt == "fp8_mx32":
+            return 3 * i * h + 2 * i // 32 * (h // 32) + h // 32 * (i // 32)
         return 3 * i * h + 4 * (-(-2 * i // 128) * -(-h // 128) + -(-h // 128) * -(-i // 128))
 
     def algorithmic_bytes(self, rows: int, union: int) -> int:
@@ -102,6 +115,17 @@ PRESETS = {
         inter=1024, shared_inter=1024, routed_fmt="mxfp4", routed_scale=2.5,
         swiglu_limit=10.0, router_parts=7, norm_eps=1e-6,
     ),
+    # DeepSeek-V4.1's MoE at TP4 (the reference's own model: stages/moe_shape.py:24,
+    # stages/dims.py:13-56, check_ffn.py:13-18): hidden 5120, 384 experts top-6 by sqrt(softplus)
+    # over one group, routed scale 1.5; MXFP4 routed experts in SGLang's loaded layout, the
+    # rank's 576 columns padded to 640; the shared expert's 576 columns FP8 with E8M0 32 x 32
+    # scales; the router in 5 parts of 1024 columns
+    "v41_tp4": MoePreset(
+        "v41_tp4", hidden=5120, experts=384, topk=6, n_group=1, topk_group=1,
+        inter=640, shared_inter=576, routed_fmt="mxfp4", routed_scale=1.5,
+        swiglu_limit=10.0, router_parts=5, scoring="sqrt_softplus", shared_fmt="fp8_mx32",
+        inter_real=576, aiter_only=True,
+    ),
     # the plumbing layer routed as V4.1 routes (sqrt(softplus) scores over one group, the
     # routed scale 1.5 of check_ffn.py:14)
     "plumbing_fp8_softplus": MoePreset(
@@ -124,6 +148,8 @@ WORKLOADS = {
     # more rows than one gate_up token group holds)
     "tp4_fp8_zipf": dict(preset="dsv3_tp4_fp8", rows=(16, 48), zipf_s=1.2),
     "tp2_mxfp4_norm_zipf": dict(preset="dsv3_tp2_mxfp4_norm", rows=(48,), zipf_s=1.2),
+    # the reference's own MoE shape: DeepSeek-V4.1 at TP4, the experts in SGLang's layout
+    "v41_tp4_mxfp4": dict(preset="v41_tp4", rows=(1, 8, 48)),
 }
 
 

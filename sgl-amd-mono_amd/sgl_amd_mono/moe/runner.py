@@ -75,7 +75,8 @@ class MoeWeights:
     sw2_s: torch.Tensor
     norm: torch.Tensor | None = None
 
-    def expected(self, p: MoePreset) -> dict:
+    @staticmethod
+    def expected(p: MoePreset) -> dict:
         """name -> (shape, accepted dtypes)."""
         e, h, i, s = p.experts, p.hidden, p.inter, p.shared_inter
         b8 = (FP8, torch.uint8)
@@ -88,6 +89,8 @@ class MoeWeights:
             "sw2": ((h, s), b8),
             "sw2_s": ((-(-h // 128), -(-s // 128)), f32),
         }
+        if p.shared_fmt == "fp8_mx32":  # E8M0 32 x 32 (gfx950/runner.py:163-166)
+            want.update(sgu_s=((2 * s // 32, h // 32), (E8M0, torch.uint8)), sw2_s=((h // 32, s // 32), (E8M0, torch.uint8)))
         if p.routed_fmt == "fp8_b128":
             want.update(
                 w13=((e, 2 * i, h), b8),
@@ -101,7 +104,8 @@ class MoeWeights:
                 w13=((e, 2 * i, h // 2), b4),
                 w13_s=((e, 2 * i, h // 32), sc),
                 w2=((e, h, i // 2), b4),
-                w2_s=((e, h, i // 32), sc),
+                # the loader pads w2_s's columns to a multiple of 8 (stages/dims.py:54-56)
+                w2_s=((e, h, -(-i // 32 // 8) * 8), sc),
             )
         if p.norm_eps is not None:
             want["norm"] = ((h,), (torch.bfloat16,))
@@ -158,10 +162,12 @@ class MoeRunner:
         deadline_s: float = DEADLINE_S,
         mfma_rows: tuple[int, int] = (MFMA_GATE_ROWS, MFMA_DOWN_ROWS),
         mxfp4_scaled_rows: int = MXFP4_SCALED_ROWS,
-        layout: str = "row_major",
+        layout: str | None = None,
         mxfp4_scaled_down_rows: int = MXFP4_SCALED_DOWN_ROWS,
     ):
         self.preset = PRESETS[preset] if isinstance(preset, str) else preset
+        if layout is None:  # a preset compiled for SGLang's loaded layout alone takes that one
+            layout = "aiter" if self.preset.aiter_only else "row_major"
         self.layout = layout
         self.deadline_s = float(deadline_s)
         self.mfma_rows = (int(mfma_rows[0]), int(mfma_rows[1]))
