@@ -114,7 +114,7 @@ __device__ __forceinline__ unsigned long long tl_now() { return 0ull; }
 #endif
 
 template <int H_, int E_, int K_, int NG_, int TG_, int I_, int S_, int FMT_, int P_, bool NORM_, bool SHUF_ = false,
-          int SCORE_ = kScoreSigmoid, int SFMT_ = kFp8>
+          int SCORE_ = kScoreSigmoid, int SFMT_ = kFp8, int IR_ = I_>
 struct Cfg {
   static constexpr int SCORE = SCORE_;  // the router's score (sigmoid or V4.1's sqrt(softplus))
   // the shared expert's weights: FP8 with fp32 128 x 128 scales (its activations and
@@ -130,6 +130,14 @@ struct Cfg {
   // every expert GEMM on MFMA (the VALU GEMVs read row-major rows)
   static constexpr bool SHUF = SHUF_;
   static_assert(!SHUF || FMT == kFp4, "the shuffled layout is MXFP4's");
+  // a routed expert's real width when the loader pads it with zero weights to I (V4.1: the
+  // rank's 576 columns padded to 640, stages/dims.py:13-46). The padding is never read: the
+  // gate_up computes the real columns only, the intermediates are quantized from the real
+  // columns (zeros past them), and the down loads no weight past K = IR (as the reference's
+  // ug tasks and down tiles skip it, stages/moe.py:696-714,788-793,1065-1093). MFMA shapes
+  // alone (the shuffled layout)
+  static constexpr int IR = IR_;
+  static_assert(IR == I || (SHUF && IR % 32 == 0 && IR < I), "real width: whole MX blocks");
   // launches of at least QROWS rows quantize the intermediates once (stage Q, a hand-off of
   // its own) instead of in every workgroup's down stage, and up to kSharedFirstRows rows run
   // the shared expert's down inside that hand-off. Measured: 7-8 % faster at 48 rows, 1.4 to
@@ -151,8 +159,10 @@ struct Cfg {
   static constexpr int SSC = SFMT == kFp8Mx ? S / 32 : (S / 128) * 4;  // scale bytes of a shared row
   static constexpr int MSC = FMT == kFp4 ? I / 32 : I / 128;  // mid scales a pick
   // 16-row blocks of a routed down unit: MXFP4 rows of 512 K are 256 bytes, so a unit of 32 rows
-  // keeps 8 KB a wave in flight (as 16 rows do at FP8, or at MXFP4 with 1024 K)
-  static constexpr int DNA = FMT == kFp4 && I <= 512 ? 2 : 1;
+  // keeps 8 KB a wave in flight (as 16 rows do at FP8, or at MXFP4 with 1024 K). At 640 K
+  // (V4.1) a tile is H / 256 = 20 rows: one 32-row unit of 10 KB covers it, where 16-row units
+  // took two, the second with 4 rows at a whole unit's latency
+  static constexpr int DNA = FMT == kFp4 && I <= 640 ? 2 : 1;
 };
 
 using CfgPlumbing = Cfg<1024, 16, 4, 1, 1, 512, 512, kFp8, 2, false>;
@@ -167,7 +177,7 @@ using CfgPlumbingSoftplus = Cfg<1024, 16, 4, 1, 1, 512, 512, kFp8, 2, false, fal
 // hidden 5120, 384 experts top-6 by sqrt(softplus) over one group, routed experts MXFP4 in
 // SGLang's aiter layout with the rank's 576 columns padded to 640 (zero weights), the shared
 // expert's 576 columns FP8 with E8M0 32 x 32 scales
-using CfgV41Tp4 = Cfg<5120, 384, 6, 1, 1, 640, 576, kFp4, 5, false, true, kScoreSqrtSoftplus, kFp8Mx>;
+using CfgV41Tp4 = Cfg<5120, 384, 6, 1, 1, 640, 576, kFp4, 5, false, true, kScoreSqrtSoftplus, kFp8Mx, 576>;
 
 // the expert GEMMs of a launch on MFMA (else the VALU GEMVs)
 template <class C>
@@ -874,6 +884,8 @@ __device__ __forceinline__ void route_scores(const Params& p, RouteSmem<C>& sm, 
   if (nj <= 1) sigmoids<C, 1>(part, sgv);
   else if (nj <= 2) sigmoids<C, (MJ < 2 ? MJ : 2)>(part, sgv);
   else if (nj <= 4) sigmoids<C, (MJ < 4 ? MJ : 4)>(part, sgv);
+  else if (MJ > 8 && nj <= 6) sigmoids<C, (MJ < 6 ? MJ : 6)>(part, sgv);  // 8 rows of 384 experts
+  else if (MJ > 8 && nj <= 8) sigmoids<C, (MJ < 8 ? MJ : 8)>(part, sgv);
   else sigmoids<C, MJ>(part, sgv);
 #pragma unroll
   for (int j = 0; j < MJ; ++j) {
@@ -1862,16 +1874,16 @@ __device__ __forceinline__ void gu_mma(const GuTile<C, WFMT, SH>& t, const GuX<C
   }
 }
 
-// MFMA gate_up of units [lo, hi) of a [2W][H] weight; unit u is token group u / (W / NC) and
-// its NC columns (u % (W / NC)) * NC ... group(tg, w, s, np) gives a group's weight, scales and
+// MFMA gate_up of units [lo, hi) of a [2W][H] weight whose first WR columns are real; unit u
+// is token group u / (WR / NC) and its NC columns (u % (WR / NC)) * NC ... group(tg, w, s, np) gives a group's weight, scales and
 // pick count, xload(tg, np, x) loads its activations into x, emit(tg, q, col, g, u) takes pick
 // q's gate and up sums of a column. A wave's K slice of the next unit is requested into its
 // LDS slot as soon as the current one is read out of it, so it streams while the current
 // unit's MFMAs run and its partial tiles add in LDS (in wave order). An FP8 weight's block
 // scales go to LDS when the group changes.
 template <class C, int WFMT, bool HALF, bool SH, class GroupFn, class XFn, class EmitFn>
-__device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h, bool scaled, GroupFn group, XFn xload,
-                                        EmitFn emit) {
+__device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int WR, int lo_h, int hi_h, bool scaled, GroupFn group,
+                                        XFn xload, EmitFn emit) {
   using T = GuTile<C, WFMT, SH>;
   if (lo_h >= hi_h) return;
   // HALF: the share is half-units [lo_h, hi_h): whole units, but at either end possibly one
@@ -1887,7 +1899,7 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
     }
   };
   const int tid = threadIdx.x, lane = tid & 63, wave = (int)(threadIdx.x >> 6);
-  const int nb = W / T::NC;
+  const int nb = WR / T::NC;  // units a token group
   constexpr uint32_t WB = T::F8 ? C::H : C::H / 2;  // bytes a weight row
   uint8_t* slot = sm.m.wslot[wave];
   uint8_t* sslot = sm.m.sslot[wave];
@@ -1990,9 +2002,12 @@ __device__ __forceinline__ void gu_mfma(GuSmem<C>& sm, int W, int lo_h, int hi_h
 // MFMA down: rows [hb, hb + 16 NA) of a [H][KD] weight (nv of them real), all K steps, in
 // registers; mma() gives C[m][n] = row hb + 16 q + m against pick column n of an LDS mid tile,
 // for each of the NA 16-row blocks q
-template <int WFMT, int KD, int NA_ = 1, bool SH = false>
+template <int WFMT, int KD, int NA_ = 1, bool SH = false, int KR = KD>
 struct DownTile {
   static constexpr int NA = NA_;  // 16-row A operands a unit
+  // K past KR is a padded layout's zero weights: not loaded (the LDS takes zeros), and its
+  // scales are taken as 1 (the shuffled layout)
+  static_assert(KR == KD || (SH && KR % 32 == 0 && KR < KD), "a real K of whole MX blocks");
   static_assert(!SH || WFMT == kFp4, "the shuffled layout is MXFP4's");
   static constexpr bool kIsTile = true;
   // FP8 (fp32 128 x 128 scales, or E8M0 32 x 32: MX, whose K may end in half a step: the last
@@ -2051,7 +2066,7 @@ struct DownTile {
         for (int ks = 0; ks < KS; ++ks)
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
               wr, (__attribute__((address_space(3))) void*)(slot + (q * KS + ks) * 1024), 16,
-              q * 16 + m < nv ? base + ks * 1024 : kNoLoad, 0, 0, kAuxNt);
+              q * 16 + m < nv && ks * 128 + 32 * j < KR ? base + ks * 1024 : kNoLoad, 0, 0, kAuxNt);
       }
       return;
     }
@@ -2185,6 +2200,9 @@ struct DownTile {
           sa[q][2 * c] = (dw >> (8 * a)) & 0xffu;
           if (2 * c + 1 < KS) sa[q][2 * c + 1] = (dw >> (8 * (2 + a))) & 0xffu;
         }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          if (ks * 128 + 96 >= KR && ks * 128 + 32 * j >= KR) sa[q][ks] = 127u;
       }
     } else if constexpr (WFMT == kFp4) {
 #pragma unroll
@@ -2576,10 +2594,11 @@ __device__ __forceinline__ void down_pipeline(DownBatch<Rows>& bt, int n, LoadFn
 constexpr int kQuantBatch = 4;
 // The rule by FMT, the weight format the rows feed: group-128 fp8 with fp32 scales (kFp8), MXFP8
 // per 32 with the "aiter" code (kFp4) or the "vllm" code (kFp8Mx), E8M0 bytes
-template <int FMT, int W, int QS, int NB = kQuantBatch, class RowFn>
+template <int FMT, int W, int QS, int NB = kQuantBatch, int WR = W, class RowFn>
 __device__ __forceinline__ void quant_rows_lds(const Params& p, RowFn src_row, int n, uint8_t* q, void* s) {
 #pragma clang fp contract(off)
   constexpr int PER = W / 8;  // 8-value chunks a row
+  constexpr int RPER = WR / 8;  // ... of them real: the rest quantize zeros (nothing is read)
   // a group's chunks lie in adjacent lanes of one wave (rows hold whole groups)
   static_assert(PER % (FMT == kFp8 ? 16 : 4) == 0, "whole groups a row");
   const int tid = threadIdx.x;
@@ -2591,7 +2610,7 @@ __device__ __forceinline__ void quant_rows_lds(const Params& p, RowFn src_row, i
 #pragma unroll
     for (int k = 0; k < NB; ++k) {
       const int idx = base + k * kThreads + tid;
-      if (idx < total) xv[k] = dld128(rs, src_row(idx / PER) + (idx % PER) * 16);
+      if (idx < total && (RPER == PER || idx % PER < RPER)) xv[k] = dld128(rs, src_row(idx / PER) + (idx % PER) * 16);
     }
 #pragma unroll
     for (int k = 0; k < NB; ++k) {
@@ -2601,7 +2620,7 @@ __device__ __forceinline__ void quant_rows_lds(const Params& p, RowFn src_row, i
       const int i = ok ? idx / PER : 0, c = ok ? idx % PER : 0;
       float v[8];
       float am = 0.0f;
-      if (ok) {
+      if (ok && (RPER == PER || c < RPER)) {
         const uint32_t xw[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -2642,10 +2661,11 @@ __device__ __forceinline__ void quant_rows_lds(const Params& p, RowFn src_row, i
 // quantize one bf16 row of W values (workspace byte src) into the workspace by one wave: codes
 // at dq (8 bytes a chunk of 8 values), scales at ds; group-128 fp8 (fp32 scales) or MXFP8
 // (E8M0 bytes), the arithmetic of quant_rows_lds
-template <int FMT, int W>
+template <int FMT, int W, int WR = W>
 __device__ __forceinline__ void quant_row_ws(const Params& p, uint32_t src, uint32_t dq, uint32_t ds, int lane) {
 #pragma clang fp contract(off)
   constexpr int PER = W / 8;  // 8-value chunks a row
+  constexpr int RPER = WR / 8;  // ... of them real: the rest quantize zeros (nothing is read)
   constexpr int CPL = (PER + 63) / 64;
   // the chunks past the row (a last round of fewer than 64) are whole groups of lanes, which
   // load and store nothing
@@ -2655,7 +2675,7 @@ __device__ __forceinline__ void quant_row_ws(const Params& p, uint32_t src, uint
   for (int t = 0; t < CPL; ++t) {
     const int c = lane + 64 * t;
     const bool ok = PER % 64 == 0 || c < PER;
-    const u32x4 xv = ok ? dld128(rs, src + c * 16) : u32x4{0u, 0u, 0u, 0u};
+    const u32x4 xv = ok && (RPER == PER || c < RPER) ? dld128(rs, src + c * 16) : u32x4{0u, 0u, 0u, 0u};
     const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
     float v[8];
     float am = 0.0f;
@@ -2877,7 +2897,7 @@ template <class C>
 __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un, GuSmem<C>& sm, int b, int nwg) {
   const auto rs = ws_rsrc(p);
   const int n_sh = (p.rows + kMfmaPicks - 1) / kMfmaPicks * (C::S / GuTile<C, C::SFMT>::NC);
-  const int n_rt = un.ntg_r * (C::I / GuTile<C, C::FMT>::NC);
+  const int n_rt = un.ntg_r * (C::IR / GuTile<C, C::FMT>::NC);
   // FP8: the share in half-units (a unit's first or last NC / 2 columns), so that shares
   // differ by half a unit at most (with MXFP4 weights the extra bookkeeping crowds the
   // registers of the gate_up loop: whole units)
@@ -2889,7 +2909,7 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
     const uint32_t qoff = C::FMT == kFp4 ? p.off[3] : p.off[1];
     const uint32_t soff = C::FMT == kFp4 ? p.off[4] : p.off[2];
     gu_mfma<C, C::SFMT, HALF, false>(
-        sm, C::S, lo, min(hi, HU * n_sh), false,
+        sm, C::S, C::S, lo, min(hi, HU * n_sh), false,
         [&](int tg, const uint8_t*& w, const void*& s, int& np) {
           w = p.sgu;
           s = p.sgu_s;
@@ -2907,7 +2927,7 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
     return un.slot_start[slot] + (tg - un.tg_start[slot]) * kMfmaPicks;
   };
   gu_mfma<C, C::FMT, HALF, C::SHUF>(
-      sm, C::I, max(lo, HU * n_sh) - HU * n_sh, hi - HU * n_sh, C::FMT == kFp4 && p.mx_scaled,
+      sm, C::I, C::IR, max(lo, HU * n_sh) - HU * n_sh, hi - HU * n_sh, C::FMT == kFp4 && p.mx_scaled,
       [&](int tg, const uint8_t*& w, const void*& s, int& np) {
         const int slot = un.tg_slot[tg];
         const int e = un.slot_e[slot];
@@ -2950,6 +2970,7 @@ struct DownSmem {
     SharedDownSmem<C> sd;  // the shared down's quantized rows, done before the routed ones
   };
   uint16_t shv[kRowsMax * kTileMax];  // the shared expert's bf16 results of the tile
+  int claim;  // MFMA down: the pick batch's next unit to be claimed by a wave
   // MFMA down: a wave's slot of weight rows (one unit)
   uint8_t wslot[kWaves][DownTile<C::FMT, C::I, C::DNA>::SLOT] __attribute__((aligned(16)));
 };
@@ -2972,7 +2993,7 @@ __device__ __forceinline__ void batch_slots(const Union<C>& un, int pb0, int pbn
 template <class C>
 using DownRowsOf = DownRows<C::FMT, C::I>;
 template <class C>
-using DownTileOf = DownTile<C::FMT, C::I, C::DNA, C::SHUF>;
+using DownTileOf = DownTile<C::FMT, C::I, C::DNA, C::SHUF, C::IR>;
 // the down stage's batch of units: MFMA (MF) or VALU
 // the MFMA down's unit in flight: its rows in the wave's LDS slot, its scales in nxt
 template <class C>
@@ -3062,7 +3083,7 @@ __device__ __forceinline__ void down_valu(const Params& p, const Union<C>& un, D
     if constexpr (GQ)
       copy_pick_batch<C>(p, pb0, pbn, sm);
     else
-      quant_rows_lds<C::FMT, C::I, C::MQS>(
+      quant_rows_lds<C::FMT, C::I, C::MQS, kQuantBatch, C::IR>(
           p, [&](int i) { return p.off[9] + (uint32_t)un.picks[pb0 + i] * C::I * 2; }, pbn, sm.q, sm.s);
     __syncthreads();
     down_pipeline<DR>(bt, n_units, load, [&](int v, const DR& wr) {
@@ -3092,6 +3113,9 @@ __device__ __forceinline__ void down_valu(const Params& p, const Union<C>& un, D
 // the same on MFMA: units (slot, 16-row block), each against its slot's picks 16 at a time. A
 // wave keeps one unit in flight: once a unit's rows are read out of its LDS slot, the wave's
 // next unit is requested into the slot, and the unit is computed while those rows stream in.
+// Wave w's first unit of a pick batch is unit w (waves 1-7 request it before the hand-offs,
+// wave 0, which polls them, only after); each next unit is claimed from an LDS counter, so a
+// wave that started late takes fewer. A unit's results are the same whichever wave computes it.
 template <class C, bool GQ, bool SHF = false>
 __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
                                           LdsUnit<C>& bt, bool first_ready) {
@@ -3118,20 +3142,21 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
       mfma_issue<C>(p, un, h0, hn, s_lo, wave, slot, bt.nxt, lane);
     ahead = false;
     const unsigned long long tb0 = tl_now();
-    __syncthreads();  // the previous batch is done with the LDS rows
+    __syncthreads();  // the previous batch is done with the LDS rows (and its claims)
     const unsigned long long tq0 = tl_now();
     TL_ADD(kTlDBar, tq0 - tb0);
+    if (threadIdx.x == 0) sm.claim = kWaves;  // units 0 .. 7 are the waves' first
     if constexpr (GQ)
       copy_pick_batch<C>(p, pb0, pbn, sm);
     else
       // the quantize requests 8 chunks a thread at once (4 where a unit's scales take more
       // registers: MXFP4, whose 8 spill there)
-      quant_rows_lds<C::FMT, C::I, C::MQS, (C::FMT == kFp4 ? 1 : 2) * kQuantBatch>(
+      quant_rows_lds<C::FMT, C::I, C::MQS, (C::FMT == kFp4 ? 1 : 2) * kQuantBatch, C::IR>(
           p, [&](int i) { return p.off[9] + (uint32_t)un.picks[pb0 + i] * C::I * 2; }, pbn, sm.q, sm.s);
     __syncthreads();
     TL_ADD(kTlDQuant, tl_now() - tq0);
     DT cur;
-    for (int v = wave; v < n_units; v += kWaves) {
+    for (int v = wave; v < n_units;) {
       const unsigned long long tw0 = tl_now();
       wait_vm0();  // the unit's rows are in the slot
       const unsigned long long tf0 = tl_now();
@@ -3143,8 +3168,11 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // and read out of it
       const unsigned long long tf1 = tl_now();
       TL_ADD(kTlDFetch, tf1 - tf0);
-      if (v + kWaves < n_units) {
-        mfma_issue<C>(p, un, h0, hn, s_lo, v + kWaves, slot, bt.nxt, lane);
+      int nv = 0;
+      if (lane == 0) nv = __hip_atomic_fetch_add(&sm.claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      nv = __builtin_amdgcn_readfirstlane(nv);
+      if (nv < n_units) {
+        mfma_issue<C>(p, un, h0, hn, s_lo, nv, slot, bt.nxt, lane);
       } else if (wave < nx_units) {
         mfma_issue<C>(p, un, h0, hn, nx_lo, wave, slot, bt.nxt, lane);
         ahead = true;
@@ -3169,6 +3197,7 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
       }
       TL_ADD(kTlDMma, tl_now() - tm0);
       if (pb0 == 0 && v == wave) TL(kTlDFirst);
+      v = nv;
     }
     s_lo = nx_lo;
     s_hi = nx_hi;
@@ -3257,7 +3286,7 @@ __device__ __forceinline__ void stage_q(const Params& p, const Union<C>& un, int
   const int n = npk + (shared ? p.rows : 0);
   for (int j = wave_slot(b, nwg); j < n; j += nwg * kWaves) {
     if (j < npk) {
-      quant_row_ws<C::FMT, C::I>(p, p.off[9] + (uint32_t)un.picks[j] * C::I * 2, p.off[12] + (uint32_t)j * C::MQS,
+      quant_row_ws<C::FMT, C::I, C::IR>(p, p.off[9] + (uint32_t)un.picks[j] * C::I * 2, p.off[12] + (uint32_t)j * C::MQS,
                                  p.off[13] + (uint32_t)j * SST, lane);
     } else {
       const int r = j - npk;

@@ -87,6 +87,65 @@ def test_parity_v41(rows):
     assert not g["nan"] and g["n_over_bar"] == 0 and g["rel_l2"] <= 1e-2 and g["cos"] >= 0.9999, g
 
 
+@pytest.mark.parametrize("rows", [1, 8, 48])
+def test_parity_v41_scaled_down(rows):
+    """The down GEMM on the scaled fp4 x fp8 MFMA (the reference's instruction,
+    common/mx.py:60-66), held to the reference's own bound against the golden (relative L2 and
+    cosine, spec.py:305-309). It misses the element bar on this shape (8 rows: 2 elements past
+    two bf16 ulps, 181 of 40960 past 2e-2, where the default path is bit-identical to the
+    golden), so the library keeps it off here by default; the case records how far it lands."""
+    from gpu_case import errors, record_accuracy
+
+    from sgl_amd_mono.moe.runner import MoeRunner
+
+    c = _case(rows)
+    run = MoeRunner(c.preset, "cuda", mxfp4_scaled_down_rows=1)
+    ids = torch.zeros(rows, c.p["topk"], dtype=torch.int32, device="cuda")
+    out = run.moe(c.w, c.x, topk_ids=ids)
+    torch.cuda.synchronize()
+    run.raise_on_device_error()
+    assert np.array_equal(ids.cpu().numpy(), c.ids), "expert ids"
+    g = errors(out.cpu(), c.golden, c.chain)
+    print(f"\n{WORKLOAD} R={rows} scaled down vs fp32-matmul golden: {g}", flush=True)
+    record_accuracy(WORKLOAD, rows, "scaled_down", g, g, True)
+    assert not g["nan"] and g["rel_l2"] <= 1e-2 and g["cos"] >= 0.9999, g
+
+
+@pytest.mark.parametrize("rows", [1, 8])
+def test_v41_padding_never_read(rows):
+    """The loader's padding (gate and up rows 576 .. 639, w2's K columns 576 .. 639 and their
+    E8M0 scales) is never read: filled with random codes and NaN scales (0xFF), the output is
+    bit for bit the zero-padded launch's. 1 row quantizes the intermediates in each workgroup,
+    8 rows once (stage Q)."""
+    from gpu_case import build
+
+    from oracle import shuffle as sh
+
+    c = _case(rows)
+    run = _runner(c)
+    ref = run.moe(c.w, c.x).clone()
+    raw = build(WORKLOAD, rows).w  # row-major, zero-padded
+    i, ir = c.p["inter"], c.p["inter_real"]
+    g = torch.Generator(device="cuda").manual_seed(7)
+    w13, w13_s, w2, w2_s = raw.w13.clone(), raw.w13_s.clone(), raw.w2.clone(), raw.w2_s.clone()
+    del raw
+    for half in (0, i):
+        rows_ = slice(half + ir, half + i)
+        w13[:, rows_] = torch.randint(0, 256, w13[:, rows_].shape, generator=g, device="cuda", dtype=torch.uint8)
+        w13_s[:, rows_] = 0xFF
+    w2[:, :, ir // 2 :] = torch.randint(0, 256, w2[:, :, ir // 2 :].shape, generator=g, device="cuda", dtype=torch.uint8)
+    w2_s[:, :, ir // 32 :] = 0xFF
+    a13, a13_s, a2, a2_s = sh.to_aiter(w13, w13_s, w2, w2_s)
+    del w13, w13_s, w2, w2_s
+    w = dataclasses.replace(
+        c.w, w13=a13, w13_s=a13_s.reshape(-1, a13_s.shape[-1]), w2=a2, w2_s=a2_s.reshape(-1, a2_s.shape[-1])
+    )
+    out = run.moe(w, c.x)
+    torch.cuda.synchronize()
+    run.raise_on_device_error()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), "the padding changed the output"
+
+
 @pytest.mark.parametrize("rows", [8, 48])
 def test_v41_staged_equals_fused_and_repeats(rows):
     c = _case(rows)
