@@ -189,6 +189,56 @@ class RowsBench:
         return us, maxrows
 
 
+class FfnRowsBench(RowsBench):
+    """DeepSeek-V4.1's FFN at one row count (``FfnRunner.ffn``: the seam, the MoE block on its
+    normed rows, the seam's gate), over the MoE layers' weights with a seam weight set each."""
+
+    def __init__(self, ffn, layers, seam_ws, preset, rows, device, seed):
+        import torch
+
+        from sgl_amd_mono.moe.ffn import FfnWeights
+
+        super().__init__(ffn.moe_runner, layers, preset, rows, device, seed)
+        self.ffn = ffn
+        h, hc = preset.hidden, SEAM_HC
+        g = torch.Generator(device=device).manual_seed(seed + 77)
+        self.fw = [FfnWeights(**vars(sw), **{k: v for k, v in vars(m).items() if k != "norm"})
+                   for sw, m in zip(seam_ws, layers)]  # fmt: skip
+        self.ins, self.fouts = [], []
+        for _ in layers:
+            res = torch.randn(rows, hc, h, generator=g, device=device)
+            res = (res * torch.rsqrt(res.pow(2).mean(-1, keepdim=True))).to(torch.bfloat16)
+            comb = torch.rand(rows, hc, hc, generator=g, device=device) + 0.1
+            comb = comb / comb.sum(-2, keepdim=True)
+            post = torch.sigmoid(torch.randn(rows, hc, 1, generator=g, device=device)) * 2
+            pre = torch.sigmoid(torch.randn(rows, hc, generator=g, device=device)) + 1e-6
+            a = (torch.randn(rows, h, generator=g, device=device) * 0.5).to(torch.bfloat16)
+            self.ins.append((a, res, post, comb, pre))
+            self.fouts.append(ffn._outs(rows, res))
+        ffn.normed(rows)  # allocated before any capture
+
+    def launch(self, j):
+        self.ffn.ffn(self.fw[j], *self.ins[j], outs=self.fouts[j], topk_ids=self.ids[j])
+
+
+def seam_weight_sets(device, n: int, seed: int = 4101) -> list:
+    """``n`` random seam weight sets (the reference test's distributions, check_ffn.py:149-152)."""
+    import torch
+
+    from sgl_amd_mono.moe.seam import SeamWeights
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    return [
+        SeamWeights(
+            hc_ffn_fn=torch.randn(SEAM_MIX, SEAM_HC * SEAM_H, generator=g, device=device) * 0.01,
+            hc_ffn_scale=torch.rand(3, generator=g, device=device) * 0.5 + 0.5,
+            hc_ffn_base=torch.randn(SEAM_MIX, generator=g, device=device) * 0.1,
+            ffn_norm=(1 + 0.1 * torch.randn(SEAM_H, generator=g, device=device)).to(torch.bfloat16),
+        )
+        for _ in range(n)
+    ]
+
+
 def summarize(preset, rb: RowsBench, reps) -> dict:
     n = sum(k for k, _ in reps)
     per = [ms * 1e3 / k for k, ms in reps if k == len(rb.layers)] or [ms * 1e3 / k for k, ms in reps]
@@ -222,21 +272,12 @@ def bench_seam(device, tokens_list, timed_n: int, layers: int = SEAM_LAYERS) -> 
     (two launches each), replayed; HIP events bracket each replay."""
     import torch
 
-    from sgl_amd_mono.moe.seam import SeamRunner, SeamWeights
+    from sgl_amd_mono.moe.seam import SeamRunner
 
     h, hc = SEAM_H, SEAM_HC
-    g = torch.Generator(device=device).manual_seed(4101)
+    ws = seam_weight_sets(device, layers)
+    g = torch.Generator(device=device).manual_seed(4102)
     run = SeamRunner(device)
-    ws = []
-    for _ in range(layers):
-        ws.append(
-            SeamWeights(
-                hc_ffn_fn=torch.randn(SEAM_MIX, hc * h, generator=g, device=device) * 0.01,
-                hc_ffn_scale=torch.rand(3, generator=g, device=device) * 0.5 + 0.5,
-                hc_ffn_base=torch.randn(SEAM_MIX, generator=g, device=device) * 0.1,
-                ffn_norm=(1 + 0.1 * torch.randn(h, generator=g, device=device)).to(torch.bfloat16),
-            )
-        )
     out = {}
     for t in tokens_list:
         ins, outs = [], []
@@ -505,6 +546,13 @@ def main() -> int:
         if preset.routed_fmt == "mxfp4" and not preset.aiter_only:
             kw["layout"] = args.layout
         runner = MoeRunner(preset, device, max_rows=max(48, max(rows_list)), **kw)
+        # V4.1: its whole FFN too (the seam, the MoE block, the seam's gate) on the same weights
+        ffn = None
+        if preset.hidden == SEAM_H and preset.aiter_only and not (args.staged or args.timeline):
+            from sgl_amd_mono.moe.ffn import FfnRunner
+
+            ffn = FfnRunner(preset, device, max_rows=max(48, max(rows_list)), **kw)
+            seam_ws = seam_weight_sets(device, len(layers), seed=4103)
         if args.staged:
             orig = runner.moe
             runner.moe = lambda *a, **k: orig(*a, staged=True, **k)
@@ -536,11 +584,27 @@ def main() -> int:
             acc = measured_accuracy(name, r)
             if acc is not None:
                 res["accuracy"] = acc
+            if ffn is not None:
+                fb = FfnRowsBench(ffn, layers, seam_ws, preset, r, device, seed=1000 * (wi + 1) + r)
+                fb.warm(max(args.warmup, 1))
+                f = summarize(preset, fb, fb.timed(timed_n))
+                b = f["alg_MB_per_layer"] * 1e6 + seam_alg_bytes(r)
+                gbps = b / (f["us_per_layer"] * 1e-6) / 1e9
+                res["ffn"] = {
+                    "what": "the FFN: seam (2 launches), MoE block, seam gate, per layer",
+                    "us_per_layer": f["us_per_layer"],
+                    "us_mean": f["us_mean"],
+                    "alg_MB_per_layer": round(b / 1e6, 2),
+                    "GBps": round(gbps, 1),
+                    "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+                    "launches_timed": 4 * f["launches_timed"],
+                }
+                del fb
             wres[str(r)] = res
             log(f"{name} rows={r}: {res}")
             del rb
         results[name] = {"preset": preset.name, "rows": wres}
-        del layers, runner
+        del layers, runner, ffn
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
     if args.timeline:

@@ -20,6 +20,8 @@ BACKEND = "amd"
 # Each spec by the model's HF architecture
 SPECS = {
     "DeepseekV3ForCausalLM": "sgl_amd_mono.moe.spec:SPEC",
+    # the reference's own model: its FFN (the seam and the MoE block) at TP 4
+    "DeepseekV4ForCausalLM": "sgl_amd_mono.moe.spec_v41:SPEC",
 }
 
 

@@ -191,6 +191,66 @@ def test_v41_graph_replay_bitwise():
     run.raise_on_device_error()
 
 
+@pytest.mark.parametrize("rows", [1, 8, 48])
+def test_v41_ffn_chain(rows):
+    """The FFN entry point (``FfnRunner.ffn``: the seam, the MoE block on the seam's normed
+    rows, then the seam's gate) against its parts: every seam output bit for bit the seam's
+    own launch's, the partial bit for bit the MoE launch's on those normed rows, and the
+    routing of the normed rows the oracle's; then a captured graph of the call, replayed."""
+    from oracle import gen
+    from oracle import routing as rt
+    from sgl_amd_mono.moe.ffn import FfnRunner, FfnWeights
+    from sgl_amd_mono.moe.runner import MoeRunner
+    from sgl_amd_mono.moe.seam import SeamRunner
+
+    c = _case(rows)
+    si = {k: v.to("cuda") for k, v in gen.seam_inputs(rows, c.p["hidden"], 300 + rows).items()}
+    sw = {k: v.to("cuda") for k, v in gen.seam_weights(c.p["hidden"], 300).items()}
+    m = c.w
+    fw = FfnWeights(
+        hc_ffn_fn=sw["fn"], hc_ffn_scale=sw["scale"], hc_ffn_base=sw["base"], ffn_norm=sw["norm"], gate_w=m.gate_w,
+        bias=m.bias, w13=m.w13, w13_s=m.w13_s, w2=m.w2, w2_s=m.w2_s, sgu=m.sgu, sgu_s=m.sgu_s, sw2=m.sw2, sw2_s=m.sw2_s,
+    )  # fmt: skip
+    args = (si["a"], si["res"], si["post"], si["comb"], si["pre"])
+    ffn = FfnRunner(c.preset, "cuda")
+    ids = torch.zeros(rows, c.p["topk"], dtype=torch.int32, device="cuda")
+    outs = ffn.ffn(fw, *args, topk_ids=ids)
+    seam = SeamRunner("cuda").ffn_seam(fw.seam(), *args)
+    moe = MoeRunner(c.preset, "cuda").moe(m, seam[0])
+    torch.cuda.synchronize()
+    ffn.moe_runner.raise_on_device_error()
+    assert torch.equal(ffn.normed(rows).view(torch.int16), seam[0].view(torch.int16)), "normed rows"
+    assert torch.equal(outs[0].view(torch.int16), moe.view(torch.int16)), "the MoE partial"
+    for k, name in enumerate(("res_out", "post_out", "comb_out", "pre_out"), start=1):
+        assert torch.equal(outs[k].reshape(-1).view(torch.int16 if k == 1 else torch.int32),
+                           seam[k].reshape(-1).view(torch.int16 if k == 1 else torch.int32)), name  # fmt: skip
+    xin = seam[0].cpu()
+    parts = rt.router_part_sums(xin, m.gate_w.cpu(), c.p["router_parts"])
+    scores = rt.score_exact(rt.logits_from_parts(parts), c.p["scoring"])
+    want, _ = rt.grouped_topk(scores, m.bias.cpu().numpy(), c.p["topk"], c.p["n_group"], c.p["topk_group"],
+                              c.p["routed_scale"])  # fmt: skip
+    assert np.array_equal(ids.cpu().numpy(), want), "expert ids of the normed rows"
+    # one captured graph of the call, replayed with eager work between the replays
+    ref = [t.clone() for t in outs]
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            ffn.ffn(fw, *args, outs=outs)
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(3):
+        for t in outs:
+            t.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for t, r in zip(outs, ref):
+            assert torch.equal(t, r), f"replay {i}"
+        ffn.ffn(fw, *args)
+        torch.cuda.synchronize()
+    ffn.moe_runner.raise_on_device_error()
+
+
 def test_v41_refuses_row_major_and_valu():
     """The V4.1 specialisation reads SGLang's layout alone and runs every GEMM on MFMA."""
     from sgl_amd_mono.moe.runner import MoeRunner
