@@ -258,3 +258,110 @@ def test_zipf_routing_is_skewed():
     _, ids, _ = rt.route(x, w["gate_w"], w["bias"], p)
     st = om.union_stats(ids)
     assert st["max_rows_per_expert"] >= 20 and st["U"] < 150, st
+
+
+# ---------------------------------------------------------------- the V4.1 shared expert, crafted bits
+# The MX shared expert (FP8 with E8M0 32 x 32 scales, its activations and intermediate by the
+# MXFP8 "vllm" rule, check_ffn.py:118-121,226-231). One row x = (448, 0, ...): its vllm code is
+# 127, so its codes are x. Gate row 0 and up row 128 hold 1 at K 0, with block codes 119 and
+# 20: g = 448 * 2^-8 = 1.75, u = 448 * 2^-107 = 1.75 * 2^-99 (no clamp). Worked by hand:
+#   silu(1.75) = 1.75 / (1 + e^-1.75) = 1.4909173 (fp32); product 1.3045527 * 2^-98, bf16
+#   smid = 1.3046875 * 2^-98 (167 / 128)
+#   vllm: smid / 448 = 1.491 * 2^-107, so code 21 (2^-106); smid / 2^-106 = 334, e4m3 320 (the
+#   step in [256, 448) is 32); back: 320 * 2^-106 = 1.25 * 2^-98
+#   down row 32 holds 1 at K 0 with block code 227 (2^100): 1.25 * 2^2 = 5.0, bf16 0x40A0 in
+#   column 32; every routed weight is zero, so out[0, 32] = bf16(0 + 5.0) and 0 elsewhere.
+# The "aiter" rule (floor 1e-10) and group-128 (scale max(amax, 1e-10) / 448) both flush that
+# intermediate to 0; block codes 126 at sgu_s[0, 4] and 125 at sw2_s[0, 1] are where a
+# transposed scale index reads, and a 128-row block index reads the default 127.
+MXC_OUT_BITS = 0x40A0
+
+
+def _mx_shared_layer():
+    p = dict(CRAFT, shared_fmt="fp8_mx32")
+    h, e, i, s = p["hidden"], p["experts"], p["inter"], p["shared_inter"]
+    x = torch.zeros(1, h)
+    x[0, 0] = 448.0
+    sgu = torch.zeros(2 * s, h)
+    sgu[0, 0] = sgu[s, 0] = 1.0
+    sgu_s = torch.full((2 * s // 32, h // 32), 127, dtype=torch.uint8)
+    sgu_s[0, 0], sgu_s[4, 0], sgu_s[0, 4] = 119, 20, 126
+    sw2 = torch.zeros(h, s)
+    sw2[32, 0] = 1.0
+    sw2_s = torch.full((h // 32, s // 32), 127, dtype=torch.uint8)
+    sw2_s[1, 0], sw2_s[0, 1] = 227, 125
+    w = {
+        "gate_w": torch.zeros(e, h, dtype=torch.bfloat16),
+        "bias": -torch.arange(e, dtype=torch.float32) / 1000,
+        "sgu": fm.e4m3_codes_from_f32(sgu),
+        "sgu_s": sgu_s,
+        "sw2": fm.e4m3_codes_from_f32(sw2),
+        "sw2_s": sw2_s,
+    }
+    src = om.ExpertSource(
+        torch.zeros(e, 2 * i, h, dtype=torch.uint8), torch.ones(e, 2 * i // 128, h // 128),
+        torch.zeros(e, h, i, dtype=torch.uint8), torch.ones(e, h // 128, i // 128),
+    )  # fmt: skip
+    return p, x.to(torch.bfloat16), w, src
+
+
+def test_mx_shared_expert_crafted_bits():
+    """moe_partial's MX shared expert on the crafted layer: the hand-worked 5.0 in column 32,
+    zero elsewhere."""
+    p, x, w, src = _mx_shared_layer()
+    out = om.moe_partial(x, w, p, experts=src, exact=False)["out"]
+    assert int(out.view(torch.int16)[0, 32]) & 0xFFFF == MXC_OUT_BITS
+    assert out[0].float().nonzero().flatten().tolist() == [32]
+
+
+def _deq_mx32_transposed(q, s):
+    """Element (i, j) scaled by block (j / 32, i / 32) (wrapped into the scale grid)."""
+    n, k = q.shape
+    nb, kb = s.shape
+    bi = (torch.arange(n)[:, None] // 32) % kb
+    bj = (torch.arange(k)[None, :] // 32) % nb
+    return fm.e4m3_to_f32(q) * fm.e8m0_to_f32(s)[bj, bi]
+
+
+def _deq_mx32_blocks128(q, s):
+    n, k = q.shape
+    sf = fm.e8m0_to_f32(s).repeat_interleave(128, 0)[:n].repeat_interleave(128, 1)[:, :k]
+    return fm.e4m3_to_f32(q) * sf
+
+
+_ACT_QDQ = om.act_qdq
+MX_MISTAKES = {
+    "aiter_rule": ("act_qdq", lambda x, fmt: _ACT_QDQ(x, om.MXFP4 if fmt == om.FP8_MX32 else fmt)),
+    "group128_rule": ("act_qdq", lambda x, fmt: _ACT_QDQ(x, om.FP8_B128 if fmt == om.FP8_MX32 else fmt)),
+    "scales_transposed": ("deq", _deq_mx32_transposed),
+    "scales_per_128": ("deq", _deq_mx32_blocks128),
+}
+
+
+@pytest.mark.parametrize("mistake", sorted(MX_MISTAKES))
+def test_mx_shared_expert_crafted_catches(mistake, monkeypatch):
+    """Each planted mistake (the shared expert's activations by another rule, its E8M0 block
+    scales indexed transposed or per 128) changes the crafted layer's bits."""
+    what, fn = MX_MISTAKES[mistake]
+    if what == "act_qdq":
+        monkeypatch.setattr(om, "act_qdq", fn)
+    else:
+        monkeypatch.setattr(fm, "deq_fp8_mx32", fn)
+    p, x, w, src = _mx_shared_layer()
+    out = om.moe_partial(x, w, p, experts=src, exact=False)["out"]
+    assert int(out.view(torch.int16)[0, 32]) & 0xFFFF != MXC_OUT_BITS
+
+
+def test_deq_fp8_mx32_hand_values():
+    """deq_fp8_mx32 on a [64, 96] matrix with a distinct E8M0 code per 32 x 32 block: element
+    (i, j) is e4m3(q[i, j]) * 2^(code[i / 32][j / 32] - 127), worked by hand at one element per
+    block (e4m3 0x38 = 1.0, 0x3C = 1.5, 0xC4 = -3.0)."""
+    q = torch.zeros(64, 96, dtype=torch.uint8)
+    s = torch.tensor([[120, 127, 130], [126, 140, 100]], dtype=torch.uint8)
+    q[0, 0], q[5, 40], q[31, 95], q[32, 0], q[40, 63], q[63, 64] = 0x38, 0x3C, 0xC4, 0x38, 0x3C, 0xC4
+    d = fm.deq_fp8_mx32(q, s)
+    want = {(0, 0): 2.0**-7, (5, 40): 1.5, (31, 95): -24.0, (32, 0): 0.5, (40, 63): 1.5 * 2.0**13,
+            (63, 64): -3.0 * 2.0**-27}  # fmt: skip
+    for (i, j), v in want.items():
+        assert float(d[i, j]) == v, (i, j, float(d[i, j]), v)
+    assert int((d != 0).sum()) == len(want)

@@ -91,3 +91,23 @@ def test_scale_dword_per_lane_and_step_pair():
         for st in (2 * c8, 2 * c8 + 1):
             for q in range(2):
                 assert flat[dw + 2 * (st % 2) + q] == s[32 * blk + 16 * q + m, 4 * st + j]
+
+
+def test_padded_down_scales_v41():
+    """V4.1's w2 scales: 640 / 32 = 20 E8M0 columns padded by zero codes to 24 (stages/dims.py:
+    54-56), shuffled over the padded width; the kernel reads a row's K steps from the dword at
+    32-row block h / 32 (24 * 32 bytes each), chunk c (256 bytes), position 16 j + h % 16, and
+    from_aiter(w2_cols=20) gives the 20 columns back. A 16-column matrix (I = 512) is left as it is."""
+    s = _bytes(2, 96, 20, seed=9)
+    p = sh.pad_scale_cols(s)
+    assert p.shape == (2, 96, 24) and torch.equal(p[..., :20], s) and not p[..., 20:].any()
+    s16 = _bytes(96, 16, seed=10)
+    assert sh.pad_scale_cols(s16) is s16
+    flat = sh.shuffle_scales(p).reshape(2, -1)
+    for e, h, st, j in itertools.product(range(2), (0, 17, 40, 95), range(5), range(4)):
+        c = st // 2
+        dw = (h // 32) * 24 * 32 + c * 256 + (16 * j + h % 16) * 4
+        assert flat[e, dw + 2 * (st % 2) + (h // 16) % 2] == s[e, h, 4 * st + j]
+    w13, w13_s, w2 = _bytes(2, 64, 128, seed=11), _bytes(2, 64, 8, seed=12), _bytes(2, 96, 320, seed=13)
+    back = sh.from_aiter(*sh.to_aiter(w13, w13_s, w2, s), w2_cols=20)
+    assert torch.equal(back[3], s) and torch.equal(back[2], w2)
