@@ -13,6 +13,8 @@ every layer has its own weights. Inputs are synthetic: x ~ N(0, 1), router
 weight ~ N(0, 1/H) (realistic routing), expert bytes random; the Zipf workload
 biases router column 0 by log p_e (p_e ~ rank^-1.2 over a seeded permutation of
 the experts) and sets x[:, 0] = 1, so expert popularity follows Zipf(1.2).
+MXFP4 experts are read in SGLang's loaded gfx950 layout (aiter's shuffles), the one
+the reference requires and reads; ``--layout row_major`` times the row-major reading.
 
 Timing: a captured graph of one launch per layer, replayed; HIP events on the
 launching stream bracket each replay. Per (workload, rows): at least 200 timed
@@ -491,13 +493,16 @@ def main() -> int:
                     help="MXFP4 launches with at least this many rows on the scaled fp4 x fp8 MFMA")
     ap.add_argument("--mxfp4-scaled-down-rows", type=int, default=None,
                     help="MXFP4 launches with at least this many rows run the down GEMM alone on the scaled MFMA")
-    ap.add_argument("--layout", default="row_major", choices=("row_major", "aiter"),
-                    help="the MXFP4 workloads' expert layout: row-major, or SGLang's loaded gfx950 layout "
-                    "(aiter's shuffles; the random weight bytes are read as such)")
+    ap.add_argument("--layout", default="aiter", choices=("row_major", "aiter"),
+                    help="the MXFP4 workloads' expert layout: SGLang's loaded gfx950 layout (aiter's shuffles, "
+                    "the default: the layout the reference reads; the random weight bytes are read as such), "
+                    "or row-major")
     ap.add_argument("--timeline", action="store_true",
                     help="phase timeline of the diagnostic build (build.py --timeline); no JSON line")
     ap.add_argument("--seam-tokens", default=SEAM_TOKENS, help="the FFN seam's token counts ('' : none)")
     ap.add_argument("--seam-only", action="store_true", help="time the FFN seam alone and print its results")
+    ap.add_argument("--no-ffn", action="store_true",
+                    help="skip V4.1's whole-FFN timing (profiles of the MoE launch alone)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain copy of MIB MiB (counter calibration) and exit")
     args = ap.parse_args()
@@ -548,7 +553,7 @@ def main() -> int:
         runner = MoeRunner(preset, device, max_rows=max(48, max(rows_list)), **kw)
         # V4.1: its whole FFN too (the seam, the MoE block, the seam's gate) on the same weights
         ffn = None
-        if preset.hidden == SEAM_H and preset.aiter_only and not (args.staged or args.timeline):
+        if preset.hidden == SEAM_H and preset.aiter_only and not (args.staged or args.timeline or args.no_ffn):
             from sgl_amd_mono.moe.ffn import FfnRunner
 
             ffn = FfnRunner(preset, device, max_rows=max(48, max(rows_list)), **kw)
