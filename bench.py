@@ -63,7 +63,7 @@ HEADLINE = ("cfg2_tp4_fp8", 8)
 # further (workload, rows) points that get a CPU baseline of their own (under ``workloads``)
 CPU_POINTS = (("cfg3_tp4_mxfp4", 8), ("cfg5_tp2_mxfp4_norm", 8))
 CPU_POINT_BUDGET_S = 15.0
-DEFAULT_WORKLOADS = "cfg2_tp4_fp8,cfg3_tp4_mxfp4,cfg4_tp4_mxfp4_zipf,cfg5_tp2_mxfp4_norm,v41_tp4_mxfp4"
+DEFAULT_WORKLOADS = "cfg2_tp4_fp8,cfg3_tp4_mxfp4,cfg4_tp4_mxfp4_zipf,cfg5_tp2_mxfp4_norm,v41_tp4_mxfp4,v41_tp2_mxfp4"
 MIN_TIMED = 200
 SEAM_TOKENS = "1,8,48"
 SEAM_LAYERS = 144

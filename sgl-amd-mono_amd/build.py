@@ -8,7 +8,7 @@
 The library holds the kernels and the C ABI of ``include/mkmoe.h``. It is built
 in place (not installed) so that the same file runs wherever the tree is copied.
 The MoE source compiles in parts, in parallel: one object per compiled MoE shape
-(``MKMOE_UNIT`` 0 .. 7) and one for the host code (``MKMOE_UNIT`` 9); the FFN
+(``MKMOE_UNIT`` 0 .. 8) and one for the host code (``MKMOE_UNIT`` 9); the FFN
 seam's source (``csrc/mkmoe_seam.hip``) is one more object; then one link.
 """
 
@@ -28,7 +28,7 @@ OUT = ROOT / "sgl_amd_mono" / "moe" / "libmkmoe.so"
 OUT_TIMELINE = ROOT / "sgl_amd_mono" / "moe" / "libmkmoe_tl.so"
 SOURCE = CSRC / "mkmoe_kernels.hip"
 SEAM_SOURCE = CSRC / "mkmoe_seam.hip"
-UNITS = (0, 1, 2, 3, 4, 5, 6, 7, 9)  # the compiled shapes, then the host code
+UNITS = (0, 1, 2, 3, 4, 5, 6, 7, 8, 9)  # the compiled shapes, then the host code
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950",

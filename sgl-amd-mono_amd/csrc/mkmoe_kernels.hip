@@ -48,6 +48,11 @@ constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kRowsMax = 48;   // rows a launch takes at most
 constexpr int kTileMax = 32;   // output rows of a down tile, at most
+// ... of a shape: a workgroup's share of H at the full grid (H / 256, a multiple of 4); with
+// fewer workgroups a workgroup takes more tiles, not larger ones (the host caps them alike)
+constexpr int tile_max(int h) {
+  return ((h + 255) / 256 + 3) / 4 * 4 < kTileMax ? ((h + 255) / 256 + 3) / 4 * 4 : kTileMax;
+}
 constexpr int kFp8 = MKMOE_FMT_FP8_B128;
 constexpr int kFp4 = MKMOE_FMT_MXFP4;
 constexpr int kFp4Aiter = MKMOE_FMT_MXFP4_AITER;  // MXFP4 in SGLang's loaded (aiter-shuffled) layout
@@ -163,6 +168,7 @@ struct Cfg {
   // (V4.1) a tile is H / 256 = 20 rows: one 32-row unit of 10 KB covers it, where 16-row units
   // took two, the second with 4 rows at a whole unit's latency
   static constexpr int DNA = FMT == kFp4 && I <= 640 ? 2 : 1;
+  static constexpr int TMAX = tile_max(H);  // output rows of a down tile, at most
 };
 
 using CfgPlumbing = Cfg<1024, 16, 4, 1, 1, 512, 512, kFp8, 2, false>;
@@ -178,6 +184,8 @@ using CfgPlumbingSoftplus = Cfg<1024, 16, 4, 1, 1, 512, 512, kFp8, 2, false, fal
 // SGLang's aiter layout with the rank's 576 columns padded to 640 (zero weights), the shared
 // expert's 576 columns FP8 with E8M0 32 x 32 scales
 using CfgV41Tp4 = Cfg<5120, 384, 6, 1, 1, 640, 576, kFp4, 5, false, true, kScoreSqrtSoftplus, kFp8Mx, 576>;
+// ... at TP2: the rank's 1152 routed and 1152 shared columns (a multiple of 128: no padding)
+using CfgV41Tp2 = Cfg<5120, 384, 6, 1, 1, 1152, 1152, kFp4, 5, false, true, kScoreSqrtSoftplus, kFp8Mx>;
 
 // the expert GEMMs of a launch on MFMA (else the VALU GEMVs)
 template <class C>
@@ -2961,7 +2969,7 @@ __device__ __forceinline__ void stage_c(const Params& p, const Union<C>& un, GuS
 // ---------------------------------------------------------------- stage D: shared and routed down + combine
 template <class C>
 struct DownSmem {
-  uint16_t contrib[kRowsMax * C::K * kTileMax];  // bf16 of a pick's down output x its weight
+  uint16_t contrib[kRowsMax * C::K * C::TMAX];  // bf16 of a pick's down output x its weight
   union {
     struct {
       uint8_t q[C::PB * C::MQS];
@@ -2969,7 +2977,7 @@ struct DownSmem {
     };
     SharedDownSmem<C> sd;  // the shared down's quantized rows, done before the routed ones
   };
-  uint16_t shv[kRowsMax * kTileMax];  // the shared expert's bf16 results of the tile
+  uint16_t shv[kRowsMax * C::TMAX];  // the shared expert's bf16 results of the tile
   int claim;  // MFMA down: the pick batch's next unit to be claimed by a wave
   // MFMA down: a wave's slot of weight rows (one unit)
   uint8_t wslot[kWaves][DownTile<C::FMT, C::I, C::DNA>::SLOT] __attribute__((aligned(16)));
@@ -3102,7 +3110,7 @@ __device__ __forceinline__ void down_valu(const Params& p, const Union<C>& un, D
           const float y = tree_sum<kDownLanes>(acc[q]);
           if (q < np && l == 0 && hl < hn) {
             const int pk = un.picks[jj + q];
-            sm.contrib[pk * kTileMax + hl] = f2bf(y * un.wts[pk]);
+            sm.contrib[pk * C::TMAX + hl] = f2bf(y * un.wts[pk]);
           }
         }
       }
@@ -3192,7 +3200,7 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             const int hl = rb * UR + q * 16 + 4 * (lane >> 4) + k;
-            if (n < np && hl < hn) sm.contrib[pk * kTileMax + hl] = f2bf(acc[q][k] * un.wts[pk]);
+            if (n < np && hl < hn) sm.contrib[pk * C::TMAX + hl] = f2bf(acc[q][k] * un.wts[pk]);
           }
       }
       TL_ADD(kTlDMma, tl_now() - tm0);
@@ -3250,7 +3258,7 @@ __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, D
 #pragma unroll
     for (int k = 0; k < C::K; ++k) {
       const int pk = t * C::K + k;
-      routed = bf_round(routed + bf2f(sm.contrib[pk * kTileMax + hl]));
+      routed = bf_round(routed + bf2f(sm.contrib[pk * C::TMAX + hl]));
     }
     p.out[(size_t)t * C::H + h0 + hl] = f2bf(routed + bf2f(sm.shv[idx]));
   }
@@ -3625,6 +3633,9 @@ MKMOE_LAUNCHER(6, CfgPlumbingSoftplus)
 #if !defined(MKMOE_UNIT) || MKMOE_UNIT == 7
 MKMOE_LAUNCHER(7, CfgV41Tp4)
 #endif
+#if !defined(MKMOE_UNIT) || MKMOE_UNIT == 8
+MKMOE_LAUNCHER(8, CfgV41Tp2)
+#endif
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg0(const Params&, int, hipStream_t, bool);
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg1(const Params&, int, hipStream_t, bool);
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg2(const Params&, int, hipStream_t, bool);
@@ -3633,6 +3644,7 @@ __attribute__((visibility("hidden"))) int mkmoe_launch_cfg4(const Params&, int, 
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg5(const Params&, int, hipStream_t, bool);
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg6(const Params&, int, hipStream_t, bool);
 __attribute__((visibility("hidden"))) int mkmoe_launch_cfg7(const Params&, int, hipStream_t, bool);
+__attribute__((visibility("hidden"))) int mkmoe_launch_cfg8(const Params&, int, hipStream_t, bool);
 
 #if !defined(MKMOE_UNIT) || MKMOE_UNIT == MKMOE_UNIT_HOST
 namespace {
@@ -3736,7 +3748,7 @@ int device_info(int dev, DevInfo* out) {
 
 enum CfgId {
   kNone = -1, kIdPlumbing = 0, kIdTp4Fp8, kIdTp4Fp4, kIdTp2Fp4Norm, kIdTp4Fp4Aiter, kIdTp2Fp4NormAiter,
-  kIdPlumbingSoftplus, kIdV41Tp4
+  kIdPlumbingSoftplus, kIdV41Tp4, kIdV41Tp2
 };
 
 template <class C>
@@ -3757,6 +3769,7 @@ int cfg_id(const mkmoe_shape* s) {
   if (shape_is<CfgTp2Fp4NormAiter>(s)) return kIdTp2Fp4NormAiter;
   if (shape_is<CfgPlumbingSoftplus>(s)) return kIdPlumbingSoftplus;
   if (shape_is<CfgV41Tp4>(s)) return kIdV41Tp4;
+  if (shape_is<CfgV41Tp2>(s)) return kIdV41Tp2;
   return kNone;
 }
 
@@ -3837,7 +3850,7 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
   p.renorm = s->renorm;
   int tr = (s->hidden + nwg - 1) / nwg;
   tr = (tr + 3) / 4 * 4;
-  if (tr > kTileMax) tr = kTileMax;
+  if (tr > tile_max(s->hidden)) tr = tile_max(s->hidden);  // the shape's tile LDS (C::TMAX)
   p.tile_rows = tr;
   p.scale = s->routed_scale;
   p.limit = s->swiglu_limit;
@@ -3867,6 +3880,7 @@ int forward_impl(const mkmoe_shape* s, const mkmoe_weights* w, const void* x, in
     case kIdTp2Fp4NormAiter: return mkmoe_launch_cfg5(p, nwg, st, staged);
     case kIdPlumbingSoftplus: return mkmoe_launch_cfg6(p, nwg, st, staged);
     case kIdV41Tp4: return mkmoe_launch_cfg7(p, nwg, st, staged);
+    case kIdV41Tp2: return mkmoe_launch_cfg8(p, nwg, st, staged);
   }
   return MKMOE_ERR_SHAPE;
 }

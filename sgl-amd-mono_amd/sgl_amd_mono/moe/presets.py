@@ -126,6 +126,12 @@ PRESETS = {
         swiglu_limit=10.0, router_parts=5, scoring="sqrt_softplus", shared_fmt="fp8_mx32",
         inter_real=576, aiter_only=True,
     ),
+    # ... at TP2: the rank's 1152 routed and shared columns (a multiple of 128, no padding)
+    "v41_tp2": MoePreset(
+        "v41_tp2", hidden=5120, experts=384, topk=6, n_group=1, topk_group=1, inter=1152,
+        shared_inter=1152, routed_fmt="mxfp4", routed_scale=1.5, swiglu_limit=10.0, router_parts=5,
+        scoring="sqrt_softplus", shared_fmt="fp8_mx32", aiter_only=True,
+    ),
     # the plumbing layer routed as V4.1 routes (sqrt(softplus) scores over one group, the
     # routed scale 1.5 of check_ffn.py:14)
     "plumbing_fp8_softplus": MoePreset(
@@ -150,6 +156,7 @@ WORKLOADS = {
     "tp2_mxfp4_norm_zipf": dict(preset="dsv3_tp2_mxfp4_norm", rows=(48,), zipf_s=1.2),
     # the reference's own MoE shape: DeepSeek-V4.1 at TP4, the experts in SGLang's layout
     "v41_tp4_mxfp4": dict(preset="v41_tp4", rows=(1, 8, 48)),
+    "v41_tp2_mxfp4": dict(preset="v41_tp2", rows=(1, 8, 48)),
 }
 
 

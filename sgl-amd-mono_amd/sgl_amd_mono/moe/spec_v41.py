@@ -9,9 +9,10 @@ this rank's shard of each layer's FP8 shared expert as the checkpoint holds it
 (``:352-404``: the experts in aiter's shuffle, the shared expert seen), the FFN weights read in
 place off SGLang's modules (``:484-530``) and a ``build`` whose forward runs one layer's FFN.
 
-Only the TP 4 share is compiled (the rank's 576 routed columns padded to 640); the reference
-also runs TP 2. The forward is the FFN's seam and MoE block (``moe/ffn.py``); the attention
-TP reduce before it and the all-reduce after it need peers.
+The TP 4 share (the rank's 576 routed columns padded to 640) and the TP 2 share (1152 columns)
+are compiled, the reference's TP sizes (``spec.py:959-967``). The forward is the FFN's seam and
+MoE block (``moe/ffn.py``); the attention TP reduce before it and the all-reduce after it need
+peers.
 """
 
 from __future__ import annotations
@@ -20,12 +21,14 @@ import logging
 import re
 
 from .. import monospec as _local
-from .ffn import V41_PRESET, FfnRunner, FfnWeights
+from .ffn import FfnRunner, FfnWeights
 from .presets import PRESETS
 
 MAX_ROWS = 48
 BLOCKS = 256
-TP_SIZES = (4,)
+# the compiled share of each TP size
+PRESET_BY_TP = {2: "v41_tp2", 4: "v41_tp4"}
+TP_SIZES = tuple(sorted(PRESET_BY_TP))
 _log = logging.getLogger(__name__)
 
 
@@ -158,11 +161,10 @@ def _weights(layer, copies: dict, i: int) -> FfnWeights:
     )
 
 
-def _shape_reasons(w: FfnWeights, i: int) -> list[str]:
+def _shape_reasons(w: FfnWeights, i: int, preset) -> list[str]:
     """Each MoE tensor against the compiled shape (no device needed)."""
     from .runner import shape_ok
 
-    preset = PRESETS[V41_PRESET]
     reasons = []
     for name, (shape, dtypes) in w.moe().expected(preset).items():
         t = getattr(w, name)
@@ -205,7 +207,7 @@ def _model_disable_reasons(model, hf_config, copies: dict, tp_size: int | None =
         if not _shared_seen(copies, i):
             reasons.append(f"layer {i}: the shared expert's FP8 tensors were not seen at load")
             continue
-        reasons += _shape_reasons(_weights(layer, copies, i), i)
+        reasons += _shape_reasons(_weights(layer, copies, i), i, PRESETS[PRESET_BY_TP[tp_size]])
     return reasons
 
 
@@ -228,14 +230,16 @@ class _Built:
 def _build(model, hf_config, ctx) -> _Built:
     from .runner import DEADLINE_S
 
+    tp = getattr(ctx, "tp_size", None)
+    preset = PRESETS[PRESET_BY_TP[int(_parallel()[1] if tp is None else tp)]]
     layers = {}
     for i in _moe_layers(model):
         w = _weights(model.model.layers[i], ctx.copies, i)
-        w.check(PRESETS[V41_PRESET])
+        w.check(preset)
         layers[i] = w
     device = next(iter(layers.values())).gate_w.device
     runner = FfnRunner(
-        V41_PRESET, device, norm_eps=float(getattr(hf_config, "rms_norm_eps", HF_CONFIG["rms_norm_eps"])),
+        preset, device, norm_eps=float(getattr(hf_config, "rms_norm_eps", HF_CONFIG["rms_norm_eps"])),
         max_rows=MAX_ROWS, deadline_s=getattr(ctx, "deadline_s", None) or DEADLINE_S,
     )  # fmt: skip
     _log.info("mkmoe: V4.1 FFN on %d layers, experts read in place in SGLang's shuffled gfx950 layout", len(layers))

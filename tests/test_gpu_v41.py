@@ -1,9 +1,10 @@
-"""The reference's own MoE shape on an MI355X: DeepSeek-V4.1 at TP4, through the C ABI.
+"""The reference's own MoE shape on an MI355X: DeepSeek-V4.1 at TP4 and TP2, through the C ABI.
 
 Hidden 5120, 384 experts, top-6 by sqrt(softplus) over one group (routed scale 1.5), MXFP4
-routed experts in SGLang's loaded gfx950 layout with the rank's 576 columns padded to 640
-(zero weights, w2's scale columns padded to 24), and the shared expert's 576 columns in FP8
-with E8M0 32 x 32 scales, its activations and intermediate quantized by the MXFP8 "vllm" rule
+routed experts in SGLang's loaded gfx950 layout (TP4: the rank's 576 columns padded to 640 with
+zero weights, w2's scale columns padded to 24; TP2: 1152 columns, w2's 36 scale columns padded
+to 40), and the shared expert's rank share (576 or 1152 columns) in FP8 with E8M0 32 x 32
+scales, its activations and intermediate quantized by the MXFP8 "vllm" rule
 (the tensors ``check_ffn.py:128-182`` makes, ``FFNWeights`` at ``gfx950/runner.py:130-168``).
 The weights are generated as ``make_weights`` draws them, row-major on the CPU, and shuffled
 by the oracle's restatement of aiter's layout.
@@ -27,25 +28,26 @@ import torch
 pytestmark = pytest.mark.gpu
 
 WORKLOAD = "v41_tp4_mxfp4"
+TP2 = "v41_tp2_mxfp4"
 _cache = {}
 
 
-def _case(rows):
+def _case(rows, workload=WORKLOAD):
     from gpu_case import build
 
     from oracle import shuffle as sh
 
-    if rows not in _cache:
+    if (workload, rows) not in _cache:
         _cache.clear()
         torch.cuda.empty_cache()
-        c = build(WORKLOAD, rows)
+        c = build(workload, rows)
         w13, w13_s, w2, w2_s = sh.to_aiter(c.w.w13, c.w.w13_s, c.w.w2, c.w.w2_s)
         # SGLang's views: fp4x2 weights, the scales as flat [E rows][cols] byte matrices
         w = dataclasses.replace(
             c.w, w13=w13, w13_s=w13_s.reshape(-1, w13_s.shape[-1]), w2=w2, w2_s=w2_s.reshape(-1, w2_s.shape[-1])
         )
-        _cache[rows] = dataclasses.replace(c, w=w)
-    return _cache[rows]
+        _cache[(workload, rows)] = dataclasses.replace(c, w=w)
+    return _cache[(workload, rows)]
 
 
 def _runner(c):
@@ -54,16 +56,19 @@ def _runner(c):
     return MoeRunner(c.preset, "cuda")
 
 
-@pytest.mark.parametrize("rows", [1, 2, 8, 16, 24, 48])
-def test_parity_v41(rows):
+@pytest.mark.parametrize(
+    "workload,rows", [(WORKLOAD, r) for r in (1, 2, 8, 16, 24, 48)] + [(TP2, r) for r in (1, 8, 48)]
+)
+def test_parity_v41(workload, rows):
     from gpu_case import errors, record_accuracy
 
     from oracle import formats as fm
 
-    c = _case(rows)
-    assert c.w.w2_s.shape == (384 * 5120, 24) and c.w.sgu_s.shape == (1152 // 32, 160)
+    c = _case(rows, workload)
+    i, s = c.p["inter"], c.p["shared_inter"]
+    assert c.w.w2_s.shape == (384 * 5120, -(-i // 32 // 8) * 8) and c.w.sgu_s.shape == (2 * s // 32, 160)
     run = _runner(c)
-    print(f"\n{WORKLOAD} R={rows} (aiter layout, MX shared expert)", flush=True)
+    print(f"\n{workload} R={rows} (aiter layout, MX shared expert)", flush=True)
     ids = torch.zeros(rows, c.p["topk"], dtype=torch.int32, device="cuda")
     wts = torch.zeros(rows, c.p["topk"], dtype=torch.float32, device="cuda")
     out = run.moe(c.w, c.x, topk_ids=ids, topk_w=wts)
@@ -83,7 +88,7 @@ def test_parity_v41(rows):
         assert torch.equal(run.region(sn)[: rows * (h // 32)].cpu().reshape(rows, -1), code), f"{rule} scales"
     g = errors(out.cpu(), c.golden, c.chain)
     print(f"  all {rows} rows vs fp32-matmul golden: {g}", flush=True)
-    record_accuracy(WORKLOAD, rows, "default", g, g, True)
+    record_accuracy(workload, rows, "default", g, g, True)
     assert not g["nan"] and g["n_over_bar"] == 0 and g["rel_l2"] <= 1e-2 and g["cos"] >= 0.9999, g
 
 
@@ -146,9 +151,9 @@ def test_v41_padding_never_read(rows):
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), "the padding changed the output"
 
 
-@pytest.mark.parametrize("rows", [8, 48])
-def test_v41_staged_equals_fused_and_repeats(rows):
-    c = _case(rows)
+@pytest.mark.parametrize("workload,rows", [(WORKLOAD, 8), (WORKLOAD, 48), (TP2, 8)])
+def test_v41_staged_equals_fused_and_repeats(workload, rows):
+    c = _case(rows, workload)
     run = _runner(c)
     a = run.moe(c.w, c.x).clone()
     b = run.moe(c.w, c.x, staged=True).clone()
@@ -159,10 +164,11 @@ def test_v41_staged_equals_fused_and_repeats(rows):
     assert torch.equal(a.view(torch.int16), d.view(torch.int16)), "repeat differs"
 
 
-def test_v41_graph_replay_bitwise():
+@pytest.mark.parametrize("workload", [WORKLOAD, TP2])
+def test_v41_graph_replay_bitwise(workload):
     """Row counts on both sides of the routing hand-off and of stage Q in one graph, replayed
     with eager work between the replays."""
-    c = _case(48)
+    c = _case(48, workload)
     run = _runner(c)
     counts = (1, 8, 24, 48)
     xs = [c.x[:r].contiguous() for r in counts]

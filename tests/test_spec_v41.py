@@ -17,22 +17,25 @@ from sgl_amd_mono.moe.presets import PRESETS
 
 META = torch.device("meta")
 FP4X2, E8M0, FP8 = torch.float4_e2m1fn_x2, torch.float8_e8m0fnu, torch.float8_e4m3fn
-H, E, I_PAD, S_FULL = 5120, 384, 640, 2304
+H, E, S_FULL = 5120, 384, 2304
+I_PAD = {4: 640, 2: 1152}  # the loader's width of a rank's share (TP 4: 576 padded)
+W2_COLS = {4: 24, 2: 40}  # w2's E8M0 columns, padded to a multiple of 8
 
 
 def _t(shape, dtype):
     return torch.empty(shape, dtype=dtype, device=META)
 
 
-def _layer(shuffled=True, pad_experts=0, experts=E):
+def _layer(shuffled=True, pad_experts=0, experts=E, tp=4):
     e = experts + pad_experts
-    w13 = _t((e, 2 * I_PAD, H // 2), FP4X2)
+    i = I_PAD[tp]
+    w13 = _t((e, 2 * i, H // 2), FP4X2)
     w13.is_shuffled = shuffled
     ex = SimpleNamespace(
         w13_weight=w13,
-        w13_weight_scale_inv=_t((e * 2 * I_PAD, H // 32), E8M0),
-        w2_weight=_t((e, H, I_PAD // 2), FP4X2),
-        w2_weight_scale_inv=_t((e * H, 24), E8M0),
+        w13_weight_scale_inv=_t((e * 2 * i, H // 32), E8M0),
+        w2_weight=_t((e, H, i // 2), FP4X2),
+        w2_weight_scale_inv=_t((e * H, W2_COLS[tp]), E8M0),
     )
     gate = SimpleNamespace(weight=_t((experts, H), torch.bfloat16), e_score_correction_bias=_t((experts,), torch.bfloat16))
     return SimpleNamespace(
@@ -67,16 +70,18 @@ def test_the_plugin_registers_the_v41_spec():
 
 def test_limits_bounds_and_config():
     lim = sv.SPEC.devices["gfx950"]
-    assert lim.widths == tuple(range(1, 49)) and lim.tp_sizes == (4,) and lim.resident_blocks == 256
+    assert lim.widths == tuple(range(1, 49)) and lim.tp_sizes == (2, 4) and lim.resident_blocks == 256
     assert sv.SPEC.numerics.bound("moe.ids.max_abs") == 0.0 and sv.SPEC.numerics.bound("moe.out.cosine") == 0.9999
     req = sv.SPEC.requires.hf_config
-    p = PRESETS["v41_tp4"]
-    # the compiled preset is the config's TP 4 share
-    assert req["model_type"] == "deepseek_v41" and req["hidden_size"] == p.hidden
-    assert req["n_routed_experts"] == p.experts and req["num_experts_per_tok"] == p.topk
-    assert req["moe_intermediate_size"] // 4 == p.inter_real == p.shared_inter
-    assert req["routed_scaling_factor"] == p.routed_scale and req["swiglu_limit"] == p.swiglu_limit
-    assert req["scoring_func"] == "sqrtsoftplus" and p.scoring == "sqrt_softplus"
+    # the compiled presets are the config's TP 4 and TP 2 shares
+    for tp, name in sv.PRESET_BY_TP.items():
+        p = PRESETS[name]
+        assert req["model_type"] == "deepseek_v41" and req["hidden_size"] == p.hidden
+        assert req["n_routed_experts"] == p.experts and req["num_experts_per_tok"] == p.topk
+        assert req["moe_intermediate_size"] // tp == (p.inter_real or p.inter) == p.shared_inter
+        assert p.inter % 128 == 0 and p.inter - (p.inter_real or p.inter) < 128  # padded to 128 (dims.py)
+        assert req["routed_scaling_factor"] == p.routed_scale and req["swiglu_limit"] == p.swiglu_limit
+        assert req["scoring_func"] == "sqrtsoftplus" and p.scoring == "sqrt_softplus"
     assert sv.SPEC.load_tensor is sv.load_tensor
 
 
@@ -105,7 +110,7 @@ def test_weights_mapping_and_a_loadable_model():
     assert sv._model_disable_reasons(model, model.config, copies, tp_size=4) == []
     w = sv._weights(layers[0], copies, 0)
     # the routed experts' rows only (padding experts follow them), the scales' bytes as uint8
-    assert w.w13.shape == (E, 2 * I_PAD, H // 2) and w.w13_s.shape == (E * 2 * I_PAD, H // 32)
+    assert w.w13.shape == (E, 2 * I_PAD[4], H // 2) and w.w13_s.shape == (E * 2 * I_PAD[4], H // 32)
     assert w.w13_s.dtype == torch.uint8 and w.w2_s.shape == (E * H, 24)
     # the shared expert: gate and up joined (rows), the rank's columns of down, E8M0 32 x 32
     assert w.sgu.shape == (1152, H) and w.sgu.dtype == FP8 and w.sgu_s.shape == (36, 160)
@@ -115,6 +120,24 @@ def test_weights_mapping_and_a_loadable_model():
     assert ("shared expert fp8", 0, "gate_up", "weight") in copies
     assert ("shared expert fp8", 0, "gate_proj", "weight") not in copies
     assert sv._weights(layers[0], copies, 0).sgu.shape == w.sgu.shape
+
+
+def test_tp2_model_maps_and_loads():
+    """TP 2: the rank's 1152 columns of every expert and of the shared expert."""
+    layers = [_layer(tp=2), _layer(tp=2, pad_experts=8)]
+    model = _model(layers)
+    copies = {}
+    for i in range(2):
+        _load_shared(copies, model, i, tp=2, rank=0)
+    assert sv._model_disable_reasons(model, model.config, copies, tp_size=2) == []
+    w = sv._weights(layers[1], copies, 1)
+    assert w.sgu.shape == (2304, H) and w.sgu_s.shape == (72, 160) and w.sw2.shape == (H, 1152)
+    assert w.w2_s.shape == (E * H, 40)
+    # TP 4's tensors at TP 2 are refused by shape
+    m4 = _model([_layer()])
+    c4 = {}
+    _load_shared(c4, m4, 0, tp=4, rank=0)
+    assert any("w13" in r for r in sv._model_disable_reasons(m4, m4.config, c4, tp_size=2))
 
 
 def test_refusal_reasons():
@@ -128,7 +151,7 @@ def test_refusal_reasons():
     assert any("layer 2" in r and "shared expert" in r for r in why)
     assert any("layer 3" in r and "gate_w" in r for r in why)
     assert not any("layer 0" in r for r in why)
-    assert "TP (4,)" in sv._model_disable_reasons(model, model.config, copies, tp_size=2)[0]
+    assert "TP (2, 4)" in sv._model_disable_reasons(model, model.config, copies, tp_size=8)[0]
 
 
 def test_ffn_runner_refuses_another_hidden_size():
