@@ -475,6 +475,18 @@ def timeline(runner, rb: RowsBench, reps: int = 8) -> dict:
             "min": round(float(v.min()), 2),
             "max": round(float(v.max()), 2),
         }
+    # every workgroup's stamps (µs from the first stamp; the loop parts' sums in µs, the counts
+    # as they are), in workgroup order
+    cols = []
+    for k, name in enumerate(_lib.TL_NAMES):
+        col = st[:, k]
+        if name in ("gate_up units", "down units"):
+            cols.append(col)
+        elif name.startswith(("gate_up ", "down ")) and name not in ("gate_up first unit", "down first unit"):
+            cols.append(col * tick_us)
+        else:
+            cols.append((col - t0) * tick_us)
+    out["workgroup_stamps"] = [[round(float(c[i]), 2) for c in cols] for i in range(st.shape[0])]
     return out
 
 

@@ -65,7 +65,9 @@ extern "C" {
 
 /* error words kept in the workspace (mkmoe_read_errors) */
 #define MKMOE_ERRW_CODE 0    /* 0, or the first device error's code */
-#define MKMOE_ERRW_STAGE 1   /* the stage whose wait ran past its deadline */
+#define MKMOE_ERRW_STAGE 1   /* the stage whose wait ran past its deadline (the first to record,
+                              * or, with a fault injected, the stalled wait's: the waits it
+                              * holds up downstream may reach their deadlines before it) */
 #define MKMOE_ERRW_BLOCK 2   /* the workgroup that saw it */
 #define MKMOE_ERRW_COUNT 3   /* how many waits ran past their deadline */
 #define MKMOE_ERRW_FAULT 4   /* 1: a wait stalled by mkmoe_options.fault_stage ran to its deadline */
@@ -172,12 +174,14 @@ typedef struct mkmoe_options {
   /* Test fault injection, the reference's SGLANG_AMD_MONO_FAULT_INJECT (common/guard.py:69-89:
    * a wait that stalls and times out). fault_stage 0: none; else workgroup fault_workgroup's
    * wait at that stage (the MKMOE_ERRW_STAGE codes of the persistent launch's waits: 1 norm,
-   * 2 router part sums and x codes, 3 route, 4 gate_up, 6 quantize) ignores what it waits for
-   * and runs to the deadline, then records the error words with MKMOE_ERRW_FAULT set and the
-   * launch goes on, as after any deadline. A stage the launch does not wait at (3 up to 16
-   * rows, 6 below the shape's stage-Q rows, 1 without the norm) and the staged launches (no
-   * waits) stall nothing. The faulted launch's output is not valid; mkmoe_clear_errors
-   * restores the workspace. */
+   * 2 router part sums and x codes, 3 route (up to 16 rows: the routing published to the
+   * workgroups that run the shared expert's gate_up meanwhile, and their shared intermediate
+   * awaited before the shared down), 4 gate_up, 6 quantize) ignores what it waits for and runs
+   * to the deadline, then records the error words with MKMOE_ERRW_FAULT set and the launch
+   * goes on, as after any deadline. A stage the launch does not wait at (6 below the shape's
+   * stage-Q rows, 1 without the norm, 3 where the gate_up runs on the VALU up to 16 rows) and
+   * the staged launches (no waits) stall nothing. The faulted launch's output is not valid;
+   * mkmoe_clear_errors restores the workspace. */
   int32_t fault_stage;
   int32_t fault_workgroup; /* 0 .. 255, and below the launch's grid (one workgroup a CU, at
                             * most 256): MKMOE_ERR_ARG otherwise */

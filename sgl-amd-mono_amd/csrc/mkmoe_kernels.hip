@@ -486,10 +486,12 @@ __device__ __forceinline__ float dot32_fp4(u32x4 w, u32x4 xa, u32x4 xb) {
 }
 
 // ---------------------------------------------------------------- hand-offs
+// the first wait past its deadline names its stage and workgroup; a wait stalled by the test
+// fault injection names its own in any case (the waits it holds up may time out first)
 __device__ __forceinline__ void record_error(const Params& p, int stage, bool fault = false) {
   uint32_t* e = ctl(p) + kCtlErr;
   uint32_t prev = atomicCAS(&e[MKMOE_ERRW_CODE], 0u, (uint32_t)MKMOE_DEVERR_DEADLINE);
-  if (prev == 0u) {
+  if (prev == 0u || fault) {
     atomicExch(&e[MKMOE_ERRW_STAGE], (uint32_t)stage);
     atomicExch(&e[MKMOE_ERRW_BLOCK], (uint32_t)blockIdx.x);
   }
@@ -530,6 +532,26 @@ __device__ __forceinline__ void await_all(const Params& p, int which, int nwg, i
       if (__ballot(!ok) == 0ull && !stall) break;
       if (__builtin_amdgcn_s_memrealtime() - t0 > p.deadline) {
         if (lane == 0) record_error(p, stage, stall);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// wait until workgroup ``wg``'s flag at ``which`` is set (or the deadline passed): wave 0 reads
+// it; the data behind it is read with sc1 loads afterwards
+__device__ __forceinline__ void await_one(const Params& p, int which, int wg, int stage) {
+  if (threadIdx.x < 64) {
+    const auto rs = ws_rsrc(p);
+    const bool stall = stalls(p, stage);
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    while (true) {
+      // (one address in every lane: a uniform exit)
+      const uint32_t f = __builtin_amdgcn_readfirstlane(dld32(rs, kCtlFlags + (which * kFlagWgs + wg) * 4));
+      if (f != 0u && !stall) break;
+      if (__builtin_amdgcn_s_memrealtime() - t0 > p.deadline) {
+        if (threadIdx.x == 0) record_error(p, stage, stall);
         break;
       }
     }
@@ -1077,10 +1099,10 @@ __device__ __forceinline__ void route_row(const Params& p, RouteSmem<C>& sm, int
 
 // every row's routing in this workgroup, into LDS (ids, wts: [rows][topk]; rows_of: the rows
 // that picked each expert, as bitmaps); wave w selects rows w, w + 8, ... of each kRouteRows
-// chunk. Workgroup 0 also writes the workspace copies and the outputs.
+// chunk. One workgroup (publish) also writes the workspace copies and the outputs.
 template <class C>
 __device__ __forceinline__ void route_all(const Params& p, RouteSmem<C>& sm, int* ids, float* wts,
-                                          uint32_t (*rows_of)[2], int b) {
+                                          uint32_t (*rows_of)[2], bool publish) {
   const int lane = threadIdx.x & 63, wave = (int)(threadIdx.x >> 6);
   const auto rs = ws_rsrc(p);
   for (int e = threadIdx.x; e < C::E; e += kThreads) rows_of[e][0] = rows_of[e][1] = 0u;
@@ -1099,7 +1121,7 @@ __device__ __forceinline__ void route_all(const Params& p, RouteSmem<C>& sm, int
         ids[r * C::K + lane] = id;
         wts[r * C::K + lane] = w;
         atomicOr(&rows_of[id][r >> 5], 1u << (r & 31));
-        if (b == 0) {
+        if (publish) {
           dst32(rs, p.off[6] + (r * C::K + lane) * 4, (uint32_t)id);
           dst32(rs, p.off[7] + (r * C::K + lane) * 4, f2u(w));
           if (p.ids_out) p.ids_out[r * C::K + lane] = id;
@@ -2899,36 +2921,92 @@ __device__ __forceinline__ void gate_up_valu(const Params& p, const Union<C>& un
   }
 }
 
-// the same on MFMA: the shared expert's (16-row group, column block) units, then the routed
-// ones, dealt evenly as one list
+// The MFMA gate_up's deal: FP8 in half-units (a unit's first or last NC / 2 columns), so that
+// shares differ by half a unit at most (with MXFP4 weights the extra bookkeeping crowds the
+// registers of the gate_up loop: whole units)
 template <class C>
-__device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un, GuSmem<C>& sm, int b, int nwg) {
+struct GuDeal {
+  static constexpr bool HALF = C::FMT == kFp8;
+  static constexpr int HU = HALF ? 2 : 1;  // deal steps a unit
+  // the shared expert's (16-row group, column block) units
+  __device__ __forceinline__ static int shared_units(int rows) {
+    return (rows + kMfmaPicks - 1) / kMfmaPicks * (C::S / GuTile<C, C::SFMT>::NC);
+  }
+};
+
+// the shared expert's gate_up units [lo, hi) (deal steps) on MFMA; before_x runs once, after
+// the first unit's weights are requested and before the activations are read
+template <class C, class PreFn>
+__device__ __forceinline__ void gate_up_shared(const Params& p, GuSmem<C>& sm, int lo, int hi, PreFn before_x) {
   const auto rs = ws_rsrc(p);
-  const int n_sh = (p.rows + kMfmaPicks - 1) / kMfmaPicks * (C::S / GuTile<C, C::SFMT>::NC);
+  const uint32_t qoff = C::FMT == kFp4 ? p.off[3] : p.off[1];
+  const uint32_t soff = C::FMT == kFp4 ? p.off[4] : p.off[2];
+  bool pre = false;
+  gu_mfma<C, C::SFMT, GuDeal<C>::HALF, false>(
+      sm, C::S, C::S, lo, hi, false,
+      [&](int tg, const uint8_t*& w, const void*& s, int& np) {
+        w = p.sgu;
+        s = p.sgu_s;
+        np = min(kMfmaPicks, p.rows - tg * kMfmaPicks);
+      },
+      [&](int tg, int np, GuX<C, C::SFMT>& x) {
+        if (!pre) {
+          before_x();
+          pre = true;
+        }
+        x.load(p, np, qoff, soff, [&](int r) { return tg * kMfmaPicks + r; }, threadIdx.x & 63, (int)(threadIdx.x >> 6));
+      },
+      [&](int tg, int q, int col, float g, float u) {
+        dst16(rs, p.off[8] + ((uint32_t)(tg * kMfmaPicks + q) * C::S + col) * 2, f2bf(swiglu_shared(g, u, p.limit)));
+      });
+  if (!pre) before_x();
+}
+
+#ifndef MKMOE_EARLY_SHARED
+#define MKMOE_EARLY_SHARED 1
+#endif
+constexpr bool kEarlyShared = MKMOE_EARLY_SHARED != 0;
+#ifndef MKMOE_PRE_SHARED
+#define MKMOE_PRE_SHARED 1
+#endif
+// ... and then every workgroup's shared down before the C wait
+constexpr bool kPreShared = MKMOE_PRE_SHARED != 0;
+// workgroups [0, n) that run the shared expert's gate_up in the routing window, a unit each
+// (half of the grid at most): launches whose every workgroup would route the step itself,
+// with the gate_up on MFMA. Its weights stream while the other workgroups route, and the
+// routed units alone are dealt afterwards (0: none, the shared units are dealt with them)
+template <class C>
+__device__ __forceinline__ int early_shared_wgs(const Params& p, int nwg) {
+  if (!kEarlyShared || p.rows > kLocalRouteMax || !gate_on_mfma<C>(p.rows, p.mfma_gate)) return 0;
+  return min(GuDeal<C>::shared_units(p.rows), nwg / 2);
+}
+
+// the same on MFMA: the shared expert's (16-row group, column block) units, then the routed
+// ones, dealt evenly as one list; nsw > 0: workgroups [0, nsw) ran the shared units already
+// (early_shared_wgs), and the routed units are dealt over the other workgroups where their
+// largest share stays the same, else over all
+template <class C>
+__device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un, GuSmem<C>& sm, int b, int nwg,
+                                             int nsw = 0) {
+  const auto rs = ws_rsrc(p);
+  const int n_sh = GuDeal<C>::shared_units(p.rows);
   const int n_rt = un.ntg_r * (C::IR / GuTile<C, C::FMT>::NC);
-  // FP8: the share in half-units (a unit's first or last NC / 2 columns), so that shares
-  // differ by half a unit at most (with MXFP4 weights the extra bookkeeping crowds the
-  // registers of the gate_up loop: whole units)
-  constexpr bool HALF = C::FMT == kFp8;
-  constexpr int HU = HALF ? 2 : 1;  // deal steps a unit
+  constexpr bool HALF = GuDeal<C>::HALF;
+  constexpr int HU = GuDeal<C>::HU;
   int lo, hi;
-  even_share(HU * (n_sh + n_rt), b, nwg, lo, hi);
-  {
-    const uint32_t qoff = C::FMT == kFp4 ? p.off[3] : p.off[1];
-    const uint32_t soff = C::FMT == kFp4 ? p.off[4] : p.off[2];
-    gu_mfma<C, C::SFMT, HALF, false>(
-        sm, C::S, C::S, lo, min(hi, HU * n_sh), false,
-        [&](int tg, const uint8_t*& w, const void*& s, int& np) {
-          w = p.sgu;
-          s = p.sgu_s;
-          np = min(kMfmaPicks, p.rows - tg * kMfmaPicks);
-        },
-        [&](int tg, int np, GuX<C, C::SFMT>& x) {
-          x.load(p, np, qoff, soff, [&](int r) { return tg * kMfmaPicks + r; }, threadIdx.x & 63, (int)(threadIdx.x >> 6));
-        },
-        [&](int tg, int q, int col, float g, float u) {
-          dst16(rs, p.off[8] + ((uint32_t)(tg * kMfmaPicks + q) * C::S + col) * 2, f2bf(swiglu_shared(g, u, p.limit)));
-        });
+  if (nsw > 0) {
+    const int n = HU * n_rt, m = (n + nwg - 1) / nwg;
+    if (n <= m * (nwg - nsw)) {
+      if (b < nsw) lo = hi = 0;
+      else even_share(n, b - nsw, nwg - nsw, lo, hi);
+    } else {
+      even_share(n, b, nwg, lo, hi);
+    }
+    lo += HU * n_sh;
+    hi += HU * n_sh;
+  } else {
+    even_share(HU * (n_sh + n_rt), b, nwg, lo, hi);
+    gate_up_shared<C>(p, sm, lo, min(hi, HU * n_sh), [] {});
   }
   auto first = [&](int tg) {
     const int slot = un.tg_slot[tg];
@@ -2959,10 +3037,12 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
       });
 }
 
+// nsw: workgroups [0, nsw) ran the shared expert's units in the routing window (MFMA)
 template <class C>
-__device__ __forceinline__ void stage_c(const Params& p, const Union<C>& un, GuSmem<C>& sm, int b, int nwg) {
-  if constexpr (C::SHUF) gate_up_mfma<C>(p, un, sm, b, nwg);  // (the VALU GEMVs read row-major rows)
-  else if (gate_on_mfma<C>(p.rows, p.mfma_gate)) gate_up_mfma<C>(p, un, sm, b, nwg);
+__device__ __forceinline__ void stage_c(const Params& p, const Union<C>& un, GuSmem<C>& sm, int b, int nwg,
+                                        int nsw = 0) {
+  if constexpr (C::SHUF) gate_up_mfma<C>(p, un, sm, b, nwg, nsw);  // (the VALU GEMVs read row-major rows)
+  else if (gate_on_mfma<C>(p.rows, p.mfma_gate)) gate_up_mfma<C>(p, un, sm, b, nwg, nsw);
   else gate_up_valu<C>(p, un, sm.x, b, nwg);
 }
 
@@ -3235,9 +3315,9 @@ __device__ __forceinline__ void down_first(const Params& p, const Union<C>& un, 
 }
 
 // tile rows [h0, h0 + hn): the routed down GEMVs (MFMA or VALU, as MF), the shared expert's
-// down, then the combine; first_ready: the routed down's first units are already requested
-// into bt (waves 1-7)
-template <class C, bool MF, bool GQ, bool SHF = false>
+// down (SHF, PRE: done before), then the combine; first_ready: the routed down's first units
+// are already requested into bt (waves 1-7)
+template <class C, bool MF, bool GQ, bool SHF = false, bool PRE = false>
 __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
                                           DownBatchOf<C, MF>& bt, bool first_ready) {
   const int tid = threadIdx.x;
@@ -3245,7 +3325,7 @@ __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, D
   if constexpr (MF) down_mfma<C, GQ, SHF>(p, un, sm, h0, hn, bt, first_ready);
   else down_valu<C, GQ>(p, un, sm, h0, hn, bt, first_ready);
   TL(kTlDRouted);
-  if constexpr (!SHF) {  // SHF: sm.shv holds the shared expert's results already
+  if constexpr (!SHF && !PRE) {  // SHF, PRE: sm.shv holds the shared expert's results already
     SharedDownBatch<C, MF> bs;
     shared_down_tile<C, MF, GQ>(p, sm.sd, sm.shv, h0, hn, bs, false);
   }
@@ -3267,12 +3347,12 @@ __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, D
 
 // this workgroup's tiles; first_ready: its first tile's first routed units are already
 // requested; GQ: stage Q has quantized the step's intermediates
-template <class C, bool MF, bool GQ, bool SHF = false>
+template <class C, bool MF, bool GQ, bool SHF = false, bool PRE = false>
 __device__ __forceinline__ void stage_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg,
                                         DownBatchOf<C, MF>& bt, bool first_ready) {
   const int tr = p.tile_rows;
   const int n_tiles = (C::H + tr - 1) / tr;
-  if (b < n_tiles) down_tile<C, MF, GQ, SHF>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt, first_ready);
+  if (b < n_tiles) down_tile<C, MF, GQ, SHF, PRE>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt, first_ready);
   // further tiles (fewer workgroups than tiles) start from batches of their own, so that bt
   // is free once the first tile's routed down is done
   for (int tile = b + nwg; tile < n_tiles; tile += nwg) {
@@ -3359,14 +3439,20 @@ __device__ __forceinline__ void shared_first_run(const Params& p, DownSmem<C>& s
 
 // the persistent launch past its C arrival: the down stage's first weights depend on the
 // union alone, so they are requested before the wait for the other workgroups' gate_up. GQ
-// (launches of C::QROWS rows or more): stage Q first. Each combination is a code path
-// of its own, so that neither path's registers are allocated around the other's
-template <class C, bool MF, bool GQ, bool SHF = false>
-__device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg) {
+// (launches of C::QROWS rows or more): stage Q first. PRE: workgroups [0, nsw) ran the shared
+// expert's gate_up in the routing window and set their flags at B, so the first tile's shared
+// down runs before the wait (its rows quantized here). Each combination is a code path of its
+// own, so that neither path's registers are allocated around the other's
+template <class C, bool MF, bool GQ, bool SHF = false, bool PRE = false>
+__device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg,
+                                            int nsw = 0) {
   static_assert(!SHF || (MF && GQ && C::SF), "the shared down first: MFMA down, stage Q, a fitting slot");
+  static_assert(!(SHF && PRE), "one place for the shared down");
   DownBatchOf<C, MF> bt;
   const int tr = p.tile_rows;
   const bool first = b * tr < C::H;
+  // (tiles past the grid's first run the shared down after the routed one, from stage Q's rows)
+  const bool more_tiles = (C::H + tr - 1) / tr > nwg;
   // from 8 rows the first units are requested across the wait only by the workgroups that
   // arrive among the first three quarters: a late one's requests would hold up its own sight
   // of the last flags (its CU's loads queue behind them), by up to 5 us at 8 rows, and the Q
@@ -3379,11 +3465,18 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
     down_first<C, MF>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt, SHF);
     if constexpr (SHF) shared_first_issue<C>(p, sm, b * tr, min(tr, C::H - b * tr), sh);
   }
+  if constexpr (PRE) {
+    if (first) {
+      await_all(p, kCtlB, nsw, kStageB);
+      SharedDownBatch<C, MF> bs;
+      shared_down_tile<C, MF, false>(p, sm.sd, sm.shv, b * tr, min(tr, C::H - b * tr), bs, false);
+    }
+  }
   await_all(p, kCtlC, nwg, kStageC);
   TL(kTlCAwaited);
   reset_parts<C>(p, b, nwg);  // every workgroup is past its routing
   if constexpr (GQ) {
-    stage_q<C>(p, un, b, nwg, !SHF);
+    stage_q<C>(p, un, b, nwg, !(SHF || PRE) || more_tiles);
     TL(kTlQDone);
     arrive(p, kCtlQ);
   }
@@ -3400,7 +3493,7 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
     TL(kTlQAwaited);
   }
   __syncthreads();  // the tile's readers are done before the down stage reuses its LDS
-  stage_d<C, MF, GQ, SHF>(p, un, sm, b, nwg, bt, early);
+  stage_d<C, MF, GQ, SHF, PRE>(p, un, sm, b, nwg, bt, early);
 }
 
 // ---------------------------------------------------------------- kernels
@@ -3429,10 +3522,29 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   TL(kTlADone);
   arrive(p, kCtlA);
   TL(kTlAArrived);
-  if (p.rows <= kLocalRouteMax) {
+  const int nsw = early_shared_wgs<C>(p, nwg);
+  if (b < nsw) {
+    // the shared expert's gate_up while the others route: its weights are requested before
+    // the A hand-off (the x codes) is awaited; then its flag at B (the shared intermediate
+    // stored), and the routing from the workgroup that publishes it
+    int lo, hi;
+    even_share(GuDeal<C>::HU * GuDeal<C>::shared_units(p.rows), b, nsw, lo, hi);
+    gate_up_shared<C>(p, sm.g, lo, hi, [&] {
+      await_all(p, kCtlA, nwg, kStageA);
+      TL(kTlAAwaited);
+    });
+    arrive(p, kCtlB);
+    await_one(p, kCtlB, nwg - 1, kStageB);
+    TL(kTlRouted);
+    build_union<C>(p, un, false);
+    TL(kTlUnion);
+  } else if (p.rows <= kLocalRouteMax) {
     // every workgroup routes the step itself, reading the router's part sums as they land:
-    // no routing hand-off; the A hand-off (the x codes) is awaited before the gate_up
-    route_all<C>(p, sm.r, un.ids, un.wts, un.rows_of, b);
+    // no routing hand-off; the A hand-off (the x codes) is awaited before the gate_up. The
+    // last workgroup publishes the routing (the workspace copies, then its flag at B) for
+    // the workgroups that ran the shared gate_up meanwhile
+    route_all<C>(p, sm.r, un.ids, un.wts, un.rows_of, b == nwg - 1);
+    if (nsw > 0 && b == nwg - 1) arrive(p, kCtlB);
     TL(kTlRouted);
     build_union<C>(p, un, true);
     TL(kTlUnion);
@@ -3448,7 +3560,7 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
     build_union<C>(p, un, false);
     TL(kTlUnion);
   }
-  stage_c<C>(p, un, sm.g, b, nwg);
+  stage_c<C>(p, un, sm.g, b, nwg, nsw);
   TL(kTlGateUp);
   arrive(p, kCtlC);
   TL(kTlCArrived);
@@ -3456,9 +3568,18 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   if (C::SHUF || down_on_mfma<C>(p.rows, p.mfma_down)) {
     // the shared down first, inside the Q hand-off, up to kSharedFirstRows rows (above, its
     // rows' quantize outlasts the hand-off)
-    if (gq && C::SF && p.rows <= kSharedFirstRows) wait_then_d<C, true, true, C::SF>(p, un, sm.d, b, nwg);
-    else if (gq) wait_then_d<C, true, true>(p, un, sm.d, b, nwg);
-    else wait_then_d<C, true, false>(p, un, sm.d, b, nwg);
+    if (nsw > 0 && kPreShared && !gq) {
+      // the shared down before the C wait (the shared intermediate was stored in the routing
+      // window). (With stage Q, from 8 rows, it cost 1-4 us there against after the routed
+      // down or inside the Q hand-off: measured)
+      wait_then_d<C, true, false, false, true>(p, un, sm.d, b, nwg, nsw);
+    } else if (gq && C::SF && p.rows <= kSharedFirstRows) {
+      wait_then_d<C, true, true, C::SF>(p, un, sm.d, b, nwg);
+    } else if (gq) {
+      wait_then_d<C, true, true>(p, un, sm.d, b, nwg);
+    } else {
+      wait_then_d<C, true, false>(p, un, sm.d, b, nwg);
+    }
   } else if constexpr (!C::SHUF) {
     if (gq) wait_then_d<C, false, true>(p, un, sm.d, b, nwg);
     else wait_then_d<C, false, false>(p, un, sm.d, b, nwg);

@@ -64,14 +64,17 @@ def test_deadline_gives_up_then_clear_restores(workload, rows):
         ("cfg2_tp4_fp8", 24, 3, 17),  # the routing hand-off (above 16 rows)
         ("cfg3_tp4_mxfp4", 16, 6, 200),  # stage Q's hand-off
         ("cfg3_tp4_mxfp4", 1, 2, 0),  # the polled router part sums and the x codes
+        ("cfg3_tp4_mxfp4", 1, 3, 10),  # the published routing (a workgroup of the early shared gate_up)
+        ("cfg2_tp4_fp8", 4, 3, 200),  # the shared intermediate, before the shared down
         ("cfg5_tp2_mxfp4_norm", 8, 1, 255),  # the RMSNorm's hand-off
     ],
 )
 def test_fault_injection_stalls_one_wait(workload, rows, stage, wg):
     """A wait stalled by the test fault injection (one workgroup, one stage: the reference's
-    SGLANG_AMD_MONO_FAULT_INJECT, common/guard.py:69-89) runs to its deadline: the first error
-    recorded is that wait's (its stage and workgroup, the fault word set), the launch ends, and
-    clear_errors restores a launch bit-identical to a fresh workspace's."""
+    SGLANG_AMD_MONO_FAULT_INJECT, common/guard.py:69-89) runs to its deadline: the error words
+    name that wait (its stage and workgroup, the fault word set; the waits it holds up may reach
+    their deadlines first), the launch ends, and clear_errors restores a launch bit-identical to
+    a fresh workspace's."""
     from test_gpu_parity import _case, _runner
 
     from sgl_amd_mono.moe import _lib
