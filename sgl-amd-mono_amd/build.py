@@ -4,6 +4,7 @@
     python sgl-amd-mono_amd/build.py --check     # and print the kernels' register / LDS use
     python sgl-amd-mono_amd/build.py --timeline  # the diagnostic build with phase stamps
                                                  # (libmkmoe_tl.so; bench.py --timeline)
+    python sgl-amd-mono_amd/build.py --lds       # the LDS budget per shape (a host program)
 
 The library holds the kernels and the C ABI of ``include/mkmoe.h``. It is built
 in place (not installed) so that the same file runs wherever the tree is copied.
@@ -85,9 +86,28 @@ def build(check: bool = False, verbose: bool = False, timeline: bool = False) ->
     return out
 
 
+def lds_budget() -> str:
+    """The persistent launch's LDS budget per compiled shape (a markdown table): a host program
+    built from csrc/mkmoe_lds.hip, which sizes each stage's member of the LDS union."""
+    with tempfile.TemporaryDirectory(prefix="mkmoe_lds_") as tmpd:
+        exe = Path(tmpd) / "mkmoe_lds"
+        res = _run([HIPCC, *FLAGS, str(CSRC / "mkmoe_lds.hip"), "-o", str(exe)])
+        if res.returncode != 0:
+            sys.stderr.write(res.stdout + res.stderr)
+            raise RuntimeError(f"mkmoe_lds build failed ({res.returncode})")
+        res = _run([str(exe)])
+        if res.returncode != 0:
+            raise RuntimeError(f"mkmoe_lds failed ({res.returncode})")
+        return res.stdout
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--check", action="store_true")
     ap.add_argument("--timeline", action="store_true")
+    ap.add_argument("--lds", action="store_true", help="print the LDS budget per shape (no library build)")
     args = ap.parse_args()
-    print(build(check=args.check, verbose=True, timeline=args.timeline))
+    if args.lds:
+        print(lds_budget(), end="")
+    else:
+        print(build(check=args.check, verbose=True, timeline=args.timeline))
