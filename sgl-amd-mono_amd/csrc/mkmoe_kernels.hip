@@ -2971,43 +2971,55 @@ constexpr bool kEarlyShared = MKMOE_EARLY_SHARED != 0;
 #endif
 // ... and then every workgroup's shared down before the C wait
 constexpr bool kPreShared = MKMOE_PRE_SHARED != 0;
-// workgroups [0, n) that run the shared expert's gate_up in the routing window, a unit each
-// (half of the grid at most): launches whose every workgroup would route the step itself,
-// with the gate_up on MFMA. Its weights stream while the other workgroups route, and the
-// routed units alone are dealt afterwards (0: none, the shared units are dealt with them)
+// The shared expert's gate_up units run while the step is routed, by workgroups [w0, w0 + n)
+// that route nothing meanwhile, with the gate_up on MFMA: its weights stream during the
+// routing, and the rest of the gate_up is dealt afterwards.
+//   - up to 16 rows (every other workgroup routes the step itself): workgroups [0, n), half of
+//     the grid at most, take all k of its units between them (a unit each where k <= n);
+//   - above (workgroups [0, R) route a row each, then the B hand-off): workgroups [R, R + n)
+//     take its first k = n units, one each; the others join the routed units' deal.
+// n = 0: none (the shared units are dealt with the routed ones).
+struct EarlyShared {
+  int w0, n, k;
+};
 template <class C>
-__device__ __forceinline__ int early_shared_wgs(const Params& p, int nwg) {
-  if (!kEarlyShared || p.rows > kLocalRouteMax || !gate_on_mfma<C>(p.rows, p.mfma_gate)) return 0;
-  return min(GuDeal<C>::shared_units(p.rows), nwg / 2);
+__device__ __forceinline__ EarlyShared early_shared(const Params& p, int nwg) {
+  if (!kEarlyShared || !gate_on_mfma<C>(p.rows, p.mfma_gate)) return {0, 0, 0};
+  const int n_sh = GuDeal<C>::shared_units(p.rows);
+  if (p.rows <= kLocalRouteMax) return {0, min(n_sh, nwg / 2), n_sh};
+  const int n = min(n_sh, nwg - p.rows);
+  return {p.rows, n, n};
 }
 
 // the same on MFMA: the shared expert's (16-row group, column block) units, then the routed
-// ones, dealt evenly as one list; nsw > 0: workgroups [0, nsw) ran the shared units already
-// (early_shared_wgs), and the routed units are dealt over the other workgroups where their
+// ones, dealt evenly as one list. es.n > 0: the list's first es.k shared units ran in the
+// routing window (early_shared), and the rest is dealt over the other workgroups where their
 // largest share stays the same, else over all
 template <class C>
 __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un, GuSmem<C>& sm, int b, int nwg,
-                                             int nsw = 0) {
+                                             EarlyShared es = {0, 0, 0}) {
   const auto rs = ws_rsrc(p);
   const int n_sh = GuDeal<C>::shared_units(p.rows);
   const int n_rt = un.ntg_r * (C::IR / GuTile<C, C::FMT>::NC);
   constexpr bool HALF = GuDeal<C>::HALF;
   constexpr int HU = GuDeal<C>::HU;
+  const int e0 = HU * es.k;                     // deal steps done in the window
+  const int n = HU * (n_sh + n_rt) - e0;        // and the rest
   int lo, hi;
-  if (nsw > 0) {
-    const int n = HU * n_rt, m = (n + nwg - 1) / nwg;
-    if (n <= m * (nwg - nsw)) {
-      if (b < nsw) lo = hi = 0;
-      else even_share(n, b - nsw, nwg - nsw, lo, hi);
+  if (es.n > 0) {
+    const int m = (n + nwg - 1) / nwg;
+    if (n <= m * (nwg - es.n)) {
+      if (b >= es.w0 && b < es.w0 + es.n) lo = hi = 0;
+      else even_share(n, b < es.w0 ? b : b - es.n, nwg - es.n, lo, hi);
     } else {
       even_share(n, b, nwg, lo, hi);
     }
-    lo += HU * n_sh;
-    hi += HU * n_sh;
   } else {
-    even_share(HU * (n_sh + n_rt), b, nwg, lo, hi);
-    gate_up_shared<C>(p, sm, lo, min(hi, HU * n_sh), [] {});
+    even_share(n, b, nwg, lo, hi);
   }
+  lo += e0;
+  hi += e0;
+  gate_up_shared<C>(p, sm, lo, min(hi, HU * n_sh), [] {});
   auto first = [&](int tg) {
     const int slot = un.tg_slot[tg];
     return un.slot_start[slot] + (tg - un.tg_start[slot]) * kMfmaPicks;
@@ -3037,12 +3049,12 @@ __device__ __forceinline__ void gate_up_mfma(const Params& p, const Union<C>& un
       });
 }
 
-// nsw: workgroups [0, nsw) ran the shared expert's units in the routing window (MFMA)
+// es: the shared expert's units that ran in the routing window (MFMA)
 template <class C>
 __device__ __forceinline__ void stage_c(const Params& p, const Union<C>& un, GuSmem<C>& sm, int b, int nwg,
-                                        int nsw = 0) {
-  if constexpr (C::SHUF) gate_up_mfma<C>(p, un, sm, b, nwg, nsw);  // (the VALU GEMVs read row-major rows)
-  else if (gate_on_mfma<C>(p.rows, p.mfma_gate)) gate_up_mfma<C>(p, un, sm, b, nwg, nsw);
+                                        EarlyShared es = {0, 0, 0}) {
+  if constexpr (C::SHUF) gate_up_mfma<C>(p, un, sm, b, nwg, es);  // (the VALU GEMVs read row-major rows)
+  else if (gate_on_mfma<C>(p.rows, p.mfma_gate)) gate_up_mfma<C>(p, un, sm, b, nwg, es);
   else gate_up_valu<C>(p, un, sm.x, b, nwg);
 }
 
@@ -3522,19 +3534,27 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   TL(kTlADone);
   arrive(p, kCtlA);
   TL(kTlAArrived);
-  const int nsw = early_shared_wgs<C>(p, nwg);
-  if (b < nsw) {
+  const EarlyShared es = early_shared<C>(p, nwg);
+  const int nsw = es.n;
+  if (b >= es.w0 && b < es.w0 + es.n) {
     // the shared expert's gate_up while the others route: its weights are requested before
-    // the A hand-off (the x codes) is awaited; then its flag at B (the shared intermediate
-    // stored), and the routing from the workgroup that publishes it
+    // the A hand-off (the x codes) is awaited. Up to 16 rows: then its flag at B (the shared
+    // intermediate stored), and the routing from the workgroup that publishes it; above: its
+    // flag at B first (no row to route), and the routing hand-off after the units
     int lo, hi;
-    even_share(GuDeal<C>::HU * GuDeal<C>::shared_units(p.rows), b, nsw, lo, hi);
+    even_share(GuDeal<C>::HU * es.k, b - es.w0, es.n, lo, hi);
+    const bool local = p.rows <= kLocalRouteMax;
+    if (!local) arrive(p, kCtlB);
     gate_up_shared<C>(p, sm.g, lo, hi, [&] {
       await_all(p, kCtlA, nwg, kStageA);
       TL(kTlAAwaited);
     });
-    arrive(p, kCtlB);
-    await_one(p, kCtlB, nwg - 1, kStageB);
+    if (local) {
+      arrive(p, kCtlB);
+      await_one(p, kCtlB, nwg - 1, kStageB);
+    } else {
+      await_all(p, kCtlB, nwg, kStageB);
+    }
     TL(kTlRouted);
     build_union<C>(p, un, false);
     TL(kTlUnion);
@@ -3560,7 +3580,7 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
     build_union<C>(p, un, false);
     TL(kTlUnion);
   }
-  stage_c<C>(p, un, sm.g, b, nwg, nsw);
+  stage_c<C>(p, un, sm.g, b, nwg, es);
   TL(kTlGateUp);
   arrive(p, kCtlC);
   TL(kTlCArrived);
