@@ -787,6 +787,18 @@ __device__ __forceinline__ void stage_a(const Params& p, RouterSmem<C>& sm, int 
   const int lane = threadIdx.x & 63, wave = (int)(threadIdx.x >> 6);
   constexpr int EB = (C::E + kWaves - 1) / kWaves;
   constexpr int n_router = C::P * EB;
+  if (n_router < nwg && n_router + p.rows > nwg) {
+    // more units than workgroups: a router unit each on workgroups [0, n_router) and the rows'
+    // quantize on the others, several rows each (a router unit of many rows outlasts several
+    // rows' quantize; dealt in turn, the first workgroups would run one of each)
+    if (b < n_router) {
+      router_unit<C>(p, sm, b % C::P, b / C::P, lane, wave);
+    } else {
+      for (int r = b - n_router; r < p.rows; r += nwg - n_router)
+        for (int c = wave; c < C::CH512; c += kWaves) quant_unit<C>(p, r, c, lane);
+    }
+    return;
+  }
   const int n = n_router + p.rows;
   for (int u = b; u < n; u += nwg) {
     if (u < n_router) {
