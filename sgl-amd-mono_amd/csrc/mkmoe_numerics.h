@@ -133,7 +133,7 @@ MKMOE_HD inline float sigmoid_exact(float x) {
   d = d > kSigClamp ? kSigClamp : (d < -kSigClamp ? -kSigClamp : d);
   double t = exp_nonpos(-fabs(d));
   double den = 1.0 + t;
-  double s = d >= 0.0 ? 1.0 / den : t / den;
+  double s = (d >= 0.0 ? 1.0 : t) / den;  // (one division: the numerator selected first)
   return (float)s;
 }
 
