@@ -861,13 +861,29 @@ __device__ __forceinline__ float segment_max(float v) {
 template <class C, int NJ, int MJ, int P>
 __device__ __forceinline__ void sigmoids(const float (&part)[MJ][P], float (&sg)[MJ]) {
 #pragma clang fp contract(off)
+  float logit[NJ], out[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    float logit = 0.0f;
+    logit[j] = 0.0f;
 #pragma unroll
-    for (int q = 0; q < P; ++q) logit = logit + part[j][q];
-    sg[j] = C::SCORE == kScoreSqrtSoftplus ? sqrt_softplus_exact(logit) : sigmoid_exact(logit);
+    for (int q = 0; q < P; ++q) logit[j] = logit[j] + part[j][q];
   }
+  // the scores step by step together, four at a time (each value's operations in the scalar
+  // order; wider, the chains' registers crowd the launch's)
+  constexpr int W = NJ < 4 ? NJ : 4;
+#pragma unroll
+  for (int j0 = 0; j0 < NJ; j0 += W) {
+    float xv[W], ov[W];
+#pragma unroll
+    for (int i = 0; i < W; ++i) xv[i] = j0 + i < NJ ? logit[j0 + i] : 0.0f;
+    if constexpr (C::SCORE == kScoreSqrtSoftplus) sqrt_softplus_exact_n<W>(xv, ov);
+    else sigmoid_exact_n<W>(xv, ov);
+#pragma unroll
+    for (int i = 0; i < W; ++i)
+      if (j0 + i < NJ) out[j0 + i] = ov[i];
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) sg[j] = out[j];
 }
 
 template <class C, bool POLL = false>
@@ -2399,6 +2415,7 @@ __device__ __forceinline__ void build_union(const Params& p, Union<C>& un, bool 
     __syncthreads();
     if (t < npk) {
       my_e = min(max((int)dld32(rs, p.off[6] + t * 4), 0), C::E - 1);
+      un.ids[t] = my_e;
       un.wts[t] = u2f(dld32(rs, p.off[7] + t * 4));
       const int r = t / C::K;
       atomicOr(&un.rows_of[my_e][r >> 5], 1u << (r & 31));
@@ -3087,24 +3104,13 @@ struct DownSmem {
   uint8_t wslot[kWaves][DownTile<C::FMT, C::I, C::DNA>::SLOT] __attribute__((aligned(16)));
 };
 
-// the slots holding picks [pb0, pb0 + pbn) of the step (picks are stored slot by slot): slot
-// starts ascend, so s_lo is the count of starts <= pb0, less one, and s_hi the count of starts
-// below pb0 + pbn, less one; each wave counts 64 starts a step with a ballot (a dependent scan
-// of the starts, one LDS read at a time, took about 2.5 us a call at 8 rows)
+// the slots holding picks [pb0, pb0 + pbn) of the step: picks are stored slot by slot, so they
+// are the slots of the batch's first and last picks (a scan of the slot starts, one dependent
+// LDS read a slot, took about 2.5 us a call at 8 rows)
 template <class C>
 __device__ __forceinline__ void batch_slots(const Union<C>& un, int pb0, int pbn, int& s_lo, int& s_hi) {
-  const int lane = threadIdx.x & 63, n = un.n;
-  int n_le = 0, n_lt = 0;
-  for (int base = 0; base < n; base += 64) {
-    const int i = base + lane;
-    const int st = i < n ? un.slot_start[i] : 0x7fffffff;
-    const uint64_t le = __ballot(st <= pb0), lt = __ballot(st < pb0 + pbn);
-    n_le += __popcll(le);
-    n_lt += __popcll(lt);
-    if (lt != ~0ull) break;  // (ascending: every later start is at least pb0 + pbn)
-  }
-  s_lo = n_le - 1;
-  s_hi = n_lt - 1;
+  s_lo = __builtin_amdgcn_readfirstlane(un.slot_of[un.ids[un.picks[pb0]]]);
+  s_hi = __builtin_amdgcn_readfirstlane(un.slot_of[un.ids[un.picks[pb0 + pbn - 1]]]);
 }
 
 // the routed down GEMVs of tile rows [h0, h0 + hn) for every pick, into sm.contrib

@@ -100,86 +100,137 @@ MKMOE_HD inline float group_scale(float amax) {
 
 // exp(y) for y <= 0 (fp64, IEEE steps only): n = rint(y / ln 2), r = y - n ln 2 (two-part
 // ln 2), the degree-13 Taylor polynomial of exp(r) in Estrin's order (pairs c_2k + c_2k+1 r,
-// then r^2, r^4 and r^8 combine them: 8 dependent steps instead of Horner's 26), times 2^n
-MKMOE_HD inline double exp_nonpos(double y) {
+// then r^2, r^4 and r^8 combine them: 8 dependent steps instead of Horner's 26), times 2^n.
+// The N-wide forms below run N values step by step together (each value's operations are the
+// scalar form's, in its order), so that their dependent chains overlap: a compiler left to
+// itself ran a thread's chains one after another
+template <int N>
+MKMOE_HD inline void exp_nonpos_n(const double (&y)[N], double (&out)[N]) {
 #pragma clang fp contract(off)
   const double kInvLn2 = 1.4426950408889634;
   const double kLn2Hi = 0x1.62e42fee00000p-1;
   const double kLn2Lo = 0x1.a39ef35793c76p-33;
-  double n = rint(y * kInvLn2);
-  double r = (y - n * kLn2Hi) - n * kLn2Lo;
-  const double r2 = r * r;
-  const double r4 = r2 * r2;
-  const double r8 = r4 * r4;
-  const double q0 = 1.0 + 1.0 * r;
-  const double q1 = 1.0 / 2.0 + (1.0 / 6.0) * r;
-  const double q2 = 1.0 / 24.0 + (1.0 / 120.0) * r;
-  const double q3 = 1.0 / 720.0 + (1.0 / 5040.0) * r;
-  const double q4 = 1.0 / 40320.0 + (1.0 / 362880.0) * r;
-  const double q5 = 1.0 / 3628800.0 + (1.0 / 39916800.0) * r;
-  const double q6 = 1.0 / 479001600.0 + (1.0 / 6227020800.0) * r;
-  const double s0 = q0 + q1 * r2;
-  const double s1 = q2 + q3 * r2;
-  const double s2 = q4 + q5 * r2;
-  const double u0 = s0 + s1 * r4;
-  const double u1 = s2 + q6 * r4;
-  const double pl = u0 + u1 * r8;
-  return ldexp(pl, (int)n);
+  // (the pairs are formed where they are used, so that few values live at once)
+  double n[N], r[N], r2[N], r4[N], s0[N], s1[N], s2[N], u0[N], u1[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) n[i] = rint(y[i] * kInvLn2);
+#pragma unroll
+  for (int i = 0; i < N; ++i) r[i] = (y[i] - n[i] * kLn2Hi) - n[i] * kLn2Lo;
+#pragma unroll
+  for (int i = 0; i < N; ++i) r2[i] = r[i] * r[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) r4[i] = r2[i] * r2[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) s0[i] = (1.0 + 1.0 * r[i]) + (1.0 / 2.0 + (1.0 / 6.0) * r[i]) * r2[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) s1[i] = (1.0 / 24.0 + (1.0 / 120.0) * r[i]) + (1.0 / 720.0 + (1.0 / 5040.0) * r[i]) * r2[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    s2[i] = (1.0 / 40320.0 + (1.0 / 362880.0) * r[i]) + (1.0 / 3628800.0 + (1.0 / 39916800.0) * r[i]) * r2[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) u0[i] = s0[i] + s1[i] * r4[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) u1[i] = s2[i] + (1.0 / 479001600.0 + (1.0 / 6227020800.0) * r[i]) * r4[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = ldexp(u0[i] + u1[i] * (r4[i] * r4[i]), (int)n[i]);
+}
+MKMOE_HD inline double exp_nonpos(double y) {
+  const double yv[1] = {y};
+  double o[1];
+  exp_nonpos_n<1>(yv, o);
+  return o[0];
 }
 
-MKMOE_HD inline float sigmoid_exact(float x) {
+// the sigmoid in fp64, rounded to fp32 once: the input clamped to [-60, 60], t = exp(-|d|),
+// then 1 / (1 + t) or t / (1 + t) by the sign (one division, the numerator selected first)
+template <int N>
+MKMOE_HD inline void sigmoid_exact_n(const float (&x)[N], float (&out)[N]) {
 #pragma clang fp contract(off)
-  double d = (double)x;
-  d = d > kSigClamp ? kSigClamp : (d < -kSigClamp ? -kSigClamp : d);
-  double t = exp_nonpos(-fabs(d));
-  double den = 1.0 + t;
-  double s = (d >= 0.0 ? 1.0 : t) / den;  // (one division: the numerator selected first)
-  return (float)s;
+  double d[N], y[N], t[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    d[i] = (double)x[i];
+    d[i] = d[i] > kSigClamp ? kSigClamp : (d[i] < -kSigClamp ? -kSigClamp : d[i]);
+    y[i] = -fabs(d[i]);
+  }
+  exp_nonpos_n<N>(y, t);
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = (float)((d[i] >= 0.0 ? 1.0 : t[i]) / (1.0 + t[i]));
+}
+MKMOE_HD inline float sigmoid_exact(float x) {
+  const float xv[1] = {x};
+  float o[1];
+  sigmoid_exact_n<1>(xv, o);
+  return o[0];
 }
 
 // log(1 + t) for t in [0, 1] (fp64, IEEE steps only): t past sqrt(2) - 1 reduced to
 // s = (t - 1) / 2 (log(1 + t) = ln 2 + log(1 + s)), then 2 atanh(s / (2 + s)) by its series,
 // terms z^(2k+1) / (2k+1) for k = 0 .. 11, in Horner's order
-MKMOE_HD inline double log1p_01(double t) {
+template <int N>
+MKMOE_HD inline void log1p_01_n(const double (&t)[N], double (&out)[N]) {
 #pragma clang fp contract(off)
   const double kSqrt2M1 = 0.41421356237309503;
   const double kLn2 = 0.6931471805599453;
-  const bool big = t > kSqrt2M1;
-  const double s = big ? (t - 1.0) * 0.5 : t;
-  const double z = s / (2.0 + s);
-  const double z2 = z * z;
-  double p = 1.0 / 23.0;
-  p = p * z2 + 1.0 / 21.0;
-  p = p * z2 + 1.0 / 19.0;
-  p = p * z2 + 1.0 / 17.0;
-  p = p * z2 + 1.0 / 15.0;
-  p = p * z2 + 1.0 / 13.0;
-  p = p * z2 + 1.0 / 11.0;
-  p = p * z2 + 1.0 / 9.0;
-  p = p * z2 + 1.0 / 7.0;
-  p = p * z2 + 1.0 / 5.0;
-  p = p * z2 + 1.0 / 3.0;
-  p = p * z2 + 1.0;
-  const double lg = 2.0 * (z * p);
-  return big ? kLn2 + lg : lg;
+  double z[N], z2[N], p[N];
+  bool big[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    big[i] = t[i] > kSqrt2M1;
+    const double s = big[i] ? (t[i] - 1.0) * 0.5 : t[i];
+    z[i] = s / (2.0 + s);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    z2[i] = z[i] * z[i];
+    p[i] = 1.0 / 23.0;
+  }
+  const double c[11] = {1.0 / 21.0, 1.0 / 19.0, 1.0 / 17.0, 1.0 / 15.0, 1.0 / 13.0, 1.0 / 11.0,
+                        1.0 / 9.0,  1.0 / 7.0,  1.0 / 5.0,  1.0 / 3.0,  1.0};
+#pragma unroll
+  for (int k = 0; k < 11; ++k)
+#pragma unroll
+    for (int i = 0; i < N; ++i) p[i] = p[i] * z2[i] + c[k];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const double lg = 2.0 * (z[i] * p[i]);
+    out[i] = big[i] ? kLn2 + lg : lg;
+  }
+}
+MKMOE_HD inline double log1p_01(double t) {
+  const double tv[1] = {t};
+  double o[1];
+  log1p_01_n<1>(tv, o);
+  return o[0];
 }
 
 // V4.1's score sqrt(softplus(x)): softplus in fp64 (x itself past 20, else
 // max(x, 0) + log1p(exp(-|x|)), the input floored at -200), rounded to fp32, then the
-// correctly rounded fp32 square root; NaN stays NaN
-MKMOE_HD inline float sqrt_softplus_exact(float x) {
+// correctly rounded fp32 square root; NaN stays NaN (the input itself)
+template <int N>
+MKMOE_HD inline void sqrt_softplus_exact_n(const float (&x)[N], float (&out)[N]) {
 #pragma clang fp contract(off)
-  if (x != x) return x;
-  double d = (double)x;
-  d = d < -200.0 ? -200.0 : d;
-  double sp;
-  if (d > 20.0) {
-    sp = d;
-  } else {
-    const double t = exp_nonpos(-fabs(d));
-    sp = (d > 0.0 ? d : 0.0) + log1p_01(t);
+  double d[N], y[N], t[N], l[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    d[i] = (double)x[i];
+    d[i] = d[i] < -200.0 ? -200.0 : d[i];
+    // (past 20, and for NaN, the exp is taken of a value whose result is never used)
+    y[i] = d[i] > 20.0 || d[i] != d[i] ? -20.0 : -fabs(d[i]);
   }
-  return sqrtf((float)sp);
+  exp_nonpos_n<N>(y, t);
+  log1p_01_n<N>(t, l);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const double sp = d[i] > 20.0 ? d[i] : (d[i] > 0.0 ? d[i] : 0.0) + l[i];
+    out[i] = x[i] != x[i] ? x[i] : sqrtf((float)sp);
+  }
+}
+MKMOE_HD inline float sqrt_softplus_exact(float x) {
+  const float xv[1] = {x};
+  float o[1];
+  sqrt_softplus_exact_n<1>(xv, o);
+  return o[0];
 }
 
 // a > b in the selection order: larger value, or equal value and lower index
