@@ -460,33 +460,32 @@ def timeline(runner, rb: RowsBench, reps: int = 8) -> dict:
     total, st, t0 = runs[len(runs) // 2]
     tick_us = 0.01  # s_memrealtime: 100 MHz
     out = {"total_us": round(total * tick_us, 2), "workgroups": int(st.shape[0]), "phases": {}}
+    counts = ("gate_up units", "down units")
+    ends = ("gate_up first unit", "down first unit")
+    cols = []  # per phase: every workgroup's value, None where it does not stamp that phase
     for k, name in enumerate(_lib.TL_NAMES):
         col = st[:, k]
-        counts = ("gate_up units", "down units")
-        ends = ("gate_up first unit", "down first unit")
         if name.startswith(("gate_up ", "down ")) and name not in counts + ends:
             v = col * tick_us  # time a workgroup's wave 0 spent in that part of its loop
         elif name in counts:
             v = col
         else:
-            v = (col - t0) * tick_us
-        out["phases"][name] = {
-            "median": round(float(v.median()), 2),
-            "min": round(float(v.min()), 2),
-            "max": round(float(v.max()), 2),
+            # a phase end: a workgroup whose path skips the phase (the early shared expert
+            # workgroups do not route the step, for one) leaves its stamp at zero
+            v = torch.where(col != 0, (col - t0) * tick_us, torch.full_like(col, float("nan")))
+        cols.append(v)
+        have = v[~torch.isnan(v)]
+        out["phases"][name] = None if have.numel() == 0 else {
+            "median": round(float(have.median()), 2),
+            "min": round(float(have.min()), 2),
+            "max": round(float(have.max()), 2),
+            "workgroups": int(have.numel()),
         }
     # every workgroup's stamps (µs from the first stamp; the loop parts' sums in µs, the counts
-    # as they are), in workgroup order
-    cols = []
-    for k, name in enumerate(_lib.TL_NAMES):
-        col = st[:, k]
-        if name in ("gate_up units", "down units"):
-            cols.append(col)
-        elif name.startswith(("gate_up ", "down ")) and name not in ("gate_up first unit", "down first unit"):
-            cols.append(col * tick_us)
-        else:
-            cols.append((col - t0) * tick_us)
-    out["workgroup_stamps"] = [[round(float(c[i]), 2) for c in cols] for i in range(st.shape[0])]
+    # as they are; None for a phase it skips), in workgroup order
+    out["workgroup_stamps"] = [
+        [None if torch.isnan(c[i]) else round(float(c[i]), 2) for c in cols] for i in range(st.shape[0])
+    ]
     return out
 
 
