@@ -3369,7 +3369,11 @@ __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, D
   __syncthreads();
   TL(kTlDShared);
   // ---- combine: top-k order, bf16 at every add, then + the shared expert's bf16 result
-  for (int idx = tid; idx < R * hn; idx += kThreads) {
+  // (the thread index passes an empty asm, so that the loop's LDS addresses are formed here
+  // rather than hoisted to the kernel's start and held, or spilled, across the stages)
+  int c0 = tid;
+  asm volatile("" : "+v"(c0));
+  for (int idx = c0; idx < R * hn; idx += kThreads) {
     const int t = idx / hn, hl = idx % hn;
     float routed = 0.0f;
 #pragma unroll
