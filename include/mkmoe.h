@@ -179,7 +179,8 @@ typedef struct mkmoe_options {
    * awaited before the shared down), 4 gate_up, 6 quantize) ignores what it waits for and runs
    * to the deadline, then records the error words with MKMOE_ERRW_FAULT set and the launch
    * goes on, as after any deadline. A stage the launch does not wait at (6 below the shape's
-   * stage-Q rows, 1 without the norm, 3 where the gate_up runs on the VALU up to 16 rows) and
+   * stage-Q rows, 1 without the norm or up to 16 rows, where every workgroup norms the rows
+   * itself, 3 where the gate_up runs on the VALU up to 16 rows) and
    * the staged launches (no waits) stall nothing. The faulted launch's output is not valid;
    * mkmoe_clear_errors restores the workspace. */
   int32_t fault_stage;
@@ -235,7 +236,8 @@ int mkmoe_read_errors(const void* ws, int32_t* words, int32_t n, void* stream);
 int mkmoe_clear_errors(const mkmoe_shape* shape, void* ws, size_t ws_bytes, void* stream);
 
 /* Byte offset and size of a workspace region, for tests that read
- * intermediate results: 0 x normed, 1 x codes (routed rule), 2 x scales,
+ * intermediate results: 0 x normed (by the norm stage, or up to 16 rows by the quantize
+ * of stage A, which norms the rows as it reads them), 1 x codes (routed rule), 2 x scales,
  * 3 x codes (shared rule), 4 x scales (shared rule), 5 router part sums
  * fp32 [rows][parts][E], 6 ids int32 [rows][topk], 7 weights fp32
  * [rows][topk], 8 shared intermediate bf16 [rows][S], 9 routed intermediate

@@ -606,17 +606,20 @@ __device__ __forceinline__ int wave_index() { return __builtin_amdgcn_readfirstl
 __device__ __forceinline__ int wave_slot(int b, int nwg) { return b + nwg * wave_index(); }
 
 // ---------------------------------------------------------------- stage N: RMSNorm
+// rows up to which every workgroup normalizes the rows itself as stage A reads them (each
+// row's 1 / rms computed by one wave of every workgroup that needs it, in the order below:
+// the same bits everywhere), so that no hand-off precedes stage A; above, stage N writes the
+// normed rows and a hand-off follows
+constexpr int kLocalNormMax = 16;
+
+// 1 / rms of a row held as v[c] = the lane's 8 columns of 512-column chunk c (every lane):
+// lane l sums the squares of its columns chunk by chunk in order, then the wave's sum
 template <class C>
-__device__ __forceinline__ void norm_row(const Params& p, int r, int lane) {
+__device__ __forceinline__ float row_rstd(const Params& p, const u32x4 (&v)[C::CH512]) {
 #pragma clang fp contract(off)
-  constexpr int CH = C::CH512;
-  const uint16_t* x = p.x + (size_t)r * C::H;
-  u32x4 v[CH];
-#pragma unroll
-  for (int c = 0; c < CH; ++c) v[c] = ld16(x + c * 512 + lane * 8);
   float acc = 0.0f;
 #pragma unroll
-  for (int c = 0; c < CH; ++c) {
+  for (int c = 0; c < C::CH512; ++c) {
     const uint32_t w4[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -626,24 +629,54 @@ __device__ __forceinline__ void norm_row(const Params& p, int r, int lane) {
   }
   float ss = wave_sum(acc);
   float mean = ss / (float)C::H;
-  float rstd = 1.0f / sqrtf(mean + p.eps);
+  return 1.0f / sqrtf(mean + p.eps);
+}
+template <class C>
+__device__ __forceinline__ void row_load(const Params& p, int r, int lane, u32x4 (&v)[C::CH512]) {
+  const uint16_t* x = p.x + (size_t)r * C::H;
+#pragma unroll
+  for (int c = 0; c < C::CH512; ++c) v[c] = ld16(x + c * 512 + lane * 8);
+}
+
+// 8 normed bf16 from 8 of x and of the norm weight: bf16((x * rstd) * w)
+__device__ __forceinline__ u32x4 norm8(u32x4 xv, u32x4 nw, float rstd) {
+#pragma clang fp contract(off)
+  const uint32_t w4[4] = {xv.x, xv.y, xv.z, xv.w};
+  const uint32_t n4[4] = {nw.x, nw.y, nw.z, nw.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float a = bf_lo(w4[q]) * rstd, b = bf_hi(w4[q]) * rstd;
+    a = a * bf_lo(n4[q]);
+    b = b * bf_hi(n4[q]);
+    o[q] = (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+  }
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
+
+template <class C>
+__device__ __forceinline__ void norm_row(const Params& p, int r, int lane) {
+  u32x4 v[C::CH512];
+  row_load<C>(p, r, lane, v);
+  const float rstd = row_rstd<C>(p, v);
   const auto rs = ws_rsrc(p);
   const uint32_t base = p.off[0] + (uint32_t)r * C::H * 2;
 #pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const uint32_t w4[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
-    u32x4 nw = ld16(p.norm_w + c * 512 + lane * 8);
-    const uint32_t n4[4] = {nw.x, nw.y, nw.z, nw.w};
-    uint32_t o[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float a = bf_lo(w4[q]) * rstd, b = bf_hi(w4[q]) * rstd;
-      a = a * bf_lo(n4[q]);
-      b = b * bf_hi(n4[q]);
-      o[q] = (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
-    }
-    dst128(rs, base + (c * 512 + lane * 8) * 2, u32x4{o[0], o[1], o[2], o[3]});
+  for (int c = 0; c < C::CH512; ++c)
+    dst128(rs, base + (c * 512 + lane * 8) * 2, norm8(v[c], ld16(p.norm_w + c * 512 + lane * 8), rstd));
+}
+
+// every row's 1 / rms into rstd[] (a wave a row), for the rows normed locally
+template <class C>
+__device__ __forceinline__ void local_rstd(const Params& p, float* rstd) {
+  const int lane = threadIdx.x & 63;
+  for (int r = wave_index(); r < p.rows; r += kWaves) {
+    u32x4 v[C::CH512];
+    row_load<C>(p, r, lane, v);
+    const float s = row_rstd<C>(p, v);
+    if (lane == 0) rstd[r] = s;
   }
+  __syncthreads();
 }
 
 template <class C>
@@ -652,10 +685,15 @@ __device__ __forceinline__ void stage_norm(const Params& p, int b, int nwg) {
   for (int r = gw; r < p.rows; r += nwg * kWaves) norm_row<C>(p, r, lane);
 }
 
-// 8 bf16 of row r from element col: the normed rows (sc1) or the input
+// 8 bf16 of row r from element col: the normed rows (sc1: written by stage N, or normed
+// here with the row's 1 / rms where the rows are normed locally, rstd non-null) or the input
 template <class C>
-__device__ __forceinline__ u32x4 x_load(const Params& p, __amdgpu_buffer_rsrc_t rs, int r, int col) {
-  if constexpr (C::NORM) return dld128(rs, p.off[0] + ((uint32_t)r * C::H + col) * 2);
+__device__ __forceinline__ u32x4 x_load(const Params& p, __amdgpu_buffer_rsrc_t rs, int r, int col,
+                                        const float* rstd = nullptr) {
+  if constexpr (C::NORM) {
+    if (rstd) return norm8(ld16(p.x + (size_t)r * C::H + col), ld16(p.norm_w + col), rstd[r]);
+    return dld128(rs, p.off[0] + ((uint32_t)r * C::H + col) * 2);
+  }
   return ld16(p.x + (size_t)r * C::H + col);
 }
 
@@ -665,6 +703,7 @@ template <class C>
 struct RouterSmem {
   static constexpr int PW = C::H / C::P;
   uint16_t x[kRowsMax * PW];
+  float rstd[kRowsMax];  // the rows' 1 / rms, where stage A norms them itself
 };
 
 // router part sums of one workgroup unit: K part ``part`` of experts eb * 8 .. eb * 8 + 7
@@ -672,7 +711,8 @@ struct RouterSmem {
 // 512-column chunk of the part in order (products rounded, then added), then the
 // wave's halving tree
 template <class C>
-__device__ __forceinline__ void router_unit(const Params& p, RouterSmem<C>& sm, int part, int eb, int lane, int wave) {
+__device__ __forceinline__ void router_unit(const Params& p, RouterSmem<C>& sm, int part, int eb, int lane, int wave,
+                                            const float* rstd) {
 #pragma clang fp contract(off)
   constexpr int CPP = C::CH512 / C::P;
   constexpr int PW = RouterSmem<C>::PW;
@@ -690,7 +730,7 @@ __device__ __forceinline__ void router_unit(const Params& p, RouterSmem<C>& sm, 
 #pragma unroll 4
   for (int i = threadIdx.x; i < n; i += kThreads) {
     const int r = i / (PW / 8), c = i % (PW / 8);
-    *(u32x4*)(sm.x + r * PW + c * 8) = x_load<C>(p, rs, r, part * PW + c * 8);
+    *(u32x4*)(sm.x + r * PW + c * 8) = x_load<C>(p, rs, r, part * PW + c * 8, rstd);
   }
   __syncthreads();
   if (e >= C::E) return;
@@ -717,12 +757,14 @@ __device__ __forceinline__ void router_unit(const Params& p, RouterSmem<C>& sm, 
 }
 
 // quantize 512 columns of row r: group-128 fp8 (fp32 scale) and, for MXFP4
-// experts, MXFP8 per 32 ("aiter" rule)
+// experts, MXFP8 per 32 ("aiter" rule); rstd non-null: the columns are normed here, and
+// stored as the normed rows (sc1) too
 template <class C>
-__device__ __forceinline__ void quant_unit(const Params& p, int r, int c, int lane) {
+__device__ __forceinline__ void quant_unit(const Params& p, int r, int c, int lane, const float* rstd) {
 #pragma clang fp contract(off)
   const auto rs = ws_rsrc(p);
-  u32x4 xv = x_load<C>(p, rs, r, c * 512 + lane * 8);
+  u32x4 xv = x_load<C>(p, rs, r, c * 512 + lane * 8, rstd);
+  if (C::NORM && rstd) dst128(rs, p.off[0] + ((uint32_t)r * C::H + c * 512 + lane * 8) * 2, xv);
   const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
   float v[8];
   float am = 0.0f;
@@ -783,28 +825,34 @@ __device__ __forceinline__ void reset_parts(const Params& p, int b, int nwg) {
 }
 
 template <class C>
-__device__ __forceinline__ void stage_a(const Params& p, RouterSmem<C>& sm, int b, int nwg) {
+__device__ __forceinline__ void stage_a(const Params& p, RouterSmem<C>& sm, int b, int nwg, bool local_norm) {
   const int lane = threadIdx.x & 63, wave = (int)(threadIdx.x >> 6);
   constexpr int EB = (C::E + kWaves - 1) / kWaves;
   constexpr int n_router = C::P * EB;
+  // local_norm: the rows' 1 / rms first, in every workgroup with a unit
+  const float* rstd = nullptr;
+  if (C::NORM && local_norm && (b < n_router + p.rows || (n_router < nwg && n_router + p.rows > nwg))) {
+    local_rstd<C>(p, sm.rstd);
+    rstd = sm.rstd;
+  }
   if (n_router < nwg && n_router + p.rows > nwg) {
     // more units than workgroups: a router unit each on workgroups [0, n_router) and the rows'
     // quantize on the others, several rows each (a router unit of many rows outlasts several
     // rows' quantize; dealt in turn, the first workgroups would run one of each)
     if (b < n_router) {
-      router_unit<C>(p, sm, b % C::P, b / C::P, lane, wave);
+      router_unit<C>(p, sm, b % C::P, b / C::P, lane, wave, rstd);
     } else {
       for (int r = b - n_router; r < p.rows; r += nwg - n_router)
-        for (int c = wave; c < C::CH512; c += kWaves) quant_unit<C>(p, r, c, lane);
+        for (int c = wave; c < C::CH512; c += kWaves) quant_unit<C>(p, r, c, lane, rstd);
     }
     return;
   }
   const int n = n_router + p.rows;
   for (int u = b; u < n; u += nwg) {
     if (u < n_router) {
-      router_unit<C>(p, sm, u % C::P, u / C::P, lane, wave);
+      router_unit<C>(p, sm, u % C::P, u / C::P, lane, wave, rstd);
     } else {
-      for (int c = wave; c < C::CH512; c += kWaves) quant_unit<C>(p, u - n_router, c, lane);
+      for (int c = wave; c < C::CH512; c += kWaves) quant_unit<C>(p, u - n_router, c, lane, rstd);
     }
   }
 }
@@ -3554,12 +3602,15 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   const int b = blockIdx.x, nwg = gridDim.x;
   TL_CLEAR();
   TL(kTlStart);
+  // (up to kLocalNormMax rows stage A norms the rows itself: no stage N, no hand-off)
   if constexpr (C::NORM) {
-    stage_norm<C>(p, b, nwg);
-    arrive(p, kCtlNorm);
-    await_all(p, kCtlNorm, nwg, kStageNorm);
+    if (p.rows > kLocalNormMax) {
+      stage_norm<C>(p, b, nwg);
+      arrive(p, kCtlNorm);
+      await_all(p, kCtlNorm, nwg, kStageNorm);
+    }
   }
-  stage_a<C>(p, sm.a, b, nwg);
+  stage_a<C>(p, sm.a, b, nwg, p.rows <= kLocalNormMax);
   TL(kTlADone);
   arrive(p, kCtlA);
   TL(kTlAArrived);
@@ -3645,7 +3696,7 @@ __global__ __launch_bounds__(kThreads) void k_norm(Params p) {
 template <class C>
 __global__ __launch_bounds__(kThreads) void k_a(Params p) {
   __shared__ RouterSmem<C> sm;
-  stage_a<C>(p, sm, blockIdx.x, gridDim.x);
+  stage_a<C>(p, sm, blockIdx.x, gridDim.x, false);
 }
 template <class C>
 __global__ __launch_bounds__(kThreads) void k_b(Params p) {

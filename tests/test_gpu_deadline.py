@@ -66,7 +66,7 @@ def test_deadline_gives_up_then_clear_restores(workload, rows):
         ("cfg3_tp4_mxfp4", 1, 2, 0),  # the polled router part sums and the x codes
         ("cfg3_tp4_mxfp4", 1, 3, 10),  # the published routing (a workgroup of the early shared gate_up)
         ("cfg2_tp4_fp8", 4, 3, 200),  # the shared intermediate, before the shared down
-        ("cfg5_tp2_mxfp4_norm", 8, 1, 255),  # the RMSNorm's hand-off
+        ("cfg5_tp2_mxfp4_norm", 24, 1, 255),  # the RMSNorm's hand-off (above 16 rows: below, none)
     ],
 )
 def test_fault_injection_stalls_one_wait(workload, rows, stage, wg):
