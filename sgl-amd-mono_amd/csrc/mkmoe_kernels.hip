@@ -1900,7 +1900,9 @@ struct GuTile {
 
 // a token group's activations for an MFMA gate_up, this wave's K steps, in registers: lane
 // (n, j) holds pick n's codes of its K places (FP8: bytes 16 j .. and 64 + 16 j .. of each
-// 128; MXFP8: 32 j .. 32 j + 31) and the scales; picks past np are zero
+// 128; MXFP8: 32 j .. 32 j + 31) and the scales. Lanes of picks past np hold pick 0's: an
+// MFMA's output column n depends on column n of its B operand alone, and the columns past np
+// are never emitted, so they are not zeroed
 template <class C, int WFMT>
 struct GuX {
   static constexpr int SPW = C::H / 128 / kWaves;
@@ -1935,9 +1937,6 @@ struct GuX {
         ex[i] = dld8(rs, soff + t * (C::H / 32) + k0 / 32 + j);
       }
     }
-#pragma unroll
-    for (int i = 0; i < SPW; ++i)
-      if (!live) lo[i] = hi[i] = u32x4{0u, 0u, 0u, 0u};
   }
 };
 
@@ -2354,9 +2353,10 @@ struct DownTile {
   template <int QS, int SST>
   __device__ __forceinline__ void mma(const uint8_t* xq, const uint8_t* xs, int lp, int np, int lane, bool scaled,
                                       f32x4 (&acc)[NA]) const {
+    // (lanes of picks past np read pick lp's row: their output columns are never stored, and
+    // an output column depends on its own B column alone)
     const int n = lane & 15, j = lane >> 4;
-    const bool live = n < np;
-    const int row = lp + (live ? n : 0);
+    const int row = lp + (n < np ? n : 0);
     const uint8_t* xr = xq + (size_t)row * QS;
 #pragma unroll
     for (int q = 0; q < NA; ++q) acc[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -2366,7 +2366,6 @@ struct DownTile {
         const bool tail = HALF && ks == KS - 1;
         u32x4 blo = *(const u32x4*)(xr + ks * 128 + 16 * j);
         u32x4 bhi = tail ? u32x4{0u, 0u, 0u, 0u} : *(const u32x4*)(xr + ks * 128 + 64 + 16 * j);
-        if (!live) blo = bhi = u32x4{0u, 0u, 0u, 0u};
         const int b0 = 4 * ks + (j >> 1);
         const float sxl = e8m0(xs[row * SST + b0]), sxh = tail ? 1.0f : e8m0(xs[row * SST + b0 + 2]);
         const uint32_t sw = sa[0][ks];
@@ -2374,7 +2373,6 @@ struct DownTile {
                                 acc[0]);
       } else if constexpr (WFMT == kFp8) {
         u32x4 blo = *(const u32x4*)(xr + ks * 128 + 16 * j), bhi = *(const u32x4*)(xr + ks * 128 + 64 + 16 * j);
-        if (!live) blo = bhi = u32x4{0u, 0u, 0u, 0u};
         const float sx = ((const float*)(xs + row * SST))[ks];
         const f32x4 c = mma_fp8_step(a[0][ks][0], a[0][ks][1], blo, bhi);
         const float f0 = s0[ks] * sx, f1 = s1[ks] * sx;
@@ -2383,13 +2381,11 @@ struct DownTile {
       } else if (scaled) {
         // the scaled MFMA's K layout for the column (see mma_fp4_scaled)
         u32x4 blo = *(const u32x4*)(xr + ks * 128 + 16 * j), bhi = *(const u32x4*)(xr + ks * 128 + 64 + 16 * j);
-        if (!live) blo = bhi = u32x4{0u, 0u, 0u, 0u};
         const uint32_t sx = xs[row * SST + ks * 4 + j];
 #pragma unroll
         for (int q = 0; q < NA; ++q) acc[q] = mma_fp4_scaled(a[q][ks][0], sa[q][ks], blo, bhi, sx, acc[q]);
       } else {
         u32x4 blo = *(const u32x4*)(xr + ks * 128 + 32 * j), bhi = *(const u32x4*)(xr + ks * 128 + 32 * j + 16);
-        if (!live) blo = bhi = u32x4{0u, 0u, 0u, 0u};
         const float sx = e8m0(xs[row * SST + ks * 4 + j]);
         if constexpr (NA == 2) {
           mma_fp4_step2(a[0][ks][0], e8m0(sa[0][ks]), a[1][ks][0], e8m0(sa[1][ks]), blo, bhi, sx, acc[0], acc[1]);
