@@ -6,11 +6,13 @@
                                                  # (libmkmoe_tl.so; bench.py --timeline)
     python sgl-amd-mono_amd/build.py --lds       # the LDS budget per shape (a host program)
 
-The library holds the kernels and the C ABI of ``include/mkmoe.h``. It is built
-in place (not installed) so that the same file runs wherever the tree is copied.
-The MoE source compiles in parts, in parallel: one object per compiled MoE shape
-(``MKMOE_UNIT`` 0 .. 8) and one for the host code (``MKMOE_UNIT`` 9); the FFN
-seam's source (``csrc/mkmoe_seam.hip``) is one more object; then one link.
+The library holds the kernels and the C ABI of ``include/mkmoe.h`` and
+``include/mkmoe_seam.h``. It is built in place (not installed) so that the same
+file runs wherever the tree is copied. The MoE source compiles in parts, in
+parallel: one object per compiled MoE shape (``MKMOE_UNIT`` 0 .. 8) and one for
+the host code (``MKMOE_UNIT`` 9); the FFN seam's source (``csrc/mkmoe_seam.hip``)
+is one more object; then one link. The test hooks of ``include/mkmoe_testing.h``
+(``csrc/mkmoe_testing.hip``) build alongside, as ``libmkmoe_testing.so``.
 """
 
 from __future__ import annotations
@@ -27,8 +29,10 @@ ROOT = Path(__file__).resolve().parent
 CSRC = ROOT / "csrc"
 OUT = ROOT / "sgl_amd_mono" / "moe" / "libmkmoe.so"
 OUT_TIMELINE = ROOT / "sgl_amd_mono" / "moe" / "libmkmoe_tl.so"
+OUT_TESTING = ROOT / "sgl_amd_mono" / "moe" / "libmkmoe_testing.so"
 SOURCE = CSRC / "mkmoe_kernels.hip"
 SEAM_SOURCE = CSRC / "mkmoe_seam.hip"
+TESTING_SOURCE = CSRC / "mkmoe_testing.hip"
 UNITS = (0, 1, 2, 3, 4, 5, 6, 7, 8, 9)  # the compiled shapes, then the host code
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -49,7 +53,8 @@ def _run(cmd: list[str]) -> subprocess.CompletedProcess:
 
 
 def build(check: bool = False, verbose: bool = False, timeline: bool = False) -> Path:
-    """Compile the library (always; about 30 s with the parts in parallel) and return its path."""
+    """Compile the library (always; about 30 s with the parts in parallel) and return its path;
+    the product build also compiles the test hooks' library (libmkmoe_testing.so)."""
     out = OUT_TIMELINE if timeline else OUT
     defs = ["-DMKMOE_TIMELINE"] if timeline else []
     with tempfile.TemporaryDirectory(prefix="mkmoe_build_") as tmpd:
@@ -58,6 +63,9 @@ def build(check: bool = False, verbose: bool = False, timeline: bool = False) ->
         for u, o in zip(UNITS, objs):
             cmds.append([HIPCC, *FLAGS, *defs, f"-DMKMOE_UNIT={u}", "-c", str(SOURCE), "-o", str(o)])
         cmds.append([HIPCC, *FLAGS, "-c", str(SEAM_SOURCE), "-o", str(objs[-1])])
+        testing_tmp = OUT_TESTING.with_suffix(".so.tmp")
+        if not timeline:
+            cmds.append([HIPCC, *FLAGS, "-shared", str(TESTING_SOURCE), "-o", str(testing_tmp)])
         if check:
             for cmd in cmds:
                 cmd.append("-Rpass-analysis=kernel-resource-usage")
@@ -83,6 +91,8 @@ def build(check: bool = False, verbose: bool = False, timeline: bool = False) ->
             sys.stderr.write(res.stdout + res.stderr)
             raise RuntimeError(f"link failed ({res.returncode})")
         os.replace(tmp, out)
+        if not timeline:
+            os.replace(testing_tmp, OUT_TESTING)
     return out
 
 

@@ -1,5 +1,5 @@
 """ctypes binding of the in-tree HIP library (the C ABI of ``include/mkmoe.h`` and
-``include/mkmoe_seam.h``).
+``include/mkmoe_seam.h``), and of its test hooks' library (``include/mkmoe_testing.h``).
 
 The library is loaded from this directory only. There is no fallback: a missing
 or unloadable library raises, so a GPU run can never silently take another path.
@@ -11,6 +11,8 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmkmoe.so"
+# the test hooks (hardware converts, the scaled MFMA, host builds of the exact arithmetic)
+TESTING_LIB_PATH = Path(__file__).resolve().parent / "libmkmoe_testing.so"
 # the diagnostic build with the persistent launch's phase stamps (build.py --timeline)
 TIMELINE_LIB_PATH = Path(__file__).resolve().parent / "libmkmoe_tl.so"
 TL_SLOTS = 32
@@ -22,7 +24,7 @@ TL_NAMES = (
     "down units", "down first unit", "down barrier",
 )  # fmt: skip
 
-ABI_VERSION = 5  # MKMOE_ABI_VERSION of include/mkmoe.h that this binding follows
+ABI_VERSION = 6  # MKMOE_ABI_VERSION of include/mkmoe.h that this binding follows
 FMT_FP8_B128 = 1
 FMT_MXFP4 = 2
 FMT_MXFP4_AITER = 3  # MXFP4 in SGLang's loaded gfx950 layout (aiter's shuffles), read in place
@@ -63,6 +65,12 @@ EXPORTS = (
     "mkmoe_clear_errors",
     "mkmoe_workspace_region",
     "mkmoe_status_string",
+    "mkmoe_seam_workspace_bytes",
+    "mkmoe_seam_forward",
+    "mkmoe_seam_gate",
+)
+# every symbol include/mkmoe_testing.h declares (libmkmoe_testing.so)
+TESTING_EXPORTS = (
     "mkmoe_device_decode",
     "mkmoe_device_e4m3_sweep",
     "mkmoe_device_mfma_scaled",
@@ -70,9 +78,6 @@ EXPORTS = (
     "mkmoe_host_sigmoid",
     "mkmoe_host_sqrt_softplus",
     "mkmoe_host_topk",
-    "mkmoe_seam_workspace_bytes",
-    "mkmoe_seam_forward",
-    "mkmoe_seam_gate",
 )
 
 
@@ -179,17 +184,6 @@ def lib() -> ctypes.CDLL:
         L.mkmoe_workspace_region.argtypes = [sp, i32, ctypes.POINTER(sz), ctypes.POINTER(sz)]
         L.mkmoe_status_string.argtypes = [ctypes.c_int]
         L.mkmoe_status_string.restype = ctypes.c_char_p
-        L.mkmoe_device_decode.argtypes = [vp, vp, vp, i32, vp]
-        L.mkmoe_device_e4m3_sweep.argtypes = [ctypes.c_uint32, ctypes.c_uint32, vp, vp, vp]
-        L.mkmoe_device_mfma_scaled.argtypes = [vp, vp, vp, vp, vp, i32, i32, vp]
-        L.mkmoe_host_e4m3_encode.argtypes = [vp, vp, ctypes.c_int64]
-        L.mkmoe_host_e4m3_encode.restype = None
-        L.mkmoe_host_sigmoid.argtypes = [vp, vp, ctypes.c_int64]
-        L.mkmoe_host_sigmoid.restype = None
-        L.mkmoe_host_sqrt_softplus.argtypes = [vp, vp, ctypes.c_int64]
-        L.mkmoe_host_sqrt_softplus.restype = None
-        L.mkmoe_host_topk.argtypes = [sp, vp, vp, vp, vp]
-        L.mkmoe_host_topk.restype = None
         L.mkmoe_seam_workspace_bytes.argtypes = [i32, i32, ctypes.POINTER(sz)]
         L.mkmoe_seam_forward.argtypes = [ctypes.POINTER(SeamIO), vp, sz, vp]
         L.mkmoe_seam_gate.argtypes = [ctypes.POINTER(SeamIO), vp, sz, vp]
@@ -199,6 +193,29 @@ def lib() -> ctypes.CDLL:
             )
         _lib = L
     return _lib
+
+
+_testing_lib = None
+
+
+def testing_lib() -> ctypes.CDLL:
+    """The test hooks' library (include/mkmoe_testing.h); raises when it has not been built."""
+    global _testing_lib
+    if _testing_lib is None:
+        if not TESTING_LIB_PATH.exists():
+            raise RuntimeError(f"{TESTING_LIB_PATH} is missing: build it with `python sgl-amd-mono_amd/build.py`")
+        T = ctypes.CDLL(str(TESTING_LIB_PATH))
+        vp, i32 = ctypes.c_void_p, ctypes.c_int32
+        T.mkmoe_device_decode.argtypes = [vp, vp, vp, i32, vp]
+        T.mkmoe_device_e4m3_sweep.argtypes = [ctypes.c_uint32, ctypes.c_uint32, vp, vp, vp]
+        T.mkmoe_device_mfma_scaled.argtypes = [vp, vp, vp, vp, vp, i32, i32, vp]
+        for name in ("mkmoe_host_e4m3_encode", "mkmoe_host_sigmoid", "mkmoe_host_sqrt_softplus"):
+            getattr(T, name).argtypes = [vp, vp, ctypes.c_int64]
+            getattr(T, name).restype = None
+        T.mkmoe_host_topk.argtypes = [ctypes.POINTER(Shape), vp, vp, vp, vp]
+        T.mkmoe_host_topk.restype = None
+        _testing_lib = T
+    return _testing_lib
 
 
 def status_string(rc: int) -> str:

@@ -75,7 +75,7 @@ def test_device_decode_matches_tables():
     f8 = torch.empty(256, device="cuda")
     f4 = torch.empty(512, device="cuda")
     _lib.check(
-        _lib.lib().mkmoe_device_decode(codes.data_ptr(), f8.data_ptr(), f4.data_ptr(), 256, torch.cuda.current_stream().cuda_stream),
+        _lib.testing_lib().mkmoe_device_decode(codes.data_ptr(), f8.data_ptr(), f4.data_ptr(), 256, torch.cuda.current_stream().cuda_stream),
         "decode",
     )
     torch.cuda.synchronize()
@@ -417,7 +417,7 @@ def test_device_e4m3_convert_equals_encoder_on_every_float():
     NaN, on the device: no code differs."""
     from sgl_amd_mono.moe import _lib
 
-    L = _lib.lib()
+    L = _lib.testing_lib()
     bad = torch.zeros(1, dtype=torch.int32, device="cuda")
     first_bad = torch.full((1,), -1, dtype=torch.int32, device="cuda")
     for k in range(16):

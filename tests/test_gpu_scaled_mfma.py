@@ -76,7 +76,7 @@ def _run(a_words, b_words, sa, sb, fmt_a):
     t = a_words.shape[0]
     dev = [torch.from_numpy(np.ascontiguousarray(v).view(np.int32)).cuda() for v in (a_words, b_words, sa, sb)]
     d = torch.zeros(t, 64, 4, dtype=torch.float32, device="cuda")
-    rc = _lib.lib().mkmoe_device_mfma_scaled(
+    rc = _lib.testing_lib().mkmoe_device_mfma_scaled(
         *(x.data_ptr() for x in dev), d.data_ptr(), fmt_a, t, torch.cuda.current_stream().cuda_stream
     )
     _lib.check(rc, "mkmoe_device_mfma_scaled")

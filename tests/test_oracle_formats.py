@@ -76,7 +76,7 @@ def test_host_e4m3_encoder_matches_torch():
                         np.array([0.0, -0.0], np.float32)])  # fmt: skip
     x = np.ascontiguousarray(x, np.float32)
     out = np.zeros(x.shape, np.uint8)
-    _lib.lib().mkmoe_host_e4m3_encode(x.ctypes.data, out.ctypes.data, x.size)
+    _lib.testing_lib().mkmoe_host_e4m3_encode(x.ctypes.data, out.ctypes.data, x.size)
     want = fm.e4m3_codes_from_f32(torch.from_numpy(x)).numpy()
     assert np.array_equal(out, want), (x[out != want][:8], out[out != want][:8], want[out != want][:8])
 
@@ -190,13 +190,29 @@ def test_host_library_exports():
 
     L = _lib.lib()
     assert L.mkmoe_abi_version() == _lib.ABI_VERSION
-    declared = set()
-    for header in sorted((Path(__file__).resolve().parents[1] / "include").glob("*.h")):
-        declared |= set(re.findall(r"^(?:int|void|const char\*)\s+(mkmoe_\w+)\(", header.read_text(), re.M))
-    assert declared == set(_lib.EXPORTS), declared ^ set(_lib.EXPORTS)
+    inc = Path(__file__).resolve().parents[1] / "include"
+
+    def declared(names):
+        out = set()
+        for n in names:
+            out |= set(re.findall(r"^(?:int|void|const char\*)\s+(mkmoe_\w+)\(", (inc / n).read_text(), re.M))
+        return out
+
+    # the product library: the drop-in surface (mkmoe.h, mkmoe_seam.h) and nothing else
+    assert sorted(h.name for h in inc.glob("*.h")) == ["mkmoe.h", "mkmoe_seam.h", "mkmoe_testing.h"]
+    product = declared(["mkmoe.h", "mkmoe_seam.h"])
+    assert product == set(_lib.EXPORTS), product ^ set(_lib.EXPORTS)
     for name in _lib.EXPORTS:
         assert hasattr(L, name), name
+    for name in _lib.TESTING_EXPORTS:
+        assert not hasattr(L, name), f"{name} is a test hook, not part of the product library"
     assert ctypes.c_char_p(L.mkmoe_status_string(-2)).value
+    # the test hooks' library: include/mkmoe_testing.h
+    testing = declared(["mkmoe_testing.h"])
+    assert testing == set(_lib.TESTING_EXPORTS), testing ^ set(_lib.TESTING_EXPORTS)
+    T = _lib.testing_lib()
+    for name in _lib.TESTING_EXPORTS:
+        assert hasattr(T, name), name
 
 
 def test_static_workspace_holds_every_compiled_shape():

@@ -75,7 +75,7 @@ def test_host_sigmoid_bitexact():
     x = np.concatenate([rng.standard_normal(100000) * 3, rng.uniform(-80, 80, 20000),
                         [0.0, -0.0, 60.0, -60.0, 1e-30, -1e-30]]).astype(np.float32)  # fmt: skip
     out = np.zeros_like(x)
-    _lib.lib().mkmoe_host_sigmoid(x.ctypes.data, out.ctypes.data, x.size)
+    _lib.testing_lib().mkmoe_host_sigmoid(x.ctypes.data, out.ctypes.data, x.size)
     assert np.array_equal(out.view(np.uint32), rt.sigmoid_exact(x).view(np.uint32))
 
 
@@ -145,7 +145,7 @@ def _host_topk(preset, scores, bias):
     shape = _lib.shape_of(preset)
     ids = np.zeros(preset.topk, np.int32)
     w = np.zeros(preset.topk, np.float32)
-    _lib.lib().mkmoe_host_topk(
+    _lib.testing_lib().mkmoe_host_topk(
         __import__("ctypes").byref(shape), scores.ctypes.data, bias.ctypes.data, ids.ctypes.data, w.ctypes.data
     )
     return ids, w
@@ -219,7 +219,7 @@ def test_unset_part_sums_route_in_bounds():
     from sgl_amd_mono.moe import _lib
     from sgl_amd_mono.moe.presets import PRESETS
 
-    L = _lib.lib()
+    L = _lib.testing_lib()
     unset = np.full(4, 0xFFFFFFFF, np.uint32).view(np.float32)
     logit = np.zeros(4, np.float32)
     for _ in range(7):  # the parts added in order, as the kernel does
@@ -301,7 +301,7 @@ def test_host_sqrt_softplus_bitexact():
     x = np.concatenate([rng.standard_normal(100000) * 8, rng.uniform(-250, 60, 20000),
                         [0.0, -0.0, 20.0, 20.000002, -200.0, -1e-30]]).astype(np.float32)  # fmt: skip
     out = np.zeros_like(x)
-    _lib.lib().mkmoe_host_sqrt_softplus(x.ctypes.data, out.ctypes.data, x.size)
+    _lib.testing_lib().mkmoe_host_sqrt_softplus(x.ctypes.data, out.ctypes.data, x.size)
     assert np.array_equal(out.view(np.uint32), rt.sqrt_softplus_exact(x).view(np.uint32))
 
 
