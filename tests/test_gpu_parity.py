@@ -195,7 +195,7 @@ def test_parity_mxfp4_scaled(workload, rows, mode):
 
     Its internal sum keeps fewer bits than fp32 (test_gpu_scaled_mfma.py bounds it), so it is
     held to the reference's own bounds (cosine 0.9999 and relative error 0.015 of the golden,
-    ffn.moe at spec.py:305-309, and the north_star's relative L2 1e-2), with routing bit for
+    ffn.moe at spec.py:305-309, and a relative L2 of 1e-2 of the output), with routing bit for
     bit; the elements beyond max-abs 2e-2 are reported (measured, both: 1 to 218 of 7168 to
     344064; down alone: 0 to 34), which is why the default launch converts the codes to bf16."""
     from gpu_case import errors, record_accuracy
