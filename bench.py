@@ -519,7 +519,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
-            "bench.py: this build runs one TP rank's MoE share on one GPU; figures at several GPUs are "
+            "bench.py: the benchmark runs one TP rank's MoE share on one GPU; figures at several GPUs are "
             "not produced (the all-reduce is outside the benchmarked path). Use --gpus 1.",
             file=sys.stderr,
         )

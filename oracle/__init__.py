@@ -1,7 +1,7 @@
 """CPU oracle of the decode MoE block (test infrastructure only).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
-leg may import this package, and only as the checker. The product path
+leg may import this package, and only to check results against. The product path
 (``sgl-amd-mono_amd/``) never imports it and fails loudly when its HIP
 library is missing.
 

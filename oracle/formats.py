@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY. This module is part of the oracle: only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg may import it,
-and only as the checker. The product path never calls it.
+and only to check results against. The product path never calls it.
 
 Formats:
 

@@ -20,7 +20,7 @@ Per token, with a the (all-reduced) attention output owed its post mix, res [HC]
    Products are rounded on their own, only the last term is fused.
 2. Collapse (``seam.py:103-118``): lin[c] = bf16(0 + pre[0] R[0][c] + ... + pre[3] R[3][c]),
    summed in stream order, products rounded.
-3. Mix partials (this build's order; the reference's runs on fp32 MFMA, ``seam.py:218-248``):
+3. Mix partials (the kernels' order; the reference's runs on fp32 MFMA, ``seam.py:218-248``):
    columns split into slices of 32; for slice s, projection j and stream o,
    q[j][o] = 0 + fn[j][o H + 32 s] R[o][32 s] + ... (the slice's 32 columns in order), and
    P[j][s] = ((q[j][0] + q[j][1]) + q[j][2]) + q[j][3]; the sum of squares of R over the
@@ -33,7 +33,7 @@ Per token, with a the (all-reduced) attention output owed its post mix, res [HC]
    (row r = (j - 8) / 4): a row softmax exp(z - rowmax) (rows summed (e0 + e1) + (e2 + e3)),
    then cv = fma(e, 1 / rowsum, 1e-6); then cv /= colsum + 1e-6 (by a multiply with the
    reciprocal); then 19 more rounds of the row step and the column step, each dividing by
-   its sum + 1e-6 the same way. The sigmoid and the exp are this build's exact fp64 ones
+   its sum + 1e-6 the same way. The sigmoid and the exp are the kernels' exact fp64 ones
    (``routing.sigmoid_exact``, ``routing.exp_nonpos``), the reciprocals and square root IEEE
    fp32; the reference's are the hardware approximations (within its 1e-4 relative bound).
 6. RMSNorm of lin with the norm weight (``routing.rmsnorm_exact``'s order; the reference's
