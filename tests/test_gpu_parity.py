@@ -30,6 +30,9 @@ CASES = [
     ("cfg5_tp2_mxfp4_norm", 1),
     ("cfg5_tp2_mxfp4_norm", 8),
     ("cfg5_tp2_mxfp4_norm", 48),
+    # the RMSNorm inside stage A (up to 16 rows) and the norm stage's hand-off (17)
+    ("cfg5_tp2_mxfp4_norm", 16),
+    ("cfg5_tp2_mxfp4_norm", 17),
     # 12 rows: stage Q with the shared expert's down inside its hand-off, pick batch whole
     ("cfg2_tp4_fp8", 12),
     ("cfg3_tp4_mxfp4", 12),
@@ -328,7 +331,15 @@ def gen_dense(c):
 
 @pytest.mark.parametrize(
     "workload,rows",
-    [("cfg2_tp4_fp8", 8), ("cfg3_tp4_mxfp4", 8), ("cfg5_tp2_mxfp4_norm", 8), ("cfg5_tp2_mxfp4_norm", 24)],
+    [
+        ("cfg2_tp4_fp8", 8),
+        ("cfg3_tp4_mxfp4", 8),
+        ("cfg5_tp2_mxfp4_norm", 1),
+        ("cfg5_tp2_mxfp4_norm", 8),
+        ("cfg5_tp2_mxfp4_norm", 16),
+        ("cfg5_tp2_mxfp4_norm", 17),
+        ("cfg5_tp2_mxfp4_norm", 24),
+    ],
 )
 def test_activation_codes_bitexact(workload, rows):
     """The kernel's quantized x (and normed x) equal the oracle's bit for bit: up to 16 rows
