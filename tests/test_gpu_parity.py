@@ -36,6 +36,10 @@ CASES = [
     # 12 rows: stage Q with the shared expert's down inside its hand-off, pick batch whole
     ("cfg2_tp4_fp8", 12),
     ("cfg3_tp4_mxfp4", 12),
+    # the last row count every workgroup routes itself (the early shared gate_up on workgroups
+    # 0 .. n-1) and the first with the routing hand-off (on the workgroups past the rows)
+    ("cfg3_tp4_mxfp4", 16),
+    ("cfg3_tp4_mxfp4", 17),
     ("tp4_fp8_zipf", 16),
     ("tp4_fp8_zipf", 48),
     ("tp2_mxfp4_norm_zipf", 48),
