@@ -3526,13 +3526,16 @@ __device__ __forceinline__ void shared_first_run(const Params& p, DownSmem<C>& s
 // union alone, so they are requested before the wait for the other workgroups' gate_up. GQ
 // (launches of C::QROWS rows or more): stage Q first. PRE: workgroups [0, nsw) ran the shared
 // expert's gate_up in the routing window and set their flags at B, so the first tile's shared
-// down runs before the wait (its rows quantized here). Each combination is a code path of its
+// down runs before the wait (its rows quantized here). MID (stage Q, shapes whose shared unit
+// does not fit a routed unit's slot): the first tile's shared down runs inside the Q hand-off,
+// from units in registers, its rows quantized here. Each combination is a code path of its
 // own, so that neither path's registers are allocated around the other's
-template <class C, bool MF, bool GQ, bool SHF = false, bool PRE = false>
+template <class C, bool MF, bool GQ, bool SHF = false, bool PRE = false, bool MID = false>
 __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg,
                                             int nsw = 0) {
   static_assert(!SHF || (MF && GQ && C::SF), "the shared down first: MFMA down, stage Q, a fitting slot");
-  static_assert(!(SHF && PRE), "one place for the shared down");
+  static_assert(!(SHF && PRE) && !(MID && (SHF || PRE)), "one place for the shared down");
+  static_assert(!MID || (MF && GQ), "the shared down inside the Q hand-off: MFMA down, stage Q");
   DownBatchOf<C, MF> bt;
   const int tr = p.tile_rows;
   const bool first = b * tr < C::H;
@@ -3561,9 +3564,17 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
   TL(kTlCAwaited);
   reset_parts<C>(p, b, nwg);  // every workgroup is past its routing
   if constexpr (GQ) {
-    stage_q<C>(p, un, b, nwg, !(SHF || PRE) || more_tiles);
+    stage_q<C>(p, un, b, nwg, !(SHF || PRE || MID) || more_tiles);
     TL(kTlQDone);
     arrive(p, kCtlQ);
+  }
+  if constexpr (MID) {
+    // its rows need only the C hand-off (the shared intermediate); the routed first units stay
+    // in flight in the waves' slots meanwhile
+    if (first) {
+      SharedDownBatch<C, MF> bs;
+      shared_down_tile<C, MF, false>(p, sm.sd, sm.shv, b * tr, min(tr, C::H - b * tr), bs, false);
+    }
   }
   if constexpr (SHF) {
     // the shared down while the other workgroups' stage Q runs: its rows need only the C
@@ -3578,7 +3589,7 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
     TL(kTlQAwaited);
   }
   __syncthreads();  // the tile's readers are done before the down stage reuses its LDS
-  stage_d<C, MF, GQ, SHF, PRE>(p, un, sm, b, nwg, bt, early);
+  stage_d<C, MF, GQ, SHF, PRE || MID>(p, un, sm, b, nwg, bt, early);
 }
 
 // ---------------------------------------------------------------- kernels
@@ -3671,6 +3682,8 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
       wait_then_d<C, true, false, false, true>(p, un, sm.d, b, nwg, nsw);
     } else if (gq && C::SF && p.rows <= kSharedFirstRows) {
       wait_then_d<C, true, true, C::SF>(p, un, sm.d, b, nwg);
+    } else if (gq && !C::SF && p.rows <= kSharedFirstRows) {
+      if constexpr (!C::SF) wait_then_d<C, true, true, false, false, true>(p, un, sm.d, b, nwg);
     } else if (gq) {
       wait_then_d<C, true, true>(p, un, sm.d, b, nwg);
     } else {
