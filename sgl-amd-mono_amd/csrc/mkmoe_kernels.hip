@@ -144,14 +144,11 @@ struct Cfg {
   static constexpr int IR = IR_;
   static_assert(IR == I || (SHUF && IR % 32 == 0 && IR < I), "real width: whole MX blocks");
   // launches of at least QROWS rows quantize the intermediates once (stage Q, a hand-off of
-  // its own) instead of in every workgroup's down stage, and up to kSharedFirstRows rows run
+  // its own) instead of in every workgroup's down stage, and up to kSharedMidRows rows run
   // the shared expert's down inside that hand-off. Measured: 7-8 % faster at 48 rows, 1.4 to
   // 4 us faster at 8 rows (MXFP4 at I = 512 gains only with the shared down inside the
   // hand-off), 0.3-2 us slower at 1 and 2 rows (the hand-off costs more than the work it saves)
   static constexpr int QROWS = 8;
-  // the persistent launch runs the shared expert's down before the routed one, its units
-  // staged through two waves' LDS slots (where a 16-row shared unit fits a routed unit's slot)
-  static constexpr bool SF = SFMT == kFp8 && 16 * S <= (FMT == kFp8 ? 16 * I : (I <= 512 ? 32 : 16) * (I / 2));
   static constexpr int CH512 = H / 512;  // router / quantize chunks of a row
   static_assert(H % 1024 == 0 && CH512 % P == 0, "router chunks, K split over 8 waves");
   // (an MX shared expert's width may end in half a 128-K step: V4.1's 2304 / 4 = 576)
@@ -3285,7 +3282,7 @@ __device__ __forceinline__ void down_valu(const Params& p, const Union<C>& un, D
 // Wave w's first unit of a pick batch is unit w (waves 1-7 request it before the hand-offs,
 // wave 0, which polls them, only after); each next unit is claimed from an LDS counter, so a
 // wave that started late takes fewer. A unit's results are the same whichever wave computes it.
-template <class C, bool GQ, bool SHF = false>
+template <class C, bool GQ>
 __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
                                           LdsUnit<C>& bt, bool first_ready) {
   const int lane = threadIdx.x & 63, wave = (int)(threadIdx.x >> 6);
@@ -3306,8 +3303,7 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
     int nx_lo = 0, nx_hi = -1;
     if (pb0 + C::PB < npk) batch_slots(un, pb0 + C::PB, min(C::PB, npk - pb0 - C::PB), nx_lo, nx_hi);
     const int nx_units = (nx_hi - nx_lo + 1) * nb;
-    // (SHF: waves 1 and 2 held the shared expert's units, and request their first now)
-    if (!ahead && (pb0 > 0 || !first_ready || wave == 0 || (SHF && wave <= 2)) && wave < n_units)
+    if (!ahead && (pb0 > 0 || !first_ready || wave == 0) && wave < n_units)
       mfma_issue<C>(p, un, h0, hn, s_lo, wave, slot, bt.nxt, lane);
     ahead = false;
     const unsigned long long tb0 = tl_now();
@@ -3377,15 +3373,14 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
 // stage goes on from them
 template <class C, bool MF>
 __device__ __forceinline__ void down_first(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
-                                           DownBatchOf<C, MF>& bt, bool shared_first) {
+                                           DownBatchOf<C, MF>& bt) {
   const int npk = p.rows * C::K;
   int s_lo, s_hi;
   batch_slots(un, 0, min(C::PB, npk), s_lo, s_hi);
   const int wave = (int)(threadIdx.x >> 6);
   // not wave 0, which polls the hand-off next: its flag reads would return only after
-  // these weights (a wave's loads return in order); with the shared down first, not waves 1
-  // and 2 either, whose slots take the shared expert's units
-  if (wave == 0 || (shared_first && wave <= 2)) return;
+  // these weights (a wave's loads return in order)
+  if (wave == 0) return;
   if constexpr (MF) {
     constexpr int UR = 16 * DownTileOf<C>::NA;
     if (wave < (s_hi - s_lo + 1) * ((hn + UR - 1) / UR))
@@ -3396,17 +3391,17 @@ __device__ __forceinline__ void down_first(const Params& p, const Union<C>& un, 
 }
 
 // tile rows [h0, h0 + hn): the routed down GEMVs (MFMA or VALU, as MF), the shared expert's
-// down (SHF, PRE: done before), then the combine; first_ready: the routed down's first units
-// are already requested into bt (waves 1-7)
-template <class C, bool MF, bool GQ, bool SHF = false, bool PRE = false>
+// down (PRE: done before), then the combine; first_ready: the routed down's first units are
+// already requested into bt (waves 1-7)
+template <class C, bool MF, bool GQ, bool PRE = false>
 __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
                                           DownBatchOf<C, MF>& bt, bool first_ready) {
   const int tid = threadIdx.x;
   const int R = p.rows;
-  if constexpr (MF) down_mfma<C, GQ, SHF>(p, un, sm, h0, hn, bt, first_ready);
+  if constexpr (MF) down_mfma<C, GQ>(p, un, sm, h0, hn, bt, first_ready);
   else down_valu<C, GQ>(p, un, sm, h0, hn, bt, first_ready);
   TL(kTlDRouted);
-  if constexpr (!SHF && !PRE) {  // SHF, PRE: sm.shv holds the shared expert's results already
+  if constexpr (!PRE) {  // PRE: sm.shv holds the shared expert's results already
     SharedDownBatch<C, MF> bs;
     shared_down_tile<C, MF, GQ>(p, sm.sd, sm.shv, h0, hn, bs, false);
   }
@@ -3432,12 +3427,12 @@ __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, D
 
 // this workgroup's tiles; first_ready: its first tile's first routed units are already
 // requested; GQ: stage Q has quantized the step's intermediates
-template <class C, bool MF, bool GQ, bool SHF = false, bool PRE = false>
+template <class C, bool MF, bool GQ, bool PRE = false>
 __device__ __forceinline__ void stage_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg,
                                         DownBatchOf<C, MF>& bt, bool first_ready) {
   const int tr = p.tile_rows;
   const int n_tiles = (C::H + tr - 1) / tr;
-  if (b < n_tiles) down_tile<C, MF, GQ, SHF, PRE>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt, first_ready);
+  if (b < n_tiles) down_tile<C, MF, GQ, PRE>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt, first_ready);
   // further tiles (fewer workgroups than tiles) start from batches of their own, so that bt
   // is free once the first tile's routed down is done
   for (int tile = b + nwg; tile < n_tiles; tile += nwg) {
@@ -3469,72 +3464,22 @@ __device__ __forceinline__ void stage_q(const Params& p, const Union<C>& un, int
   }
 }
 
-// launches of up to this many rows (and with stage Q) run the shared expert's down first
-constexpr int kSharedFirstRows = 16;
-// The shared expert's down first (C::SF): waves 1 and 2 stage its units 0 and 1 (tile rows
-// [h0, h0 + 16) and [h0 + 16, hn)) in their LDS slots, as the routed units are staged, and
-// hold the units' block scales in sh
-template <class C>
-__device__ __forceinline__ void shared_first_issue(const Params& p, DownSmem<C>& sm, int h0, int hn,
-                                                   DownTile<C::SFMT, C::S>& sh) {
-  using DT = DownTile<kFp8, C::S>;
-  static_assert(C::SFMT == kFp8, "the shared down first: FP8 128 x 128 units");
-  static_assert(DT::SLOT <= DownTileOf<C>::SLOT, "a shared unit fits a routed unit's slot");
-  const int wave = (int)(threadIdx.x >> 6), v = wave - 1;
-  if (v < 0 || v >= 2 || v * 16 >= hn) return;
-  const int hb = h0 + v * 16, nv = min(16, hn - v * 16);
-  static_assert((long long)C::H * C::S < (1ll << 31), "offsets within a 32-bit resource");
-  DT::issue(weight_rsrc(p.sw2, (uint32_t)(C::H * C::S)), (uint32_t)hb * C::S, nv, sm.wslot[wave], threadIdx.x & 63);
-  sh.load_scales(p.sw2_s, hb, nv, threadIdx.x & 63);
-}
-// ... and its rows quantized into LDS (group-128 FP8, from the shared intermediate), then the
-// two units against every row of the step into sm.shv (bf16 [R][hn]); ends with sm.shv
-// complete and the LDS rows free
-template <class C>
-__device__ __forceinline__ void shared_first_run(const Params& p, DownSmem<C>& sm, int h0, int hn,
-                                                 DownTile<C::SFMT, C::S>& sh) {
-  using DT = DownTile<kFp8, C::S>;
-  const int R = p.rows, lane = threadIdx.x & 63, wave = (int)(threadIdx.x >> 6), v = wave - 1;
-  __syncthreads();  // the LDS's previous users are done
-  quant_rows_lds<kFp8, C::S, C::SQS, C::FMT == kFp4 ? 2 : kQuantBatch>(
-      p, [&](int i) { return p.off[8] + (uint32_t)i * C::S * 2; }, R, sm.sd.q, sm.sd.s);
-  __syncthreads();
-  if (v >= 0 && v < 2 && v * 16 < hn) {
-    wait_vm0();  // the unit's rows are in the slot
-    DT cur;
-    cur.fetch(sm.wslot[wave], lane);
-    cur.take_scales(sh, h0 + v * 16, lane);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    const int n = lane & 15;
-#pragma unroll 1
-    for (int t0 = 0; t0 < R; t0 += kMfmaPicks) {
-      const int np = min(kMfmaPicks, R - t0);
-      f32x4 acc[1];
-      cur.opaque();
-      cur.template mma<C::SQS, C::SSC>(sm.sd.q, (const uint8_t*)sm.sd.s, t0, np, lane, false, acc);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int hl = v * 16 + 4 * (lane >> 4) + k;
-        if (n < np && hl < hn) sm.shv[(t0 + n) * hn + hl] = f2bf(acc[0][k]);
-      }
-    }
-  }
-  __syncthreads();  // sm.shv complete; the LDS rows free for the routed down
-}
+// launches of up to this many rows (and with stage Q) run the shared expert's down inside the
+// Q hand-off (above, its rows' quantize outlasts the hand-off)
+constexpr int kSharedMidRows = 16;
 
 // the persistent launch past its C arrival: the down stage's first weights depend on the
 // union alone, so they are requested before the wait for the other workgroups' gate_up. GQ
 // (launches of C::QROWS rows or more): stage Q first. PRE: workgroups [0, nsw) ran the shared
 // expert's gate_up in the routing window and set their flags at B, so the first tile's shared
-// down runs before the wait (its rows quantized here). MID (stage Q, shapes whose shared unit
-// does not fit a routed unit's slot): the first tile's shared down runs inside the Q hand-off,
-// from units in registers, its rows quantized here. Each combination is a code path of its
-// own, so that neither path's registers are allocated around the other's
-template <class C, bool MF, bool GQ, bool SHF = false, bool PRE = false, bool MID = false>
+// down runs before the wait (its rows quantized here). MID (with stage Q, up to
+// kSharedMidRows rows): the first tile's shared down runs inside the Q hand-off, from units
+// in registers, its rows quantized here. Each combination is a code path of its own, so that
+// neither path's registers are allocated around the other's
+template <class C, bool MF, bool GQ, bool PRE = false, bool MID = false>
 __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg,
                                             int nsw = 0) {
-  static_assert(!SHF || (MF && GQ && C::SF), "the shared down first: MFMA down, stage Q, a fitting slot");
-  static_assert(!(SHF && PRE) && !(MID && (SHF || PRE)), "one place for the shared down");
+  static_assert(!(MID && PRE), "one place for the shared down");
   static_assert(!MID || (MF && GQ), "the shared down inside the Q hand-off: MFMA down, stage Q");
   DownBatchOf<C, MF> bt;
   const int tr = p.tile_rows;
@@ -3546,13 +3491,7 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
   // of the last flags (its CU's loads queue behind them), by up to 5 us at 8 rows, and the Q
   // hand-off with it. (Below 8 rows the wait is short and the look costs more than it saves.)
   const bool early = first && (p.rows < 8 || 4 * flags_set_count(p, kCtlC, nwg) < 3 * nwg);
-  // SHF: the shared expert's down first, during the Q hand-off; its units are requested with
-  // the routed ones
-  DownTile<C::SFMT, C::S> sh;
-  if (early) {
-    down_first<C, MF>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt, SHF);
-    if constexpr (SHF) shared_first_issue<C>(p, sm, b * tr, min(tr, C::H - b * tr), sh);
-  }
+  if (early) down_first<C, MF>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt);
   if constexpr (PRE) {
     if (first) {
       await_all(p, kCtlB, nsw, kStageB);
@@ -3564,7 +3503,7 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
   TL(kTlCAwaited);
   reset_parts<C>(p, b, nwg);  // every workgroup is past its routing
   if constexpr (GQ) {
-    stage_q<C>(p, un, b, nwg, !(SHF || PRE || MID) || more_tiles);
+    stage_q<C>(p, un, b, nwg, !(PRE || MID) || more_tiles);
     TL(kTlQDone);
     arrive(p, kCtlQ);
   }
@@ -3576,20 +3515,12 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
       shared_down_tile<C, MF, false>(p, sm.sd, sm.shv, b * tr, min(tr, C::H - b * tr), bs, false);
     }
   }
-  if constexpr (SHF) {
-    // the shared down while the other workgroups' stage Q runs: its rows need only the C
-    // hand-off (the shared intermediate), quantized here
-    if (first) {
-      if (!early) shared_first_issue<C>(p, sm, b * tr, min(tr, C::H - b * tr), sh);
-      shared_first_run<C>(p, sm, b * tr, min(tr, C::H - b * tr), sh);
-    }
-  }
   if constexpr (GQ) {
     await_all(p, kCtlQ, nwg, kStageQ);
     TL(kTlQAwaited);
   }
   __syncthreads();  // the tile's readers are done before the down stage reuses its LDS
-  stage_d<C, MF, GQ, SHF, PRE || MID>(p, un, sm, b, nwg, bt, early);
+  stage_d<C, MF, GQ, PRE || MID>(p, un, sm, b, nwg, bt, early);
 }
 
 // ---------------------------------------------------------------- kernels
@@ -3673,17 +3604,15 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   TL(kTlCArrived);
   const bool gq = p.rows >= C::QROWS;
   if (C::SHUF || down_on_mfma<C>(p.rows, p.mfma_down)) {
-    // the shared down first, inside the Q hand-off, up to kSharedFirstRows rows (above, its
-    // rows' quantize outlasts the hand-off)
+    // the shared down before the C wait below stage Q's rows, inside the Q hand-off up to
+    // kSharedMidRows rows, else after the routed down
     if (nsw > 0 && kPreShared && !gq) {
       // the shared down before the C wait (the shared intermediate was stored in the routing
       // window). (With stage Q, from 8 rows, it cost 1-4 us there against after the routed
       // down or inside the Q hand-off: measured)
-      wait_then_d<C, true, false, false, true>(p, un, sm.d, b, nwg, nsw);
-    } else if (gq && C::SF && p.rows <= kSharedFirstRows) {
-      wait_then_d<C, true, true, C::SF>(p, un, sm.d, b, nwg);
-    } else if (gq && !C::SF && p.rows <= kSharedFirstRows) {
-      if constexpr (!C::SF) wait_then_d<C, true, true, false, false, true>(p, un, sm.d, b, nwg);
+      wait_then_d<C, true, false, true>(p, un, sm.d, b, nwg, nsw);
+    } else if (gq && p.rows <= kSharedMidRows) {
+      wait_then_d<C, true, true, false, true>(p, un, sm.d, b, nwg);
     } else if (gq) {
       wait_then_d<C, true, true>(p, un, sm.d, b, nwg);
     } else {
