@@ -3284,7 +3284,7 @@ __device__ __forceinline__ void down_valu(const Params& p, const Union<C>& un, D
 // wave that started late takes fewer. A unit's results are the same whichever wave computes it.
 template <class C, bool GQ>
 __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
-                                          LdsUnit<C>& bt, bool first_ready) {
+                                          LdsUnit<C>& bt, int first_ready) {
   const int lane = threadIdx.x & 63, wave = (int)(threadIdx.x >> 6);
   const int npk = p.rows * C::K;
   using DT = DownTileOf<C>;
@@ -3303,7 +3303,7 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
     int nx_lo = 0, nx_hi = -1;
     if (pb0 + C::PB < npk) batch_slots(un, pb0 + C::PB, min(C::PB, npk - pb0 - C::PB), nx_lo, nx_hi);
     const int nx_units = (nx_hi - nx_lo + 1) * nb;
-    if (!ahead && (pb0 > 0 || !first_ready || wave == 0) && wave < n_units)
+    if (!ahead && (pb0 > 0 || first_ready == 0 || (wave == 0 && first_ready < 2)) && wave < n_units)
       mfma_issue<C>(p, un, h0, hn, s_lo, wave, slot, bt.nxt, lane);
     ahead = false;
     const unsigned long long tb0 = tl_now();
@@ -3373,14 +3373,14 @@ __device__ __forceinline__ void down_mfma(const Params& p, const Union<C>& un, D
 // stage goes on from them
 template <class C, bool MF>
 __device__ __forceinline__ void down_first(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
-                                           DownBatchOf<C, MF>& bt) {
+                                           DownBatchOf<C, MF>& bt, bool wave0 = false) {
   const int npk = p.rows * C::K;
   int s_lo, s_hi;
   batch_slots(un, 0, min(C::PB, npk), s_lo, s_hi);
   const int wave = (int)(threadIdx.x >> 6);
   // not wave 0, which polls the hand-off next: its flag reads would return only after
-  // these weights (a wave's loads return in order)
-  if (wave == 0) return;
+  // these weights (a wave's loads return in order); wave0: wave 0 alone, later
+  if ((wave == 0) != wave0) return;
   if constexpr (MF) {
     constexpr int UR = 16 * DownTileOf<C>::NA;
     if (wave < (s_hi - s_lo + 1) * ((hn + UR - 1) / UR))
@@ -3392,10 +3392,10 @@ __device__ __forceinline__ void down_first(const Params& p, const Union<C>& un, 
 
 // tile rows [h0, h0 + hn): the routed down GEMVs (MFMA or VALU, as MF), the shared expert's
 // down (PRE: done before), then the combine; first_ready: the routed down's first units are
-// already requested into bt (waves 1-7)
+// already requested into bt (1: by waves 1-7, 2: by every wave)
 template <class C, bool MF, bool GQ, bool PRE = false>
 __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, DownSmem<C>& sm, int h0, int hn,
-                                          DownBatchOf<C, MF>& bt, bool first_ready) {
+                                          DownBatchOf<C, MF>& bt, int first_ready) {
   const int tid = threadIdx.x;
   const int R = p.rows;
   if constexpr (MF) down_mfma<C, GQ>(p, un, sm, h0, hn, bt, first_ready);
@@ -3429,7 +3429,7 @@ __device__ __forceinline__ void down_tile(const Params& p, const Union<C>& un, D
 // requested; GQ: stage Q has quantized the step's intermediates
 template <class C, bool MF, bool GQ, bool PRE = false>
 __device__ __forceinline__ void stage_d(const Params& p, const Union<C>& un, DownSmem<C>& sm, int b, int nwg,
-                                        DownBatchOf<C, MF>& bt, bool first_ready) {
+                                        DownBatchOf<C, MF>& bt, int first_ready) {
   const int tr = p.tile_rows;
   const int n_tiles = (C::H + tr - 1) / tr;
   if (b < n_tiles) down_tile<C, MF, GQ, PRE>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt, first_ready);
@@ -3437,7 +3437,7 @@ __device__ __forceinline__ void stage_d(const Params& p, const Union<C>& un, Dow
   // is free once the first tile's routed down is done
   for (int tile = b + nwg; tile < n_tiles; tile += nwg) {
     DownBatchOf<C, MF> bl;
-    down_tile<C, MF, GQ>(p, un, sm, tile * tr, min(tr, C::H - tile * tr), bl, false);
+    down_tile<C, MF, GQ>(p, un, sm, tile * tr, min(tr, C::H - tile * tr), bl, 0);
   }
 }
 
@@ -3491,12 +3491,21 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
   // of the last flags (its CU's loads queue behind them), by up to 5 us at 8 rows, and the Q
   // hand-off with it. (Below 8 rows the wait is short and the look costs more than it saves.)
   const bool early = first && (p.rows < 8 || 4 * flags_set_count(p, kCtlC, nwg) < 3 * nwg);
+  int ready = early ? 1 : 0;
   if (early) down_first<C, MF>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt);
   if constexpr (PRE) {
     if (first) {
       await_all(p, kCtlB, nsw, kStageB);
       SharedDownBatch<C, MF> bs;
       shared_down_tile<C, MF, false>(p, sm.sd, sm.shv, b * tr, min(tr, C::H - b * tr), bs, false);
+      // the shared down outlasts most of the gate_up's end spread: wave 0 requests its first
+      // routed unit before its C poll too
+      if constexpr (MF) {
+        if (early) {
+          down_first<C, MF>(p, un, sm, b * tr, min(tr, C::H - b * tr), bt, true);
+          ready = 2;
+        }
+      }
     }
   }
   await_all(p, kCtlC, nwg, kStageC);
@@ -3520,7 +3529,7 @@ __device__ __forceinline__ void wait_then_d(const Params& p, const Union<C>& un,
     TL(kTlQAwaited);
   }
   __syncthreads();  // the tile's readers are done before the down stage reuses its LDS
-  stage_d<C, MF, GQ, PRE || MID>(p, un, sm, b, nwg, bt, early);
+  stage_d<C, MF, GQ, PRE || MID>(p, un, sm, b, nwg, bt, ready);
 }
 
 // ---------------------------------------------------------------- kernels
