@@ -246,9 +246,10 @@ int mkmoe_clear_errors(const mkmoe_shape* shape, void* ws, size_t ws_bytes, void
  * word 0xFFFFFFFF between launches), 11 the phase stamps of a diagnostic build
  * compiled with MKMOE_TIMELINE (u64 s_memrealtime ticks [workgroup][32]; other
  * builds leave it untouched), 12 / 13 the routed intermediates quantized once
- * (codes [rows * topk][I + 16] in the union's pick order, E8M0 [..][I / 32] or
- * fp32 [..][I / 128] scales), 14 / 15 the shared intermediate quantized (codes
- * [rows][S + 16], fp32 scales [rows][S / 128]). */
+ * (from 8 rows: codes [rows * topk][I + 16] in the union's pick order, E8M0 [..][I / 32]
+ * or fp32 [..][I / 128] scales), 14 / 15 the shared intermediate quantized (above 16 rows:
+ * codes [rows][S + 16], fp32 scales [rows][S / 128] or E8M0 [rows][S / 32]; up to 16 rows
+ * every workgroup quantizes the shared rows into LDS itself). */
 int mkmoe_workspace_region(const mkmoe_shape* shape, int32_t region, size_t* offset,
                            size_t* bytes);
 
