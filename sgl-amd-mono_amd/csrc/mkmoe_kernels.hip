@@ -7,8 +7,8 @@
 //   N  RMSNorm of x (fused-norm shape only)                   wave per row
 //   A  router GEMV part sums (fixed order) + activation quantization
 //                                                              wave per (expert, K part) / (row, 512 cols)
-//   B  routing (sigmoid, grouped top-k, weights): up to 16 rows every workgroup routes the
-//      whole step itself, reading the part sums as they land; above 16 a workgroup a row
+//   B  routing (sigmoid, grouped top-k, weights): up to 8 rows every workgroup routes the
+//      whole step itself, reading the part sums as they land; above 8 a workgroup a row
 //   C  gate_up + SwiGLU of the step's union of experts and of the shared expert, dealt
 //      as one list of units over the workgroups
 //   D  down GEMMs (routed + shared) and the weighted combine   workgroup per tile of output rows
@@ -857,8 +857,11 @@ __device__ __forceinline__ void stage_a(const Params& p, RouterSmem<C>& sm, int 
 // ---------------------------------------------------------------- stage B: routing
 // Scores and choices of kRouteRows rows at a time, in LDS
 constexpr int kRouteRows = 16;
-// rows up to which every workgroup routes the whole step itself (no routing hand-off)
-constexpr int kLocalRouteMax = 16;
+// rows up to which every workgroup routes the whole step itself (no routing hand-off). Above,
+// a workgroup a row and the hand-off cost less than every workgroup's scores of all the rows:
+// 8 against 16 at 12 and 16 rows, cfg 2 -2.8 / -3.4 us, cfg 3 -3.6 / -5.6, V4.1 TP4 -6.1 /
+// -5.4 (its 384 sqrt(softplus) scores a row); lower, mixed (measured)
+constexpr int kLocalRouteMax = 8;
 
 template <class C>
 struct RouteSmem {
@@ -3044,8 +3047,9 @@ constexpr bool kPreShared = MKMOE_PRE_SHARED != 0;
 // The shared expert's gate_up units run while the step is routed, by workgroups [w0, w0 + n)
 // that route nothing meanwhile, with the gate_up on MFMA: its weights stream during the
 // routing, and the rest of the gate_up is dealt afterwards.
-//   - up to 16 rows (every other workgroup routes the step itself): workgroups [0, n), half of
-//     the grid at most, take all k of its units between them (a unit each where k <= n);
+//   - up to kLocalRouteMax rows (every other workgroup routes the step itself): workgroups
+//     [0, n), three quarters of the grid at most, take all k of its units between them (a
+//     unit each where k <= n);
 //   - above (workgroups [0, R) route a row each, then the B hand-off): workgroups [R, R + n)
 //     take its first k = n units, one each; the others join the routed units' deal.
 // n = 0: none (the shared units are dealt with the routed ones).
@@ -3056,7 +3060,7 @@ template <class C>
 __device__ __forceinline__ EarlyShared early_shared(const Params& p, int nwg) {
   if (!kEarlyShared || !gate_on_mfma<C>(p.rows, p.mfma_gate)) return {0, 0, 0};
   const int n_sh = GuDeal<C>::shared_units(p.rows);
-  if (p.rows <= kLocalRouteMax) return {0, min(n_sh, nwg / 2), n_sh};
+  if (p.rows <= kLocalRouteMax) return {0, min(n_sh, 3 * nwg / 4), n_sh};
   const int n = min(n_sh, nwg - p.rows);
   return {p.rows, n, n};
 }
@@ -3565,7 +3569,7 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   const int nsw = es.n;
   if (b >= es.w0 && b < es.w0 + es.n) {
     // the shared expert's gate_up while the others route: its weights are requested before
-    // the A hand-off (the x codes) is awaited. Up to 16 rows: then its flag at B (the shared
+    // the A hand-off (the x codes) is awaited. Up to 8 rows: then its flag at B (the shared
     // intermediate stored), and the routing from the workgroup that publishes it; above: its
     // flag at B first (no row to route), and the routing hand-off after the units
     int lo, hi;

@@ -61,7 +61,7 @@ def test_deadline_gives_up_then_clear_restores(workload, rows):
     "workload,rows,stage,wg",
     [
         ("cfg2_tp4_fp8", 8, 4, 5),  # the gate_up hand-off (C)
-        ("cfg2_tp4_fp8", 24, 3, 17),  # the routing hand-off (above 16 rows)
+        ("cfg2_tp4_fp8", 24, 3, 17),  # the routing hand-off (above 8 rows)
         ("cfg3_tp4_mxfp4", 16, 6, 200),  # stage Q's hand-off
         ("cfg3_tp4_mxfp4", 1, 2, 0),  # the polled router part sums and the x codes
         ("cfg3_tp4_mxfp4", 1, 3, 10),  # the published routing (a workgroup of the early shared gate_up)

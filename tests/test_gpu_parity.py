@@ -36,15 +36,17 @@ CASES = [
     # 12 rows: stage Q with the shared expert's down inside its hand-off, pick batch whole
     ("cfg2_tp4_fp8", 12),
     ("cfg3_tp4_mxfp4", 12),
-    # the last row count every workgroup routes itself (the early shared gate_up on workgroups
-    # 0 .. n-1) and the first with the routing hand-off (on the workgroups past the rows)
+    # the last row count every workgroup routes itself (8: the early shared gate_up on
+    # workgroups 0 .. n-1) and the first with the routing hand-off (9: on the workgroups past
+    # the rows); 16 and 17: the shared down inside the Q hand-off and after the routed one
+    ("cfg3_tp4_mxfp4", 9),
     ("cfg3_tp4_mxfp4", 16),
     ("cfg3_tp4_mxfp4", 17),
     ("tp4_fp8_zipf", 16),
     ("tp4_fp8_zipf", 48),
     ("tp2_mxfp4_norm_zipf", 48),
     # V4.1's router scores (sqrt(softplus), one group, check_ffn.py:201-206) on the plumbing
-    # shape: local routing (up to 16 rows) and the routing hand-off (24)
+    # shape: local routing (up to 8 rows) and the routing hand-off (16, 24)
     ("plumbing_fp8_softplus", 1),
     ("plumbing_fp8_softplus", 4),
     ("plumbing_fp8_softplus", 16),
@@ -268,8 +270,8 @@ def test_parity_aiter_layout(workload, rows):
 @pytest.mark.parametrize("workload,rows", [("cfg1_plumbing_fp8", 4), ("cfg2_tp4_fp8", 1), ("cfg2_tp4_fp8", 16), ("cfg2_tp4_fp8", 24)])
 def test_routing_ties(workload, rows, bias_kind):
     """Zero rows score 0.5 for every expert, so choices tie wherever the bias does: groups and
-    experts then go by lower index, as in the oracle's stable sorts (16 rows: every workgroup
-    routes the step; 24: a workgroup a row)."""
+    experts then go by lower index, as in the oracle's stable sorts (1 row: every workgroup
+    routes the step; 16 and 24: a workgroup a row)."""
     import dataclasses
 
     from oracle import routing as rt
