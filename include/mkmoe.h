@@ -246,7 +246,8 @@ int mkmoe_clear_errors(const mkmoe_shape* shape, void* ws, size_t ws_bytes, void
  * word 0xFFFFFFFF between launches), 11 the phase stamps of a diagnostic build
  * compiled with MKMOE_TIMELINE (u64 s_memrealtime ticks [workgroup][32]; other
  * builds leave it untouched), 12 / 13 the routed intermediates quantized once
- * (from 8 rows: codes [rows * topk][I + 16] in the union's pick order, E8M0 [..][I / 32]
+ * (from 6 rows on the FP8 shapes and at I >= 1024, else from 8: codes [rows * topk][I + 16]
+ * in the union's pick order, E8M0 [..][I / 32]
  * or fp32 [..][I / 128] scales), 14 / 15 the shared intermediate quantized (above 16 rows:
  * codes [rows][S + 16], fp32 scales [rows][S / 128] or E8M0 [rows][S / 32]; up to 16 rows
  * every workgroup quantizes the shared rows into LDS itself). */

@@ -147,8 +147,11 @@ struct Cfg {
   // its own) instead of in every workgroup's down stage, and up to kSharedMidRows rows run
   // the shared expert's down inside that hand-off. Measured: 7-8 % faster at 48 rows, 1.4 to
   // 4 us faster at 8 rows (MXFP4 at I = 512 gains only with the shared down inside the
-  // hand-off), 0.3-2 us slower at 1 and 2 rows (the hand-off costs more than the work it saves)
-  static constexpr int QROWS = 8;
+  // hand-off), 0.3-2 us slower at 1 and 2 rows (the hand-off costs more than the work it saves).
+  // From 6 rows where each workgroup's own quantize of the picks costs more (FP8's group-128
+  // rule, or I of 1024 and more): at 6 / 7 rows cfg 2 -1.2 / -1.1 us, cfg 5 -3.0 / -3.1, V4.1
+  // TP2 -0.9 / -1.2, where cfg 3 (+1.7 / +1.2) and V4.1 TP4 (+2.3 / +2.3) lost (measured)
+  static constexpr int QROWS = FMT == kFp8 || I >= 1024 ? 6 : 8;
   static constexpr int CH512 = H / 512;  // router / quantize chunks of a row
   static_assert(H % 1024 == 0 && CH512 % P == 0, "router chunks, K split over 8 waves");
   // (an MX shared expert's width may end in half a 128-K step: V4.1's 2304 / 4 = 576)
