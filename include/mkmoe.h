@@ -248,9 +248,10 @@ int mkmoe_clear_errors(const mkmoe_shape* shape, void* ws, size_t ws_bytes, void
  * builds leave it untouched), 12 / 13 the routed intermediates quantized once
  * (from 6 rows on the FP8 shapes and at I >= 1024, else from 8: codes [rows * topk][I + 16]
  * in the union's pick order, E8M0 [..][I / 32]
- * or fp32 [..][I / 128] scales), 14 / 15 the shared intermediate quantized (above 16 rows:
- * codes [rows][S + 16], fp32 scales [rows][S / 128] or E8M0 [rows][S / 32]; up to 16 rows
- * every workgroup quantizes the shared rows into LDS itself). */
+ * or fp32 [..][I / 128] scales), 14 / 15 the shared intermediate quantized (above 16 rows,
+ * or 24 on the MXFP4 shapes with inter <= 640 and the MX shared expert: codes [rows][S + 16],
+ * fp32 scales [rows][S / 128] or E8M0 [rows][S / 32]; below, every workgroup quantizes the
+ * shared rows into LDS itself). */
 int mkmoe_workspace_region(const mkmoe_shape* shape, int32_t region, size_t* offset,
                            size_t* bytes);
 

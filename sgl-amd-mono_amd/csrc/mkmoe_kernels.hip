@@ -144,7 +144,7 @@ struct Cfg {
   static constexpr int IR = IR_;
   static_assert(IR == I || (SHUF && IR % 32 == 0 && IR < I), "real width: whole MX blocks");
   // launches of at least QROWS rows quantize the intermediates once (stage Q, a hand-off of
-  // its own) instead of in every workgroup's down stage, and up to kSharedMidRows rows run
+  // its own) instead of in every workgroup's down stage, and up to shared_mid_rows<C>() rows run
   // the shared expert's down inside that hand-off. Measured: 7-8 % faster at 48 rows, 1.4 to
   // 4 us faster at 8 rows (MXFP4 at I = 512 gains only with the shared down inside the
   // hand-off), 0.3-2 us slower at 1 and 2 rows (the hand-off costs more than the work it saves).
@@ -3472,15 +3472,21 @@ __device__ __forceinline__ void stage_q(const Params& p, const Union<C>& un, int
 }
 
 // launches of up to this many rows (and with stage Q) run the shared expert's down inside the
-// Q hand-off (above, its rows' quantize outlasts the hand-off)
-constexpr int kSharedMidRows = 16;
+// Q hand-off; above, the shared rows' quantize and units outlast the hand-off and hold up the
+// routed down. 16 where the routed down is FP8 or wide (at 24 rows cfg 2 +1.9 us, cfg 5 +2.1),
+// 24 on the narrow MXFP4 and the MX shared shapes (cfg 3 -1.9, cfg 4 -1.3, V4.1 TP2 -1.1, TP4
+// -0.3; at 48 rows +0.5 to +2.7: measured)
+template <class C>
+constexpr int shared_mid_rows() {
+  return C::SFMT == kFp8Mx || (C::FMT == kFp4 && C::I <= 640) ? 24 : 16;
+}
 
 // the persistent launch past its C arrival: the down stage's first weights depend on the
 // union alone, so they are requested before the wait for the other workgroups' gate_up. GQ
 // (launches of C::QROWS rows or more): stage Q first. PRE: workgroups [0, nsw) ran the shared
 // expert's gate_up in the routing window and set their flags at B, so the first tile's shared
 // down runs before the wait (its rows quantized here). MID (with stage Q, up to
-// kSharedMidRows rows): the first tile's shared down runs inside the Q hand-off, from units
+// shared_mid_rows<C>() rows): the first tile's shared down runs inside the Q hand-off, from units
 // in registers, its rows quantized here. Each combination is a code path of its own, so that
 // neither path's registers are allocated around the other's
 template <class C, bool MF, bool GQ, bool PRE = false, bool MID = false>
@@ -3621,13 +3627,13 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
   const bool gq = p.rows >= C::QROWS;
   if (C::SHUF || down_on_mfma<C>(p.rows, p.mfma_down)) {
     // the shared down before the C wait below stage Q's rows, inside the Q hand-off up to
-    // kSharedMidRows rows, else after the routed down
+    // shared_mid_rows<C>() rows, else after the routed down
     if (nsw > 0 && kPreShared && !gq) {
       // the shared down before the C wait (the shared intermediate was stored in the routing
       // window). (With stage Q, from 8 rows, it cost 1-4 us there against after the routed
       // down or inside the Q hand-off: measured)
       wait_then_d<C, true, false, true>(p, un, sm.d, b, nwg, nsw);
-    } else if (gq && p.rows <= kSharedMidRows) {
+    } else if (gq && p.rows <= shared_mid_rows<C>()) {
       wait_then_d<C, true, true, false, true>(p, un, sm.d, b, nwg);
     } else if (gq) {
       wait_then_d<C, true, true>(p, un, sm.d, b, nwg);
