@@ -175,8 +175,9 @@ typedef struct mkmoe_options {
   /* Test fault injection, the reference's SGLANG_AMD_MONO_FAULT_INJECT (common/guard.py:69-89:
    * a wait that stalls and times out). fault_stage 0: none; else workgroup fault_workgroup's
    * wait at that stage (the MKMOE_ERRW_STAGE codes of the persistent launch's waits: 1 norm,
-   * 2 router part sums and x codes, 3 route (up to 8 rows: the routing published to the
-   * workgroups that run the shared expert's gate_up meanwhile, and their shared intermediate
+   * 2 router part sums and x codes, 3 route (up to 8 rows, 4 on the 384-expert shape at
+   * inter 1152: the routing published to the workgroups that run the shared expert's gate_up
+   * meanwhile, and their shared intermediate
    * awaited before the shared down), 4 gate_up, 6 quantize) ignores what it waits for and runs
    * to the deadline, then records the error words with MKMOE_ERRW_FAULT set and the launch
    * goes on, as after any deadline. A stage the launch does not wait at (6 below the shape's

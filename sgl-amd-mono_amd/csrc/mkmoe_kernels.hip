@@ -863,8 +863,13 @@ constexpr int kRouteRows = 16;
 // rows up to which every workgroup routes the whole step itself (no routing hand-off). Above,
 // a workgroup a row and the hand-off cost less than every workgroup's scores of all the rows:
 // 8 against 16 at 12 and 16 rows, cfg 2 -2.8 / -3.4 us, cfg 3 -3.6 / -5.6, V4.1 TP4 -6.1 /
-// -5.4 (its 384 sqrt(softplus) scores a row); lower, mixed (measured)
+// -5.4 (its 384 sqrt(softplus) scores a row); lower, mixed, but V4.1 at TP2 gains with 4
+// (-0.6 / -1.6 / -1.8 us at 5 / 6 / 8 rows: measured)
 constexpr int kLocalRouteMax = 8;
+template <class C>
+constexpr int local_route_max() {
+  return C::E > 256 && C::I >= 1024 ? 4 : kLocalRouteMax;
+}
 
 template <class C>
 struct RouteSmem {
@@ -3050,7 +3055,7 @@ constexpr bool kPreShared = MKMOE_PRE_SHARED != 0;
 // The shared expert's gate_up units run while the step is routed, by workgroups [w0, w0 + n)
 // that route nothing meanwhile, with the gate_up on MFMA: its weights stream during the
 // routing, and the rest of the gate_up is dealt afterwards.
-//   - up to kLocalRouteMax rows (every other workgroup routes the step itself): workgroups
+//   - up to local_route_max<C>() rows (every other workgroup routes the step itself): workgroups
 //     [0, n), three quarters of the grid at most, take all k of its units between them (a
 //     unit each where k <= n);
 //   - above (workgroups [0, R) route a row each, then the B hand-off): workgroups [R, R + n)
@@ -3063,7 +3068,7 @@ template <class C>
 __device__ __forceinline__ EarlyShared early_shared(const Params& p, int nwg) {
   if (!kEarlyShared || !gate_on_mfma<C>(p.rows, p.mfma_gate)) return {0, 0, 0};
   const int n_sh = GuDeal<C>::shared_units(p.rows);
-  if (p.rows <= kLocalRouteMax) return {0, min(n_sh, 3 * nwg / 4), n_sh};
+  if (p.rows <= local_route_max<C>()) return {0, min(n_sh, 3 * nwg / 4), n_sh};
   const int n = min(n_sh, nwg - p.rows);
   return {p.rows, n, n};
 }
@@ -3583,7 +3588,7 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
     // flag at B first (no row to route), and the routing hand-off after the units
     int lo, hi;
     even_share(GuDeal<C>::HU * es.k, b - es.w0, es.n, lo, hi);
-    const bool local = p.rows <= kLocalRouteMax;
+    const bool local = p.rows <= local_route_max<C>();
     if (!local) arrive(p, kCtlB);
     gate_up_shared<C>(p, sm.g, lo, hi, [&] {
       await_all(p, kCtlA, nwg, kStageA);
@@ -3598,7 +3603,7 @@ __global__ __launch_bounds__(kThreads) void k_fused(Params p) {
     TL(kTlRouted);
     build_union<C>(p, un, false);
     TL(kTlUnion);
-  } else if (p.rows <= kLocalRouteMax) {
+  } else if (p.rows <= local_route_max<C>()) {
     // every workgroup routes the step itself, reading the router's part sums as they land:
     // no routing hand-off; the A hand-off (the x codes) is awaited before the gate_up. The
     // last workgroup publishes the routing (the workspace copies, then its flag at B) for

@@ -57,7 +57,7 @@ def _runner(c):
 
 
 @pytest.mark.parametrize(
-    "workload,rows", [(WORKLOAD, r) for r in (1, 2, 8, 9, 16, 17, 24, 48)] + [(TP2, r) for r in (1, 8, 9, 16, 17, 48)]
+    "workload,rows", [(WORKLOAD, r) for r in (1, 2, 8, 9, 16, 17, 24, 48)] + [(TP2, r) for r in (1, 4, 5, 8, 9, 16, 17, 48)]
 )
 def test_parity_v41(workload, rows):
     from gpu_case import errors, record_accuracy
